@@ -1,0 +1,287 @@
+/*
+ * xdna_engine.h -- C ABI of the MI355X (gfx950) decode backend.
+ *
+ * Drop-in for xdna-engine's fused decode hot path: the device layer replaces
+ * the XRT shim (rust/npu-xrt/shim/xrt_shim.h:16-113), the op layer replaces
+ * CtxDecode (rust/npu-asr/src/ctx_decode.rs:142-694) and the decoder layer
+ * replaces the decode-backend contract of HostDecoder / FusedDecoder /
+ * BatchedFusedDecoder (rust/npu-engine/src/asr/whisper_decoder.rs:204-1831)
+ * and Opt::step/generate (rust/npu-whisper/src/bin/opt125m_decode.rs:252-315).
+ *
+ * Conventions (mirroring rust/npu-capi/src/lib.rs:11-41 and
+ * rust/npu-xrt/shim/xrt_shim.cpp:42-56):
+ *   - Every entry point catches all C++ exceptions; failures return NULL or a
+ *     negative value and set a thread-local message read by xe_last_error().
+ *   - Handles are opaque; the caller destroys what it creates.
+ *   - Host buffers passed in are only read (or written) during the call.
+ *   - A handle is not thread-safe; one decode context per stream.
+ *   - Weight matrices are [M, K] row-major (out-major, nn.Linear layout)
+ *     unless XE_LAYOUT_KN is given, which is the reference's [K, N] layout
+ *     (opt125m_decode.rs:30-31, ctx_decode.rs:269-317).
+ */
+#ifndef XDNA_ENGINE_H
+#define XDNA_ENGINE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define XE_ABI_VERSION 1
+
+typedef struct xe_device xe_device;
+typedef struct xe_buf xe_buf;
+typedef struct xe_ctx xe_ctx;
+typedef struct xe_weight xe_weight;
+typedef struct xe_decoder xe_decoder;
+
+/* element types */
+enum xe_dtype {
+  XE_F32 = 0,
+  XE_BF16 = 1,
+  XE_I8 = 2,    /* int8 symmetric, per-output-row fp32 scale */
+  XE_BFP16 = 3, /* 8 int8 mantissas per block + one biased 8-bit exponent */
+  XE_I32 = 4
+};
+
+/* pre-norm of the fused norm+GEMV (ctx_decode.rs:74-79 Norm) */
+enum xe_norm {
+  XE_NORM_NONE = 0,
+  XE_NORM_LN = 1,    /* LayerNorm(gamma, beta, eps), population variance */
+  XE_NORM_RMS = 2,   /* RMSNorm: x * inv_rms * gamma */
+  XE_NORM_RMS1P = 3  /* Gemma RMSNorm: x * inv_rms * (1 + w) */
+};
+
+enum xe_layout { XE_LAYOUT_MK = 0, XE_LAYOUT_KN = 1 };
+
+/* ------------------------------------------------------------------------ */
+/* errors / version                                                         */
+/* ------------------------------------------------------------------------ */
+
+/* Thread-local message of the last failed call (xrt_shim.cpp:42-56,
+ * npu-capi/src/lib.rs:11-16).  Never NULL; "" when no error. */
+const char *xe_last_error(void);
+int xe_abi_version(void);
+
+/* ------------------------------------------------------------------------ */
+/* device layer (xrt_shim.h:16-113)                                         */
+/* ------------------------------------------------------------------------ */
+
+/* Number of visible GPUs (0 when none). */
+int xe_device_count(void);
+/* shim_device_open(index) (xrt_shim.h:20). */
+xe_device *xe_device_open(int ordinal);
+/* shim_device_close (xrt_shim.h:21). */
+void xe_device_close(xe_device *dev);
+/* Wait for all work queued on the device's stream. */
+int xe_device_synchronize(xe_device *dev);
+/* Device name (e.g. "gfx950") into buf; returns bytes written or -1. */
+int xe_device_name(xe_device *dev, char *buf, int cap);
+
+/* shim_bo_alloc (xrt_shim.h:30-33): device memory of nbytes. */
+xe_buf *xe_buf_alloc(xe_device *dev, size_t nbytes);
+/* shim_bo_free (xrt_shim.h:34). */
+void xe_buf_free(xe_buf *buf);
+/* shim_bo_write + sync_to_device (xrt_shim.h:37-40): host -> device. */
+int xe_buf_write(xe_buf *buf, const void *src, size_t nbytes, size_t offset);
+/* sync_from_device + shim_bo_read (xrt_shim.h:38-41): device -> host. */
+int xe_buf_read(xe_buf *buf, void *dst, size_t nbytes, size_t offset);
+/* Device address of the buffer (for the *_dev entry points). */
+void *xe_buf_device_ptr(xe_buf *buf);
+size_t xe_buf_size(xe_buf *buf);
+
+/* ------------------------------------------------------------------------ */
+/* op layer (CtxDecode, ctx_decode.rs:142-694)                              */
+/* ------------------------------------------------------------------------ */
+
+/* CtxDecode::new (ctx_decode.rs:174-200). */
+xe_ctx *xe_ctx_create(xe_device *dev);
+void xe_ctx_destroy(xe_ctx *ctx);
+/* Kernel launches issued so far / reset (ctx_decode.rs:148-172). */
+uint64_t xe_ctx_dispatches(xe_ctx *ctx);
+void xe_ctx_reset_dispatches(xe_ctx *ctx);
+
+/* CtxDecode::register_weight (ctx_decode.rs:269-317): copy W (fp32, layout
+ * MK [m,k] or KN [k,m]) to the device, quantised to wdtype (XE_I8: per-row
+ * symmetric int8, scale = amax/127, round half away from zero, clamp +-127 --
+ * opt125m_decode.rs:45-62; XE_BFP16; XE_BF16 RNE).  bias may be NULL. */
+xe_weight *xe_register_weight(xe_ctx *ctx, int wdtype, int m, int k,
+                              const float *w, int layout, const float *bias);
+/* Pre-quantised int8 weight: q [m,k] row-major, scales [m] (fp32). */
+xe_weight *xe_register_weight_q8(xe_ctx *ctx, int m, int k, const int8_t *q,
+                                 const float *scales, const float *bias);
+/* Pre-encoded bfp16 weight: mant [m,k] int8, exps [m,k/8] biased (e+127). */
+xe_weight *xe_register_weight_bfp16(xe_ctx *ctx, int m, int k,
+                                    const int8_t *mant, const uint8_t *exps,
+                                    const float *bias);
+/* Pre-rounded bf16 weight: bits [m,k]. */
+xe_weight *xe_register_weight_bf16(xe_ctx *ctx, int m, int k,
+                                   const uint16_t *bits, const float *bias);
+/* CtxDecode::register_fused (ctx_decode.rs:566-612): a weight plus a pre-norm
+ * (enum xe_norm) applied to x on the device before the GEMV.  gamma/beta have
+ * k elements (beta only for XE_NORM_LN). */
+xe_weight *xe_register_fused(xe_ctx *ctx, int wdtype, int m, int k,
+                             const float *w, int layout, int norm,
+                             const float *gamma, const float *beta, float eps,
+                             const float *bias);
+/* Attach a pre-norm to an already registered weight (q8/bfp16/bf16). */
+int xe_weight_set_norm(xe_weight *w, int norm, const float *gamma,
+                       const float *beta, float eps);
+void xe_weight_free(xe_weight *w);
+int xe_weight_shape(const xe_weight *w, int *m, int *k, int *wdtype);
+
+/* CtxDecode::gemv (ctx_decode.rs:325-366), batched: y[b,m] = W x[b,k]
+ * (+ bias), fp32 out.  x_dtype XE_F32 or XE_BF16 (host pointer). */
+int xe_gemv(xe_ctx *ctx, const xe_weight *w, const void *x, int x_dtype,
+            int batch, float *y);
+/* CtxDecode::fused_norm_gemv (ctx_decode.rs:617-643). */
+int xe_fused_norm_gemv(xe_ctx *ctx, const xe_weight *w, const void *x,
+                       int x_dtype, int batch, float *y);
+/* Device-pointer form of xe_gemv / xe_fused_norm_gemv (no host copies; the
+ * weight's pre-norm, if any, is applied).  Asynchronous on the ctx stream. */
+int xe_gemv_dev(xe_ctx *ctx, const xe_weight *w, const void *x_dev,
+                int x_dtype, int batch, float *y_dev);
+
+/* int8 activations x int8 weights -> int32 (ctx2.rs:771-830 device part):
+ * acc[b,m] = sum_k xq[b,k] * q[m,k], exact.  w must be XE_I8. */
+int xe_gemv_i8act(xe_ctx *ctx, const xe_weight *w, const int8_t *xq,
+                  int batch, int32_t *acc);
+int xe_gemv_i8act_dev(xe_ctx *ctx, const xe_weight *w, const int8_t *xq_dev,
+                      int batch, int32_t *acc_dev);
+/* W8A8 dynamic linear (ctx2.rs:771-830, 1352-1435): per-tensor activation
+ * scale amax/127, int8 x int8 -> i32 on the device, dequant in the order
+ * (acc * scale_a) * ws[c] + bias[c].  scale_a_out may be NULL. */
+int xe_w8a8_linear(xe_ctx *ctx, const xe_weight *w, const float *x,
+                   int batch, float *y, float *scale_a_out);
+
+/* Single-query attention over a bf16 KV cache (CtxDecode::attn,
+ * ctx_decode.rs:468-555; mha_decode.cc:90-175), generalised to GQA,
+ * per-sequence lengths and long contexts.
+ *   q     fp32 [batch, hq, hd]
+ *   kc,vc bf16 [batch, hkv, max_ctx, hd]
+ *   lens  int32 [batch] (1 <= lens[i] <= max_ctx)
+ *   out   fp32 [batch, hq, hd]
+ * scores = (q . k) * scale; softmax over positions [0, lens[i]). */
+int xe_attn_decode(xe_ctx *ctx, const float *q, const uint16_t *kc,
+                   const uint16_t *vc, const int32_t *lens, int batch, int hq,
+                   int hkv, int hd, int max_ctx, float scale, float *out);
+int xe_attn_decode_dev(xe_ctx *ctx, const float *q_dev, const uint16_t *kc_dev,
+                       const uint16_t *vc_dev, const int32_t *lens_dev,
+                       int batch, int hq, int hkv, int hd, int max_ctx,
+                       float scale, float *out_dev);
+
+/* Wait for the ctx stream; returns 0 or -1. */
+int xe_ctx_synchronize(xe_ctx *ctx);
+
+/* ------------------------------------------------------------------------ */
+/* decoder layer (decode-backend contract)                                  */
+/* ------------------------------------------------------------------------ */
+
+enum xe_family { XE_OPT = 0, XE_WHISPER = 1, XE_GEMMA3 = 2 };
+
+typedef struct xe_model_config {
+  int family;      /* enum xe_family */
+  int n_layers;
+  int d_model;
+  int n_heads;     /* query heads */
+  int n_kv_heads;
+  int head_dim;
+  int ffn;
+  int vocab;
+  int max_pos;     /* learned position rows (OPT table has max_pos + 2) */
+  int max_ctx;     /* KV capacity per sequence */
+  int wdtype;      /* XE_I8 / XE_BF16 / XE_BFP16 for linears + embedding */
+  float eps;
+  float rope_theta;
+  int n_cross;     /* Whisper encoder frames (0 otherwise) */
+} xe_model_config;
+
+/* Tensor kinds of a decoder (names follow the reference weight files:
+ * opt125m_decode.rs:155-181, whisper_decoder.rs LayerWeights, HF Gemma3).
+ * Layer tensors are addressed with (kind, layer); global ones use layer -1.
+ * Matrices are [out, in]. */
+enum xe_tensor {
+  XE_T_TOK_EMB = 0, /* [vocab, d]; also the tied lm-head */
+  XE_T_POS_EMB = 1, /* [max_pos(+2 for OPT), d] learned positions */
+  XE_T_LNF_W = 2,   /* final norm (OPT ln_final, Whisper ln_post, Gemma norm) */
+  XE_T_LNF_B = 3,
+  XE_T_ENC_OUT = 4, /* synthetic Whisper encoder output [n_cross, d] */
+  XE_T_LN1_W = 8,   /* self-attn pre-norm */
+  XE_T_LN1_B = 9,
+  XE_T_Q_W = 10,
+  XE_T_Q_B = 11,
+  XE_T_K_W = 12,
+  XE_T_K_B = 13,
+  XE_T_V_W = 14,
+  XE_T_V_B = 15,
+  XE_T_O_W = 16,
+  XE_T_O_B = 17,
+  XE_T_LN2_W = 18,  /* FFN pre-norm (Gemma pre_feedforward_layernorm) */
+  XE_T_LN2_B = 19,
+  XE_T_FC1_W = 20,  /* fc1 / Gemma gate_proj */
+  XE_T_FC1_B = 21,
+  XE_T_UP_W = 22,   /* Gemma up_proj */
+  XE_T_FC2_W = 23,  /* fc2 / Gemma down_proj */
+  XE_T_FC2_B = 24,
+  XE_T_QNORM_W = 25,
+  XE_T_KNORM_W = 26,
+  XE_T_POST_ATTN_W = 27,
+  XE_T_POST_FFN_W = 28,
+  XE_T_LNX_W = 29,  /* Whisper cross-attn pre-norm */
+  XE_T_LNX_B = 30,
+  XE_T_XQ_W = 31,
+  XE_T_XQ_B = 32,
+  XE_T_XK_W = 33,
+  XE_T_XV_W = 34,
+  XE_T_XV_B = 35,
+  XE_T_XO_W = 36,
+  XE_T_XO_B = 37,
+  XE_T_COUNT = 38
+};
+
+/* Synthetic-weight stream id of a tensor (the counter-based generator keys
+ * every element by (seed, id, index)). */
+#define XE_SYNTH_ID(kind, layer) \
+  ((uint32_t)((layer) < 0 ? (kind) : 64 * ((layer) + 1) + (kind)))
+
+/* Create a decoder (weights uninitialised).  max_batch streams. */
+xe_decoder *xe_decoder_create(xe_device *dev, const xe_model_config *cfg,
+                              int max_batch);
+void xe_decoder_destroy(xe_decoder *dec);
+/* Fill every weight with the seeded synthetic generator, on the device. */
+int xe_decoder_init_synthetic(xe_decoder *dec, uint64_t seed);
+/* Upload one fp32 tensor ([out,in] for matrices); quantised like
+ * xe_register_weight.  Returns 0 or -1 (unknown kind / wrong size). */
+int xe_decoder_set_tensor(xe_decoder *dec, int kind, int layer,
+                          const float *data, size_t count);
+/* Read back a quantised int8 tensor (q [rows*cols], scales [rows]). */
+int xe_decoder_get_tensor_q8(xe_decoder *dec, int kind, int layer, int8_t *q,
+                             float *scales);
+/* reset() (whisper_decoder.rs:1235-1243): clear every stream's KV cache. */
+int xe_decoder_reset(xe_decoder *dec);
+/* precompute_cross (whisper_decoder.rs:1143-1232): enc [n_cross, d] fp32, or
+ * NULL to use the synthetic XE_T_ENC_OUT tensor of the last init. */
+int xe_decoder_set_cross(xe_decoder *dec, const float *enc);
+/* step(tok, pos) -> logits (whisper_decoder.rs:1293-1349) for `batch`
+ * streams with per-stream positions.  logits [batch, vocab] may be NULL;
+ * next [batch] receives the greedy token (argmax with the family's tie
+ * rule: OPT last max, Whisper/Gemma first max) and may be NULL. */
+int xe_decoder_step(xe_decoder *dec, const int32_t *tokens,
+                    const int32_t *pos, int batch, float *logits,
+                    int32_t *next);
+/* Greedy generation (Opt::generate, opt125m_decode.rs:296-315): feed
+ * prompt [batch, n_prompt] from position 0, then emit n_new tokens per
+ * stream into out [batch, n_new].  The token loop runs in a HIP graph. */
+int xe_decoder_generate(xe_decoder *dec, const int32_t *prompt, int n_prompt,
+                        int batch, int n_new, int32_t *out);
+/* Mean device time (microseconds) of the last generate's decode steps. */
+double xe_decoder_last_step_us(xe_decoder *dec);
+/* Bytes of weights one decode step streams (int8/bf16/bfp16 + scales). */
+uint64_t xe_decoder_weight_bytes(xe_decoder *dec);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

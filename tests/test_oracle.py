@@ -1,0 +1,395 @@
+"""Pins of the CPU oracle (CPU only).
+
+Each test checks an oracle function against something other than its own
+formula: the reference's in-source known-answer vectors
+(tests/golden/reference_vectors.json, extracted by extract_reference_vectors.py),
+an independent implementation (torch's bfloat16 cast, math.erf, numpy int64),
+closed forms, invariants, or brute force.  A plausible mistake (dropped term,
+wrong sign/index, transposed operand, wrong rounding mode) fails one of them.
+"""
+import ctypes as C
+import json
+import math
+import os
+
+import numpy as np
+import pytest
+
+import oracle_lib as O
+
+GOLD = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "reference_vectors.json")))
+
+
+def L():
+    return O.lib()
+
+
+def lcg_bits(seed, n):
+    """The reference's LCG (npu-xrt/src/lib.rs:1109-1113): s = s*1664525 + 1013904223."""
+    out = np.empty(n, np.uint32)
+    s = seed
+    for i in range(n):
+        s = (s * 1664525 + 1013904223) & 0xFFFFFFFF
+        out[i] = s
+    return out
+
+
+# ---------------------------------------------------------------- bf16 ----
+
+def test_bf16_round_reference_values():
+    for case in GOLD["bf16_round"]:
+        got = L().xo_bf16_round(case["x"])
+        assert abs(got - case["expected"]) <= case["tol"], case
+    assert math.isnan(L().xo_bf16_round(float("nan")))
+
+
+def test_bf16_unpack_exhaustive():
+    # every bf16 pattern (npu-xrt/src/lib.rs:1063-1074): unpack is <<16
+    bits = np.arange(65536, dtype=np.uint32)
+    got = np.empty(65536, np.float32)
+    L().xo_unpack_bf16(bits.astype(np.uint16), got, 65536)
+    assert np.array_equal(got.view(np.uint32), bits << 16)
+
+
+def test_bf16_pack_matches_torch_rne_on_lcg_sweep():
+    torch = pytest.importorskip("torch")
+    specials = np.array([0.0, -0.0, 1.0, -1.0, 0.5, -0.5, 1e-30, -1e-30, 1e30, -1e30,
+                         np.finfo(np.float32).tiny, np.finfo(np.float32).max,
+                         -np.finfo(np.float32).max, np.inf, -np.inf, 3.14159, 2.71828,
+                         65504.0, 1.0 / 3.0, 1.5, -2.5, 0.123], np.float32)
+    sweep = lcg_bits(0x12345678, 200_000).view(np.float32)
+    x = np.concatenate([specials, sweep])
+    got = O.bf16_bits(x)
+    finite = ~np.isnan(x)
+    want = torch.from_numpy(x[finite].copy()).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(got[finite], want)
+    # NaN rule of f32_to_bf16_bits: (bits >> 16) | 0x40 (quiet), payload kept
+    nb = x[~finite].view(np.uint32)
+    assert np.array_equal(got[~finite], ((nb >> 16) | 0x40).astype(np.uint16))
+
+
+def test_bf16_pack_unpack_roundtrip_idempotent():
+    src = (lcg_bits(0xC0FFEE11, 4099) & 0xFFFF0000).view(np.float32)
+    ok = ~np.isnan(src)
+    back = O.bf16_to_f32(O.bf16_bits(src))
+    assert np.array_equal(back[ok].view(np.uint32), src[ok].view(np.uint32))
+
+
+# ------------------------------------------------------- norms / acts ----
+
+def test_layer_norm_reference_vectors():
+    g = GOLD["layer_norm"]
+    x = np.array(g["x"], np.float32)
+    out = np.empty(8, np.float32)
+    L().xo_layer_norm(x, g["rows"], g["d"], np.array(g["gamma"], np.float32),
+                      np.array(g["beta"], np.float32), g["eps"], out)
+    assert np.max(np.abs(out - np.array(g["expected"], np.float32))) < g["tol"]
+
+
+def test_layer_norm_normalize_reference_vectors():
+    g = GOLD["layer_norm_normalize"]
+    x = np.array(g["x"], np.float32)
+    out = np.empty(8, np.float32)
+    L().xo_layer_norm_normalize(x, g["rows"], g["d"], g["eps"], out)
+    assert np.max(np.abs(out - np.array(g["expected"], np.float32))) < g["tol"]
+
+
+def test_layer_norm_constant_row_gives_beta():
+    x = np.full(64, 3.25, np.float32)
+    gamma = np.linspace(0.5, 2, 64).astype(np.float32)
+    beta = np.linspace(-1, 1, 64).astype(np.float32)
+    out = np.empty(64, np.float32)
+    L().xo_layer_norm(x, 1, 64, gamma, beta, 1e-5, out)
+    assert np.array_equal(out, beta)
+
+
+def test_rmsnorm_reference_unit_and_closed_form():
+    # rmsnorm_unit (npu-gemma/src/lib.rs:83-91)
+    x = np.array([3.0, -3.0, 3.0, -3.0], np.float32)
+    out = np.empty(4, np.float32)
+    L().xo_rmsnorm(x, 4, np.zeros(4, np.float32), 1e-6, out)
+    assert np.all(np.abs(np.abs(out) - 1.0) < 1e-3)
+    # closed form: +-c with weight w -> sign * c / sqrt(c^2 + eps) * (1 + w)
+    w = np.array([0.5, -0.25, 0.0, 1.0], np.float32)
+    L().xo_rmsnorm(x, 4, w, 1e-6, out)
+    want = np.sign(x) * 3.0 / math.sqrt(9.0 + 1e-6) * (1.0 + w)
+    assert np.allclose(out, want, rtol=1e-6)
+
+
+def test_rope_reference_vectors():
+    g = GOLD["rope"]
+    x = np.array(g["x"], np.float32)
+    out = np.empty_like(x)
+    L().xo_rope(x, g["rows"], g["n_heads"], g["head_dim"], np.array(g["cos"], np.float32),
+                np.array(g["sin"], np.float32), out)
+    assert np.max(np.abs(out - np.array(g["expected"], np.float32))) < g["tol"]
+
+
+def test_erf_as_published_bound_and_symmetry():
+    xs = np.linspace(-6, 6, 4001)
+    for v in xs[::7]:
+        a = L().xo_erf_as(float(v))
+        assert abs(a - math.erf(float(v))) < 5e-7   # A&S 1.5e-7 + f32 evaluation
+        assert a == -L().xo_erf_as(float(-v)) or v == 0
+
+
+def test_gelu_erf_properties():
+    assert L().xo_gelu_erf(0.0) == 0.0
+    for v in np.linspace(-5, 5, 101):
+        v = float(np.float32(v))
+        g, gm = L().xo_gelu_erf(v), L().xo_gelu_erf(-v)
+        assert abs((g - gm) - v) < 1e-5          # gelu(x) - gelu(-x) = x
+        exact = 0.5 * v * (1 + math.erf(v / math.sqrt(2)))
+        assert abs(g - exact) < 2e-6 * max(1.0, abs(v))
+
+
+def test_gelu_tanh_reference_and_bound():
+    # geglu_shapes: gelu(0) = 0 (npu-gemma/src/lib.rs:93-99)
+    assert L().xo_gelu_tanh(0.0) == 0.0
+    for v in np.linspace(-6, 6, 241):
+        v = float(v)
+        exact = 0.5 * v * (1 + math.erf(v / math.sqrt(2)))
+        assert abs(L().xo_gelu_tanh(v) - exact) < 1e-3
+
+
+def test_fast_exp_accuracy_reference_bound():
+    # test_fast_exp_accuracy (npu-asr-host/src/lib.rs:847-859)
+    xs = np.arange(-60.0, 0.0, 0.013)
+    worst = max(abs(L().xo_fast_exp_nonpos(float(v)) - math.exp(v)) / math.exp(v) for v in xs)
+    assert worst < 5e-4
+
+
+# ------------------------------------------------------------- quant ----
+
+def test_quant_i8_rounding_half_away_and_clamp():
+    q = L().xo_quant_i8
+    assert q(0.5, 1.0) == 1 and q(-0.5, 1.0) == -1      # Rust round(), not half-even
+    assert q(2.5, 1.0) == 3 and q(-2.5, 1.0) == -3
+    assert q(1.49, 1.0) == 1 and q(200.0, 1.0) == 127 and q(-200.0, 1.0) == -127
+
+
+def test_quant_rows_equals_reference_column_layout():
+    rng = np.random.default_rng(0)
+    w_kn = rng.standard_normal((48, 40)).astype(np.float32) * 0.02
+    w_kn[:, 7] = 0.0                               # all-zero column -> scale 1.0
+    qk = np.empty((48, 40), np.int8)
+    sk = np.empty(40, np.float32)
+    L().xo_quant_cols_i8(w_kn, 48, 40, qk, sk)
+    qr, sr = O.quant_rows_i8(w_kn.T.copy())
+    assert np.array_equal(qr, qk.T) and np.array_equal(sr, sk)
+    assert sk[7] == 1.0 and not qk[:, 7].any()
+    # the max-magnitude element of each column lands exactly on +-127
+    idx = np.argmax(np.abs(w_kn), axis=0)
+    cols = [c for c in range(40) if c != 7]
+    assert all(abs(int(qk[idx[c], c])) == 127 for c in cols)
+
+
+def test_gemv_i8_matches_reference_kn_loop_bitwise():
+    rng = np.random.default_rng(1)
+    k, n, b = 96, 80, 3
+    w_kn = rng.standard_normal((k, n)).astype(np.float32)
+    qk = np.empty((k, n), np.int8)
+    s = np.empty(n, np.float32)
+    L().xo_quant_cols_i8(w_kn, k, n, qk, s)
+    x = rng.standard_normal((b, k)).astype(np.float32)
+    bias = rng.standard_normal(n).astype(np.float32)
+    y_kn = np.empty((b, n), np.float32)
+    L().xo_lin_fwd_i8_kn(x, b, k, n, qk, s, O.ptr(bias), y_kn)
+    y_mk = O.gemv_i8(x, qk.T.copy(), s, bias)
+    assert np.array_equal(y_kn.view(np.uint32), y_mk.view(np.uint32))
+
+
+def test_gemv_i8_integer_inputs_exact():
+    rng = np.random.default_rng(2)
+    q = rng.integers(-127, 128, (33, 64)).astype(np.int8)
+    x = rng.integers(-8, 9, (2, 64)).astype(np.float32)
+    s = np.ones(33, np.float32)
+    want = x.astype(np.int64) @ q.astype(np.int64).T
+    assert np.array_equal(O.gemv_i8(x, q, s), want.astype(np.float32))
+
+
+def test_w8a8_int32_bruteforce_and_dequant_order():
+    rng = np.random.default_rng(3)
+    a = rng.integers(-127, 128, (5, 64)).astype(np.int8)
+    w = rng.integers(-127, 128, (24, 64)).astype(np.int8)
+    acc = np.empty((5, 24), np.int32)
+    L().xo_gemm_i8i8_i32(a, 5, 64, w, 24, acc)
+    assert np.array_equal(acc, a.astype(np.int64) @ w.astype(np.int64).T)
+    # dequant order (acc * scale_a) * ws + bias: differs from acc * (scale_a * ws)
+    sa = np.float32(0.0123)
+    ws = rng.uniform(0.001, 0.02, 24).astype(np.float32)
+    bias = rng.standard_normal(24).astype(np.float32)
+    out = np.empty((5, 24), np.float32)
+    L().xo_dequant_epi(acc, 5, 24, sa, ws, O.ptr(bias), out)
+    want = (acc.astype(np.float32) * sa) * ws[None, :] + bias[None, :]
+    other = acc.astype(np.float32) * (sa * ws[None, :]) + bias[None, :]
+    assert np.array_equal(out, want.astype(np.float32))
+    assert not np.array_equal(want.astype(np.float32), other.astype(np.float32))
+
+
+def test_quant_scale_zero_guard():
+    assert L().xo_quant_scale(np.zeros(16, np.float32), 16) == 1.0
+    assert L().xo_quant_scale(np.array([0.0, -2.54, 1.0], np.float32), 3) == np.float32(2.54) / np.float32(127.0)
+
+
+# ------------------------------------------------------------- bfp16 ----
+
+def test_bfp16_exact_on_representable_blocks():
+    rng = np.random.default_rng(4)
+    # blocks whose values are integer multiples of their quantum with |q| <= 127
+    m, k = 6, 64
+    e = rng.integers(-10, 10, (m, k // 8))
+    q = rng.integers(-127, 128, (m, k))
+    q[:, ::8] = np.where(rng.random((m, k // 8)) < 0.5, 127, 64)  # block max sets exponent
+    w = (q * np.ldexp(1.0, np.repeat(e, 8, axis=1) - 6)).astype(np.float32)
+    mant, exps = O.bfp16_encode(w)
+    back = O.bfp16_decode(mant, exps)
+    assert np.array_equal(back, w)
+    assert np.array_equal(exps.astype(np.int64) - 127, e)
+
+
+def test_bfp16_error_bound_and_saturation():
+    rng = np.random.default_rng(5)
+    w = rng.standard_normal((16, 128)).astype(np.float32)
+    mant, exps = O.bfp16_encode(w)
+    back = O.bfp16_decode(mant, exps)
+    wb = O.bf16_to_f32(O.bf16_bits(w)).reshape(w.shape)
+    quantum = np.repeat(np.ldexp(1.0, exps.astype(np.int64) - 127 - 6), 8, axis=1)
+    # within half a quantum, except the saturated +128 case (one quantum)
+    err = np.abs(back - wb)
+    assert np.all(err <= quantum * 1.0 + 1e-30)
+    sat = mant == 127
+    assert np.all(err[~sat] <= quantum[~sat] * 0.5 + 1e-30)
+    # block max magnitude lies in [64, 128) quanta -> mantissa of the max is 64..127 in size
+    blk = np.abs(wb).reshape(16, 16, 8).max(axis=2)
+    qmax = np.abs(mant.astype(np.int64)).reshape(16, 16, 8).max(axis=2)
+    assert np.all((qmax >= 64) & (qmax <= 128)) and np.all(blk > 0)
+
+
+# -------------------------------------------------- fused norm + gemv ----
+
+def _selftest_inputs():
+    """norm_gemv_probe.rs:79-83 deterministic 8x4 inputs (W as [K,N])."""
+    k, n = 8, 4
+    x = np.array([((i * 7 % 11) - 5.0) * 0.3 for i in range(k)])
+    gamma = np.array([1.0 + 0.1 * i for i in range(k)])
+    beta = np.array([0.05 * (i - 3.0) for i in range(k)])
+    bias = np.array([0.2 * (i - 1.0) for i in range(n)])
+    w = np.array([[(((kk * 5 + nn * 3) % 13) - 6.0) * 0.1 for nn in range(n)] for kk in range(k)])
+    return x, gamma, beta, bias, w
+
+
+def test_fold_identity_reference_selftest():
+    x, gamma, beta, bias, w_kn = _selftest_inputs()
+    f = lambda a: np.ascontiguousarray(a, np.float32)
+    w_mk = f(w_kn.T)
+    # direct: LN(x) then W, in f64 (the probe's golden)
+    mean, var = x.mean(), ((x - x.mean()) ** 2).mean()
+    xn = (x - mean) / math.sqrt(var + 1e-5) * gamma + beta
+    direct = w_kn.T @ xn + bias
+    # oracle norm + gemv (f32)
+    h = np.empty(8, np.float32)
+    L().xo_norm_row(f(x), 8, 1, O.ptr(f(gamma)), O.ptr(f(beta)), 1e-5, h)
+    y = np.array([float(np.dot(w_mk[r].astype(np.float64), h)) for r in range(4)]) + bias
+    assert np.max(np.abs(y - direct)) < 1e-5
+    # oracle fold: W'' and bias'; inv_std * ((x - mean) . W'') + bias'
+    wf = np.empty_like(w_mk)
+    bf = np.empty(4, np.float32)
+    L().xo_fold_weight(w_mk, 4, 8, f(gamma), O.ptr(f(beta)), O.ptr(f(bias)), wf, bf)
+    folded = (wf.astype(np.float64) @ (x - mean)) / math.sqrt(var + 1e-5) + bf
+    assert np.max(np.abs(folded - direct)) < 1e-5
+
+
+# --------------------------------------------------------- attention ----
+
+def test_attend_one_reference_mha_vectors():
+    g = GOLD["mha_no_round"]
+    t, H, hd = g["t"], g["n_heads"], g["head_dim"]
+    q = np.array(g["q"], np.float32).reshape(t, H * hd)
+    k = np.array(g["k"], np.float32)
+    v = np.array(g["v"], np.float32)
+    exp = np.array(g["expected"], np.float32).reshape(t, H * hd)
+    for i in range(t):  # unmasked mha row i = attend_one(q_i, K, V, t)
+        ctx = np.empty(H * hd, np.float32)
+        L().xo_attend_one(np.ascontiguousarray(q[i]), k, v, t, H, hd, ctx)
+        assert np.max(np.abs(ctx - exp[i])) < g["tol"]
+
+
+def _rand_cache(rng, b, hkv, ctx, hd):
+    kf = rng.standard_normal((b, hkv, ctx, hd)).astype(np.float32)
+    vf = rng.standard_normal((b, hkv, ctx, hd)).astype(np.float32)
+    return O.bf16_bits(kf), O.bf16_bits(vf)
+
+
+def test_attn_decode_closed_forms():
+    rng = np.random.default_rng(6)
+    kc, vc = _rand_cache(rng, 1, 1, 16, 64)
+    q = rng.standard_normal((1, 1, 64)).astype(np.float32)
+    # one key -> the value row
+    out = O.attn_decode(q, kc, vc, [1], 0.125)
+    assert np.array_equal(out[0, 0], O.bf16_to_f32(vc[0, 0, 0]))
+    # identical keys -> mean of the values
+    kc2 = np.repeat(kc[:, :, :1], 16, axis=2)
+    out = O.attn_decode(q, kc2, vc, [10], 0.125)
+    want = O.bf16_to_f32(vc[0, 0, :10]).astype(np.float64).mean(axis=0)
+    assert np.allclose(out[0, 0], want, rtol=1e-5, atol=1e-6)
+
+
+def test_attn_decode_matches_attend_one_and_online():
+    rng = np.random.default_rng(7)
+    H, hd, S = 4, 64, 37
+    kc, vc = _rand_cache(rng, 1, H, S, hd)
+    q = rng.standard_normal((1, H, hd)).astype(np.float32)
+    out = O.attn_decode(q, kc, vc, [S], 1.0 / math.sqrt(hd))
+    # attend_one on [S, H*hd] rows of the same (bf16-valued) data
+    kf = O.bf16_to_f32(kc[0]).transpose(1, 0, 2).reshape(S, H * hd).copy()
+    vf = O.bf16_to_f32(vc[0]).transpose(1, 0, 2).reshape(S, H * hd).copy()
+    ctx = np.empty(H * hd, np.float32)
+    L().xo_attend_one(np.ascontiguousarray(q.reshape(-1)), kf, vf, S, H, hd, ctx)
+    assert np.allclose(out.reshape(-1), ctx, rtol=1e-6, atol=1e-7)
+    for h in range(H):
+        on = np.empty(hd, np.float32)
+        L().xo_attn_online(np.ascontiguousarray(q[0, h]), np.ascontiguousarray(kc[0, h]),
+                           np.ascontiguousarray(vc[0, h]), S, hd, 1.0 / math.sqrt(hd), on)
+        assert np.allclose(on, out[0, h], rtol=1e-5, atol=1e-6)
+
+
+def test_attn_decode_gqa_mapping_and_lengths():
+    rng = np.random.default_rng(8)
+    b, hq, hkv, hd, ctx = 3, 4, 1, 64, 50
+    kc, vc = _rand_cache(rng, b, hkv, ctx, hd)
+    q = rng.standard_normal((b, hq, hd)).astype(np.float32)
+    lens = np.array([50, 7, 23], np.int32)
+    out = O.attn_decode(q, kc, vc, lens, 0.125)
+    for bi in range(b):
+        for h in range(hq):  # each q head against the single kv head, own length
+            o1 = O.attn_decode(q[bi:bi + 1, h:h + 1].copy(), kc[bi:bi + 1].copy(),
+                               vc[bi:bi + 1].copy(), lens[bi:bi + 1], 0.125)
+            assert np.array_equal(o1[0, 0], out[bi, h])
+    # positions beyond the length are ignored
+    kc2 = kc.copy()
+    kc2[1, 0, 7:] = 0x7F80  # +inf keys past the length
+    assert np.array_equal(O.attn_decode(q, kc2, vc, lens, 0.125)[1], out[1])
+
+
+# ---------------------------------------------------------------- argmax --
+
+def test_argmax_tie_rules():
+    v = np.array([1.0, 3.0, 2.0, 3.0, 0.0], np.float32)
+    assert L().xo_argmax_first(v, 5) == 1      # whisper.rs:749-757 (strict >)
+    assert L().xo_argmax_last(v, 5) == 3       # Iterator::max_by: last of equal maxima
+
+
+# ------------------------------------------------------------- synth ----
+
+def test_synth_statistics_and_determinism():
+    a = O.synth_fill(7, 1234, 0.0, 0.02, 400_000)
+    b = O.synth_fill(7, 1234, 0.0, 0.02, 400_000)
+    c = O.synth_fill(7, 1235, 0.0, 0.02, 400_000)
+    assert np.array_equal(a, b) and not np.array_equal(a, c)
+    assert abs(a.mean()) < 2e-4 and abs(a.std() - 0.02) < 2e-4
+    one = O.synth_fill(3, 9, 1.0, 0.02, 200_000)
+    assert abs(one.mean() - 1.0) < 2e-4
+    # element i depends only on (seed, tensor, i)
+    base = L().xo_synth_base(7, 1234)
+    assert all(L().xo_synth_value(base, i, 0.0, 0.02) == a[i] for i in (0, 1, 99_999, 399_999))

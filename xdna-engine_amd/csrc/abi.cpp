@@ -1,0 +1,670 @@
+// abi.cpp -- extern "C" boundary of libxdna_engine.so: device layer (the
+// XRT-shim analog, rust/npu-xrt/shim/xrt_shim.h:16-113) and op layer (the
+// CtxDecode analog, rust/npu-asr/src/ctx_decode.rs:142-694).
+//
+// Every entry point runs its body inside guard(): C++ exceptions and HIP
+// errors become a NULL / -1 return plus a thread-local message, the
+// convention of xrt_shim.cpp:42-56 and npu-capi/src/lib.rs:11-41.
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <mutex>
+
+#include "common.h"
+#include "quant.h"
+
+namespace xe {
+
+static thread_local std::string g_err;
+
+void set_error(const std::string &msg) { g_err = msg; }
+
+void fail(const std::string &msg) { throw Error(msg); }
+
+void hip_check(hipError_t e, const char *what, const char *file, int line) {
+  if (e != hipSuccess) {
+    char buf[512];
+    snprintf(buf, sizeof(buf), "%s failed: %s (%s:%d)", what, hipGetErrorString(e), file, line);
+    throw Error(buf);
+  }
+}
+
+DeviceGuard::DeviceGuard(int ordinal) {
+  XE_HIP(hipGetDevice(&prev));
+  if (prev != ordinal) XE_HIP(hipSetDevice(ordinal));
+}
+DeviceGuard::~DeviceGuard() {
+  int cur = -1;
+  if (hipGetDevice(&cur) == hipSuccess && prev >= 0 && cur != prev) (void)hipSetDevice(prev);
+}
+
+template <typename F>
+static auto guard(F &&f, decltype(f()) on_error) -> decltype(f()) {
+  try {
+    g_err.clear();
+    return f();
+  } catch (const std::exception &e) {
+    g_err = e.what();
+  } catch (...) {
+    g_err = "unknown C++ exception";
+  }
+  return on_error;
+}
+
+}  // namespace xe
+
+using namespace xe;
+
+// ---------------------------------------------------------------------------
+// ctx staging helpers
+// ---------------------------------------------------------------------------
+void *xe_ctx::ensure_scratch(size_t n) {
+  if (n > scratch_size) {
+    if (scratch) XE_HIP(hipFree(scratch));
+    scratch = nullptr;
+    scratch_size = 0;
+    XE_HIP(hipMalloc(&scratch, n));
+    scratch_size = n;
+  }
+  return scratch;
+}
+
+void *xe_ctx::ensure_pinned(size_t n) {
+  if (n > host_pinned_size) {
+    if (host_pinned) XE_HIP(hipHostFree(host_pinned));
+    host_pinned = nullptr;
+    host_pinned_size = 0;
+    XE_HIP(hipHostMalloc(&host_pinned, n, hipHostMallocDefault));
+    host_pinned_size = n;
+  }
+  return host_pinned;
+}
+
+void xe_ctx::ensure_attn(size_t work_floats, size_t counters) {
+  if (work_floats > attn_work_floats) {
+    if (attn_work) XE_HIP(hipFree(attn_work));
+    attn_work = nullptr;
+    attn_work_floats = 0;
+    XE_HIP(hipMalloc(&attn_work, work_floats * sizeof(float)));
+    attn_work_floats = work_floats;
+  }
+  if (counters > attn_counter_count) {
+    if (attn_counters) XE_HIP(hipFree(attn_counters));
+    attn_counters = nullptr;
+    attn_counter_count = 0;
+    XE_HIP(hipMalloc(&attn_counters, counters * sizeof(unsigned int)));
+    XE_HIP(hipMemsetAsync(attn_counters, 0, counters * sizeof(unsigned int), dev->stream));
+    attn_counter_count = counters;
+  }
+}
+
+namespace {
+
+template <typename T>
+T *dev_upload(const T *src, size_t n, hipStream_t s) {
+  T *d = nullptr;
+  XE_HIP(hipMalloc(reinterpret_cast<void **>(&d), n * sizeof(T)));
+  if (src) {
+    XE_HIP(hipMemcpyAsync(d, src, n * sizeof(T), hipMemcpyHostToDevice, s));
+    XE_HIP(hipStreamSynchronize(s));
+  }
+  return d;
+}
+
+void free_weight(xe_weight *w) {
+  if (!w) return;
+  if (w->owns) {
+    (void)hipFree(w->w);
+    (void)hipFree(w->scale);
+    (void)hipFree(w->exps);
+    (void)hipFree(w->bias);
+    (void)hipFree(w->gamma);
+    (void)hipFree(w->beta);
+  }
+  delete w;
+}
+
+xe_weight *new_weight(xe_ctx *ctx, int wdtype, int m, int k) {
+  XE_REQUIRE(ctx && ctx->dev, "null ctx");
+  XE_REQUIRE(m > 0 && k > 0, "weight shape must be positive");
+  XE_REQUIRE(k % 16 == 0, "weight K must be a multiple of 16");
+  XE_REQUIRE(wdtype == XE_I8 || wdtype == XE_BF16 || wdtype == XE_BFP16, "unknown weight dtype");
+  auto *w = new xe_weight;
+  w->ctx = ctx;
+  w->wdtype = wdtype;
+  w->m = m;
+  w->k = k;
+  return w;
+}
+
+// Row-major [m,k] fp32 from either layout.
+std::vector<float> to_mk(const float *w, int m, int k, int layout) {
+  std::vector<float> out(static_cast<size_t>(m) * k);
+  if (layout == XE_LAYOUT_MK) {
+    std::memcpy(out.data(), w, out.size() * sizeof(float));
+  } else {
+    XE_REQUIRE(layout == XE_LAYOUT_KN, "unknown weight layout");
+    for (int r = 0; r < k; r++)
+      for (int c = 0; c < m; c++) out[static_cast<size_t>(c) * k + r] = w[static_cast<size_t>(r) * m + c];
+  }
+  return out;
+}
+
+void fill_weight_from_f32(xe_weight *wt, const float *w_mk, const float *bias) {
+  const int m = wt->m, k = wt->k;
+  hipStream_t s = wt->ctx->dev->stream;
+  const size_t n = static_cast<size_t>(m) * k;
+  if (wt->wdtype == XE_I8) {
+    std::vector<int8_t> q(n);
+    std::vector<float> sc(m);
+    quant_rows_i8(w_mk, m, k, q.data(), sc.data());
+    wt->w = dev_upload(q.data(), n, s);
+    wt->scale = dev_upload(sc.data(), m, s);
+  } else if (wt->wdtype == XE_BF16) {
+    std::vector<uint16_t> b(n);
+    for (size_t i = 0; i < n; i++) b[i] = f32_to_bf16_bits(w_mk[i]);
+    wt->w = dev_upload(b.data(), n, s);
+  } else {
+    std::vector<int8_t> mant(n);
+    std::vector<uint8_t> ex(n / 8);
+    bfp16_encode(w_mk, m, k, mant.data(), ex.data());
+    wt->w = dev_upload(mant.data(), n, s);
+    wt->exps = dev_upload(ex.data(), n / 8, s);
+  }
+  if (bias) wt->bias = dev_upload(bias, m, s);
+}
+
+void set_norm(xe_weight *w, int norm, const float *gamma, const float *beta, float eps) {
+  XE_REQUIRE(norm >= XE_NORM_NONE && norm <= XE_NORM_RMS1P, "unknown norm kind");
+  hipStream_t s = w->ctx->dev->stream;
+  if (w->owns) {
+    (void)hipFree(w->gamma);
+    (void)hipFree(w->beta);
+  }
+  w->gamma = w->beta = nullptr;
+  w->norm = norm;
+  w->eps = eps;
+  if (norm == XE_NORM_NONE) return;
+  XE_REQUIRE(gamma, "norm needs gamma");
+  w->gamma = dev_upload(gamma, w->k, s);
+  if (norm == XE_NORM_LN) {
+    XE_REQUIRE(beta, "LayerNorm needs beta");
+    w->beta = dev_upload(beta, w->k, s);
+  }
+}
+
+GemvLaunch gemv_args(const xe_weight *w, const void *x, int x_dtype, int batch, float *y) {
+  GemvLaunch g;
+  g.wdtype = w->wdtype;
+  g.w = w->w;
+  g.scale = w->scale;
+  g.exps = w->exps;
+  g.bias = w->bias;
+  g.m = w->m;
+  g.k = w->k;
+  g.x = x;
+  g.x_dtype = x_dtype;
+  g.ldx = w->k;
+  g.batch = batch;
+  g.norm = w->norm;
+  g.gamma = w->gamma;
+  g.beta = w->beta;
+  g.eps = w->eps;
+  g.y = y;
+  g.ldy = w->m;
+  return g;
+}
+
+int run_gemv_host(xe_ctx *ctx, const xe_weight *w, const void *x, int x_dtype, int batch,
+                  float *y) {
+  XE_REQUIRE(ctx && w && x && y, "null argument");
+  XE_REQUIRE(x_dtype == XE_F32 || x_dtype == XE_BF16, "x dtype must be XE_F32 or XE_BF16");
+  XE_REQUIRE(batch >= 1 && batch <= 8, "gemv batch must be 1..8");
+  DeviceGuard dg(ctx->dev->ordinal);
+  hipStream_t s = ctx->dev->stream;
+  const size_t xbytes = static_cast<size_t>(batch) * w->k * (x_dtype == XE_F32 ? 4 : 2);
+  const size_t ybytes = static_cast<size_t>(batch) * w->m * 4;
+  char *d = static_cast<char *>(ctx->ensure_scratch(xbytes + ybytes + 256));
+  void *dx = d;
+  float *dy = reinterpret_cast<float *>(d + ((xbytes + 255) / 256) * 256);
+  XE_HIP(hipMemcpyAsync(dx, x, xbytes, hipMemcpyHostToDevice, s));
+  launch_gemv(gemv_args(w, dx, x_dtype, batch, dy), s);
+  ctx->dispatches++;
+  XE_HIP(hipMemcpyAsync(y, dy, ybytes, hipMemcpyDeviceToHost, s));
+  XE_HIP(hipStreamSynchronize(s));
+  return 0;
+}
+
+}  // namespace
+
+// ===========================================================================
+// extern "C"
+// ===========================================================================
+extern "C" {
+
+const char *xe_last_error(void) { return g_err.c_str(); }
+int xe_abi_version(void) { return XE_ABI_VERSION; }
+
+int xe_device_count(void) {
+  return guard([&]() -> int {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) return 0;
+    return n;
+  }, -1);
+}
+
+xe_device *xe_device_open(int ordinal) {
+  return guard([&]() -> xe_device * {
+    int n = 0;
+    XE_HIP(hipGetDeviceCount(&n));
+    XE_REQUIRE(ordinal >= 0 && ordinal < n, "device ordinal out of range");
+    XE_HIP(hipSetDevice(ordinal));
+    auto *d = new xe_device;
+    d->ordinal = ordinal;
+    hipDeviceProp_t prop;
+    XE_HIP(hipGetDeviceProperties(&prop, ordinal));
+    d->arch = prop.gcnArchName;
+    d->num_cus = prop.multiProcessorCount;
+    d->max_lds = prop.sharedMemPerBlock;
+    // default priority: other priorities have hung on this hardware pool
+    XE_HIP(hipStreamCreateWithFlags(&d->stream, hipStreamNonBlocking));
+    return d;
+  }, nullptr);
+}
+
+void xe_device_close(xe_device *dev) {
+  guard([&]() -> int {
+    if (!dev) return 0;
+    DeviceGuard dg(dev->ordinal);
+    (void)hipStreamSynchronize(dev->stream);
+    (void)hipStreamDestroy(dev->stream);
+    delete dev;
+    return 0;
+  }, -1);
+}
+
+int xe_device_synchronize(xe_device *dev) {
+  return guard([&]() -> int {
+    XE_REQUIRE(dev, "null device");
+    DeviceGuard dg(dev->ordinal);
+    XE_HIP(hipStreamSynchronize(dev->stream));
+    return 0;
+  }, -1);
+}
+
+int xe_device_name(xe_device *dev, char *buf, int cap) {
+  return guard([&]() -> int {
+    XE_REQUIRE(dev && buf && cap > 0, "null argument");
+    int n = snprintf(buf, cap, "%s", dev->arch.c_str());
+    return n < cap ? n : cap - 1;
+  }, -1);
+}
+
+xe_buf *xe_buf_alloc(xe_device *dev, size_t nbytes) {
+  return guard([&]() -> xe_buf * {
+    XE_REQUIRE(dev, "null device");
+    XE_REQUIRE(nbytes > 0, "zero-size buffer");
+    DeviceGuard dg(dev->ordinal);
+    auto *b = new xe_buf;
+    b->dev = dev;
+    b->size = nbytes;
+    if (hipMalloc(&b->ptr, nbytes) != hipSuccess) {
+      delete b;
+      fail("hipMalloc of " + std::to_string(nbytes) + " bytes failed");
+    }
+    return b;
+  }, nullptr);
+}
+
+void xe_buf_free(xe_buf *buf) {
+  guard([&]() -> int {
+    if (!buf) return 0;
+    DeviceGuard dg(buf->dev->ordinal);
+    (void)hipStreamSynchronize(buf->dev->stream);
+    (void)hipFree(buf->ptr);
+    delete buf;
+    return 0;
+  }, -1);
+}
+
+int xe_buf_write(xe_buf *buf, const void *src, size_t nbytes, size_t offset) {
+  return guard([&]() -> int {
+    XE_REQUIRE(buf && src, "null argument");
+    XE_REQUIRE(offset <= buf->size && nbytes <= buf->size - offset, "write out of bounds");
+    DeviceGuard dg(buf->dev->ordinal);
+    XE_HIP(hipMemcpyAsync(static_cast<char *>(buf->ptr) + offset, src, nbytes,
+                          hipMemcpyHostToDevice, buf->dev->stream));
+    XE_HIP(hipStreamSynchronize(buf->dev->stream));
+    return 0;
+  }, -1);
+}
+
+int xe_buf_read(xe_buf *buf, void *dst, size_t nbytes, size_t offset) {
+  return guard([&]() -> int {
+    XE_REQUIRE(buf && dst, "null argument");
+    XE_REQUIRE(offset <= buf->size && nbytes <= buf->size - offset, "read out of bounds");
+    DeviceGuard dg(buf->dev->ordinal);
+    XE_HIP(hipMemcpyAsync(dst, static_cast<char *>(buf->ptr) + offset, nbytes,
+                          hipMemcpyDeviceToHost, buf->dev->stream));
+    XE_HIP(hipStreamSynchronize(buf->dev->stream));
+    return 0;
+  }, -1);
+}
+
+void *xe_buf_device_ptr(xe_buf *buf) { return buf ? buf->ptr : nullptr; }
+size_t xe_buf_size(xe_buf *buf) { return buf ? buf->size : 0; }
+
+// ---- op layer ------------------------------------------------------------
+
+xe_ctx *xe_ctx_create(xe_device *dev) {
+  return guard([&]() -> xe_ctx * {
+    XE_REQUIRE(dev, "null device");
+    auto *c = new xe_ctx;
+    c->dev = dev;
+    return c;
+  }, nullptr);
+}
+
+void xe_ctx_destroy(xe_ctx *ctx) {
+  guard([&]() -> int {
+    if (!ctx) return 0;
+    DeviceGuard dg(ctx->dev->ordinal);
+    (void)hipStreamSynchronize(ctx->dev->stream);
+    if (ctx->scratch) (void)hipFree(ctx->scratch);
+    if (ctx->host_pinned) (void)hipHostFree(ctx->host_pinned);
+    if (ctx->attn_work) (void)hipFree(ctx->attn_work);
+    if (ctx->attn_counters) (void)hipFree(ctx->attn_counters);
+    delete ctx;
+    return 0;
+  }, -1);
+}
+
+uint64_t xe_ctx_dispatches(xe_ctx *ctx) { return ctx ? ctx->dispatches : 0; }
+void xe_ctx_reset_dispatches(xe_ctx *ctx) {
+  if (ctx) ctx->dispatches = 0;
+}
+
+int xe_ctx_synchronize(xe_ctx *ctx) {
+  return guard([&]() -> int {
+    XE_REQUIRE(ctx, "null ctx");
+    DeviceGuard dg(ctx->dev->ordinal);
+    XE_HIP(hipStreamSynchronize(ctx->dev->stream));
+    return 0;
+  }, -1);
+}
+
+xe_weight *xe_register_weight(xe_ctx *ctx, int wdtype, int m, int k, const float *w,
+                              int layout, const float *bias) {
+  return guard([&]() -> xe_weight * {
+    XE_REQUIRE(w, "null weight");
+    DeviceGuard dg(ctx ? ctx->dev->ordinal : 0);
+    xe_weight *wt = new_weight(ctx, wdtype, m, k);
+    try {
+      std::vector<float> mk = to_mk(w, m, k, layout);
+      fill_weight_from_f32(wt, mk.data(), bias);
+    } catch (...) {
+      free_weight(wt);
+      throw;
+    }
+    return wt;
+  }, nullptr);
+}
+
+xe_weight *xe_register_weight_q8(xe_ctx *ctx, int m, int k, const int8_t *q, const float *scales,
+                                 const float *bias) {
+  return guard([&]() -> xe_weight * {
+    XE_REQUIRE(q && scales, "null weight or scales");
+    DeviceGuard dg(ctx ? ctx->dev->ordinal : 0);
+    xe_weight *wt = new_weight(ctx, XE_I8, m, k);
+    hipStream_t s = ctx->dev->stream;
+    wt->w = dev_upload(q, static_cast<size_t>(m) * k, s);
+    wt->scale = dev_upload(scales, m, s);
+    if (bias) wt->bias = dev_upload(bias, m, s);
+    return wt;
+  }, nullptr);
+}
+
+xe_weight *xe_register_weight_bfp16(xe_ctx *ctx, int m, int k, const int8_t *mant,
+                                    const uint8_t *exps, const float *bias) {
+  return guard([&]() -> xe_weight * {
+    XE_REQUIRE(mant && exps, "null mantissas or exponents");
+    DeviceGuard dg(ctx ? ctx->dev->ordinal : 0);
+    xe_weight *wt = new_weight(ctx, XE_BFP16, m, k);
+    hipStream_t s = ctx->dev->stream;
+    wt->w = dev_upload(mant, static_cast<size_t>(m) * k, s);
+    wt->exps = dev_upload(exps, static_cast<size_t>(m) * k / 8, s);
+    if (bias) wt->bias = dev_upload(bias, m, s);
+    return wt;
+  }, nullptr);
+}
+
+xe_weight *xe_register_weight_bf16(xe_ctx *ctx, int m, int k, const uint16_t *bits,
+                                   const float *bias) {
+  return guard([&]() -> xe_weight * {
+    XE_REQUIRE(bits, "null weight");
+    DeviceGuard dg(ctx ? ctx->dev->ordinal : 0);
+    xe_weight *wt = new_weight(ctx, XE_BF16, m, k);
+    hipStream_t s = ctx->dev->stream;
+    wt->w = dev_upload(bits, static_cast<size_t>(m) * k, s);
+    if (bias) wt->bias = dev_upload(bias, m, s);
+    return wt;
+  }, nullptr);
+}
+
+xe_weight *xe_register_fused(xe_ctx *ctx, int wdtype, int m, int k, const float *w, int layout,
+                             int norm, const float *gamma, const float *beta, float eps,
+                             const float *bias) {
+  return guard([&]() -> xe_weight * {
+    XE_REQUIRE(w, "null weight");
+    DeviceGuard dg(ctx ? ctx->dev->ordinal : 0);
+    xe_weight *wt = new_weight(ctx, wdtype, m, k);
+    try {
+      std::vector<float> mk = to_mk(w, m, k, layout);
+      fill_weight_from_f32(wt, mk.data(), bias);
+      set_norm(wt, norm, gamma, beta, eps);
+    } catch (...) {
+      free_weight(wt);
+      throw;
+    }
+    return wt;
+  }, nullptr);
+}
+
+int xe_weight_set_norm(xe_weight *w, int norm, const float *gamma, const float *beta, float eps) {
+  return guard([&]() -> int {
+    XE_REQUIRE(w, "null weight");
+    DeviceGuard dg(w->ctx->dev->ordinal);
+    set_norm(w, norm, gamma, beta, eps);
+    return 0;
+  }, -1);
+}
+
+void xe_weight_free(xe_weight *w) {
+  guard([&]() -> int {
+    if (!w) return 0;
+    DeviceGuard dg(w->ctx->dev->ordinal);
+    (void)hipStreamSynchronize(w->ctx->dev->stream);
+    free_weight(w);
+    return 0;
+  }, -1);
+}
+
+int xe_weight_shape(const xe_weight *w, int *m, int *k, int *wdtype) {
+  if (!w) {
+    set_error("null weight");
+    return -1;
+  }
+  if (m) *m = w->m;
+  if (k) *k = w->k;
+  if (wdtype) *wdtype = w->wdtype;
+  return 0;
+}
+
+int xe_gemv(xe_ctx *ctx, const xe_weight *w, const void *x, int x_dtype, int batch, float *y) {
+  return guard([&]() -> int {
+    XE_REQUIRE(!w || w->norm == XE_NORM_NONE,
+               "xe_gemv on a fused weight: use xe_fused_norm_gemv");
+    return run_gemv_host(ctx, w, x, x_dtype, batch, y);
+  }, -1);
+}
+
+int xe_fused_norm_gemv(xe_ctx *ctx, const xe_weight *w, const void *x, int x_dtype, int batch,
+                       float *y) {
+  return guard([&]() -> int { return run_gemv_host(ctx, w, x, x_dtype, batch, y); }, -1);
+}
+
+int xe_gemv_dev(xe_ctx *ctx, const xe_weight *w, const void *x_dev, int x_dtype, int batch,
+                float *y_dev) {
+  return guard([&]() -> int {
+    XE_REQUIRE(ctx && w && x_dev && y_dev, "null argument");
+    XE_REQUIRE(x_dtype == XE_F32 || x_dtype == XE_BF16, "x dtype must be XE_F32 or XE_BF16");
+    XE_REQUIRE(batch >= 1 && batch <= 8, "gemv batch must be 1..8");
+    DeviceGuard dg(ctx->dev->ordinal);
+    launch_gemv(gemv_args(w, x_dev, x_dtype, batch, y_dev), ctx->dev->stream);
+    ctx->dispatches++;
+    return 0;
+  }, -1);
+}
+
+int xe_gemv_i8act_dev(xe_ctx *ctx, const xe_weight *w, const int8_t *xq_dev, int batch,
+                      int32_t *acc_dev) {
+  return guard([&]() -> int {
+    XE_REQUIRE(ctx && w && xq_dev && acc_dev, "null argument");
+    XE_REQUIRE(w->wdtype == XE_I8, "xe_gemv_i8act needs an XE_I8 weight");
+    DeviceGuard dg(ctx->dev->ordinal);
+    launch_gemv_i8act(static_cast<const int8_t *>(w->w), xq_dev, w->m, w->k, batch, acc_dev,
+                      ctx->dev->stream);
+    ctx->dispatches++;
+    return 0;
+  }, -1);
+}
+
+int xe_gemv_i8act(xe_ctx *ctx, const xe_weight *w, const int8_t *xq, int batch, int32_t *acc) {
+  return guard([&]() -> int {
+    XE_REQUIRE(ctx && w && xq && acc, "null argument");
+    XE_REQUIRE(w->wdtype == XE_I8, "xe_gemv_i8act needs an XE_I8 weight");
+    XE_REQUIRE(batch >= 1 && batch <= 8, "batch must be 1..8");
+    DeviceGuard dg(ctx->dev->ordinal);
+    hipStream_t s = ctx->dev->stream;
+    const size_t xb = static_cast<size_t>(batch) * w->k;
+    const size_t ab = static_cast<size_t>(batch) * w->m * 4;
+    char *d = static_cast<char *>(ctx->ensure_scratch(xb + ab + 256));
+    int32_t *da = reinterpret_cast<int32_t *>(d + ((xb + 255) / 256) * 256);
+    XE_HIP(hipMemcpyAsync(d, xq, xb, hipMemcpyHostToDevice, s));
+    launch_gemv_i8act(static_cast<const int8_t *>(w->w), reinterpret_cast<int8_t *>(d), w->m,
+                      w->k, batch, da, s);
+    ctx->dispatches++;
+    XE_HIP(hipMemcpyAsync(acc, da, ab, hipMemcpyDeviceToHost, s));
+    XE_HIP(hipStreamSynchronize(s));
+    return 0;
+  }, -1);
+}
+
+int xe_w8a8_linear(xe_ctx *ctx, const xe_weight *w, const float *x, int batch, float *y,
+                   float *scale_a_out) {
+  return guard([&]() -> int {
+    XE_REQUIRE(ctx && w && x && y, "null argument");
+    XE_REQUIRE(w->wdtype == XE_I8, "xe_w8a8_linear needs an XE_I8 weight");
+    XE_REQUIRE(batch >= 1 && batch <= 8, "batch must be 1..8");
+    // forward_view_int8 (ctx2.rs:771-830): host activation quant, device
+    // int8 x int8 -> i32, host dequant in the exact order of dequant_epi.
+    const size_t n = static_cast<size_t>(batch) * w->k;
+    const float scale_a = quant_scale(x, n);
+    std::vector<int8_t> xq(n);
+    for (size_t i = 0; i < n; i++) xq[i] = quant_i8(x[i], scale_a);
+    std::vector<int32_t> acc(static_cast<size_t>(batch) * w->m);
+    XE_REQUIRE(xe_gemv_i8act(ctx, w, xq.data(), batch, acc.data()) == 0, g_err);
+    std::vector<float> ws(w->m), bias;
+    DeviceGuard dg(ctx->dev->ordinal);
+    XE_HIP(hipMemcpy(ws.data(), w->scale, w->m * 4, hipMemcpyDeviceToHost));
+    if (w->bias) {
+      bias.resize(w->m);
+      XE_HIP(hipMemcpy(bias.data(), w->bias, w->m * 4, hipMemcpyDeviceToHost));
+    }
+    dequant_epi(acc.data(), batch, w->m, scale_a, ws.data(), w->bias ? bias.data() : nullptr, y);
+    if (scale_a_out) *scale_a_out = scale_a;
+    return 0;
+  }, -1);
+}
+
+static int attn_impl(xe_ctx *ctx, const float *q, const uint16_t *kc, const uint16_t *vc,
+                     const int32_t *lens, int batch, int hq, int hkv, int hd, int max_ctx,
+                     float scale, float *out) {
+  AttnLaunch a;
+  a.q = q;
+  a.kc = const_cast<uint16_t *>(kc);
+  a.vc = const_cast<uint16_t *>(vc);
+  a.kv_batch_stride = static_cast<size_t>(hkv) * max_ctx * hd;
+  a.max_ctx = max_ctx;
+  a.batch = batch;
+  a.hq = hq;
+  a.hkv = hkv;
+  a.hd = hd;
+  a.scale = scale;
+  a.lens = lens;
+  a.out = out;
+  const int target = 4 * ctx->dev->num_cus;
+  int ms = target / (batch * hkv);
+  const int cap = (max_ctx + 31) / 32;
+  ms = ms < 1 ? 1 : ms;
+  ms = ms > cap ? cap : ms;
+  ms = ms > 256 ? 256 : ms;
+  a.max_splits = ms;
+  ctx->ensure_attn(attn_work_floats(batch, hq, hd, ms), static_cast<size_t>(batch) * hkv);
+  a.work = ctx->attn_work;
+  a.counters = ctx->attn_counters;
+  launch_attn(a, ctx->dev->stream);
+  ctx->dispatches++;
+  return 0;
+}
+
+int xe_attn_decode_dev(xe_ctx *ctx, const float *q_dev, const uint16_t *kc_dev,
+                       const uint16_t *vc_dev, const int32_t *lens_dev, int batch, int hq, int hkv,
+                       int hd, int max_ctx, float scale, float *out_dev) {
+  return guard([&]() -> int {
+    XE_REQUIRE(ctx && q_dev && kc_dev && vc_dev && lens_dev && out_dev, "null argument");
+    XE_REQUIRE(batch > 0 && hq > 0 && hkv > 0 && hd > 0, "bad shape");
+    DeviceGuard dg(ctx->dev->ordinal);
+    return attn_impl(ctx, q_dev, kc_dev, vc_dev, lens_dev, batch, hq, hkv, hd, max_ctx, scale,
+                     out_dev);
+  }, -1);
+}
+
+int xe_attn_decode(xe_ctx *ctx, const float *q, const uint16_t *kc, const uint16_t *vc,
+                   const int32_t *lens, int batch, int hq, int hkv, int hd, int max_ctx,
+                   float scale, float *out) {
+  return guard([&]() -> int {
+    XE_REQUIRE(ctx && q && kc && vc && lens && out, "null argument");
+    XE_REQUIRE(batch > 0 && hq > 0 && hkv > 0 && hd > 0 && max_ctx > 0, "bad shape");
+    for (int b = 0; b < batch; b++)
+      XE_REQUIRE(lens[b] >= 1 && lens[b] <= max_ctx, "lens[b] must be in [1, max_ctx]");
+    DeviceGuard dg(ctx->dev->ordinal);
+    hipStream_t s = ctx->dev->stream;
+    const size_t qn = static_cast<size_t>(batch) * hq * hd;
+    const size_t kvn = static_cast<size_t>(batch) * hkv * max_ctx * hd;
+    float *dq = nullptr, *dout = nullptr;
+    uint16_t *dk = nullptr, *dv = nullptr;
+    int32_t *dl = nullptr;
+    XE_HIP(hipMalloc(&dq, qn * 4));
+    XE_HIP(hipMalloc(&dout, qn * 4));
+    XE_HIP(hipMalloc(&dk, kvn * 2));
+    XE_HIP(hipMalloc(&dv, kvn * 2));
+    XE_HIP(hipMalloc(&dl, batch * 4));
+    struct Free {
+      void *p[5];
+      ~Free() {
+        for (void *x : p) (void)hipFree(x);
+      }
+    } fr{{dq, dout, dk, dv, dl}};
+    XE_HIP(hipMemcpyAsync(dq, q, qn * 4, hipMemcpyHostToDevice, s));
+    XE_HIP(hipMemcpyAsync(dk, kc, kvn * 2, hipMemcpyHostToDevice, s));
+    XE_HIP(hipMemcpyAsync(dv, vc, kvn * 2, hipMemcpyHostToDevice, s));
+    XE_HIP(hipMemcpyAsync(dl, lens, batch * 4, hipMemcpyHostToDevice, s));
+    attn_impl(ctx, dq, dk, dv, dl, batch, hq, hkv, hd, max_ctx, scale, dout);
+    XE_HIP(hipMemcpyAsync(out, dout, qn * 4, hipMemcpyDeviceToHost, s));
+    XE_HIP(hipStreamSynchronize(s));
+    return 0;
+  }, -1);
+}
+
+}  // extern "C"

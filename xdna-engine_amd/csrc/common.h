@@ -1,0 +1,179 @@
+// common.h -- internals shared by the HIP sources of libxdna_engine.so.
+//
+// Error model (rust/npu-xrt/shim/xrt_shim.cpp:42-56): internal code throws
+// xe::Error; every extern "C" entry point catches it (and anything else),
+// stores the message in a thread-local string and returns NULL / -1.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstring>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "../../include/xdna_engine.h"
+
+namespace xe {
+
+struct Error : std::runtime_error {
+  using std::runtime_error::runtime_error;
+};
+
+[[noreturn]] void fail(const std::string &msg);
+void hip_check(hipError_t e, const char *what, const char *file, int line);
+#define XE_HIP(call) ::xe::hip_check((call), #call, __FILE__, __LINE__)
+#define XE_REQUIRE(cond, msg)                        \
+  do {                                               \
+    if (!(cond)) ::xe::fail(std::string(msg));       \
+  } while (0)
+
+void set_error(const std::string &msg);
+
+// Scoped "make this device current" guard.
+struct DeviceGuard {
+  int prev = -1;
+  explicit DeviceGuard(int ordinal);
+  ~DeviceGuard();
+};
+
+}  // namespace xe
+
+// ---------------------------------------------------------------------------
+// Opaque handle bodies
+// ---------------------------------------------------------------------------
+
+struct xe_device {
+  int ordinal = 0;
+  hipStream_t stream = nullptr;  // default-priority stream owned by the device
+  std::string arch;
+  int num_cus = 0;
+  size_t max_lds = 0;
+};
+
+struct xe_buf {
+  xe_device *dev = nullptr;
+  void *ptr = nullptr;
+  size_t size = 0;
+};
+
+// A registered weight matrix [m, k] resident in HBM.
+//   XE_I8    q int8 [m,k] row-major + scale fp32 [m]
+//   XE_BF16  bits uint16 [m,k]
+//   XE_BFP16 mant int8 [m,k] + exps uint8 [m, k/8] (biased exponent e+127)
+struct xe_weight {
+  xe_ctx *ctx = nullptr;
+  int wdtype = XE_I8;
+  int m = 0, k = 0;
+  void *w = nullptr;       // device
+  float *scale = nullptr;  // device, XE_I8 only
+  uint8_t *exps = nullptr; // device, XE_BFP16 only
+  float *bias = nullptr;   // device or null
+  int norm = XE_NORM_NONE;
+  float *gamma = nullptr;  // device, k
+  float *beta = nullptr;   // device, k
+  float eps = 1e-5f;
+  bool owns = true;        // false for views into a decoder's arena
+};
+
+struct xe_ctx {
+  xe_device *dev = nullptr;
+  uint64_t dispatches = 0;
+  // reusable staging for the host-pointer entry points
+  void *scratch = nullptr;
+  size_t scratch_size = 0;
+  void *host_pinned = nullptr;
+  size_t host_pinned_size = 0;
+  // split-K attention workspace: partials + arrival counters (kept zeroed:
+  // the merging workgroup re-arms its counter)
+  float *attn_work = nullptr;
+  size_t attn_work_floats = 0;
+  unsigned int *attn_counters = nullptr;
+  size_t attn_counter_count = 0;
+  void *ensure_scratch(size_t n);
+  void *ensure_pinned(size_t n);
+  void ensure_attn(size_t work_floats, size_t counters);
+};
+
+namespace xe {
+
+// ---------------------------------------------------------------------------
+// Kernel launch surfaces (implemented in gemv.hip / attn.hip)
+// ---------------------------------------------------------------------------
+
+enum Act { ACT_NONE = 0, ACT_RELU = 1, ACT_GELU_ERF = 2, ACT_GEGLU_TANH = 3 };
+
+// One fused norm + GEMV launch.  y[b, m'] = epilogue(W . prologue(x)[b]).
+struct GemvLaunch {
+  // weights
+  int wdtype = XE_I8;
+  const void *w = nullptr;
+  const float *scale = nullptr;
+  const uint8_t *exps = nullptr;
+  const float *bias = nullptr;
+  int m = 0, k = 0;
+  // activations: x [batch, k] (x_dtype XE_F32 / XE_BF16), row stride ldx
+  const void *x = nullptr;
+  int x_dtype = XE_F32;
+  int ldx = 0;
+  int batch = 1;
+  // prologue: t = x (+ post(sub)); res_out <- t (block 0); h = norm(t)
+  const float *sub = nullptr;      // optional sublayer output [batch, k]
+  const float *post_w = nullptr;   // optional Gemma (1+w) RMSNorm on sub
+  float *res_out = nullptr;        // optional: updated residual [batch, k]
+  int norm = XE_NORM_NONE;
+  const float *gamma = nullptr;
+  const float *beta = nullptr;
+  float eps = 1e-5f;
+  // epilogue
+  int act = ACT_NONE;              // GEGLU pairs rows (2r gate, 2r+1 up)
+  float out_scale = 1.0f;          // multiplies (acc*scale + bias)
+  float *y = nullptr;              // [batch, ldy]
+  int ldy = 0;
+};
+
+void launch_gemv(const GemvLaunch &p, hipStream_t s);
+// int8 activations x int8 weights -> int32 (exact).
+void launch_gemv_i8act(const int8_t *q, const int8_t *xq, int m, int k, int batch,
+                       int32_t *acc, hipStream_t s);
+
+struct AttnLaunch {
+  // q fp32 [batch, q_stride] with the hq heads at q_off (head h at h*hd)
+  const float *q = nullptr;
+  int q_stride = 0;
+  // KV cache bf16 [batch, hkv, max_ctx, hd] (kv_batch_stride 0 = shared)
+  uint16_t *kc = nullptr;
+  uint16_t *vc = nullptr;
+  size_t kv_batch_stride = 0;  // elements between streams (0 = shared cache)
+  int max_ctx = 0;
+  int batch = 1, hq = 1, hkv = 1, hd = 64;
+  float scale = 1.0f;
+  // lengths: lens[b] if non-null, else (pos[b] + 1), else fixed_len
+  const int32_t *lens = nullptr;
+  const int32_t *pos = nullptr;
+  int fixed_len = 0;
+  // optional append of the new token's k/v (fp32 [batch, kv_stride]) at pos
+  const float *k_new = nullptr;
+  const float *v_new = nullptr;
+  int kv_new_stride = 0;
+  // optional Gemma per-head RMSNorm (1+w) + RoPE on q and the new k
+  const float *q_norm_w = nullptr;
+  const float *k_norm_w = nullptr;
+  float norm_eps = 1e-6f;
+  const float *rope_cos = nullptr;  // [max_ctx, hd/2]
+  const float *rope_sin = nullptr;
+  int div_norm = 0;                 // p = e / sum (OPT) instead of e * (1/sum)
+  // output fp32 [batch, out_stride], head h at h*hd
+  float *out = nullptr;
+  int out_stride = 0;
+  // workspace: partials + per-(b, kvh) arrival counters (zeroed once)
+  float *work = nullptr;
+  unsigned int *counters = nullptr;
+  int max_splits = 0;
+};
+
+size_t attn_work_floats(int batch, int hq, int hd, int max_splits);
+void launch_attn(const AttnLaunch &p, hipStream_t s);
+
+}  // namespace xe

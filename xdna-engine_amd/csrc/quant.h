@@ -1,0 +1,100 @@
+// quant.h -- host-side weight encoders of the product library (run once at
+// weight registration; the decode hot path never calls them).
+//
+//   quant_rows_i8   Lin::load int8 branch (opt125m_decode.rs:41-62) on an
+//                   out-major [m,k] matrix: scale = max|row|/127 (1.0 for an
+//                   all-zero row), q = round-half-away(w/scale) clamped +-127.
+//   f32_to_bf16_bits  npu-xrt/src/lib.rs:809-817 (RNE by integer bias).
+//   bfp16_encode    bfp16ebs8 of ffn_bfp16/golden_ffn_gemm.py:21-49: bf16 RNE
+//                   first, blocks of 8 along k share e = floor(log2 max|x|),
+//                   mantissa = round-half-even(x / 2^(e-6)); +128 (the sim's
+//                   overflow case) saturates to 127; stored exponent e + 127.
+//   quant_scale / quant_i8 / dequant_epi   W8A8 (ctx2.rs:1352-1435).
+#pragma once
+
+#include <cmath>
+#include <cstdint>
+#include <cstring>
+
+namespace xe {
+
+inline uint16_t f32_to_bf16_bits(float x) {
+  uint32_t bits;
+  std::memcpy(&bits, &x, 4);
+  if ((bits & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((bits >> 16) | 0x0040u);
+  const uint32_t bias = 0x00007fffu + ((bits >> 16) & 1u);
+  return static_cast<uint16_t>((bits + bias) >> 16);
+}
+
+inline float bf16_round(float x) {
+  const uint32_t b = static_cast<uint32_t>(f32_to_bf16_bits(x)) << 16;
+  float r;
+  std::memcpy(&r, &b, 4);
+  return r;
+}
+
+inline int8_t quant_i8(float x, float scale) {
+  float v = std::round(x / scale);
+  v = v < -127.0f ? -127.0f : (v > 127.0f ? 127.0f : v);
+  return static_cast<int8_t>(v);
+}
+
+inline float quant_scale(const float *a, size_t n) {
+  float amax = 0.f;
+  for (size_t i = 0; i < n; i++) {
+    const float v = std::fabs(a[i]);
+    amax = v > amax ? v : amax;
+  }
+  return amax > 0.0f ? amax / 127.0f : 1.0f;
+}
+
+inline void quant_rows_i8(const float *w, int m, int k, int8_t *q, float *s) {
+  for (int r = 0; r < m; r++) {
+    const float *row = w + static_cast<size_t>(r) * k;
+    float amax = 0.f;
+    for (int j = 0; j < k; j++) {
+      const float v = std::fabs(row[j]);
+      amax = v > amax ? v : amax;
+    }
+    const float sc = amax > 0.0f ? amax / 127.0f : 1.0f;
+    s[r] = sc;
+    for (int j = 0; j < k; j++) q[static_cast<size_t>(r) * k + j] = quant_i8(row[j], sc);
+  }
+}
+
+inline void bfp16_encode(const float *w, int m, int k, int8_t *mant, uint8_t *exps) {
+  const int nb = k / 8;
+  for (int r = 0; r < m; r++)
+    for (int bk = 0; bk < nb; bk++) {
+      float v[8];
+      float maxabs = 0.f;
+      for (int i = 0; i < 8; i++) {
+        v[i] = bf16_round(w[static_cast<size_t>(r) * k + bk * 8 + i]);
+        const float a = std::fabs(v[i]);
+        maxabs = a > maxabs ? a : maxabs;
+      }
+      if (maxabs == 0.0f) maxabs = 1.0f;
+      int e2 = 0;
+      (void)std::frexp(maxabs, &e2);  // maxabs = f * 2^e2, f in [0.5, 1)
+      int e = e2 - 1;                 // floor(log2(maxabs))
+      e = e < -127 ? -127 : (e > 127 ? 127 : e);
+      const float quantum = std::ldexp(1.0f, e - 6);
+      for (int i = 0; i < 8; i++) {
+        float qv = std::nearbyint(v[i] / quantum);
+        qv = qv > 127.0f ? 127.0f : (qv < -128.0f ? -128.0f : qv);
+        mant[static_cast<size_t>(r) * k + bk * 8 + i] = static_cast<int8_t>(qv);
+      }
+      exps[static_cast<size_t>(r) * nb + bk] = static_cast<uint8_t>(e + 127);
+    }
+}
+
+inline void dequant_epi(const int32_t *acc, int mp, int n, float scale_a, const float *ws,
+                        const float *bias, float *out) {
+  for (int r = 0; r < mp; r++)
+    for (int c = 0; c < n; c++) {
+      const float v = static_cast<float>(acc[static_cast<size_t>(r) * n + c]) * scale_a * ws[c];
+      out[static_cast<size_t>(r) * n + c] = bias ? v + bias[c] : v;
+    }
+}
+
+}  // namespace xe
