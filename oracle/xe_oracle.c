@@ -327,7 +327,9 @@ void xo_bfp16_encode(const float *w, int m, int k, int8_t *mant, uint8_t *exps) 
         maxabs = a > maxabs ? a : maxabs;
       }
       if (maxabs == 0.0f) maxabs = 1.0f;
-      int e = (int)floor(log2((double)maxabs));
+      int e2;
+      (void)frexpf(maxabs, &e2); /* maxabs = f * 2^e2, f in [0.5, 1): exact */
+      int e = e2 - 1;            /* floor(log2(maxabs)) */
       if (e < -127) e = -127;
       if (e > 127) e = 127;
       float quantum = ldexpf(1.0f, e - 6);
