@@ -276,6 +276,21 @@ int xe_decoder_step(xe_decoder *dec, const int32_t *tokens,
  * stream into out [batch, n_new].  The token loop runs in a HIP graph. */
 int xe_decoder_generate(xe_decoder *dec, const int32_t *prompt, int n_prompt,
                         int batch, int n_new, int32_t *out);
+/* Split form of generate: feed() resets positions to 0 and runs the prompt
+ * (the last prompt step emits the first new token); decode() runs n_steps
+ * more greedy steps from the device state, returning the tokens they emit
+ * (out [batch, n_steps], may be NULL) and the device time of the whole run
+ * measured with HIP events on the decoder stream (device_us, may be NULL). */
+int xe_decoder_feed(xe_decoder *dec, const int32_t *prompt, int n_prompt, int batch);
+int xe_decoder_decode(xe_decoder *dec, int batch, int n_steps, int32_t *out,
+                      double *device_us);
+/* One eager decode step with a HIP event after every launch (the step
+ * advances the streams like decode).  Per launch: a label (32-byte slots in
+ * labels), device microseconds and algorithmic bytes.  Returns the number of
+ * launches recorded (<= max_entries) or -1.  Phase-timing aid, the
+ * counterpart of FUSED_PHASE_TIMING (whisper_decoder.rs:741-779). */
+int xe_decoder_profile_step(xe_decoder *dec, int batch, int max_entries, char *labels,
+                            double *us, double *bytes);
 /* Mean device time (microseconds) of the last generate's decode steps. */
 double xe_decoder_last_step_us(xe_decoder *dec);
 /* Bytes of weights one decode step streams (int8/bf16/bfp16 + scales). */

@@ -80,21 +80,13 @@ void *xe_ctx::ensure_pinned(size_t n) {
   return host_pinned;
 }
 
-void xe_ctx::ensure_attn(size_t work_floats, size_t counters) {
+void xe_ctx::ensure_attn(size_t work_floats) {
   if (work_floats > attn_work_floats) {
     if (attn_work) XE_HIP(hipFree(attn_work));
     attn_work = nullptr;
     attn_work_floats = 0;
     XE_HIP(hipMalloc(&attn_work, work_floats * sizeof(float)));
     attn_work_floats = work_floats;
-  }
-  if (counters > attn_counter_count) {
-    if (attn_counters) XE_HIP(hipFree(attn_counters));
-    attn_counters = nullptr;
-    attn_counter_count = 0;
-    XE_HIP(hipMalloc(&attn_counters, counters * sizeof(unsigned int)));
-    XE_HIP(hipMemsetAsync(attn_counters, 0, counters * sizeof(unsigned int), dev->stream));
-    attn_counter_count = counters;
   }
 }
 
@@ -373,7 +365,6 @@ void xe_ctx_destroy(xe_ctx *ctx) {
     if (ctx->scratch) (void)hipFree(ctx->scratch);
     if (ctx->host_pinned) (void)hipHostFree(ctx->host_pinned);
     if (ctx->attn_work) (void)hipFree(ctx->attn_work);
-    if (ctx->attn_counters) (void)hipFree(ctx->attn_counters);
     delete ctx;
     return 0;
   }, -1);
@@ -605,14 +596,13 @@ static int attn_impl(xe_ctx *ctx, const float *q, const uint16_t *kc, const uint
   a.out = out;
   const int target = 4 * ctx->dev->num_cus;
   int ms = target / (batch * hkv);
-  const int cap = (max_ctx + 31) / 32;
+  const int cap = (max_ctx + 63) / 64;
   ms = ms < 1 ? 1 : ms;
   ms = ms > cap ? cap : ms;
-  ms = ms > 256 ? 256 : ms;
+  ms = ms > 64 ? 64 : ms;
   a.max_splits = ms;
-  ctx->ensure_attn(attn_work_floats(batch, hq, hd, ms), static_cast<size_t>(batch) * hkv);
+  ctx->ensure_attn(attn_work_floats(batch, hq, hd, ms));
   a.work = ctx->attn_work;
-  a.counters = ctx->attn_counters;
   launch_attn(a, ctx->dev->stream);
   ctx->dispatches++;
   return 0;

@@ -17,10 +17,12 @@
 //   * Each lane group keeps an online-softmax state (m, l, acc) per query head
 //     in registers, updated once per block of UK keys (log2 domain, exp2).
 //   * Lane groups merge by xor-shuffles, waves through LDS; the workgroup
-//     writes (m, l, acc) to the workspace.
-//   * The last workgroup of a (stream, kv head) to arrive -- an agent-scope
-//     acq_rel counter -- merges the partials and writes the output, then
-//     re-arms the counter.  No workgroup ever waits on another.
+//     writes (m, l, acc) to the workspace (or the output when one split
+//     covers the whole length).
+//   * A second small launch merges the splits of each (stream, kv head).
+//     (A last-arriving-workgroup merge needs device-scope release/acquire
+//     fences, which write back and invalidate L2 on this part and measured
+//     ~80 us per launch; the kernel boundary is cheaper.)
 // Fused in front (decode step): the Gemma per-head RMSNorm (1 + w) and RoPE of
 // q and the new k, and the bf16 append of the new k/v at position pos, done
 // by the workgroup whose range holds pos (the only one that reads it).
@@ -32,7 +34,7 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kWaves = 4;
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr int kMinChunk = 32;
+constexpr int kMinChunk = 64;  // keys per split at least (amortises per-workgroup setup)
 
 struct AttnParams {
   const float *q;
@@ -54,7 +56,6 @@ struct AttnParams {
   float *out;
   int out_stride;
   float *work;
-  unsigned int *counters;
   int max_splits;
 };
 
@@ -145,7 +146,6 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnParams p) {
 
   __shared__ float qs[G][HD];
   __shared__ float red[kWaves][G][HD + 2];
-  __shared__ int s_flag;
 
   const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
   const int len = stream_len(p, b);
@@ -177,9 +177,8 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnParams p) {
       kbase[static_cast<size_t>(posi) * HD + j] = f32_to_bf16_rne(kt[j]);
       vbase[static_cast<size_t>(posi) * HD + j] = f32_to_bf16_rne(vsrc[j]);
     }
-    __threadfence();
   }
-  __syncthreads();
+  __syncthreads();  // the appended row is read back by this workgroup only
 
   // ---- main loop: online softmax per lane group ----
   const int kg = lane / L, kl = lane % L;
@@ -321,73 +320,84 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(AttnParams p) {
       }
     }
   }
-  if (single) return;
+}
 
-  // ---- last arriving workgroup merges the splits ----
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    unsigned int *ctr = p.counters + b * p.hkv + kvh;
-    const unsigned int prev =
-        __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-    const bool last = prev == static_cast<unsigned int>(nsplits - 1);
-    if (last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_flag = last;
-  }
-  __syncthreads();
-  if (!s_flag) return;
-  __threadfence();
-
-  // weights per (head, split) in LDS (reuse red: needs G * nsplits floats)
-  float *wts = &red[0][0][0];
-  float *lsum = wts + G * p.max_splits;
-  for (int g = wave; g < G; g += kWaves) {
+// Merge the split partials of one (stream, kv head): weights exp2(m_s - M),
+// out = sum_s acc_s * w_s / sum_s l_s * w_s.  Grid (element block, kv head,
+// stream): each workgroup finishes 256 of the G*HD outputs.  A separate
+// launch: the kernel boundary publishes the partials, so no workgroup needs a
+// device-scope fence.
+template <int HD, int G>
+__global__ __launch_bounds__(kThreads) void attn_merge_kernel(AttnParams p) {
+  constexpr int MAXS = 256;
+  constexpr int HPB = kThreads >= HD ? kThreads / HD : 1;  // heads per block
+  __shared__ float wts[HPB][MAXS];
+  __shared__ float lsum[HPB];
+  const int kvh = blockIdx.y, b = blockIdx.z;
+  const int len = stream_len(p, b);
+  if (len <= 0) return;
+  int chunk, nsplits;
+  split_range(len, p.max_splits, chunk, nsplits);
+  if (nsplits == 1) return;  // the partial kernel wrote the output
+  const int t0 = blockIdx.x * kThreads;  // first output element of this block
+  if (t0 >= G * HD) return;
+  const int g0 = t0 / HD;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const float *wbase = p.work + (static_cast<size_t>(b) * p.hq + kvh * G) * p.max_splits * (HD + 2);
+  for (int hh = wave; hh < HPB; hh += kWaves) {
+    const int g = g0 + hh;
+    if (g >= G) break;
     float mx = -INFINITY;
     for (int sidx = lane; sidx < nsplits; sidx += 64)
-      mx = fmaxf(mx, __builtin_nontemporal_load(wbase + (static_cast<size_t>(g) * p.max_splits + sidx) * (HD + 2)));
+      mx = fmaxf(mx, wbase[(static_cast<size_t>(g) * p.max_splits + sidx) * (HD + 2)]);
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
     float ls = 0.f;
     for (int sidx = lane; sidx < nsplits; sidx += 64) {
       const float *src = wbase + (static_cast<size_t>(g) * p.max_splits + sidx) * (HD + 2);
-      const float ms = __builtin_nontemporal_load(src);
+      const float ms = src[0];
       const float f = ms == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ms - mx);
-      wts[g * p.max_splits + sidx] = f;
-      ls += __builtin_nontemporal_load(src + 1) * f;
+      wts[hh][sidx] = f;
+      ls += src[1] * f;
     }
     ls = wave_sum(ls);
-    if (lane == 0) lsum[g] = ls;
+    if (lane == 0) lsum[hh] = ls;
   }
   __syncthreads();
-  for (int t = threadIdx.x; t < G * HD; t += kThreads) {
-    const int g = t / HD, e = t % HD;
-    float at = 0.f;
-    for (int sidx = 0; sidx < nsplits; sidx++)
-      at += __builtin_nontemporal_load(wbase + (static_cast<size_t>(g) * p.max_splits + sidx) * (HD + 2) + 2 + e) *
-            wts[g * p.max_splits + sidx];
-    const float o = p.div_norm ? at / lsum[g] : at * (1.0f / lsum[g]);
-    p.out[static_cast<size_t>(b) * p.out_stride + (kvh * G + g) * HD + e] = o;
+  const int t = t0 + threadIdx.x;
+  if (t >= G * HD) return;
+  const int g = t / HD, e = t % HD, hh = g - g0;
+  const float *src = wbase + static_cast<size_t>(g) * p.max_splits * (HD + 2) + 2 + e;
+  float at0 = 0.f, at1 = 0.f;
+  int sidx = 0;
+  for (; sidx + 1 < nsplits; sidx += 2) {
+    at0 += src[static_cast<size_t>(sidx) * (HD + 2)] * wts[hh][sidx];
+    at1 += src[static_cast<size_t>(sidx + 1) * (HD + 2)] * wts[hh][sidx + 1];
   }
+  if (sidx < nsplits) at0 += src[static_cast<size_t>(sidx) * (HD + 2)] * wts[hh][sidx];
+  const float at = at0 + at1;
+  const float o = p.div_norm ? at / lsum[hh] : at * (1.0f / lsum[hh]);
+  p.out[static_cast<size_t>(b) * p.out_stride + (kvh * G + g) * HD + e] = o;
 }
 
 using AttnFn = void (*)(AttnParams);
 
 template <int HD>
-AttnFn pick_g(int g) {
+AttnFn pick_g(int g, bool merge) {
   switch (g) {
-    case 1: return attn_kernel<HD, 1>;
-    case 2: return attn_kernel<HD, 2>;
-    case 4: return attn_kernel<HD, 4>;
-    case 8: return attn_kernel<HD, 8>;
+    case 1: return merge ? attn_merge_kernel<HD, 1> : attn_kernel<HD, 1>;
+    case 2: return merge ? attn_merge_kernel<HD, 2> : attn_kernel<HD, 2>;
+    case 4: return merge ? attn_merge_kernel<HD, 4> : attn_kernel<HD, 4>;
+    case 8: return merge ? attn_merge_kernel<HD, 8> : attn_kernel<HD, 8>;
   }
   return nullptr;
 }
 
-AttnFn pick(int hd, int g) {
+AttnFn pick(int hd, int g, bool merge) {
   switch (hd) {
-    case 64: return pick_g<64>(g);
-    case 128: return pick_g<128>(g);
-    case 256: return pick_g<256>(g);
+    case 64: return pick_g<64>(g, merge);
+    case 128: return pick_g<128>(g, merge);
+    case 256: return pick_g<256>(g, merge);
   }
   return nullptr;
 }
@@ -401,14 +411,12 @@ size_t attn_work_floats(int batch, int hq, int hd, int max_splits) {
 void launch_attn(const AttnLaunch &L, hipStream_t s) {
   XE_REQUIRE(L.batch > 0 && L.hq > 0 && L.hkv > 0 && L.hq % L.hkv == 0, "attn: bad heads");
   XE_REQUIRE(L.max_ctx > 0, "attn: max_ctx must be > 0");
-  XE_REQUIRE(L.max_splits >= 1 && L.max_splits <= 1024, "attn: max_splits out of range");
-  XE_REQUIRE(L.work && L.counters, "attn: workspace missing");
+  XE_REQUIRE(L.max_splits >= 1 && L.max_splits <= 256, "attn: max_splits must be 1..256");
+  XE_REQUIRE(L.work, "attn: workspace missing");
   const int g = L.hq / L.hkv;
-  AttnFn fn = pick(L.hd, g);
-  XE_REQUIRE(fn, "attn: unsupported head_dim / GQA group (hd 64/128/256, group 1/2/4/8)");
-  // the merge reuses red[][][] for G * max_splits weights + G sums
-  XE_REQUIRE(static_cast<size_t>(g) * (L.max_splits + 1) <= static_cast<size_t>(kWaves) * g * (L.hd + 2),
-             "attn: max_splits too large for the merge scratch");
+  AttnFn fn = pick(L.hd, g, false);
+  AttnFn merge = pick(L.hd, g, true);
+  XE_REQUIRE(fn && merge, "attn: unsupported head_dim / GQA group (hd 64/128/256, group 1/2/4/8)");
   XE_REQUIRE(!L.rope_cos || (L.rope_sin && L.pos), "attn: RoPE needs sin table and positions");
   XE_REQUIRE(!L.k_new || (L.v_new && (L.pos || L.lens || L.fixed_len)), "attn: append needs v_new");
   AttnParams p{};
@@ -437,10 +445,14 @@ void launch_attn(const AttnLaunch &L, hipStream_t s) {
   p.out = L.out;
   p.out_stride = L.out_stride ? L.out_stride : L.hq * L.hd;
   p.work = L.work;
-  p.counters = L.counters;
   p.max_splits = L.max_splits;
   hipLaunchKernelGGL(fn, dim3(L.max_splits, L.hkv, L.batch), dim3(kThreads), 0, s, p);
   XE_HIP(hipGetLastError());
+  if (L.max_splits > 1) {
+    const int blocks = (g * L.hd + kThreads - 1) / kThreads;
+    hipLaunchKernelGGL(merge, dim3(blocks, L.hkv, L.batch), dim3(kThreads), 0, s, p);
+    XE_HIP(hipGetLastError());
+  }
 }
 
 }  // namespace xe

@@ -85,15 +85,12 @@ struct xe_ctx {
   size_t scratch_size = 0;
   void *host_pinned = nullptr;
   size_t host_pinned_size = 0;
-  // split-K attention workspace: partials + arrival counters (kept zeroed:
-  // the merging workgroup re-arms its counter)
+  // split-K attention workspace (partials)
   float *attn_work = nullptr;
   size_t attn_work_floats = 0;
-  unsigned int *attn_counters = nullptr;
-  size_t attn_counter_count = 0;
   void *ensure_scratch(size_t n);
   void *ensure_pinned(size_t n);
-  void ensure_attn(size_t work_floats, size_t counters);
+  void ensure_attn(size_t work_floats);
 };
 
 namespace xe {
@@ -167,9 +164,8 @@ struct AttnLaunch {
   // output fp32 [batch, out_stride], head h at h*hd
   float *out = nullptr;
   int out_stride = 0;
-  // workspace: partials + per-(b, kvh) arrival counters (zeroed once)
+  // workspace for the split partials
   float *work = nullptr;
-  unsigned int *counters = nullptr;
   int max_splits = 0;
 };
 

@@ -170,7 +170,7 @@ __global__ void cross_pack_kernel(const float *src, int t_rows, int heads, int h
   }
 }
 
-// Greedy argmax over logits[b, :]: block partials + last-arriving merge.
+// Greedy argmax over logits[b, :]: block partials, then a merge launch.
 // last_max = 1: Iterator::max_by (opt125m_decode.rs:303) keeps the LAST of
 // equal maxima; else strict > keeps the first (whisper.rs:749-757).
 // The winner becomes the next input token; pos advances; hist[b][pos] gets it.
@@ -184,11 +184,10 @@ __device__ inline bool better(float v, int i, float bv, int bi, int last_max) {
   return false;
 }
 
-__global__ __launch_bounds__(256) void argmax_kernel(const float *logits, int vocab, int last_max,
-                                                     float *part_v, int *part_i,
-                                                     unsigned int *counters, int32_t *next,
-                                                     int32_t *tokens, int32_t *pos, int32_t *hist,
-                                                     int hist_stride) {
+// Partials: block k of row b reduces its slice of the logits.
+__global__ __launch_bounds__(256) void argmax_partial_kernel(const float *logits, int vocab,
+                                                             int last_max, float *part_v,
+                                                             int *part_i) {
   const int b = blockIdx.y;
   const int per = (vocab + kArgBlocks - 1) / kArgBlocks;
   const int lo = blockIdx.x * per, hi = min(vocab, lo + per);
@@ -204,7 +203,6 @@ __global__ __launch_bounds__(256) void argmax_kernel(const float *logits, int vo
   }
   __shared__ float sv[256];
   __shared__ int si[256];
-  __shared__ int s_last;
   sv[threadIdx.x] = bv;
   si[threadIdx.x] = bi;
   __syncthreads();
@@ -222,25 +220,36 @@ __global__ __launch_bounds__(256) void argmax_kernel(const float *logits, int vo
   if (threadIdx.x == 0) {
     part_v[b * kArgBlocks + blockIdx.x] = sv[0];
     part_i[b * kArgBlocks + blockIdx.x] = si[0];
-    __threadfence();
-    const unsigned prev =
-        __hip_atomic_fetch_add(counters + b, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-    s_last = prev == kArgBlocks - 1;
-    if (s_last) __hip_atomic_store(counters + b, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
-  __syncthreads();
-  if (!s_last || threadIdx.x != 0) return;
-  __threadfence();
+}
+
+// Final: one wave per stream merges the partials; the winner becomes the
+// next input token, pos advances, hist[b][pos] records it.
+__global__ __launch_bounds__(64) void argmax_final_kernel(const float *part_v, const int *part_i,
+                                                          int last_max, int32_t *next,
+                                                          int32_t *tokens, int32_t *pos,
+                                                          int32_t *hist, int hist_stride) {
+  const int b = blockIdx.x;
   float v = -INFINITY;
   int idx = -1;
-  for (int k = 0; k < kArgBlocks; k++) {
-    const float pv = __builtin_nontemporal_load(part_v + b * kArgBlocks + k);
-    const int pi = __builtin_nontemporal_load(part_i + b * kArgBlocks + k);
+  for (int k = threadIdx.x; k < kArgBlocks; k += 64) {
+    const float pv = part_v[b * kArgBlocks + k];
+    const int pi = part_i[b * kArgBlocks + k];
     if (pi >= 0 && better(pv, pi, v, idx, last_max)) {
       v = pv;
       idx = pi;
     }
   }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const float ov = __shfl_xor(v, off, 64);
+    const int oi = __shfl_xor(idx, off, 64);
+    if (oi >= 0 && better(ov, oi, v, idx, last_max)) {
+      v = ov;
+      idx = oi;
+    }
+  }
+  if (threadIdx.x != 0) return;
   if (idx < 0) idx = 0;
   next[b] = idx;
   tokens[b] = idx;
@@ -389,14 +398,30 @@ struct xe_decoder {
   int32_t *tokens = nullptr, *pos = nullptr, *next = nullptr, *hist = nullptr;
   float *arg_v = nullptr;
   int *arg_i = nullptr;
-  unsigned int *arg_ctr = nullptr;
   float *attn_work = nullptr;
-  unsigned int *attn_ctr = nullptr;
   int attn_splits = 1;
   int32_t *host_tok = nullptr;  // pinned staging [max_ctx + 1][max_batch] x 2
   std::map<int, hipGraphExec_t> graphs;
   double last_step_us = 0.0;
   bool cross_ready = false;
+  int fed = 0;      // prompt length of the current streams
+  int decoded = 0;  // steps decoded after the prompt
+  // per-launch profiling (xe_decoder_profile_step): an event after each
+  // launch on the decoder stream, with the launch's algorithmic bytes
+  struct ProfEntry {
+    std::string label;
+    double bytes;
+    hipEvent_t ev;
+  };
+  std::vector<ProfEntry> *prof = nullptr;
+  std::vector<int32_t> prof_pos;  // host copy of positions for the byte counts
+  void mark(const std::string &label, double bytes) {
+    if (!prof) return;
+    hipEvent_t e;
+    XE_HIP(hipEventCreate(&e));
+    XE_HIP(hipEventRecord(e, s));
+    prof->push_back({label, bytes, e});
+  }
 
   size_t nqkv() const { return static_cast<size_t>(c.n_heads + 2 * c.n_kv_heads) * c.head_dim; }
   size_t kv_layer_elems() const {
@@ -538,15 +563,13 @@ void alloc_decoder(xe_decoder *d) {
   d->hist = dalloc<int32_t>(static_cast<size_t>(B) * (c.max_ctx + 1), s);
   d->arg_v = dalloc<float>(static_cast<size_t>(B) * kArgBlocks, s);
   d->arg_i = dalloc<int>(static_cast<size_t>(B) * kArgBlocks, s);
-  d->arg_ctr = dalloc<unsigned int>(B, s);
   // split-K attention: ~4 workgroups per CU at the largest batch, chunks >= 32 keys
   const int hkv_max = std::max(c.n_kv_heads, wh ? c.n_heads : 0);
   int ms = (4 * d->dev->num_cus) / std::max(1, hkv_max);
-  const int cap = (std::max(c.max_ctx, wh ? c.n_cross : 0) + 31) / 32;
-  ms = std::max(1, std::min(std::min(ms, cap), 256));
+  const int cap = (std::max(c.max_ctx, wh ? c.n_cross : 0) + 63) / 64;
+  ms = std::max(1, std::min(std::min(ms, cap), 64));
   d->attn_splits = ms;
   d->attn_work = dalloc<float>(attn_work_floats(B, std::max(c.n_heads, 1), c.head_dim, ms), s, false);
-  d->attn_ctr = dalloc<unsigned int>(static_cast<size_t>(B) * std::max(c.n_kv_heads, c.n_heads), s);
   if (gem) {
     const int half = c.head_dim / 2;
     std::vector<float> cs(static_cast<size_t>(c.max_ctx) * half), sn(cs.size());
@@ -599,8 +622,7 @@ void free_decoder(xe_decoder *d) {
                   static_cast<void *>(d->tokens), static_cast<void *>(d->pos),
                   static_cast<void *>(d->next), static_cast<void *>(d->hist),
                   static_cast<void *>(d->arg_v), static_cast<void *>(d->arg_i),
-                  static_cast<void *>(d->arg_ctr), static_cast<void *>(d->attn_work),
-                  static_cast<void *>(d->attn_ctr)})
+                  static_cast<void *>(d->attn_work)})
     if (p) (void)hipFree(p);
   if (d->host_tok) (void)hipHostFree(d->host_tok);
   if (d->s) (void)hipStreamDestroy(d->s);
@@ -622,6 +644,18 @@ struct GemvCall {
   float *y = nullptr;
   int ldy = 0;
 };
+
+// Algorithmic bytes of one GEMV over `batch` rows: weights (+ int8 scales,
+// bias), activations in, outputs out, and the residual prologue's traffic.
+double gemv_bytes(const GemvCall &g, int batch) {
+  const Mat &m = *g.m;
+  double b = static_cast<double>(m.bytes());
+  if (g.bias) b += 4.0 * m.rows;
+  const int out_cols = g.act == ACT_GEGLU_TANH ? m.rows / 2 : m.rows;
+  b += 4.0 * batch * (static_cast<double>(m.cols) + out_cols);
+  if (g.sub) b += 4.0 * batch * m.cols * (g.res_out ? 2 : 1);
+  return b;
+}
 
 void run_gemv(const GemvCall &g, int batch, hipStream_t s) {
   for (int b0 = 0; b0 < batch; b0 += 8) {
@@ -672,6 +706,7 @@ void enqueue_step(xe_decoder *d, int B) {
                        c.wdtype, d->pos_emb, pos_off, prow, sqrtf(static_cast<float>(D)),
                        gem ? 1 : 0, d->tokens, d->pos, c.vocab, D, d->xa);
     XE_HIP(hipGetLastError());
+    d->mark("embed", static_cast<double>(B) * D * (wbytes(c.wdtype, 1) + 4 + (d->pos_emb ? 4 : 0)));
   }
   float *xcur = d->xa, *xalt = d->xb;
   const float *pend = nullptr, *pend_post = nullptr;
@@ -705,6 +740,7 @@ void enqueue_step(xe_decoder *d, int B) {
       g.y = d->qkv;
       g.ldy = nq;
       run_gemv(g, B, s);
+      d->mark("gemv_qkv", gemv_bytes(g, B));
       after_pending();
     }
     // ---- self attention (append k/v at pos) ----
@@ -736,9 +772,13 @@ void enqueue_step(xe_decoder *d, int B) {
       a.out = d->att;
       a.out_stride = hq;
       a.work = d->attn_work;
-      a.counters = d->attn_ctr;
       a.max_splits = d->attn_splits;
       launch_attn(a, s);
+      if (d->prof) {
+        double kv = 0;
+        for (int b = 0; b < B; b++) kv += static_cast<double>(d->prof_pos[b] + 1) * hk * 2 * 2;
+        d->mark("attn_self", kv + 4.0 * B * (nq + hq) + 4.0 * B * hk);
+      }
     }
     // ---- O projection ----
     {
@@ -750,6 +790,7 @@ void enqueue_step(xe_decoder *d, int B) {
       g.y = d->sub;
       g.ldy = D;
       run_gemv(g, B, s);
+      d->mark("gemv_o", gemv_bytes(g, B));
       pend = d->sub;
       pend_post = gem ? l.post_attn : nullptr;
     }
@@ -766,6 +807,7 @@ void enqueue_step(xe_decoder *d, int B) {
       g.y = d->qx;
       g.ldy = D;
       run_gemv(g, B, s);
+      d->mark("gemv_xq", gemv_bytes(g, B));
       after_pending();
       AttnLaunch a;
       a.q = d->qx;
@@ -783,9 +825,9 @@ void enqueue_step(xe_decoder *d, int B) {
       a.out = d->att;
       a.out_stride = D;
       a.work = d->attn_work;
-      a.counters = d->attn_ctr;
       a.max_splits = d->attn_splits;
       launch_attn(a, s);
+      d->mark("attn_cross", static_cast<double>(c.n_cross) * D * 2 * 2 + 8.0 * B * D);
       GemvCall o;
       o.m = &l.xo;
       o.bias = l.xo_b;
@@ -794,6 +836,7 @@ void enqueue_step(xe_decoder *d, int B) {
       o.y = d->sub;
       o.ldy = D;
       run_gemv(o, B, s);
+      d->mark("gemv_xo", gemv_bytes(o, B));
       pend = d->sub;
       pend_post = nullptr;
     }
@@ -811,6 +854,7 @@ void enqueue_step(xe_decoder *d, int B) {
       g.y = d->ffn;
       g.ldy = F;
       run_gemv(g, B, s);
+      d->mark(gem ? "gemv_gateup" : "gemv_fc1", gemv_bytes(g, B));
       after_pending();
       GemvCall o;
       o.m = &l.fc2;
@@ -820,6 +864,7 @@ void enqueue_step(xe_decoder *d, int B) {
       o.y = d->sub;
       o.ldy = D;
       run_gemv(o, B, s);
+      d->mark(gem ? "gemv_down" : "gemv_fc2", gemv_bytes(o, B));
       pend = d->sub;
       pend_post = gem ? l.post_ffn : nullptr;
     }
@@ -837,12 +882,16 @@ void enqueue_step(xe_decoder *d, int B) {
     g.y = d->logits;
     g.ldy = c.vocab;
     run_gemv(g, B, s);
+    d->mark("gemv_lmhead", gemv_bytes(g, B));
   }
   // ---- greedy argmax -> next token, pos + 1 ----
-  hipLaunchKernelGGL(argmax_kernel, dim3(kArgBlocks, B), dim3(256), 0, s, d->logits, c.vocab,
-                     opt ? 1 : 0, d->arg_v, d->arg_i, d->arg_ctr, d->next, d->tokens, d->pos,
-                     d->hist, c.max_ctx + 1);
+  hipLaunchKernelGGL(argmax_partial_kernel, dim3(kArgBlocks, B), dim3(256), 0, s, d->logits,
+                     c.vocab, opt ? 1 : 0, d->arg_v, d->arg_i);
   XE_HIP(hipGetLastError());
+  hipLaunchKernelGGL(argmax_final_kernel, dim3(B), dim3(64), 0, s, d->arg_v, d->arg_i,
+                     opt ? 1 : 0, d->next, d->tokens, d->pos, d->hist, c.max_ctx + 1);
+  XE_HIP(hipGetLastError());
+  d->mark("argmax", 4.0 * B * c.vocab);
 }
 
 hipGraphExec_t graph_for(xe_decoder *d, int B) {
@@ -1134,55 +1183,160 @@ int xe_decoder_step(xe_decoder *d, const int32_t *tokens, const int32_t *pos, in
   }, -1);
 }
 
+}  // extern "C"
+
+namespace {
+
+void check_ready(xe_decoder *d, int batch) {
+  XE_REQUIRE(batch >= 1 && batch <= d->max_batch, "batch out of range");
+  XE_REQUIRE(d->c.family != XE_WHISPER || d->cross_ready, "Whisper: set_cross first");
+}
+
+// Positions start at 0; the prompt's tokens are fed one step at a time (the
+// argmax kernel leaves the next token and pos + 1 on the device).
+void feed(xe_decoder *d, const int32_t *prompt, int n_prompt, int batch) {
+  check_ready(d, batch);
+  XE_REQUIRE(prompt && n_prompt >= 1, "empty prompt");
+  XE_REQUIRE(n_prompt <= d->c.max_ctx, "prompt exceeds max_ctx");
+  if (d->c.family != XE_GEMMA3) XE_REQUIRE(n_prompt <= d->c.max_pos, "prompt exceeds the position table");
+  for (size_t i = 0; i < static_cast<size_t>(batch) * n_prompt; i++)
+    XE_REQUIRE(prompt[i] >= 0 && prompt[i] < d->c.vocab, "prompt token out of range");
+  XE_HIP(hipStreamSynchronize(d->s));
+  int32_t *h = d->host_tok;
+  XE_REQUIRE(static_cast<size_t>(n_prompt + 1) * batch <= static_cast<size_t>(2) * (d->c.max_ctx + 2) * d->max_batch,
+             "prompt too long for staging");
+  for (int p = 0; p < n_prompt; p++)
+    for (int b = 0; b < batch; b++) h[static_cast<size_t>(p) * batch + b] = prompt[static_cast<size_t>(b) * n_prompt + p];
+  int32_t *zpos = h + static_cast<size_t>(n_prompt) * batch;
+  for (int b = 0; b < batch; b++) zpos[b] = 0;
+  XE_HIP(hipMemcpyAsync(d->pos, zpos, batch * 4, hipMemcpyHostToDevice, d->s));
+  if (!getenv("XE_NO_GRAPH")) (void)graph_for(d, batch);
+  for (int p = 0; p < n_prompt; p++) {
+    XE_HIP(hipMemcpyAsync(d->tokens, h + static_cast<size_t>(p) * batch, batch * 4,
+                          hipMemcpyHostToDevice, d->s));
+    run_step(d, batch);
+  }
+  XE_HIP(hipStreamSynchronize(d->s));
+  d->fed = n_prompt;
+  d->decoded = 0;
+}
+
+// n_steps further greedy steps from the device state; out [batch, n_steps]
+// receives the tokens those steps emit (may be NULL).
+void decode(xe_decoder *d, int batch, int n_steps, int32_t *out, double *device_us) {
+  check_ready(d, batch);
+  XE_REQUIRE(d->fed > 0, "feed a prompt first");
+  XE_REQUIRE(n_steps >= 0, "negative step count");
+  const int first_pos = d->fed + d->decoded;  // position the next step processes
+  XE_REQUIRE(first_pos + n_steps <= d->c.max_ctx, "decode would run past max_ctx");
+  if (d->c.family != XE_GEMMA3)
+    XE_REQUIRE(first_pos + n_steps <= d->c.max_pos, "decode would run past the position table");
+  hipEvent_t e0, e1;
+  XE_HIP(hipEventCreate(&e0));
+  XE_HIP(hipEventCreate(&e1));
+  XE_HIP(hipEventRecord(e0, d->s));
+  for (int i = 0; i < n_steps; i++) run_step(d, batch);
+  XE_HIP(hipEventRecord(e1, d->s));
+  XE_HIP(hipEventSynchronize(e1));
+  float ms = 0.f;
+  XE_HIP(hipEventElapsedTime(&ms, e0, e1));
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  if (n_steps > 0) d->last_step_us = 1000.0 * ms / n_steps;
+  if (device_us) *device_us = 1000.0 * ms;
+  d->decoded += n_steps;
+  if (out && n_steps > 0) {
+    std::vector<int32_t> hist(static_cast<size_t>(batch) * (d->c.max_ctx + 1));
+    XE_HIP(hipMemcpy(hist.data(), d->hist, hist.size() * 4, hipMemcpyDeviceToHost));
+    for (int b = 0; b < batch; b++)
+      for (int i = 0; i < n_steps; i++)
+        out[static_cast<size_t>(b) * n_steps + i] =
+            hist[static_cast<size_t>(b) * (d->c.max_ctx + 1) + first_pos + i];
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+int xe_decoder_feed(xe_decoder *d, const int32_t *prompt, int n_prompt, int batch) {
+  return guard_d([&]() -> int {
+    XE_REQUIRE(d, "null decoder");
+    DeviceGuard dg(d->dev->ordinal);
+    feed(d, prompt, n_prompt, batch);
+    return 0;
+  }, -1);
+}
+
+int xe_decoder_decode(xe_decoder *d, int batch, int n_steps, int32_t *out, double *device_us) {
+  return guard_d([&]() -> int {
+    XE_REQUIRE(d, "null decoder");
+    DeviceGuard dg(d->dev->ordinal);
+    decode(d, batch, n_steps, out, device_us);
+    return 0;
+  }, -1);
+}
+
 int xe_decoder_generate(xe_decoder *d, const int32_t *prompt, int n_prompt, int batch, int n_new,
                         int32_t *out) {
   return guard_d([&]() -> int {
     XE_REQUIRE(d && prompt && out, "null argument");
-    XE_REQUIRE(batch >= 1 && batch <= d->max_batch, "batch out of range");
-    XE_REQUIRE(n_prompt >= 1 && n_new >= 1, "need a prompt and at least one new token");
+    XE_REQUIRE(n_new >= 1, "need at least one new token");
     XE_REQUIRE(n_prompt + n_new - 1 <= d->c.max_ctx, "prompt + new tokens exceed max_ctx");
-    if (d->c.family != XE_GEMMA3)
-      XE_REQUIRE(n_prompt + n_new - 1 <= d->c.max_pos, "prompt + new tokens exceed the position table");
-    XE_REQUIRE(d->c.family != XE_WHISPER || d->cross_ready, "Whisper: set_cross first");
-    for (size_t i = 0; i < static_cast<size_t>(batch) * n_prompt; i++)
-      XE_REQUIRE(prompt[i] >= 0 && prompt[i] < d->c.vocab, "prompt token out of range");
+    DeviceGuard dg(d->dev->ordinal);
+    feed(d, prompt, n_prompt, batch);
+    // the first new token was emitted by the last prompt step (hist[pos n_prompt-1])
+    std::vector<int32_t> first(batch);
+    {
+      std::vector<int32_t> hist(static_cast<size_t>(batch) * (d->c.max_ctx + 1));
+      XE_HIP(hipMemcpy(hist.data(), d->hist, hist.size() * 4, hipMemcpyDeviceToHost));
+      for (int b = 0; b < batch; b++) first[b] = hist[static_cast<size_t>(b) * (d->c.max_ctx + 1) + n_prompt - 1];
+    }
+    std::vector<int32_t> rest(static_cast<size_t>(batch) * std::max(0, n_new - 1));
+    decode(d, batch, n_new - 1, rest.data(), nullptr);
+    for (int b = 0; b < batch; b++) {
+      out[static_cast<size_t>(b) * n_new] = first[b];
+      for (int i = 0; i + 1 < n_new; i++)
+        out[static_cast<size_t>(b) * n_new + 1 + i] = rest[static_cast<size_t>(b) * (n_new - 1) + i];
+    }
+    return 0;
+  }, -1);
+}
+
+int xe_decoder_profile_step(xe_decoder *d, int batch, int max_entries, char *labels, double *us,
+                            double *bytes) {
+  return guard_d([&]() -> int {
+    XE_REQUIRE(d && labels && us && bytes, "null argument");
+    check_ready(d, batch);
+    XE_REQUIRE(d->fed > 0, "feed a prompt first");
+    XE_REQUIRE(d->fed + d->decoded < d->c.max_ctx, "no room for another step");
     DeviceGuard dg(d->dev->ordinal);
     XE_HIP(hipStreamSynchronize(d->s));
-    // pinned staging: [n_prompt][batch] tokens, then zero positions
-    int32_t *h = d->host_tok;
-    XE_REQUIRE(static_cast<size_t>(n_prompt + 1) * batch <= static_cast<size_t>(2) * (d->c.max_ctx + 2) * d->max_batch,
-               "prompt too long for staging");
-    for (int p = 0; p < n_prompt; p++)
-      for (int b = 0; b < batch; b++) h[static_cast<size_t>(p) * batch + b] = prompt[static_cast<size_t>(b) * n_prompt + p];
-    int32_t *zpos = h + static_cast<size_t>(n_prompt) * batch;
-    for (int b = 0; b < batch; b++) zpos[b] = 0;
-    XE_HIP(hipMemcpyAsync(d->pos, zpos, batch * 4, hipMemcpyHostToDevice, d->s));
-    // build the graph before timing (first use captures it)
-    if (!getenv("XE_NO_GRAPH")) (void)graph_for(d, batch);
-    for (int p = 0; p < n_prompt; p++) {
-      XE_HIP(hipMemcpyAsync(d->tokens, h + static_cast<size_t>(p) * batch, batch * 4,
-                            hipMemcpyHostToDevice, d->s));
-      run_step(d, batch);
+    d->prof_pos.assign(batch, 0);
+    XE_HIP(hipMemcpy(d->prof_pos.data(), d->pos, batch * 4, hipMemcpyDeviceToHost));
+    std::vector<xe_decoder::ProfEntry> entries;
+    d->prof = &entries;
+    try {
+      d->mark("start", 0.0);
+      enqueue_step(d, batch);  // eager, one event after each launch
+    } catch (...) {
+      d->prof = nullptr;
+      for (auto &e : entries) (void)hipEventDestroy(e.ev);
+      throw;
     }
-    hipEvent_t e0, e1;
-    XE_HIP(hipEventCreate(&e0));
-    XE_HIP(hipEventCreate(&e1));
-    XE_HIP(hipEventRecord(e0, d->s));
-    for (int i = 1; i < n_new; i++) run_step(d, batch);
-    XE_HIP(hipEventRecord(e1, d->s));
-    XE_HIP(hipEventSynchronize(e1));
-    float ms = 0.f;
-    XE_HIP(hipEventElapsedTime(&ms, e0, e1));
-    (void)hipEventDestroy(e0);
-    (void)hipEventDestroy(e1);
-    d->last_step_us = n_new > 1 ? 1000.0 * ms / (n_new - 1) : 0.0;
-    // token emitted after position p sits in hist[b][p]
-    std::vector<int32_t> hist(static_cast<size_t>(batch) * (d->c.max_ctx + 1));
-    XE_HIP(hipMemcpy(hist.data(), d->hist, hist.size() * 4, hipMemcpyDeviceToHost));
-    for (int b = 0; b < batch; b++)
-      for (int i = 0; i < n_new; i++)
-        out[static_cast<size_t>(b) * n_new + i] = hist[static_cast<size_t>(b) * (d->c.max_ctx + 1) + n_prompt - 1 + i];
-    return 0;
+    d->prof = nullptr;
+    XE_HIP(hipStreamSynchronize(d->s));
+    d->decoded += 1;
+    int n = 0;
+    for (size_t i = 1; i < entries.size() && n < max_entries; i++, n++) {
+      float ms = 0.f;
+      XE_HIP(hipEventElapsedTime(&ms, entries[i - 1].ev, entries[i].ev));
+      us[n] = 1000.0 * ms;
+      bytes[n] = entries[i].bytes;
+      std::snprintf(labels + 32 * n, 32, "%s", entries[i].label.c_str());
+    }
+    for (auto &e : entries) (void)hipEventDestroy(e.ev);
+    return n;
   }, -1);
 }
 

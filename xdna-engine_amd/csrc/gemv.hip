@@ -19,6 +19,8 @@
 //   * The group reduction is an xor-butterfly over LPR lanes (DPP/swizzle).
 //   * int8 -> fp32 dequant happens in registers; the per-row fp32 scale is
 //     applied after the sum, as in Lin::fwd (opt125m_decode.rs:120-122).
+#include <algorithm>
+
 #include "common.h"
 
 namespace xe {
@@ -55,23 +57,28 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
-// Block-wide sum over WPB waves; red must hold WPB floats.
-template <int WPB>
-__device__ __forceinline__ float block_sum(float v, float *red) {
-  v = wave_sum(v);
-  if constexpr (WPB == 1) return v;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  __syncthreads();
-  if (lane == 0) red[wave] = v;
-  __syncthreads();
-  float s = 0.f;
+// Block-wide sums of N values over WPB waves with one barrier; `slot`
+// alternates so back-to-back reductions never overwrite a slot still being
+// read.  red holds 2 * 4 * kMaxWaves floats.
+template <int WPB, int N>
+__device__ __forceinline__ void block_sums(float (&v)[N], float *red, int &slot) {
 #pragma unroll
-  for (int i = 0; i < WPB; i++) s += red[i];
-  return s;
-}
-
-__device__ __forceinline__ float bf16_to_f32(uint16_t b) {
-  return __uint_as_float(static_cast<uint32_t>(b) << 16);
+  for (int i = 0; i < N; i++) v[i] = wave_sum(v[i]);
+  if constexpr (WPB == 1) return;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  float *r = red + slot * 4 * kMaxWaves;
+  slot ^= 1;
+  if (lane == 0)
+#pragma unroll
+    for (int i = 0; i < N; i++) r[i * kMaxWaves + wave] = v[i];
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < N; i++) {
+    float t = 0.f;
+#pragma unroll
+    for (int w = 0; w < WPB; w++) t += r[i * kMaxWaves + w];
+    v[i] = t;
+  }
 }
 
 __device__ __forceinline__ float gelu_erf(float x) {
@@ -193,66 +200,134 @@ __device__ __forceinline__ float chunk_dot(const Chunk<WT> &ch, const float4 (&x
 }
 
 // Prologue: x (+ post(sub)) -> res_out (block 0) -> norm -> LDS (transposed).
+// Prologue: x (+ post(sub)) -> res_out (block 0) -> norm -> LDS, fp32.
+// Statistics are reduced once per row:
+//   Gemma (sub + post_w, RMS1P): t = x + sub*inv_s*(1+w) and
+//     sum t^2 = sum x^2 + 2 inv_s sum x*s' + inv_s^2 sum s'^2 (s' = sub*(1+w)),
+//     so sum sub^2, sum x^2, sum x*s', sum s'^2 come out of one reduction.
+//   LayerNorm: two passes (sum t, then sum (t - mean)^2) as the reference's
+//     layer_norm (npu-asr-host/src/lib.rs:79-109); one-pass variance loses
+//     everything on near-constant rows.
 template <int NB, int WPB>
 __device__ void gemv_prologue(const GemvParams &p, float4 *xs4, float *red) {
   constexpr int kThreads = 64 * WPB;
-  const int K = p.k;
+  constexpr int UNR = 4;  // float4 loads in flight per thread
+  const int K = p.k, K4 = K / 4;
+  const float fk = static_cast<float>(K);
   float *xs = reinterpret_cast<float *>(xs4);
+  float *sb = xs + static_cast<size_t>(NB) * K;  // sub staging (one row)
+  int slot = 0;
   for (int b = 0; b < p.batch && b < NB; b++) {
-    float *xb = xs + static_cast<size_t>(b) * K;  // staged row-major first
-    float inv_sub = 1.f;
-    if (p.sub && p.post_w) {
-      float ss = 0.f;
-      for (int i = threadIdx.x; i < K; i += kThreads) {
-        float v = p.sub[static_cast<size_t>(b) * K + i];
-        ss = __builtin_fmaf(v, v, ss);
-      }
-      ss = block_sum<WPB>(ss, red);
-      inv_sub = 1.0f / sqrtf(ss / static_cast<float>(K) + p.eps);
-    }
-    for (int i = threadIdx.x; i < K; i += kThreads) {
-      float v;
-      if (p.x_bf16)
-        v = bf16_to_f32(static_cast<const uint16_t *>(p.x)[static_cast<size_t>(b) * p.ldx + i]);
-      else
-        v = static_cast<const float *>(p.x)[static_cast<size_t>(b) * p.ldx + i];
-      if (p.sub) {
-        float s = p.sub[static_cast<size_t>(b) * K + i];
-        if (p.post_w) s = s * inv_sub * (1.0f + p.post_w[i]);
-        v = v + s;
-      }
-      xb[i] = v;
-      if (p.res_out && blockIdx.x == 0) p.res_out[static_cast<size_t>(b) * K + i] = v;
-    }
-    if (p.norm != XE_NORM_NONE) {
-      __syncthreads();
-      float mean = 0.f, inv = 1.f;
-      if (p.norm == XE_NORM_LN) {
-        float s = 0.f;
-        for (int i = threadIdx.x; i < K; i += kThreads) s += xb[i];
-        mean = block_sum<WPB>(s, red) / static_cast<float>(K);
-        float vs = 0.f;
-        for (int i = threadIdx.x; i < K; i += kThreads) {
-          float c = xb[i] - mean;
-          vs = __builtin_fmaf(c, c, vs);
+    float4 *xb4 = xs4 + static_cast<size_t>(b) * K4;
+    float *xb = xs + static_cast<size_t>(b) * K;
+    const float4 *sub4 = p.sub ? reinterpret_cast<const float4 *>(p.sub + static_cast<size_t>(b) * K) : nullptr;
+    const bool fold = p.sub && p.post_w;  // Gemma post-norm + residual
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};  // fold: sum sub^2, x^2, x*s', s'^2
+    for (int i0 = threadIdx.x; i0 < K4; i0 += kThreads * UNR) {
+      float4 v[UNR], sv[UNR];
+#pragma unroll
+      for (int u = 0; u < UNR; u++) {
+        const int i = i0 + u * kThreads;
+        if (i < K4) {
+          if (p.x_bf16) {
+            const uint2 r = reinterpret_cast<const uint2 *>(static_cast<const uint16_t *>(p.x) +
+                                                            static_cast<size_t>(b) * p.ldx)[i];
+            v[u] = make_float4(__uint_as_float(r.x << 16), __uint_as_float(r.x & 0xffff0000u),
+                               __uint_as_float(r.y << 16), __uint_as_float(r.y & 0xffff0000u));
+          } else {
+            v[u] = reinterpret_cast<const float4 *>(static_cast<const float *>(p.x) +
+                                                    static_cast<size_t>(b) * p.ldx)[i];
+          }
+          if (sub4) sv[u] = sub4[i];
         }
-        inv = 1.0f / sqrtf(block_sum<WPB>(vs, red) / static_cast<float>(K) + p.eps);
-      } else {
-        float ss = 0.f;
-        for (int i = threadIdx.x; i < K; i += kThreads) ss = __builtin_fmaf(xb[i], xb[i], ss);
-        inv = 1.0f / sqrtf(block_sum<WPB>(ss, red) / static_cast<float>(K) + p.eps);
       }
-      for (int i = threadIdx.x; i < K; i += kThreads) {
-        float v = xb[i];
-        if (p.norm == XE_NORM_LN)
-          v = (v - mean) * inv * p.gamma[i] + p.beta[i];
-        else if (p.norm == XE_NORM_RMS1P)
-          v = v * inv * (1.0f + p.gamma[i]);
-        else
-          v = v * inv * p.gamma[i];
-        xb[i] = v;
+#pragma unroll
+      for (int u = 0; u < UNR; u++) {
+        const int i = i0 + u * kThreads;
+        if (i >= K4) continue;
+        xb4[i] = v[u];
+        if (sub4) reinterpret_cast<float4 *>(sb)[i] = sv[u];
+        if (fold) {
+          const float4 w = reinterpret_cast<const float4 *>(p.post_w)[i];
+          const float xv[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+          const float su[4] = {sv[u].x, sv[u].y, sv[u].z, sv[u].w};
+          const float wv[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+          for (int j = 0; j < 4; j++) {
+            const float sp = su[j] * (1.0f + wv[j]);
+            acc[0] = __builtin_fmaf(su[j], su[j], acc[0]);
+            acc[1] = __builtin_fmaf(xv[j], xv[j], acc[1]);
+            acc[2] = __builtin_fmaf(xv[j], sp, acc[2]);
+            acc[3] = __builtin_fmaf(sp, sp, acc[3]);
+          }
+        }
       }
     }
+    if (fold) {
+      block_sums<WPB, 4>(acc, red, slot);
+      const float inv_s = 1.0f / sqrtf(acc[0] / fk + p.eps);
+      const float st2 = acc[1] + 2.0f * inv_s * acc[2] + inv_s * inv_s * acc[3];
+      const float inv_t = p.norm != XE_NORM_NONE ? 1.0f / sqrtf(fmaxf(st2, 0.f) / fk + p.eps) : 1.f;
+      __syncthreads();  // staging complete (block_sums' barrier is skipped for WPB == 1)
+      for (int i = threadIdx.x; i < K; i += kThreads) {
+        const float t = xb[i] + sb[i] * inv_s * (1.0f + p.post_w[i]);
+        if (p.res_out && blockIdx.x == 0) p.res_out[static_cast<size_t>(b) * K + i] = t;
+        float h = t;
+        if (p.norm == XE_NORM_RMS1P) h = t * inv_t * (1.0f + p.gamma[i]);
+        else if (p.norm == XE_NORM_RMS) h = t * inv_t * p.gamma[i];
+        xb[i] = h;
+      }
+      if (p.norm == XE_NORM_LN) {  // not a model combination; keep it exact anyway
+        __syncthreads();
+        float v1[1] = {0.f};
+        for (int i = threadIdx.x; i < K; i += kThreads) v1[0] += xb[i];
+        block_sums<WPB, 1>(v1, red, slot);
+        const float mean = v1[0] / fk;
+        float v2[1] = {0.f};
+        for (int i = threadIdx.x; i < K; i += kThreads) {
+          const float c = xb[i] - mean;
+          v2[0] = __builtin_fmaf(c, c, v2[0]);
+        }
+        block_sums<WPB, 1>(v2, red, slot);
+        const float inv = 1.0f / sqrtf(v2[0] / fk + p.eps);
+        __syncthreads();
+        for (int i = threadIdx.x; i < K; i += kThreads)
+          xb[i] = (xb[i] - mean) * inv * p.gamma[i] + p.beta[i];
+      }
+    } else {
+      __syncthreads();
+      if (p.sub) {
+        for (int i = threadIdx.x; i < K; i += kThreads) {
+          const float t = xb[i] + sb[i];
+          xb[i] = t;
+          if (p.res_out && blockIdx.x == 0) p.res_out[static_cast<size_t>(b) * K + i] = t;
+        }
+        if (p.norm != XE_NORM_NONE) __syncthreads();
+      }
+      if (p.norm == XE_NORM_LN) {
+        float v1[1] = {0.f};
+        for (int i = threadIdx.x; i < K; i += kThreads) v1[0] += xb[i];
+        block_sums<WPB, 1>(v1, red, slot);
+        const float mean = v1[0] / fk;
+        float v2[1] = {0.f};
+        for (int i = threadIdx.x; i < K; i += kThreads) {
+          const float c = xb[i] - mean;
+          v2[0] = __builtin_fmaf(c, c, v2[0]);
+        }
+        block_sums<WPB, 1>(v2, red, slot);
+        const float inv = 1.0f / sqrtf(v2[0] / fk + p.eps);
+        for (int i = threadIdx.x; i < K; i += kThreads)
+          xb[i] = (xb[i] - mean) * inv * p.gamma[i] + p.beta[i];
+      } else if (p.norm != XE_NORM_NONE) {
+        float v1[1] = {0.f};
+        for (int i = threadIdx.x; i < K; i += kThreads) v1[0] = __builtin_fmaf(xb[i], xb[i], v1[0]);
+        block_sums<WPB, 1>(v1, red, slot);
+        const float inv = 1.0f / sqrtf(v1[0] / fk + p.eps);
+        for (int i = threadIdx.x; i < K; i += kThreads)
+          xb[i] = p.norm == XE_NORM_RMS1P ? xb[i] * inv * (1.0f + p.gamma[i]) : xb[i] * inv * p.gamma[i];
+      }
+    }
+    if (p.sub && b + 1 < p.batch && b + 1 < NB) __syncthreads();  // sub staging is reused
   }
   __syncthreads();
 }
@@ -260,118 +335,124 @@ __device__ void gemv_prologue(const GemvParams &p, float4 *xs4, float *red) {
 template <int WT, int NB, int LPR, int RPL, int WPB>
 __global__ __launch_bounds__(64 * WPB) void gemv_kernel(GemvParams p) {
   extern __shared__ float4 xs4[];
-  __shared__ float red[kMaxWaves];
+  __shared__ float red[2 * 4 * kMaxWaves];
   constexpr int RG = 64 / LPR;
   constexpr int U = (RPL >= 2) ? 2 : 4;  // chunks prefetched per row
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int rg = lane / LPR, kl = lane % LPR;
-  const int rows_per_wave = RG * RPL;
-  const int row0 = (blockIdx.x * WPB + wave) * rows_per_wave + rg * RPL;
+  constexpr int rows_per_wave = RG * RPL;
+  constexpr int rows_per_block = WPB * rows_per_wave;
   const int K = p.k, nch = K / 16;
   const int n_it = (nch + LPR - 1) / LPR;
-
-  bool row_ok[RPL];
-  int row[RPL];
-#pragma unroll
-  for (int i = 0; i < RPL; i++) {
-    row[i] = row0 + i;
-    row_ok[i] = row[i] < p.m;
-    if (!row_ok[i]) row[i] = p.m - 1;  // clamp: loads stay in bounds, result dropped
-  }
-
-  // Issue the first U chunks of weight loads before the prologue.
-  Chunk<WT> pre[U][RPL];
-#pragma unroll
-  for (int u = 0; u < U; u++) {
-    const int c = u * LPR + kl;
-#pragma unroll
-    for (int i = 0; i < RPL; i++)
-      if (c < nch) load_chunk<WT>(p, row[i], c, pre[u][i]);
-  }
-
-  // ---- prologue: stage x into LDS as [b][K] fp32 ----
-  gemv_prologue<NB, WPB>(p, xs4, red);
-
-  float acc[NB][RPL];
-#pragma unroll
-  for (int b = 0; b < NB; b++)
-#pragma unroll
-    for (int i = 0; i < RPL; i++) acc[b][i] = 0.f;
-
+  const int ntiles = (p.m + rows_per_block - 1) / rows_per_block;
   const float *xs = reinterpret_cast<const float *>(xs4);
-  auto compute = [&](const Chunk<WT>(&chs)[RPL], int c) {
-#pragma unroll
-    for (int b = 0; b < NB; b++) {
-      if (b < p.batch) {
-        float4 xv[4];
-        const float4 *xr = reinterpret_cast<const float4 *>(xs + static_cast<size_t>(b) * K + c * 16);
-#pragma unroll
-        for (int j = 0; j < 4; j++) xv[j] = xr[j];
-#pragma unroll
-        for (int i = 0; i < RPL; i++) acc[b][i] = chunk_dot<WT>(chs[i], xv, acc[b][i]);
-      }
-    }
-  };
 
+  // The grid may be smaller than the tile count: each workgroup stages x once
+  // (the prologue) and walks tiles blockIdx.x, + gridDim.x, ...
+  for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+    const int row0 = tile * rows_per_block + wave * rows_per_wave + rg * RPL;
+    bool row_ok[RPL];
+    int row[RPL];
 #pragma unroll
-  for (int u = 0; u < U; u++) {
-    const int c = u * LPR + kl;
-    if (c < nch) compute(pre[u], c);
-  }
-  for (int it = U; it < n_it; it += U) {
-    Chunk<WT> cur[U][RPL];
+    for (int i = 0; i < RPL; i++) {
+      row[i] = row0 + i;
+      row_ok[i] = row[i] < p.m;
+      if (!row_ok[i]) row[i] = p.m - 1;  // clamp: loads stay in bounds, result dropped
+    }
+
+    // Issue the first U chunks of this tile's weights (before the prologue
+    // on the first tile, so it overlaps the HBM latency).
+    Chunk<WT> pre[U][RPL];
 #pragma unroll
     for (int u = 0; u < U; u++) {
-      const int c = (it + u) * LPR + kl;
+      const int c = u * LPR + kl;
 #pragma unroll
       for (int i = 0; i < RPL; i++)
-        if (c < nch) load_chunk<WT>(p, row[i], c, cur[u][i]);
+        if (c < nch) load_chunk<WT>(p, row[i], c, pre[u][i]);
     }
+    if (tile == static_cast<int>(blockIdx.x)) gemv_prologue<NB, WPB>(p, xs4, red);
+
+    float acc[NB][RPL];
+#pragma unroll
+    for (int b = 0; b < NB; b++)
+#pragma unroll
+      for (int i = 0; i < RPL; i++) acc[b][i] = 0.f;
+
+    auto compute = [&](const Chunk<WT>(&chs)[RPL], int c) {
+#pragma unroll
+      for (int b = 0; b < NB; b++) {
+        if (b < p.batch) {
+          float4 xv[4];
+          const float4 *xr = reinterpret_cast<const float4 *>(xs + static_cast<size_t>(b) * K + c * 16);
+#pragma unroll
+          for (int j = 0; j < 4; j++) xv[j] = xr[j];
+#pragma unroll
+          for (int i = 0; i < RPL; i++) acc[b][i] = chunk_dot<WT>(chs[i], xv, acc[b][i]);
+        }
+      }
+    };
+
 #pragma unroll
     for (int u = 0; u < U; u++) {
-      const int c = (it + u) * LPR + kl;
-      if (c < nch) compute(cur[u], c);
+      const int c = u * LPR + kl;
+      if (c < nch) compute(pre[u], c);
     }
-  }
+    for (int it = U; it < n_it; it += U) {
+      Chunk<WT> cur[U][RPL];
+#pragma unroll
+      for (int u = 0; u < U; u++) {
+        const int c = (it + u) * LPR + kl;
+#pragma unroll
+        for (int i = 0; i < RPL; i++)
+          if (c < nch) load_chunk<WT>(p, row[i], c, cur[u][i]);
+      }
+#pragma unroll
+      for (int u = 0; u < U; u++) {
+        const int c = (it + u) * LPR + kl;
+        if (c < nch) compute(cur[u], c);
+      }
+    }
 
-  // ---- reduce over the LPR lanes of the group ----
+    // ---- reduce over the LPR lanes of the group ----
 #pragma unroll
-  for (int b = 0; b < NB; b++)
-#pragma unroll
-    for (int i = 0; i < RPL; i++) {
-      float v = acc[b][i];
-#pragma unroll
-      for (int off = LPR / 2; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-      acc[b][i] = v;
-    }
-
-  if (kl != 0) return;
-  // ---- epilogue ----
-#pragma unroll
-  for (int b = 0; b < NB; b++) {
-    if (b >= p.batch) break;
-    float v[RPL];
-#pragma unroll
-    for (int i = 0; i < RPL; i++) {
-      float t = acc[b][i];
-      if (WT == XE_I8) t = t * p.scale[row[i]];
-      if (p.bias) t = t + p.bias[row[i]];
-      v[i] = t;
-    }
-    if (p.act == ACT_GEGLU_TANH) {
-#pragma unroll
-      for (int i = 0; i + 1 < RPL; i += 2)
-        if (row_ok[i])
-          p.y[static_cast<size_t>(b) * p.ldy + row[i] / 2] =
-              gelu_tanh(v[i]) * v[i + 1] * p.out_scale;
-    } else {
+    for (int b = 0; b < NB; b++)
 #pragma unroll
       for (int i = 0; i < RPL; i++) {
-        if (!row_ok[i]) continue;
-        float t = v[i];
-        if (p.act == ACT_RELU) t = t > 0.f ? t : 0.f;
-        else if (p.act == ACT_GELU_ERF) t = gelu_erf(t);
-        p.y[static_cast<size_t>(b) * p.ldy + row[i]] = t * p.out_scale;
+        float v = acc[b][i];
+#pragma unroll
+        for (int off = LPR / 2; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+        acc[b][i] = v;
+      }
+
+    // ---- epilogue (lane 0 of each group) ----
+    if (kl == 0) {
+#pragma unroll
+      for (int b = 0; b < NB; b++) {
+        if (b >= p.batch) break;
+        float v[RPL];
+#pragma unroll
+        for (int i = 0; i < RPL; i++) {
+          float t = acc[b][i];
+          if (WT == XE_I8) t = t * p.scale[row[i]];
+          if (p.bias) t = t + p.bias[row[i]];
+          v[i] = t;
+        }
+        if (p.act == ACT_GEGLU_TANH) {
+#pragma unroll
+          for (int i = 0; i + 1 < RPL; i += 2)
+            if (row_ok[i])
+              p.y[static_cast<size_t>(b) * p.ldy + row[i] / 2] =
+                  gelu_tanh(v[i]) * v[i + 1] * p.out_scale;
+        } else {
+#pragma unroll
+          for (int i = 0; i < RPL; i++) {
+            if (!row_ok[i]) continue;
+            float t = v[i];
+            if (p.act == ACT_RELU) t = t > 0.f ? t : 0.f;
+            else if (p.act == ACT_GELU_ERF) t = gelu_erf(t);
+            p.y[static_cast<size_t>(b) * p.ldy + row[i]] = t * p.out_scale;
+          }
+        }
       }
     }
   }
@@ -445,7 +526,7 @@ GemvFn pick_lpr_rpl(int lpr, int rpl) {
 
 template <int WT, int NB>
 GemvFn pick_wpb(int wpb, int lpr, int rpl) {
-  if (wpb == 1) return pick_lpr_rpl<WT, NB, 1>(lpr, rpl);
+  // 4-wave workgroups only: 1-wave ones lost every measured shape
   if (wpb == 4) return pick_lpr_rpl<WT, NB, 4>(lpr, rpl);
   return nullptr;
 }
@@ -486,37 +567,43 @@ struct Tile {
   int lpr, rpl, wpb;
 };
 
-// Tile choice.  Decode GEMVs are small (1-60 MB), so the first goal is enough
-// workgroups to put loads in flight on every CU: the widest lane split LPR
-// whose K chunks keep >= 70% of lanes busy, RPL = 2 only when 2x fewer rows
-// still leaves >= 2 workgroups per CU, and 1-wave workgroups when 4-wave ones
-// would leave CUs idle.  XE_GEMV_TILE="lpr,rpl,wpb" overrides (tuning).
+// Tile choice, from a graph-replay sweep on MI355X (weights rotated past the
+// 256 MB Infinity Cache): 4-wave workgroups always win; with enough rows, a
+// narrow lane split with 2 rows per lane keeps the most bytes in flight
+// (lm-head 262144 x 1152: LPR 8, RPL 2 -> 6.1 TB/s); with few rows, a wide
+// split gives the workgroup count (down 1152 x 6912: LPR 64).  Candidates in
+// order of preference; the first with >= one workgroup per CU and >= 70% of
+// lanes busy on K wins, else the one with the most workgroups.
+// XE_GEMV_TILE="lpr,rpl,wpb" overrides (tuning).
 Tile choose_tile(int m, int k, int act) {
-  Tile t{16, 1, 4};
   const char *env = getenv("XE_GEMV_TILE");
   if (env) {
     int a = 0, b = 0, c = 4;
     if (sscanf(env, "%d,%d,%d", &a, &b, &c) >= 2) {
-      t = Tile{a, b, c};
+      Tile t{a, b, c};
       if (act == ACT_GEGLU_TANH && t.rpl < 2) t.rpl = 2;
       return t;
     }
   }
   const int nch = k / 16;
-  const int cands[4] = {64, 32, 16, 8};
-  t.lpr = 8;
-  for (int L : cands) {
-    const int it = (nch + L - 1) / L;
-    if (static_cast<double>(nch) / (it * L) >= 0.7) {
-      t.lpr = L;
-      break;
+  const int cus = cu_count();
+  static const Tile cands[] = {{8, 2, 4}, {16, 2, 4}, {16, 1, 4}, {32, 2, 4},
+                               {32, 1, 4}, {64, 2, 4}, {64, 1, 4}};
+  Tile best{32, 2, 4};
+  int best_wgs = -1;
+  for (const Tile &t : cands) {
+    if (act == ACT_GEGLU_TANH && t.rpl < 2) continue;
+    const int it = (nch + t.lpr - 1) / t.lpr;
+    const bool eff = static_cast<double>(nch) / (it * t.lpr) >= 0.7;
+    const int rows = t.wpb * (64 / t.lpr) * t.rpl;
+    const int wgs = (m + rows - 1) / rows;
+    if (eff && wgs >= cus) return t;
+    if (eff && wgs > best_wgs) {
+      best = t;
+      best_wgs = wgs;
     }
   }
-  const int cus = cu_count();
-  auto wgs = [&](int rpl, int wpb) { return (m + (wpb * (64 / t.lpr) * rpl) - 1) / (wpb * (64 / t.lpr) * rpl); };
-  t.rpl = (act == ACT_GEGLU_TANH || wgs(2, 4) >= 2 * cus) ? 2 : 1;
-  t.wpb = wgs(t.rpl, 4) >= 2 * cus ? 4 : 1;
-  return t;
+  return best;
 }
 
 }  // namespace
@@ -556,13 +643,15 @@ void launch_gemv(const GemvLaunch &L, hipStream_t s) {
   p.out_scale = L.out_scale;
   p.y = L.y;
   p.ldy = L.ldy ? L.ldy : (L.act == ACT_GEGLU_TANH ? L.m / 2 : L.m);
-  const size_t lds = static_cast<size_t>(nb) * L.k * sizeof(float);
+  const size_t lds = static_cast<size_t>(nb + (L.sub ? 1 : 0)) * L.k * sizeof(float);
   XE_REQUIRE(lds <= 160 * 1024 - 1024, "gemv: batch*K too large for LDS staging");
   if (lds > 64 * 1024)
     XE_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(fn),
                                hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
   const int rows_per_block = t.wpb * (64 / t.lpr) * t.rpl;
-  const int grid = (L.m + rows_per_block - 1) / rows_per_block;
+  const int tiles = (L.m + rows_per_block - 1) / rows_per_block;
+  // at most 4 workgroups per CU: large GEMVs loop over tiles and stage x once
+  const int grid = std::min(tiles, 4 * cu_count());
   hipLaunchKernelGGL(fn, dim3(grid), dim3(64 * t.wpb), lds, s, p);
   XE_HIP(hipGetLastError());
 }

@@ -41,6 +41,7 @@ EXPORTS = [
     "xe_decoder_destroy", "xe_decoder_init_synthetic", "xe_decoder_set_tensor",
     "xe_decoder_get_tensor_q8", "xe_decoder_reset", "xe_decoder_set_cross", "xe_decoder_step",
     "xe_decoder_generate", "xe_decoder_last_step_us", "xe_decoder_weight_bytes",
+    "xe_decoder_feed", "xe_decoder_decode", "xe_decoder_profile_step",
 ]
 
 
@@ -143,6 +144,9 @@ def lib():
         "xe_decoder_step": (i, [vp, vp, vp, i, vp, vp]),
         "xe_decoder_generate": (i, [vp, vp, i, i, i, vp]),
         "xe_decoder_last_step_us": (C.c_double, [vp]),
+        "xe_decoder_feed": (i, [vp, vp, i, i]),
+        "xe_decoder_decode": (i, [vp, i, i, vp, C.POINTER(C.c_double)]),
+        "xe_decoder_profile_step": (i, [vp, i, i, vp, vp, vp]),
         "xe_decoder_weight_bytes": (u64, [vp]),
     }
     for name, (res, args) in sig.items():
@@ -436,6 +440,31 @@ class Decoder:
         out = np.empty((b, n_new), np.int32)
         _check(lib().xe_decoder_generate(self.h, _p(prompt), n_prompt, b, n_new, _p(out)))
         return out
+
+    def feed(self, prompt):
+        prompt = np.ascontiguousarray(np.atleast_2d(prompt), np.int32)
+        b, n = prompt.shape
+        _check(lib().xe_decoder_feed(self.h, _p(prompt), n, b))
+        self.batch = b
+
+    def decode(self, n_steps, batch=None, want_tokens=True):
+        """Returns (tokens [batch, n_steps] or None, device microseconds)."""
+        b = batch or self.batch
+        out = np.empty((b, n_steps), np.int32) if want_tokens else None
+        us = C.c_double()
+        _check(lib().xe_decoder_decode(self.h, b, n_steps, _p(out), C.byref(us)))
+        return out, us.value
+
+    def profile_step(self, batch=None, max_entries=4096):
+        """One eager step, an event after each launch: [(label, us, bytes)]."""
+        b = batch or self.batch
+        labels = C.create_string_buffer(32 * max_entries)
+        us = np.empty(max_entries, np.float64)
+        by = np.empty(max_entries, np.float64)
+        n = _check(lib().xe_decoder_profile_step(self.h, b, max_entries, labels, _p(us), _p(by)))
+        raw = labels.raw
+        return [(raw[32 * i:32 * i + 32].split(b"\0")[0].decode(), float(us[i]), float(by[i]))
+                for i in range(n)]
 
     def last_step_us(self):
         return lib().xe_decoder_last_step_us(self.h)
