@@ -151,7 +151,8 @@ def main():
                                "ctx %d" % (B, args.prompt, args.ctx),
                    "layers": cfg.n_layers, "hidden": cfg.d_model, "heads": "4q/1kv x 256",
                    "ffn": cfg.ffn, "vocab": cfg.vocab, "batch": B, "prompt": args.prompt,
-                   "ctx": args.ctx, "seed": args.seed},
+                   "ctx": args.ctx, "seed": args.seed,
+                   "executor": os.environ.get("XE_STEP", "graph")},
         "device_us_per_step": round(dev_us / max(K, 1), 3),
         "hbm": {"achieved": round(hbm_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                 "frac": round(hbm_gbps / HBM_PEAK_GBPS, 4),

@@ -12,12 +12,26 @@ Tiny configs of every family and weight format run to many steps; the real
 OPT-125m and Gemma-3-1B shapes run shorter streams the oracle finishes in
 seconds.  The full-length runs (Gemma prompt 512 -> ctx 4096) are in bench.py.
 """
+import os
+
 import numpy as np
 import pytest
 
 import oracle_lib as O
 
 pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(params=["graph", "persistent"])
+def executor(request):
+    """Run the test under each step executor (XE_STEP is read at every step)."""
+    old = os.environ.get("XE_STEP")
+    os.environ["XE_STEP"] = request.param
+    yield request.param
+    if old is None:
+        os.environ.pop("XE_STEP", None)
+    else:
+        os.environ["XE_STEP"] = old
 
 
 def tiny(xe, family, wdtype):
@@ -87,12 +101,12 @@ CASES = [(f, w) for f in ("opt", "whisper", "gemma") for w in ("i8", "bf16", "bf
 
 
 @pytest.mark.parametrize("family,wd", CASES)
-def test_tiny_greedy_identity(gpu, xe, family, wd):
+def test_tiny_greedy_identity(gpu, xe, executor, family, wd):
     fam = {"opt": xe.XE_OPT, "whisper": xe.XE_WHISPER, "gemma": xe.XE_GEMMA3}[family]
     wdtype = {"i8": xe.XE_I8, "bf16": xe.XE_BF16, "bfp16": xe.XE_BFP16}[wd]
     cfg = tiny(xe, fam, wdtype)
     batch = 3
-    print("[case] tiny %s %s batch %d" % (family, wd, batch), flush=True)
+    print("[case] tiny %s %s batch %d %s" % (family, wd, batch, executor), flush=True)
     dec, om = build(xe, gpu, cfg, seed=11, batch=batch)
     pr = prompts(cfg, batch, 6, seed=1)
     got = dec.generate(pr, 40)
@@ -103,7 +117,7 @@ def test_tiny_greedy_identity(gpu, xe, family, wd):
 
 
 @pytest.mark.parametrize("family", ["opt", "whisper", "gemma"])
-def test_tiny_step_logits(gpu, xe, family):
+def test_tiny_step_logits(gpu, xe, executor, family):
     """step() logits (per-stream positions) vs the oracle's, step by step."""
     fam = {"opt": xe.XE_OPT, "whisper": xe.XE_WHISPER, "gemma": xe.XE_GEMMA3}[family]
     cfg = tiny(xe, fam, xe.XE_I8)
@@ -125,7 +139,7 @@ def test_tiny_step_logits(gpu, xe, family):
     om.close()
 
 
-def test_opt125m_config1(gpu, xe):
+def test_opt125m_config1(gpu, xe, executor):
     """Config 1: OPT-125m shape, int8, seed 0, 32-token prompt, 128 greedy steps."""
     cfg = xe.OPT_125M
     dec, om = build(xe, gpu, cfg, seed=0, batch=1)
@@ -137,7 +151,7 @@ def test_opt125m_config1(gpu, xe):
     om.close()
 
 
-def test_gemma3_1b_short(gpu, xe):
+def test_gemma3_1b_short(gpu, xe, executor):
     """Config 5 shape (Gemma-3-1B, int8, seed 2): a short prompt and stream the
     oracle finishes in seconds, plus step logits."""
     cfg = xe.GEMMA3_1B.replace(max_ctx=512)
@@ -150,7 +164,7 @@ def test_gemma3_1b_short(gpu, xe):
     om.close()
 
 
-def test_whisper_small_short(gpu, xe):
+def test_whisper_small_short(gpu, xe, executor):
     """Config 4 shape (Whisper-small, int8, seed 1, 1500 encoder frames, 4-token
     start prompt)."""
     cfg = xe.WHISPER_SMALL

@@ -23,8 +23,8 @@
 #include <map>
 #include <memory>
 
-#include "common.h"
 #include "quant.h"
+#include "step_dev.h"
 
 namespace xe {
 namespace {
@@ -131,32 +131,6 @@ __global__ void synth_vec_kernel(uint64_t base, float mean, float k, size_t n, f
 // step kernels
 // --------------------------------------------------------------------------
 
-// x[b] = dequant(E[tok[b]]) (+ P[pos[b] + pos_off]) (* emb_scale)
-__global__ void embed_kernel(const void *emb, const float *emb_scale_rows, const uint8_t *emb_exps,
-                             int wdtype, const float *pos_emb, int pos_off, int pos_rows,
-                             float mul, int use_mul, const int32_t *tokens, const int32_t *pos,
-                             int vocab, int d, float *x) {
-  const int b = blockIdx.y;
-  int tok = tokens[b];
-  tok = tok < 0 ? 0 : (tok >= vocab ? vocab - 1 : tok);
-  int prow = pos[b] + pos_off;
-  prow = prow < 0 ? 0 : (prow >= pos_rows ? pos_rows - 1 : prow);
-  for (int j = blockIdx.x * blockDim.x + threadIdx.x; j < d; j += gridDim.x * blockDim.x) {
-    const size_t i = static_cast<size_t>(tok) * d + j;
-    float v;
-    if (wdtype == XE_I8)
-      v = static_cast<float>(static_cast<const int8_t *>(emb)[i]) * emb_scale_rows[tok];
-    else if (wdtype == XE_BF16)
-      v = __uint_as_float(static_cast<uint32_t>(static_cast<const uint16_t *>(emb)[i]) << 16);
-    else
-      v = ldexpf(static_cast<float>(static_cast<const int8_t *>(emb)[i]),
-                 static_cast<int>(emb_exps[i / 8]) - 133);
-    if (pos_emb) v = v + pos_emb[static_cast<size_t>(prow) * d + j];
-    if (use_mul) v = v * mul;
-    x[static_cast<size_t>(b) * d + j] = v;
-  }
-}
-
 // f32 [T, H*hd] rows -> bf16 head-major [H, T, hd]
 __global__ void cross_pack_kernel(const float *src, int t_rows, int heads, int hd, uint16_t *dst) {
   const size_t n = static_cast<size_t>(t_rows) * heads * hd;
@@ -168,94 +142,6 @@ __global__ void cross_pack_kernel(const float *src, int t_rows, int heads, int h
     const int t = static_cast<int>(r / heads);
     dst[(static_cast<size_t>(h) * t_rows + t) * hd + j] = bf16_bits_dev(src[i]);
   }
-}
-
-// Greedy argmax over logits[b, :]: block partials, then a merge launch.
-// last_max = 1: Iterator::max_by (opt125m_decode.rs:303) keeps the LAST of
-// equal maxima; else strict > keeps the first (whisper.rs:749-757).
-// The winner becomes the next input token; pos advances; hist[b][pos] gets it.
-constexpr int kArgBlocks = 64;
-
-__device__ inline bool better(float v, int i, float bv, int bi, int last_max) {
-  if (v != v) return false;  // NaN never wins
-  if (bi < 0) return true;
-  if (v > bv) return true;
-  if (v == bv) return last_max ? i > bi : i < bi;
-  return false;
-}
-
-// Partials: block k of row b reduces its slice of the logits.
-__global__ __launch_bounds__(256) void argmax_partial_kernel(const float *logits, int vocab,
-                                                             int last_max, float *part_v,
-                                                             int *part_i) {
-  const int b = blockIdx.y;
-  const int per = (vocab + kArgBlocks - 1) / kArgBlocks;
-  const int lo = blockIdx.x * per, hi = min(vocab, lo + per);
-  const float *row = logits + static_cast<size_t>(b) * vocab;
-  float bv = -INFINITY;
-  int bi = -1;
-  for (int i = lo + threadIdx.x; i < hi; i += 256) {
-    const float v = row[i];
-    if (better(v, i, bv, bi, last_max)) {
-      bv = v;
-      bi = i;
-    }
-  }
-  __shared__ float sv[256];
-  __shared__ int si[256];
-  sv[threadIdx.x] = bv;
-  si[threadIdx.x] = bi;
-  __syncthreads();
-  for (int w = 128; w >= 1; w >>= 1) {
-    if (threadIdx.x < w) {
-      const float ov = sv[threadIdx.x + w];
-      const int oi = si[threadIdx.x + w];
-      if (oi >= 0 && better(ov, oi, sv[threadIdx.x], si[threadIdx.x], last_max)) {
-        sv[threadIdx.x] = ov;
-        si[threadIdx.x] = oi;
-      }
-    }
-    __syncthreads();
-  }
-  if (threadIdx.x == 0) {
-    part_v[b * kArgBlocks + blockIdx.x] = sv[0];
-    part_i[b * kArgBlocks + blockIdx.x] = si[0];
-  }
-}
-
-// Final: one wave per stream merges the partials; the winner becomes the
-// next input token, pos advances, hist[b][pos] records it.
-__global__ __launch_bounds__(64) void argmax_final_kernel(const float *part_v, const int *part_i,
-                                                          int last_max, int32_t *next,
-                                                          int32_t *tokens, int32_t *pos,
-                                                          int32_t *hist, int hist_stride) {
-  const int b = blockIdx.x;
-  float v = -INFINITY;
-  int idx = -1;
-  for (int k = threadIdx.x; k < kArgBlocks; k += 64) {
-    const float pv = part_v[b * kArgBlocks + k];
-    const int pi = part_i[b * kArgBlocks + k];
-    if (pi >= 0 && better(pv, pi, v, idx, last_max)) {
-      v = pv;
-      idx = pi;
-    }
-  }
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) {
-    const float ov = __shfl_xor(v, off, 64);
-    const int oi = __shfl_xor(idx, off, 64);
-    if (oi >= 0 && better(ov, oi, v, idx, last_max)) {
-      v = ov;
-      idx = oi;
-    }
-  }
-  if (threadIdx.x != 0) return;
-  if (idx < 0) idx = 0;
-  next[b] = idx;
-  tokens[b] = idx;
-  const int p = pos[b];
-  if (p >= 0 && p < hist_stride) hist[static_cast<size_t>(b) * hist_stride + p] = idx;
-  pos[b] = p + 1;
 }
 
 // --------------------------------------------------------------------------
@@ -401,7 +287,22 @@ struct xe_decoder {
   float *attn_work = nullptr;
   int attn_splits = 1;
   int32_t *host_tok = nullptr;  // pinned staging [max_ctx + 1][max_batch] x 2
-  std::map<int, hipGraphExec_t> graphs;
+  // persistent step kernel: one flag slot (128 B) per workgroup + status word
+  unsigned int *step_flags = nullptr;
+  unsigned int *step_status = nullptr;
+  int step_grid = 0;
+  // one execution plan per batch size: the phase list of a step
+  struct Plan {
+    std::vector<sdev::Phase> phases;
+    std::vector<std::string> labels;
+    std::vector<double> bytes;  // algorithmic bytes per phase
+    sdev::Phase *dev_phases = nullptr;
+    size_t step_lds = 0;
+    int step_nb = 1;
+    bool persistent = false;
+    hipGraphExec_t graph = nullptr;
+  };
+  std::map<int, Plan> plans;
   double last_step_us = 0.0;
   bool cross_ready = false;
   int fed = 0;      // prompt length of the current streams
@@ -561,8 +462,11 @@ void alloc_decoder(xe_decoder *d) {
   d->pos = dalloc<int32_t>(B, s);
   d->next = dalloc<int32_t>(B, s);
   d->hist = dalloc<int32_t>(static_cast<size_t>(B) * (c.max_ctx + 1), s);
-  d->arg_v = dalloc<float>(static_cast<size_t>(B) * kArgBlocks, s);
-  d->arg_i = dalloc<int>(static_cast<size_t>(B) * kArgBlocks, s);
+  d->arg_v = dalloc<float>(static_cast<size_t>(B) * sdev::kArgBlocks, s);
+  d->arg_i = dalloc<int>(static_cast<size_t>(B) * sdev::kArgBlocks, s);
+  d->step_grid = d->dev->num_cus > 0 ? d->dev->num_cus : 256;
+  d->step_flags = dalloc<unsigned int>(static_cast<size_t>(d->step_grid) * 32, s);
+  d->step_status = dalloc<unsigned int>(64, s);
   // split-K attention: ~4 workgroups per CU at the largest batch, chunks >= 32 keys
   const int hkv_max = std::max(c.n_kv_heads, wh ? c.n_heads : 0);
   int ms = (4 * d->dev->num_cus) / std::max(1, hkv_max);
@@ -595,7 +499,12 @@ void alloc_decoder(xe_decoder *d) {
 
 void free_decoder(xe_decoder *d) {
   if (d->s) (void)hipStreamSynchronize(d->s);
-  for (auto &kv : d->graphs) (void)hipGraphExecDestroy(kv.second);
+  for (auto &kv : d->plans) {
+    if (kv.second.graph) (void)hipGraphExecDestroy(kv.second.graph);
+    if (kv.second.dev_phases) (void)hipFree(kv.second.dev_phases);
+  }
+  if (d->step_flags) (void)hipFree(d->step_flags);
+  if (d->step_status) (void)hipFree(d->step_status);
   d->emb.release();
   for (auto &l : d->L) {
     for (Mat *m : {&l.qkv, &l.o, &l.fc1, &l.fc2, &l.xq, &l.xk, &l.xv, &l.xo}) m->release();
@@ -628,7 +537,7 @@ void free_decoder(xe_decoder *d) {
   if (d->s) (void)hipStreamDestroy(d->s);
 }
 
-// ---- one GEMV over `batch` rows, chunked by 8 (the GEMV kernel's limit) ----
+// ---- host-side description of one GEMV over `batch` rows ----
 struct GemvCall {
   const Mat *m = nullptr;
   const float *bias = nullptr;
@@ -657,56 +566,106 @@ double gemv_bytes(const GemvCall &g, int batch) {
   return b;
 }
 
-void run_gemv(const GemvCall &g, int batch, hipStream_t s) {
-  for (int b0 = 0; b0 < batch; b0 += 8) {
-    const int nb = std::min(8, batch - b0);
-    GemvLaunch p;
-    p.wdtype = g.m->wdtype;
-    p.w = g.m->w;
-    p.scale = g.m->scale;
-    p.exps = g.m->exps;
-    p.bias = g.bias;
-    p.m = g.m->rows;
-    p.k = g.m->cols;
-    p.x = g.x + static_cast<size_t>(b0) * g.ldx;
-    p.x_dtype = XE_F32;
-    p.ldx = g.ldx;
-    p.batch = nb;
-    p.sub = g.sub ? g.sub + static_cast<size_t>(b0) * g.m->cols : nullptr;
-    p.post_w = g.post_w;
-    p.res_out = g.res_out ? g.res_out + static_cast<size_t>(b0) * g.m->cols : nullptr;
-    p.norm = g.norm;
-    p.gamma = g.gamma;
-    p.beta = g.beta;
-    p.eps = g.eps;
-    p.act = g.act;
-    p.y = g.y + static_cast<size_t>(b0) * g.ldy;
-    p.ldy = g.ldy;
-    launch_gemv(p, s);
+struct PlanBuilder {
+  xe_decoder::Plan &plan;
+  int step_nb;
+  void push(const sdev::Phase &ph, const std::string &label, double bytes, size_t lds) {
+    plan.phases.push_back(ph);
+    plan.labels.push_back(label);
+    plan.bytes.push_back(bytes);
+    plan.step_lds = std::max(plan.step_lds, lds);
   }
-}
+  // one GEMV, in chunks of 8 streams (the GEMV tile's batch limit)
+  void gemv(const GemvCall &g, int batch, const std::string &label) {
+    for (int b0 = 0; b0 < batch; b0 += 8) {
+      const int nb = std::min(8, batch - b0);
+      GemvLaunch L;
+      L.wdtype = g.m->wdtype;
+      L.w = g.m->w;
+      L.scale = g.m->scale;
+      L.exps = g.m->exps;
+      L.bias = g.bias;
+      L.m = g.m->rows;
+      L.k = g.m->cols;
+      L.x = g.x + static_cast<size_t>(b0) * g.ldx;
+      L.x_dtype = XE_F32;
+      L.ldx = g.ldx;
+      L.batch = nb;
+      L.sub = g.sub ? g.sub + static_cast<size_t>(b0) * g.m->cols : nullptr;
+      L.post_w = g.post_w;
+      L.res_out = g.res_out ? g.res_out + static_cast<size_t>(b0) * g.m->cols : nullptr;
+      L.norm = g.norm;
+      L.gamma = g.gamma;
+      L.beta = g.beta;
+      L.eps = g.eps;
+      L.act = g.act;
+      L.y = g.y + static_cast<size_t>(b0) * g.ldy;
+      L.ldy = g.ldy;
+      XE_REQUIRE(L.k % 16 == 0, "gemv: K must be a multiple of 16");
+      sdev::Phase ph{};
+      ph.kind = sdev::PH_GEMV;
+      ph.variant = L.wdtype;
+      const gdev::Tile t = gdev::choose_tile(L.m, L.k, L.act);
+      ph.lpr = t.lpr;
+      ph.rpl = t.rpl;
+      const int rows = 4 * (64 / t.lpr) * t.rpl;
+      ph.nblocks = (L.m + rows - 1) / rows;
+      ph.u.gemv = gdev::to_params(L);
+      push(ph, label, gemv_bytes(g, nb),
+           gdev::gemv_lds_floats(step_nb, L.k, L.sub != nullptr) * sizeof(float));
+    }
+  }
+  void attn(const AttnLaunch &a, const std::string &label, double bytes) {
+    sdev::Phase ph{};
+    ph.kind = sdev::PH_ATTN;
+    ph.hd = a.hd;
+    ph.g = a.hq / a.hkv;
+    ph.nblocks = a.max_splits * a.hkv * a.batch;
+    ph.u.attn = adev::to_params(a);
+    push(ph, label, bytes, adev::attn_lds_floats(ph.hd, ph.g) * sizeof(float));
+    if (a.max_splits > 1) {
+      ph.kind = sdev::PH_MERGE;
+      ph.nblocks = ((ph.g * ph.hd + 255) / 256) * a.hkv * a.batch;
+      push(ph, label + "_merge",
+           4.0 * a.batch * a.hq * (a.hd + 2) * std::min(a.max_splits, 64), adev::merge_lds_floats() * sizeof(float));
+    }
+  }
+};
 
-// Enqueue one decode step for streams [0, B) (tokens/pos already on device).
-void enqueue_step(xe_decoder *d, int B) {
+// The phase list of one decode step for streams [0, B) (tokens/pos on device).
+void build_plan(xe_decoder *d, int B, xe_decoder::Plan &plan) {
   const auto &c = d->c;
-  hipStream_t s = d->s;
   const int D = c.d_model, F = c.ffn, hd = c.head_dim;
   const int hq = c.n_heads * hd, hk = c.n_kv_heads * hd;
   const bool gem = c.family == XE_GEMMA3, wh = c.family == XE_WHISPER, opt = c.family == XE_OPT;
   const int nq = static_cast<int>(d->nqkv());
   const int norm = gem ? XE_NORM_RMS1P : XE_NORM_LN;
+  plan.step_nb = B <= 1 ? 1 : B <= 2 ? 2 : 4;
+  PlanBuilder pb{plan, plan.step_nb};
 
   // embedding
   {
-    const int pos_off = opt ? 2 : 0;
+    sdev::Phase ph{};
+    ph.kind = sdev::PH_EMBED;
     Spec sp;
-    const int prow = tensor_spec(c, XE_T_POS_EMB, -1, sp) ? sp.rows : 1;
-    dim3 grid((D + 255) / 256, B);
-    hipLaunchKernelGGL(embed_kernel, grid, dim3(256), 0, s, d->emb.w, d->emb.scale, d->emb.exps,
-                       c.wdtype, d->pos_emb, pos_off, prow, sqrtf(static_cast<float>(D)),
-                       gem ? 1 : 0, d->tokens, d->pos, c.vocab, D, d->xa);
-    XE_HIP(hipGetLastError());
-    d->mark("embed", static_cast<double>(B) * D * (wbytes(c.wdtype, 1) + 4 + (d->pos_emb ? 4 : 0)));
+    sdev::EmbedParams &e = ph.u.emb;
+    e.emb = d->emb.w;
+    e.emb_scale = d->emb.scale;
+    e.emb_exps = d->emb.exps;
+    e.wdtype = c.wdtype;
+    e.pos_emb = d->pos_emb;
+    e.pos_off = opt ? 2 : 0;
+    e.pos_rows = tensor_spec(c, XE_T_POS_EMB, -1, sp) ? sp.rows : 1;
+    e.mul = sqrtf(static_cast<float>(D));
+    e.use_mul = gem ? 1 : 0;
+    e.tokens = d->tokens;
+    e.pos = d->pos;
+    e.vocab = c.vocab;
+    e.d = D;
+    e.batch = B;
+    e.x = d->xa;
+    ph.nblocks = B * ((D + 255) / 256);
+    pb.push(ph, "embed", static_cast<double>(B) * D * (wbytes(c.wdtype, 1) + 4 + (d->pos_emb ? 4 : 0)), 0);
   }
   float *xcur = d->xa, *xalt = d->xb;
   const float *pend = nullptr, *pend_post = nullptr;
@@ -739,8 +698,7 @@ void enqueue_step(xe_decoder *d, int B) {
       g.eps = c.eps;
       g.y = d->qkv;
       g.ldy = nq;
-      run_gemv(g, B, s);
-      d->mark("gemv_qkv", gemv_bytes(g, B));
+      pb.gemv(g, B, "gemv_qkv");
       after_pending();
     }
     // ---- self attention (append k/v at pos) ----
@@ -773,12 +731,8 @@ void enqueue_step(xe_decoder *d, int B) {
       a.out_stride = hq;
       a.work = d->attn_work;
       a.max_splits = d->attn_splits;
-      launch_attn(a, s);
-      if (d->prof) {
-        double kv = 0;
-        for (int b = 0; b < B; b++) kv += static_cast<double>(d->prof_pos[b] + 1) * hk * 2 * 2;
-        d->mark("attn_self", kv + 4.0 * B * (nq + hq) + 4.0 * B * hk);
-      }
+      // KV bytes depend on the positions; profile_step fills them in
+      pb.attn(a, "attn_self", 4.0 * B * (nq + hq) + 4.0 * B * hk);
     }
     // ---- O projection ----
     {
@@ -789,8 +743,7 @@ void enqueue_step(xe_decoder *d, int B) {
       g.ldx = hq;
       g.y = d->sub;
       g.ldy = D;
-      run_gemv(g, B, s);
-      d->mark("gemv_o", gemv_bytes(g, B));
+      pb.gemv(g, B, "gemv_o");
       pend = d->sub;
       pend_post = gem ? l.post_attn : nullptr;
     }
@@ -806,8 +759,7 @@ void enqueue_step(xe_decoder *d, int B) {
       g.eps = c.eps;
       g.y = d->qx;
       g.ldy = D;
-      run_gemv(g, B, s);
-      d->mark("gemv_xq", gemv_bytes(g, B));
+      pb.gemv(g, B, "gemv_xq");
       after_pending();
       AttnLaunch a;
       a.q = d->qx;
@@ -826,8 +778,7 @@ void enqueue_step(xe_decoder *d, int B) {
       a.out_stride = D;
       a.work = d->attn_work;
       a.max_splits = d->attn_splits;
-      launch_attn(a, s);
-      d->mark("attn_cross", static_cast<double>(c.n_cross) * D * 2 * 2 + 8.0 * B * D);
+      pb.attn(a, "attn_cross", static_cast<double>(c.n_cross) * D * 2 * 2 + 8.0 * B * D);
       GemvCall o;
       o.m = &l.xo;
       o.bias = l.xo_b;
@@ -835,8 +786,7 @@ void enqueue_step(xe_decoder *d, int B) {
       o.ldx = D;
       o.y = d->sub;
       o.ldy = D;
-      run_gemv(o, B, s);
-      d->mark("gemv_xo", gemv_bytes(o, B));
+      pb.gemv(o, B, "gemv_xo");
       pend = d->sub;
       pend_post = nullptr;
     }
@@ -853,8 +803,7 @@ void enqueue_step(xe_decoder *d, int B) {
       g.act = gem ? ACT_GEGLU_TANH : (opt ? ACT_RELU : ACT_GELU_ERF);
       g.y = d->ffn;
       g.ldy = F;
-      run_gemv(g, B, s);
-      d->mark(gem ? "gemv_gateup" : "gemv_fc1", gemv_bytes(g, B));
+      pb.gemv(g, B, gem ? "gemv_gateup" : "gemv_fc1");
       after_pending();
       GemvCall o;
       o.m = &l.fc2;
@@ -863,8 +812,7 @@ void enqueue_step(xe_decoder *d, int B) {
       o.ldx = F;
       o.y = d->sub;
       o.ldy = D;
-      run_gemv(o, B, s);
-      d->mark(gem ? "gemv_down" : "gemv_fc2", gemv_bytes(o, B));
+      pb.gemv(o, B, gem ? "gemv_down" : "gemv_fc2");
       pend = d->sub;
       pend_post = gem ? l.post_ffn : nullptr;
     }
@@ -881,26 +829,65 @@ void enqueue_step(xe_decoder *d, int B) {
     g.eps = c.eps;
     g.y = d->logits;
     g.ldy = c.vocab;
-    run_gemv(g, B, s);
-    d->mark("gemv_lmhead", gemv_bytes(g, B));
+    pb.gemv(g, B, "gemv_lmhead");
   }
   // ---- greedy argmax -> next token, pos + 1 ----
-  hipLaunchKernelGGL(argmax_partial_kernel, dim3(kArgBlocks, B), dim3(256), 0, s, d->logits,
-                     c.vocab, opt ? 1 : 0, d->arg_v, d->arg_i);
-  XE_HIP(hipGetLastError());
-  hipLaunchKernelGGL(argmax_final_kernel, dim3(B), dim3(64), 0, s, d->arg_v, d->arg_i,
-                     opt ? 1 : 0, d->next, d->tokens, d->pos, d->hist, c.max_ctx + 1);
-  XE_HIP(hipGetLastError());
-  d->mark("argmax", 4.0 * B * c.vocab);
+  {
+    sdev::Phase ph{};
+    sdev::ArgmaxParams &ap = ph.u.arg;
+    ap.logits = d->logits;
+    ap.vocab = c.vocab;
+    ap.batch = B;
+    ap.last_max = opt ? 1 : 0;
+    ap.part_v = d->arg_v;
+    ap.part_i = d->arg_i;
+    ap.next = d->next;
+    ap.tokens = d->tokens;
+    ap.pos = d->pos;
+    ap.hist = d->hist;
+    ap.hist_stride = c.max_ctx + 1;
+    ph.kind = sdev::PH_ARGMAX_PART;
+    ph.nblocks = B * sdev::kArgBlocks;
+    pb.push(ph, "argmax", 4.0 * B * c.vocab, 512 * sizeof(float));
+    ph.kind = sdev::PH_ARGMAX_FINAL;
+    ph.nblocks = B;
+    pb.push(ph, "argmax_final", 8.0 * B * sdev::kArgBlocks, 0);
+  }
+  plan.persistent = !getenv("XE_NO_PERSIST") && B <= 4 &&
+                    step_kernel_supported(c.wdtype, plan.step_nb, hd, c.n_heads / c.n_kv_heads) &&
+                    plan.step_lds <= 150 * 1024;
 }
 
-hipGraphExec_t graph_for(xe_decoder *d, int B) {
-  auto it = d->graphs.find(B);
-  if (it != d->graphs.end()) return it->second;
+xe_decoder::Plan &plan_for(xe_decoder *d, int B) {
+  auto it = d->plans.find(B);
+  if (it != d->plans.end()) return it->second;
+  xe_decoder::Plan &plan = d->plans[B];
+  build_plan(d, B, plan);
+  const size_t bytes = plan.phases.size() * sizeof(sdev::Phase);
+  XE_HIP(hipMalloc(reinterpret_cast<void **>(&plan.dev_phases), bytes));
+  XE_HIP(hipMemcpy(plan.dev_phases, plan.phases.data(), bytes, hipMemcpyHostToDevice));
+  return plan;
+}
+
+// Executor choice: the phases as kernels in one HIP graph per token (the
+// default); XE_STEP=persistent selects the persistent step kernel where the
+// plan allows it (one launch per token, a grid barrier between phases);
+// XE_STEP=eager launches the phases one by one (profiling).
+enum class Exec { Persistent, Graph, Eager };
+
+Exec exec_for(const xe_decoder::Plan &plan) {
+  const char *e = getenv("XE_STEP");
+  if (getenv("XE_NO_GRAPH") || (e && std::string(e) == "eager")) return Exec::Eager;
+  if (e && std::string(e) == "persistent" && plan.persistent) return Exec::Persistent;
+  return Exec::Graph;
+}
+
+hipGraphExec_t graph_for(xe_decoder *d, xe_decoder::Plan &plan) {
+  if (plan.graph) return plan.graph;
   hipGraph_t g = nullptr;
   XE_HIP(hipStreamBeginCapture(d->s, hipStreamCaptureModeRelaxed));
   try {
-    enqueue_step(d, B);
+    for (const auto &ph : plan.phases) launch_phase(ph, d->s);
   } catch (...) {
     hipGraph_t junk = nullptr;
     (void)hipStreamEndCapture(d->s, &junk);
@@ -911,16 +898,56 @@ hipGraphExec_t graph_for(xe_decoder *d, int B) {
   hipGraphExec_t ex = nullptr;
   XE_HIP(hipGraphInstantiate(&ex, g, nullptr, nullptr, 0));
   (void)hipGraphDestroy(g);
-  d->graphs[B] = ex;
+  plan.graph = ex;
   return ex;
 }
 
-void run_step(xe_decoder *d, int B) {
-  if (getenv("XE_NO_GRAPH")) {
-    enqueue_step(d, B);
-    return;
+void run_step(xe_decoder *d, int B, uint64_t *trace = nullptr) {
+  xe_decoder::Plan &plan = plan_for(d, B);
+  switch (exec_for(plan)) {
+    case Exec::Persistent: {
+      StepLaunch L;
+      L.trace = trace;
+      L.phases = plan.dev_phases;
+      L.nphases = static_cast<int>(plan.phases.size());
+      L.flags = d->step_flags;
+      L.status = d->step_status;
+      L.wdtype = d->c.wdtype;
+      L.nb = plan.step_nb;
+      L.hd = d->c.head_dim;
+      L.g = d->c.n_heads / d->c.n_kv_heads;
+      L.lds_bytes = plan.step_lds;
+      L.grid = d->step_grid;
+      launch_step(L, d->s);
+      return;
+    }
+    case Exec::Graph:
+      XE_HIP(hipGraphLaunch(graph_for(d, plan), d->s));
+      return;
+    case Exec::Eager:
+      for (const auto &ph : plan.phases) launch_phase(ph, d->s);
+      return;
   }
-  XE_HIP(hipGraphLaunch(graph_for(d, B), d->s));
+}
+
+// Run one GEMV over `batch` rows now (standalone kernels; chunks of 8).
+void run_gemv_now(const GemvCall &g, int batch, hipStream_t s) {
+  xe_decoder::Plan tmp;
+  PlanBuilder pb{tmp, 1};
+  pb.gemv(g, batch, "gemv");
+  for (const auto &ph : tmp.phases) launch_phase(ph, s);
+}
+
+// After a run of persistent steps: a barrier wait that timed out leaves
+// status set; report it and re-arm the flags.
+void check_step_status(xe_decoder *d) {
+  unsigned st = 0;
+  XE_HIP(hipMemcpy(&st, d->step_status, 4, hipMemcpyDeviceToHost));
+  if (st) {
+    XE_HIP(hipMemset(d->step_flags, 0, static_cast<size_t>(d->step_grid) * 128));
+    XE_HIP(hipMemset(d->step_status, 0, 4));
+    fail("persistent step kernel: a phase barrier timed out (flags re-armed); results are invalid");
+  }
 }
 
 void synth_matrix(xe_decoder *d, uint64_t seed, int kind, int layer, const Spec &sp, const Place &p) {
@@ -997,7 +1024,7 @@ void precompute_cross(xe_decoder *d) {
       g.ldx = D;
       g.y = tmp;
       g.ldy = D;
-      run_gemv(g, T, d->s);
+      run_gemv_now(g, T, d->s);
       hipLaunchKernelGGL(cross_pack_kernel, dim3(1024), dim3(256), 0, d->s, tmp, T, c.n_heads,
                          c.head_dim, which == 0 ? l.ck : l.cv);
       XE_HIP(hipGetLastError());
@@ -1179,6 +1206,7 @@ int xe_decoder_step(xe_decoder *d, const int32_t *tokens, const int32_t *pos, in
                             hipMemcpyDeviceToHost, d->s));
     if (next) XE_HIP(hipMemcpyAsync(next, d->next, batch * 4, hipMemcpyDeviceToHost, d->s));
     XE_HIP(hipStreamSynchronize(d->s));
+    check_step_status(d);
     return 0;
   }, -1);
 }
@@ -1210,13 +1238,17 @@ void feed(xe_decoder *d, const int32_t *prompt, int n_prompt, int batch) {
   int32_t *zpos = h + static_cast<size_t>(n_prompt) * batch;
   for (int b = 0; b < batch; b++) zpos[b] = 0;
   XE_HIP(hipMemcpyAsync(d->pos, zpos, batch * 4, hipMemcpyHostToDevice, d->s));
-  if (!getenv("XE_NO_GRAPH")) (void)graph_for(d, batch);
+  {
+    xe_decoder::Plan &plan = plan_for(d, batch);  // build (and capture) before timing
+    if (exec_for(plan) == Exec::Graph) (void)graph_for(d, plan);
+  }
   for (int p = 0; p < n_prompt; p++) {
     XE_HIP(hipMemcpyAsync(d->tokens, h + static_cast<size_t>(p) * batch, batch * 4,
                           hipMemcpyHostToDevice, d->s));
     run_step(d, batch);
   }
   XE_HIP(hipStreamSynchronize(d->s));
+  check_step_status(d);
   d->fed = n_prompt;
   d->decoded = 0;
 }
@@ -1242,6 +1274,7 @@ void decode(xe_decoder *d, int batch, int n_steps, int32_t *out, double *device_
   XE_HIP(hipEventElapsedTime(&ms, e0, e1));
   (void)hipEventDestroy(e0);
   (void)hipEventDestroy(e1);
+  check_step_status(d);
   if (n_steps > 0) d->last_step_us = 1000.0 * ms / n_steps;
   if (device_us) *device_us = 1000.0 * ms;
   d->decoded += n_steps;
@@ -1316,9 +1349,55 @@ int xe_decoder_profile_step(xe_decoder *d, int batch, int max_entries, char *lab
     XE_HIP(hipMemcpy(d->prof_pos.data(), d->pos, batch * 4, hipMemcpyDeviceToHost));
     std::vector<xe_decoder::ProfEntry> entries;
     d->prof = &entries;
+    xe_decoder::Plan &plan = plan_for(d, batch);
+    const double hk4 = static_cast<double>(d->c.n_kv_heads) * d->c.head_dim * 4;
+    double kv_bytes = 0;
+    for (int b = 0; b < batch; b++) kv_bytes += (d->prof_pos[b] + 1) * hk4;
+    auto phase_bytes = [&](size_t i) {
+      return plan.bytes[i] + (plan.labels[i] == "attn_self" ? kv_bytes : 0.0);
+    };
+    if (exec_for(plan) == Exec::Persistent) {
+      // One persistent launch with the wall-clock trace: phase i's time is the
+      // advance of the latest publication (critical path), so the entries sum
+      // to the launch's span from the first workgroup's start.
+      const size_t np = plan.phases.size(), G = static_cast<size_t>(d->step_grid);
+      uint64_t *tr = nullptr;
+      XE_HIP(hipMalloc(reinterpret_cast<void **>(&tr), np * G * 2 * sizeof(uint64_t)));
+      std::vector<uint64_t> h(np * G * 2);
+      try {
+        run_step(d, batch, tr);
+        XE_HIP(hipStreamSynchronize(d->s));
+        XE_HIP(hipMemcpy(h.data(), tr, h.size() * sizeof(uint64_t), hipMemcpyDeviceToHost));
+      } catch (...) {
+        (void)hipFree(tr);
+        throw;
+      }
+      (void)hipFree(tr);
+      check_step_status(d);
+      d->decoded += 1;
+      int khz = 0;
+      XE_HIP(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, d->dev->ordinal));
+      XE_REQUIRE(khz > 0, "device wall clock rate unknown");
+      const double us_per_tick = 1000.0 / khz;
+      uint64_t prev = ~0ull;
+      for (size_t w = 0; w < G; w++) prev = std::min(prev, h[2 * w]);
+      int n = 0;
+      for (size_t i = 0; i < np && n < max_entries; i++, n++) {
+        uint64_t done = 0;
+        for (size_t w = 0; w < G; w++) done = std::max(done, h[2 * (i * G + w) + 1]);
+        us[n] = done > prev ? (done - prev) * us_per_tick : 0.0;
+        bytes[n] = phase_bytes(i);
+        std::snprintf(labels + 32 * n, 32, "%s", plan.labels[i].c_str());
+        prev = std::max(prev, done);
+      }
+      return n;
+    }
     try {
       d->mark("start", 0.0);
-      enqueue_step(d, batch);  // eager, one event after each launch
+      for (size_t i = 0; i < plan.phases.size(); i++) {  // eager, one event after each launch
+        launch_phase(plan.phases[i], d->s);
+        d->mark(plan.labels[i], phase_bytes(i));
+      }
     } catch (...) {
       d->prof = nullptr;
       for (auto &e : entries) (void)hipEventDestroy(e.ev);

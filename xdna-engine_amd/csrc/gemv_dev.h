@@ -1,0 +1,546 @@
+// gemv_dev.h -- device side of the decode GEMV: y[b] = epilogue(W . prologue(x[b])).
+//
+// Replaces the reference's resident GEMV dispatch (CtxDecode::gemv,
+// rust/npu-asr/src/ctx_decode.rs:325-366, and the whole-array design
+// route_b_kernels/decode_norm_gemv/norm_gemv_iron.py:52-216) and its fused
+// pre-norm (ctx_decode.rs:566-643, aie_kernels/norm_gemv_prologue.cc:31-75).
+//
+// Batch <= 8 decode is HBM-bound on the weight stream, so the work is built
+// around the weight bytes:
+//   * Each wave covers RG = 64/LPR row groups; a group's LPR lanes split K in
+//     16-element chunks (16 B of int8 / bfp16 mantissas, 32 B of bf16), so one
+//     load instruction of the wave reads RG rows x LPR*16 B contiguous runs:
+//     whole 128-byte lines from HBM.
+//   * RPL rows per lane share the x chunk held in registers.
+//   * Weight loads run as a ping-pong of two sets of U chunks per row; the
+//     first two sets are issued before the prologue (and, in the persistent
+//     step kernel, before waiting for the inputs), so they overlap HBM
+//     latency and the synchronisation.
+//   * x (after the prologue) lives in LDS as fp32 [b][K]; a lane reads its
+//     16-element chunk as four 16 B words.
+//   * The group reduction is an xor-butterfly over LPR lanes.
+//   * int8 -> fp32 dequant happens in registers; the per-row fp32 scale is
+//     applied after the sum, as in Lin::fwd (opt125m_decode.rs:120-122).
+//
+// COH selects how activations (x, sub, residual, y) are accessed: plain
+// loads/stores in standalone kernels (the kernel boundary publishes them), or
+// coherent (sc1) loads and agent-scope stores in the persistent step kernel,
+// where a phase reads what another XCD wrote in the same launch and the XCDs'
+// L2s are not coherent with each other.  Weights are read-only and always use
+// plain streaming loads.
+#pragma once
+
+#include "common.h"
+
+namespace xe {
+namespace gdev {
+
+constexpr int kMaxWaves = 8;
+
+struct GemvParams {
+  const void *w;
+  const float *scale;
+  const uint8_t *exps;
+  const float *bias;
+  int m, k;
+  const void *x;
+  int x_bf16;
+  int ldx;
+  int batch;
+  const float *sub;
+  const float *post_w;
+  float *res_out;
+  int norm;
+  const float *gamma;
+  const float *beta;
+  float eps;
+  int act;
+  float out_scale;
+  float *y;
+  int ldy;
+};
+
+// ---- coherent (agent-scope) or plain activation access ----
+// A coherent load is a buffer load with the sc1 cache-policy bit: the
+// instruction an agent-scope relaxed atomic load compiles to on gfx950 (it
+// misses the XCD's own L2), but issued as a plain load, so the compiler can
+// keep many in flight under one wait and use the 16-byte form.  Ordering with
+// the phase barrier comes from the barrier's workgroup fence (__syncthreads).
+// `base` must be the same in every lane of the wave (it becomes the buffer
+// descriptor); `idx` is the per-lane element index, < 2^29.
+constexpr int kCoherentSc1 = 16;  // cache-policy operand: sc1
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t coherent_rsrc(const void *base) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  // readfirstlane returns int: widen through uint32_t, never sign-extend
+  const uint64_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(a)));
+  const uint64_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(a >> 32)));
+  // 0x00020000: 32-bit data format (raw buffer, no swizzle, no stride)
+  return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void *>(hi << 32 | lo), static_cast<short>(0),
+                                           0x7ffffff0, 0x00020000);
+}
+
+template <bool COH>
+__device__ __forceinline__ float act_ld(const float *base, int idx) {
+  if constexpr (COH) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(coherent_rsrc(base), idx * 4, 0,
+                                                                          kCoherentSc1));
+  } else {
+    return base[idx];
+  }
+}
+
+// idx is a multiple of 4 (16-byte aligned element)
+template <bool COH>
+__device__ __forceinline__ float4 act_ld4(const float *base, int idx) {
+  if constexpr (COH) {
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
+    const f32x4 v = __builtin_bit_cast(
+        f32x4, __builtin_amdgcn_raw_buffer_load_b128(coherent_rsrc(base), idx * 4, 0, kCoherentSc1));
+    return make_float4(v.x, v.y, v.z, v.w);
+  } else {
+    return *reinterpret_cast<const float4 *>(base + idx);
+  }
+}
+
+template <bool COH>
+__device__ __forceinline__ void act_st(float *p, float v) {
+  if constexpr (COH) {
+    __hip_atomic_store(reinterpret_cast<unsigned int *>(p), __float_as_uint(v), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+  } else {
+    *p = v;
+  }
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+// Block-wide sums of N values over WPB waves with one barrier; `slot`
+// alternates so back-to-back reductions never overwrite a slot still being
+// read.  red holds 2 * 4 * kMaxWaves floats.
+template <int WPB, int N>
+__device__ __forceinline__ void block_sums(float (&v)[N], float *red, int &slot) {
+#pragma unroll
+  for (int i = 0; i < N; i++) v[i] = wave_sum(v[i]);
+  if constexpr (WPB == 1) return;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  float *r = red + slot * 4 * kMaxWaves;
+  slot ^= 1;
+  if (lane == 0)
+#pragma unroll
+    for (int i = 0; i < N; i++) r[i * kMaxWaves + wave] = v[i];
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < N; i++) {
+    float t = 0.f;
+#pragma unroll
+    for (int w = 0; w < WPB; w++) t += r[i * kMaxWaves + w];
+    v[i] = t;
+  }
+}
+
+__device__ __forceinline__ float gelu_erf(float x) {
+  // Abramowitz & Stegun 7.1.26 erf, the reference's host GELU
+  // (rust/npu-asr-host/src/lib.rs:464-489).
+  float z = x * 0.70710678118654752f;
+  float sgn = z < 0.f ? -1.f : 1.f;
+  float a = fabsf(z);
+  float t = 1.0f / (1.0f + 0.3275911f * a);
+  float y = 1.0f - (((((1.061405429f * t - 1.453152027f) * t) + 1.421413741f) * t -
+                     0.284496736f) * t + 0.254829592f) * t * expf(-a * a);
+  return 0.5f * x * (1.0f + sgn * y);
+}
+
+__device__ __forceinline__ float gelu_tanh(float x) {
+  // gelu_pytorch_tanh (rust/npu-gemma/src/lib.rs:74-77).
+  const float c = 0.79788456f;
+  return 0.5f * x * (1.0f + tanhf(c * (x + 0.044715f * x * x * x)));
+}
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+// 16-byte streaming load (weights are read once per step: nontemporal).
+__device__ __forceinline__ uint4 ld_nt16(const void *ptr) {
+  const u32x4 v = __builtin_nontemporal_load(static_cast<const u32x4 *>(ptr));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// One 16-element chunk of a weight row, raw.
+template <int WT>
+struct Chunk;
+template <>
+struct Chunk<XE_I8> {
+  uint4 q;
+};
+template <>
+struct Chunk<XE_BFP16> {
+  uint4 q;
+  uint32_t e;  // two biased exponents (low 16 bits)
+};
+template <>
+struct Chunk<XE_BF16> {
+  uint4 lo, hi;
+};
+
+template <int WT>
+__device__ __forceinline__ void load_chunk(const GemvParams &p, int row, int c, Chunk<WT> &out) {
+  if constexpr (WT == XE_I8) {
+    const uint4 *base = reinterpret_cast<const uint4 *>(static_cast<const int8_t *>(p.w) +
+                                                        static_cast<size_t>(row) * p.k);
+    out.q = ld_nt16(base + c);
+  } else if constexpr (WT == XE_BFP16) {
+    const uint4 *base = reinterpret_cast<const uint4 *>(static_cast<const int8_t *>(p.w) +
+                                                        static_cast<size_t>(row) * p.k);
+    out.q = ld_nt16(base + c);
+    const uint16_t *eb = reinterpret_cast<const uint16_t *>(p.exps + static_cast<size_t>(row) * (p.k / 8));
+    out.e = eb[c];
+  } else {
+    const uint4 *base = reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(p.w) +
+                                                        static_cast<size_t>(row) * p.k);
+    out.lo = ld_nt16(base + 2 * c);
+    out.hi = ld_nt16(base + 2 * c + 1);
+  }
+}
+
+__device__ __forceinline__ float sb(uint32_t w, int j) {
+  return static_cast<float>(static_cast<int>(static_cast<int8_t>(w >> (8 * j))));
+}
+
+// acc += dot(chunk, x[16])
+template <int WT>
+__device__ __forceinline__ float chunk_dot(const Chunk<WT> &ch, const float4 (&xv)[4], float acc) {
+  if constexpr (WT == XE_I8) {
+    const uint32_t w4[4] = {ch.q.x, ch.q.y, ch.q.z, ch.q.w};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      acc = __builtin_fmaf(xv[i].x, sb(w4[i], 0), acc);
+      acc = __builtin_fmaf(xv[i].y, sb(w4[i], 1), acc);
+      acc = __builtin_fmaf(xv[i].z, sb(w4[i], 2), acc);
+      acc = __builtin_fmaf(xv[i].w, sb(w4[i], 3), acc);
+    }
+    return acc;
+  } else if constexpr (WT == XE_BFP16) {
+    const uint32_t w4[4] = {ch.q.x, ch.q.y, ch.q.z, ch.q.w};
+    float d[2];
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      float s = 0.f;
+#pragma unroll
+      for (int i = 2 * h; i < 2 * h + 2; i++) {
+        s = __builtin_fmaf(xv[i].x, sb(w4[i], 0), s);
+        s = __builtin_fmaf(xv[i].y, sb(w4[i], 1), s);
+        s = __builtin_fmaf(xv[i].z, sb(w4[i], 2), s);
+        s = __builtin_fmaf(xv[i].w, sb(w4[i], 3), s);
+      }
+      d[h] = s;
+    }
+    const int e0 = static_cast<int>(ch.e & 0xff) - 133;  // e - 127 - 6
+    const int e1 = static_cast<int>((ch.e >> 8) & 0xff) - 133;
+    acc += __builtin_ldexpf(d[0], e0);
+    acc += __builtin_ldexpf(d[1], e1);
+    return acc;
+  } else {
+    const uint32_t w8[8] = {ch.lo.x, ch.lo.y, ch.lo.z, ch.lo.w, ch.hi.x, ch.hi.y, ch.hi.z, ch.hi.w};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const uint32_t a = w8[2 * i], b = w8[2 * i + 1];
+      acc = __builtin_fmaf(xv[i].x, __uint_as_float(a << 16), acc);
+      acc = __builtin_fmaf(xv[i].y, __uint_as_float(a & 0xffff0000u), acc);
+      acc = __builtin_fmaf(xv[i].z, __uint_as_float(b << 16), acc);
+      acc = __builtin_fmaf(xv[i].w, __uint_as_float(b & 0xffff0000u), acc);
+    }
+    return acc;
+  }
+}
+
+// LDS the GEMV needs: x rows + one staged sub row (floats).
+__host__ __device__ inline size_t gemv_lds_floats(int nb, int k, bool sub) {
+  return static_cast<size_t>(nb + (sub ? 1 : 0)) * k;
+}
+
+// Prologue: x (+ post(sub)) -> res_out (block 0) -> norm -> LDS, fp32.
+// Statistics are reduced once per row:
+//   Gemma (sub + post_w, RMS1P): t = x + sub*inv_s*(1+w) and
+//     sum t^2 = sum x^2 + 2 inv_s sum x*s' + inv_s^2 sum s'^2 (s' = sub*(1+w)),
+//     so sum sub^2, sum x^2, sum x*s', sum s'^2 come out of one reduction.
+//   LayerNorm: two passes (sum t, then sum (t - mean)^2) as the reference's
+//     layer_norm (npu-asr-host/src/lib.rs:79-109); one-pass variance loses
+//     everything on near-constant rows.
+// `writer` marks the one workgroup that stores the updated residual.
+template <int NB, int WPB, bool COH>
+__device__ __forceinline__ void gemv_prologue(const GemvParams &p, float4 *xs4, float *red, bool writer) {
+  constexpr int kThreads = 64 * WPB;
+  constexpr int UNR = 4;  // float4 loads in flight per thread
+  const int K = p.k, K4 = K / 4;
+  const float fk = static_cast<float>(K);
+  float *xs = reinterpret_cast<float *>(xs4);
+  float *sb = xs + static_cast<size_t>(NB) * K;  // sub staging (one row)
+  int slot = 0;
+  for (int b = 0; b < p.batch && b < NB; b++) {
+    float4 *xb4 = xs4 + static_cast<size_t>(b) * K4;
+    float *xb = xs + static_cast<size_t>(b) * K;
+    const float *subr = p.sub ? p.sub + static_cast<size_t>(b) * K : nullptr;
+    const float *xrow = static_cast<const float *>(p.x) + static_cast<size_t>(b) * p.ldx;
+    const bool fold = p.sub && p.post_w;  // Gemma post-norm + residual
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};  // fold: sum sub^2, x^2, x*s', s'^2
+    for (int i0 = threadIdx.x; i0 < K4; i0 += kThreads * UNR) {
+      float4 v[UNR], sv[UNR];
+#pragma unroll
+      for (int u = 0; u < UNR; u++) {
+        const int i = i0 + u * kThreads;
+        if (i < K4) {
+          if (!COH && p.x_bf16) {
+            const uint2 r = reinterpret_cast<const uint2 *>(static_cast<const uint16_t *>(p.x) +
+                                                            static_cast<size_t>(b) * p.ldx)[i];
+            v[u] = make_float4(__uint_as_float(r.x << 16), __uint_as_float(r.x & 0xffff0000u),
+                               __uint_as_float(r.y << 16), __uint_as_float(r.y & 0xffff0000u));
+          } else {
+            v[u] = act_ld4<COH>(xrow, 4 * i);
+          }
+          if (subr) sv[u] = act_ld4<COH>(subr, 4 * i);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < UNR; u++) {
+        const int i = i0 + u * kThreads;
+        if (i >= K4) continue;
+        xb4[i] = v[u];
+        if (subr) reinterpret_cast<float4 *>(sb)[i] = sv[u];
+        if (fold) {
+          const float4 w = reinterpret_cast<const float4 *>(p.post_w)[i];
+          const float xv[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+          const float su[4] = {sv[u].x, sv[u].y, sv[u].z, sv[u].w};
+          const float wv[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+          for (int j = 0; j < 4; j++) {
+            const float sp = su[j] * (1.0f + wv[j]);
+            acc[0] = __builtin_fmaf(su[j], su[j], acc[0]);
+            acc[1] = __builtin_fmaf(xv[j], xv[j], acc[1]);
+            acc[2] = __builtin_fmaf(xv[j], sp, acc[2]);
+            acc[3] = __builtin_fmaf(sp, sp, acc[3]);
+          }
+        }
+      }
+    }
+    if (fold) {
+      block_sums<WPB, 4>(acc, red, slot);
+      const float inv_s = 1.0f / sqrtf(acc[0] / fk + p.eps);
+      const float st2 = acc[1] + 2.0f * inv_s * acc[2] + inv_s * inv_s * acc[3];
+      const float inv_t = p.norm != XE_NORM_NONE ? 1.0f / sqrtf(fmaxf(st2, 0.f) / fk + p.eps) : 1.f;
+      __syncthreads();  // staging complete (block_sums skips its barrier for one wave)
+      for (int i = threadIdx.x; i < K; i += kThreads) {
+        const float t = xb[i] + sb[i] * inv_s * (1.0f + p.post_w[i]);
+        if (p.res_out && writer) act_st<COH>(p.res_out + static_cast<size_t>(b) * K + i, t);
+        float h = t;
+        if (p.norm == XE_NORM_RMS1P) h = t * inv_t * (1.0f + p.gamma[i]);
+        else if (p.norm == XE_NORM_RMS) h = t * inv_t * p.gamma[i];
+        xb[i] = h;
+      }
+      if (p.norm == XE_NORM_LN) {  // not a model combination; kept exact anyway
+        __syncthreads();
+        float v1[1] = {0.f};
+        for (int i = threadIdx.x; i < K; i += kThreads) v1[0] += xb[i];
+        block_sums<WPB, 1>(v1, red, slot);
+        const float mean = v1[0] / fk;
+        float v2[1] = {0.f};
+        for (int i = threadIdx.x; i < K; i += kThreads) {
+          const float c = xb[i] - mean;
+          v2[0] = __builtin_fmaf(c, c, v2[0]);
+        }
+        block_sums<WPB, 1>(v2, red, slot);
+        const float inv = 1.0f / sqrtf(v2[0] / fk + p.eps);
+        __syncthreads();
+        for (int i = threadIdx.x; i < K; i += kThreads) xb[i] = (xb[i] - mean) * inv * p.gamma[i] + p.beta[i];
+      }
+    } else {
+      __syncthreads();
+      if (subr) {
+        for (int i = threadIdx.x; i < K; i += kThreads) {
+          const float t = xb[i] + sb[i];
+          xb[i] = t;
+          if (p.res_out && writer) act_st<COH>(p.res_out + static_cast<size_t>(b) * K + i, t);
+        }
+        if (p.norm != XE_NORM_NONE) __syncthreads();
+      }
+      if (p.norm == XE_NORM_LN) {
+        float v1[1] = {0.f};
+        for (int i = threadIdx.x; i < K; i += kThreads) v1[0] += xb[i];
+        block_sums<WPB, 1>(v1, red, slot);
+        const float mean = v1[0] / fk;
+        float v2[1] = {0.f};
+        for (int i = threadIdx.x; i < K; i += kThreads) {
+          const float c = xb[i] - mean;
+          v2[0] = __builtin_fmaf(c, c, v2[0]);
+        }
+        block_sums<WPB, 1>(v2, red, slot);
+        const float inv = 1.0f / sqrtf(v2[0] / fk + p.eps);
+        for (int i = threadIdx.x; i < K; i += kThreads) xb[i] = (xb[i] - mean) * inv * p.gamma[i] + p.beta[i];
+      } else if (p.norm != XE_NORM_NONE) {
+        float v1[1] = {0.f};
+        for (int i = threadIdx.x; i < K; i += kThreads) v1[0] = __builtin_fmaf(xb[i], xb[i], v1[0]);
+        block_sums<WPB, 1>(v1, red, slot);
+        const float inv = 1.0f / sqrtf(v1[0] / fk + p.eps);
+        for (int i = threadIdx.x; i < K; i += kThreads)
+          xb[i] = p.norm == XE_NORM_RMS1P ? xb[i] * inv * (1.0f + p.gamma[i]) : xb[i] * inv * p.gamma[i];
+      }
+    }
+    if (subr && b + 1 < p.batch && b + 1 < NB) __syncthreads();  // sub staging is reused
+  }
+  __syncthreads();
+}
+
+struct NoWait {
+  __device__ void operator()() const {}
+};
+
+// Row tiles first_tile, first_tile + stride, ... of one GEMV.  `wait` runs
+// after the first tile's weight loads are issued and before the prologue
+// reads any activation (the persistent kernel waits for its inputs there).
+// Returns false when this workgroup had no tile (wait was still called).
+template <int WT, int NB, int LPR, int RPL, int WPB, bool COH, typename Wait>
+__device__ __forceinline__ void gemv_tiles(const GemvParams &p, float4 *xs4, float *red, int first_tile, int stride,
+                           bool writer, Wait wait) {
+  constexpr int RG = 64 / LPR;
+  // Chunks per row in one load set.  Two sets are in flight (ping-pong).  The
+  // persistent kernel runs one wave per SIMD, so it needs deeper sets than a
+  // standalone launch, where other waves cover the latency.
+  constexpr int U = COH ? ((RPL >= 2) ? 4 : 8) : ((RPL >= 2) ? 2 : 4);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int rg = lane / LPR, kl = lane % LPR;
+  constexpr int rows_per_wave = RG * RPL;
+  constexpr int rows_per_block = WPB * rows_per_wave;
+  const int K = p.k, nch = K / 16;
+  const int n_it = (nch + LPR - 1) / LPR;
+  const int ntiles = (p.m + rows_per_block - 1) / rows_per_block;
+  const float *xs = reinterpret_cast<const float *>(xs4);
+
+  if (first_tile >= ntiles) {
+    wait();
+    return;
+  }
+  for (int tile = first_tile; tile < ntiles; tile += stride) {
+    const int row0 = tile * rows_per_block + wave * rows_per_wave + rg * RPL;
+    bool row_ok[RPL];
+    int row[RPL];
+#pragma unroll
+    for (int i = 0; i < RPL; i++) {
+      row[i] = row0 + i;
+      row_ok[i] = row[i] < p.m;
+      if (!row_ok[i]) row[i] = p.m - 1;  // clamp: loads stay in bounds, result dropped
+    }
+
+    // Load set s covers chunk iterations [s*U, s*U + U).
+    Chunk<WT> ca[U][RPL], cb[U][RPL];
+    auto load_set = [&](Chunk<WT>(&dst)[U][RPL], int it0) {
+#pragma unroll
+      for (int u = 0; u < U; u++) {
+        const int c = (it0 + u) * LPR + kl;
+#pragma unroll
+        for (int i = 0; i < RPL; i++)
+          if (c < nch) load_chunk<WT>(p, row[i], c, dst[u][i]);
+      }
+    };
+    load_set(ca, 0);
+    if (U < n_it) load_set(cb, U);
+    if (tile == first_tile) {
+      wait();
+      gemv_prologue<NB, WPB, COH>(p, xs4, red, writer);
+    }
+
+    float acc[NB][RPL];
+#pragma unroll
+    for (int b = 0; b < NB; b++)
+#pragma unroll
+      for (int i = 0; i < RPL; i++) acc[b][i] = 0.f;
+
+    auto compute = [&](const Chunk<WT>(&chs)[RPL], int c) {
+#pragma unroll
+      for (int b = 0; b < NB; b++) {
+        if (b < p.batch) {
+          float4 xv[4];
+          const float4 *xr = reinterpret_cast<const float4 *>(xs + static_cast<size_t>(b) * K + c * 16);
+#pragma unroll
+          for (int j = 0; j < 4; j++) xv[j] = xr[j];
+#pragma unroll
+          for (int i = 0; i < RPL; i++) acc[b][i] = chunk_dot<WT>(chs[i], xv, acc[b][i]);
+        }
+      }
+    };
+
+    auto compute_set = [&](const Chunk<WT>(&src)[U][RPL], int it0) {
+#pragma unroll
+      for (int u = 0; u < U; u++) {
+        const int c = (it0 + u) * LPR + kl;
+        if (c < nch) compute(src[u], c);
+      }
+    };
+    // ping-pong: while one set is consumed the other is in flight
+    for (int it = 0; it < n_it; it += 2 * U) {
+      compute_set(ca, it);
+      if (it + 2 * U < n_it) load_set(ca, it + 2 * U);
+      if (it + U < n_it) {
+        compute_set(cb, it + U);
+        if (it + 3 * U < n_it) load_set(cb, it + 3 * U);
+      }
+    }
+
+    // ---- reduce over the LPR lanes of the group ----
+#pragma unroll
+    for (int b = 0; b < NB; b++)
+#pragma unroll
+      for (int i = 0; i < RPL; i++) {
+        float v = acc[b][i];
+#pragma unroll
+        for (int off = LPR / 2; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+        acc[b][i] = v;
+      }
+
+    // ---- epilogue (lane 0 of each group) ----
+    if (kl == 0) {
+#pragma unroll
+      for (int b = 0; b < NB; b++) {
+        if (b >= p.batch) break;
+        float v[RPL];
+#pragma unroll
+        for (int i = 0; i < RPL; i++) {
+          float t = acc[b][i];
+          if (WT == XE_I8) t = t * p.scale[row[i]];
+          if (p.bias) t = t + p.bias[row[i]];
+          v[i] = t;
+        }
+        if (p.act == ACT_GEGLU_TANH) {
+#pragma unroll
+          for (int i = 0; i + 1 < RPL; i += 2)
+            if (row_ok[i])
+              act_st<COH>(p.y + static_cast<size_t>(b) * p.ldy + row[i] / 2,
+                          gelu_tanh(v[i]) * v[i + 1] * p.out_scale);
+        } else {
+#pragma unroll
+          for (int i = 0; i < RPL; i++) {
+            if (!row_ok[i]) continue;
+            float t = v[i];
+            if (p.act == ACT_RELU) t = t > 0.f ? t : 0.f;
+            else if (p.act == ACT_GELU_ERF) t = gelu_erf(t);
+            act_st<COH>(p.y + static_cast<size_t>(b) * p.ldy + row[i], t * p.out_scale);
+          }
+        }
+      }
+    }
+  }
+}
+
+// ---- host: tile choice (shared by the standalone kernel and the step kernel) ----
+struct Tile {
+  int lpr, rpl, wpb;
+};
+
+int cu_count();
+Tile choose_tile(int m, int k, int act);
+GemvParams to_params(const GemvLaunch &L);
+
+}  // namespace gdev
+}  // namespace xe
