@@ -49,7 +49,7 @@ def cpu_baseline(cfg, prompt_len, budget_s, seed):
     oc = O.ModelConfig()
     for name, _ in O.ModelConfig._fields_:
         setattr(oc, name, getattr(cfg, name))
-    oc.max_ctx = 64
+    oc.max_ctx = 2048
     threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or (os.cpu_count() or 1)
     O.lib().xo_set_threads(threads)
     om = O.OracleModel(oc, seed, 1)
