@@ -9,11 +9,16 @@ prompt and W warm-up steps are untimed; exactly K steps are timed between
 device synchronisations (default: every remaining step up to ctx 4096).
 
 Extra fields of the JSON line:
-  roofline      the decode GEMV family (the dominant kernels): algorithmic
-                bytes / device time, per-launch HIP events on the decoder
-                stream, in one profiled step at the end context
-  hbm           whole-step algorithmic bytes (weights + scales + KV + small
-                tensors) / measured step time
+  roofline      the dominant kernel.  Low-latency executor (the default where
+                it supports the model and batch): the step kernel, one
+                cooperative launch per run of up to 256 tokens that does the
+                whole step (every layer's GEMVs and attention, the lm-head,
+                the argmax), so achieved = algorithmic bytes of the timed
+                steps / their device time (HIP events on the decoder
+                stream).  Phase-kernel executors: the GEMV family, from
+                per-launch events in one profiled step at the end context.
+  hbm           whole-step algorithmic bytes (weights + scales + KV read at
+                the mean context of the timed steps) / measured step time
   cpu_baseline  the CPU oracle (oracle/, a C restatement of the reference's
                 decode arithmetic) on a bounded sample of the same workload,
                 timed on this host's cores
@@ -118,9 +123,8 @@ def main():
     step_s = (t1 - t0) / K
     tok_s = B * K / (t1 - t0)
 
+    executor = dec.executor(B)
     prof = dec.profile_step()
-    g_bytes = sum(b for l, u, b in prof if l.startswith("gemv"))
-    g_us = sum(u for l, u, b in prof if l.startswith("gemv"))
     by_label = {}
     for l, u, b in prof:
         e = by_label.setdefault(l, [0, 0.0, 0.0])
@@ -132,6 +136,17 @@ def main():
     kv_bytes = B * cfg.n_layers * mean_ctx * cfg.n_kv_heads * cfg.head_dim * 2 * 2
     step_bytes = dec.weight_bytes() + kv_bytes
     hbm_gbps = step_bytes / step_s / 1e9
+    if executor == "ll":
+        # one launch per run of <= 256 tokens: bytes and time summed over the
+        # timed launches give the per-launch average ratio
+        r_bytes, r_us = step_bytes * K, dev_us
+        r_kernel = ("ll_step_kernel (whole decode step per token; %d launches of <= 256 "
+                    "steps in the timed region)" % ((K + 255) // 256))
+    else:
+        r_bytes = sum(b for l, u, b in prof if l.startswith("gemv"))
+        r_us = sum(u for l, u, b in prof if l.startswith("gemv"))
+        r_kernel = "gemv (decode GEMV family, one profiled step)"
+    r_gbps = r_bytes / r_us / 1e3
 
     out = {
         "metric": "int8 decode tok/s, Gemma3-1B-shape b=%d" % B,
@@ -152,15 +167,15 @@ def main():
                    "layers": cfg.n_layers, "hidden": cfg.d_model, "heads": "4q/1kv x 256",
                    "ffn": cfg.ffn, "vocab": cfg.vocab, "batch": B, "prompt": args.prompt,
                    "ctx": args.ctx, "seed": args.seed,
-                   "executor": os.environ.get("XE_STEP", "graph")},
+                   "executor": executor},
         "device_us_per_step": round(dev_us / max(K, 1), 3),
         "hbm": {"achieved": round(hbm_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                 "frac": round(hbm_gbps / HBM_PEAK_GBPS, 4),
                 "bytes_per_step": int(step_bytes)},
-        "roofline": {"bound": "hbm", "kernel": "gemv (decode GEMV family, one profiled step)",
-                     "achieved": round(g_bytes / g_us / 1e3, 1), "peak": HBM_PEAK_GBPS,
-                     "unit": "GB/s", "frac": round(g_bytes / g_us / 1e3 / HBM_PEAK_GBPS, 4),
-                     "traffic": None, "bytes": int(g_bytes), "us": round(g_us, 2)},
+        "roofline": {"bound": "hbm", "kernel": r_kernel,
+                     "achieved": round(r_gbps, 1), "peak": HBM_PEAK_GBPS,
+                     "unit": "GB/s", "frac": round(r_gbps / HBM_PEAK_GBPS, 4),
+                     "traffic": None, "bytes": int(r_bytes), "us": round(r_us, 2)},
         "phases": {l: {"launches": v[0], "us": round(v[1], 2),
                        "gbps": round(v[2] / v[1] / 1e3, 1) if v[1] > 0 else None}
                    for l, v in by_label.items()},

@@ -291,6 +291,15 @@ int xe_decoder_decode(xe_decoder *dec, int batch, int n_steps, int32_t *out,
  * counterpart of FUSED_PHASE_TIMING (whisper_decoder.rs:741-779). */
 int xe_decoder_profile_step(xe_decoder *dec, int batch, int max_entries, char *labels,
                             double *us, double *bytes);
+/* Executor a decode step of `batch` streams runs on.  XE_EXEC_LL is the
+ * default wherever its plan supports the model and batch: one cooperative
+ * launch per token run, workgroups exchanging activations through HBM.  The
+ * others launch one kernel per phase (HIP graph, a persistent kernel with
+ * grid barriers, or eager launches), selected with XE_STEP=graph|persistent|
+ * eager.  No counterpart in the reference (its executors are fixed per
+ * backend); returns -1 on error. */
+enum { XE_EXEC_GRAPH = 0, XE_EXEC_PERSISTENT = 1, XE_EXEC_EAGER = 2, XE_EXEC_LL = 3 };
+int xe_decoder_executor(xe_decoder *dec, int batch);
 /* Mean device time (microseconds) of the last generate's decode steps. */
 double xe_decoder_last_step_us(xe_decoder *dec);
 /* Bytes of weights one decode step streams (int8/bf16/bfp16 + scales). */

@@ -22,7 +22,7 @@ import oracle_lib as O
 pytestmark = pytest.mark.gpu
 
 
-@pytest.fixture(params=["graph", "persistent"])
+@pytest.fixture(params=["graph", "persistent", "ll"])
 def executor(request):
     """Run the test under each step executor (XE_STEP is read at every step)."""
     old = os.environ.get("XE_STEP")

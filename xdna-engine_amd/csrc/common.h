@@ -172,4 +172,39 @@ struct AttnLaunch {
 size_t attn_work_floats(int batch, int hq, int hd, int max_splits);
 void launch_attn(const AttnLaunch &p, hipStream_t s);
 
+// ---------------------------------------------------------------------------
+// Address-space views.  A pointer read from a descriptor in memory (rather
+// than a kernel argument) is generic to the compiler, which then emits flat
+// instructions: they count against both the vector-memory and the LDS wait
+// counters, so every LDS wait would also wait for the weight stream.  These
+// casts give global (1) and LDS (3) instructions.
+// ---------------------------------------------------------------------------
+#define XE_GLOBAL __attribute__((address_space(1)))
+#define XE_LDS __attribute__((address_space(3)))
+// Constant (4): read-only for the kernel's lifetime.  Loads through it at a
+// uniform address become scalar loads, so descriptor fields (loop bounds,
+// pointers) are known wave-uniform and branches on them stay scalar.
+#define XE_CONST __attribute__((address_space(4)))
+
+template <typename T>
+__device__ __forceinline__ const XE_GLOBAL T *gptr(const T *p) {
+  return (const XE_GLOBAL T *)p;
+}
+template <typename T>
+__device__ __forceinline__ XE_GLOBAL T *gptr_w(T *p) {
+  return (XE_GLOBAL T *)p;
+}
+template <typename T>
+__device__ __forceinline__ const XE_CONST T *cptr(const T *p) {
+  return (const XE_CONST T *)p;
+}
+template <typename T>
+__device__ __forceinline__ XE_LDS T *lptr(T *p) {
+  return (XE_LDS T *)p;
+}
+template <typename T>
+__device__ __forceinline__ const XE_LDS T *lptr(const T *p) {
+  return (const XE_LDS T *)p;
+}
+
 }  // namespace xe

@@ -23,6 +23,7 @@
 #include <map>
 #include <memory>
 
+#include "ll_dev.h"
 #include "quant.h"
 #include "step_dev.h"
 
@@ -303,6 +304,23 @@ struct xe_decoder {
     hipGraphExec_t graph = nullptr;
   };
   std::map<int, Plan> plans;
+  // low-latency persistent executor (ll_dev.h): one plan per batch size
+  struct LLPlan {
+    bool ok = false;
+    std::string why;  // reason it is unsupported
+    std::vector<ll::Phase> a, f;
+    std::vector<std::string> a_labels, f_labels;
+    std::vector<double> a_bytes, f_bytes;  // algorithmic bytes per phase (KV added per step)
+    ll::Phase *dev_a = nullptr, *dev_f = nullptr;
+    uint64_t *arena = nullptr;  // every exchange vector of the step
+    ll::Vec arg{};
+    int kin = 0, scratch = 0, nb_t = 1, grid = 0, hd = 64, g = 1;
+    size_t lds_bytes = 0;
+    int head_lpr = 8, head_rpl = 2;
+  };
+  std::map<int, LLPlan> ll_plans;
+  unsigned ll_epoch = 1;           // epoch of the next step (exchange buffers start at 0)
+  int32_t *ll_forced = nullptr;    // device [max_ctx + 1][max_batch] prompt tokens
   double last_step_us = 0.0;
   bool cross_ready = false;
   int fed = 0;      // prompt length of the current streams
@@ -467,6 +485,7 @@ void alloc_decoder(xe_decoder *d) {
   d->step_grid = d->dev->num_cus > 0 ? d->dev->num_cus : 256;
   d->step_flags = dalloc<unsigned int>(static_cast<size_t>(d->step_grid) * 32, s);
   d->step_status = dalloc<unsigned int>(64, s);
+  d->ll_forced = dalloc<int32_t>(static_cast<size_t>(c.max_ctx + 1) * B, s);
   // split-K attention: ~4 workgroups per CU at the largest batch, chunks >= 32 keys
   const int hkv_max = std::max(c.n_kv_heads, wh ? c.n_heads : 0);
   int ms = (4 * d->dev->num_cus) / std::max(1, hkv_max);
@@ -504,6 +523,12 @@ void free_decoder(xe_decoder *d) {
     if (kv.second.dev_phases) (void)hipFree(kv.second.dev_phases);
   }
   if (d->step_flags) (void)hipFree(d->step_flags);
+  for (auto &kv : d->ll_plans) {
+    if (kv.second.dev_a) (void)hipFree(kv.second.dev_a);
+    if (kv.second.dev_f) (void)hipFree(kv.second.dev_f);
+    if (kv.second.arena) (void)hipFree(kv.second.arena);
+  }
+  if (d->ll_forced) (void)hipFree(d->ll_forced);
   if (d->step_status) (void)hipFree(d->step_status);
   d->emb.release();
   for (auto &l : d->L) {
@@ -869,6 +894,355 @@ xe_decoder::Plan &plan_for(xe_decoder *d, int B) {
   return plan;
 }
 
+// ---------------------------------------------------------------------------
+// low-latency persistent executor: phase lists per role (ll_dev.h)
+// ---------------------------------------------------------------------------
+// GEMV tile for `ranks` workgroups of kT threads sharing m rows: lanes per
+// row LPR in {8, 16, 32, 64}, two rows per lane (ll_dev.h gemv_rows).  Each
+// tile costs one memory round trip per load round (NIT chunk iterations per
+// row: ll_dev.h Round); then fewer valid chunks per lane (serial FMA work).
+void ll_tile(int m, int ranks, int k, bool geglu, int wdtype, int &lpr, int &rpl) {
+  (void)geglu;
+  const int rows = (m + ranks - 1) / ranks, nch = k / 16;
+  const int nit = wdtype == XE_BF16 ? 4 : 9;
+  long best = -1;
+  rpl = 2;
+  for (int cand : {8, 16, 32, 64}) {
+    const int per_tile = ll::kW * (64 / cand) * 2;
+    const long tiles = (rows + per_tile - 1) / per_tile;
+    const long n_it = (nch + cand - 1) / cand;
+    const long rounds = (n_it + nit - 1) / nit;
+    const long cost = tiles * rounds * 1000 + tiles * std::min<long>(n_it, nit) * 20;
+    if (best < 0 || cost < best) {
+      best = cost;
+      lpr = cand;
+    }
+  }
+}
+
+void build_ll_plan(xe_decoder *d, int B, xe_decoder::LLPlan &P) {
+  const auto &c = d->c;
+  const int D = c.d_model, F = c.ffn, hd = c.head_dim;
+  const int hq = c.n_heads * hd, hk = c.n_kv_heads * hd;
+  const bool gem = c.family == XE_GEMMA3, wh = c.family == XE_WHISPER, opt = c.family == XE_OPT;
+  const int nq = static_cast<int>(d->nqkv());
+  const int norm = gem ? XE_NORM_RMS1P : XE_NORM_LN;
+  const int g = c.n_heads / c.n_kv_heads;
+  P.ok = false;
+  if (B > ll::kMaxNB) { P.why = "batch > 4"; return; }
+  P.nb_t = B <= 1 ? 1 : B <= 2 ? 2 : 4;
+  P.hd = hd;
+  P.g = g;
+  if (!ll::step_supported(c.wdtype, P.nb_t, hd, g)) { P.why = "head_dim / group not instantiated"; return; }
+  if (hd % ll::kDM != 0) { P.why = "head_dim not a multiple of 16"; return; }
+  for (int k : {D, F, hq}) if (k % 16) { P.why = "K not a multiple of 16"; return; }
+  P.grid = d->dev->num_cus > 0 ? d->dev->num_cus : 256;
+  const int n_a = (P.grid + ll::kRoleStride - 1) / ll::kRoleStride, n_f = P.grid - n_a;
+
+  // exchange arena: offsets first, one allocation after
+  size_t pairs = 0;
+  std::vector<std::pair<size_t, int>> vecs;  // (offset, ld)
+  auto vec = [&](int n) -> int {  // returns index into vecs
+    const int ld = (n + 1) / 2 * 2;
+    vecs.push_back({pairs, ld});
+    pairs += static_cast<size_t>(ld) * B;
+    pairs = (pairs + 1) / 2 * 2;
+    return static_cast<int>(vecs.size()) - 1;
+  };
+  // phases refer to vectors by index until the arena exists: (list, phase, field) -> vec
+  enum Field { F_GEMV_IN, F_GEMV_OUT, F_FOLD_SRC, F_ATTN_Q, F_ATTN_PART, F_MERGE_PART, F_MERGE_OUT,
+               F_GEMV_FOLD0, F_GEMV_FOLD1, F_GEMV_FOLD2 };
+  struct Fix {
+    std::vector<ll::Phase> *list;
+    size_t idx;
+    Field field;
+    int vec;
+  };
+  std::vector<Fix> fix;
+  auto field_of = [](ll::Phase &ph, Field f) -> ll::Vec & {
+    switch (f) {
+      case F_GEMV_IN: return ph.u.gemv.in;
+      case F_GEMV_OUT: return ph.u.gemv.out;
+      case F_FOLD_SRC: return ph.u.fold.src;
+      case F_ATTN_Q: return ph.u.attn.q;
+      case F_ATTN_PART: return ph.u.attn.part;
+      case F_MERGE_PART: return ph.u.merge.part;
+      case F_GEMV_FOLD0: return ph.u.gemv.folds[0].src;
+      case F_GEMV_FOLD1: return ph.u.gemv.folds[1].src;
+      case F_GEMV_FOLD2: return ph.u.gemv.folds[2].src;
+      default: return ph.u.merge.out;
+    }
+  };
+  auto splits_for = [&](int heads_kv, int len_cap) {
+    int ms = n_a / std::max(1, heads_kv * B);
+    const int gran = ll::round_keys(hd);
+    const int cap = (len_cap + gran - 1) / gran;
+    return std::max(1, std::min(std::min(ms, cap), ll::kMaxSplits));
+  };
+  const int ms_self = splits_for(c.n_kv_heads, c.max_ctx);
+  const int ms_cross = wh ? splits_for(c.n_heads, c.n_cross) : 1;
+
+  auto labels_of = [&](std::vector<ll::Phase> &list) -> std::vector<std::string> & {
+    return &list == &P.a ? P.a_labels : P.f_labels;
+  };
+  auto bytes_of = [&](std::vector<ll::Phase> &list) -> std::vector<double> & {
+    return &list == &P.a ? P.a_bytes : P.f_bytes;
+  };
+  struct PreFold {
+    int vec;
+    const float *post_w;
+  };
+  auto gemv = [&](std::vector<ll::Phase> &list, int ranks, const Mat &m, const float *bias, int in_vec,
+                  int norm_kind, const float *gamma, const float *beta, int act, int out_vec, const char *label,
+                  std::vector<PreFold> pre = {}) {
+    ll::Phase ph{};
+    ph.kind = ll::LK_GEMV;
+    ll::GemvD &gd = ph.u.gemv;
+    gd.w = m.w;
+    gd.scale = m.scale;
+    gd.exps = m.exps;
+    gd.bias = bias;
+    gd.m = m.rows;
+    gd.k = m.cols;
+    ll_tile(m.rows, ranks, m.cols, act == ACT_GEGLU_TANH, m.wdtype, gd.lpr, gd.rpl);
+    gd.in_vec = in_vec >= 0 ? 1 : 0;
+    gd.norm = norm_kind;
+    gd.gamma = gamma;
+    gd.beta = beta;
+    gd.eps = c.eps;
+    gd.act = act;
+    XE_REQUIRE(pre.size() <= 3, "internal: too many residual updates before one GEMV");
+    gd.nfold = static_cast<int>(pre.size());
+    for (size_t f = 0; f < pre.size(); f++) {
+      gd.folds[f].post_w = pre[f].post_w;
+      gd.folds[f].eps = c.eps;
+    }
+    list.push_back(ph);
+    labels_of(list).push_back(label);
+    bytes_of(list).push_back(static_cast<double>(m.bytes()) + (bias ? 4.0 * m.rows : 0.0) +
+                             4.0 * B * (m.cols + (act == ACT_GEGLU_TANH ? m.rows / 2 : m.rows)));
+    for (size_t f = 0; f < pre.size(); f++)
+      fix.push_back({&list, list.size() - 1, static_cast<Field>(F_GEMV_FOLD0 + f), pre[f].vec});
+    if (in_vec >= 0) fix.push_back({&list, list.size() - 1, F_GEMV_IN, in_vec});
+    fix.push_back({&list, list.size() - 1, F_GEMV_OUT, out_vec});
+  };
+  auto fold = [&](std::vector<ll::Phase> &list, int src, const float *post_w, const char *label) {
+    ll::Phase ph{};
+    ph.kind = ll::LK_FOLD;
+    ph.u.fold.post_w = post_w;
+    ph.u.fold.eps = c.eps;
+    list.push_back(ph);
+    labels_of(list).push_back(label);
+    bytes_of(list).push_back(4.0 * B * D);
+    fix.push_back({&list, list.size() - 1, F_FOLD_SRC, src});
+  };
+  auto attn = [&](int qv, int qn, int q_off, int k_off, int v_off, bool append, uint16_t *kc, uint16_t *vc,
+                  size_t bstride, int max_ctx, int heads, int heads_kv, float scale, int fixed_len,
+                  const float *qnw, const float *knw, bool rope, int ms, int part, int out, int div_norm,
+                  const char *label) {
+    ll::Phase ph{};
+    ph.kind = ll::LK_ATTN;
+    ll::AttnD &a = ph.u.attn;
+    a.qn = qn;
+    a.q_off = q_off;
+    a.k_off = k_off;
+    a.v_off = v_off;
+    a.append = append ? 1 : 0;
+    a.kc = kc;
+    a.vc = vc;
+    a.kv_bstride = bstride;
+    a.max_ctx = max_ctx;
+    a.hq = heads;
+    a.hkv = heads_kv;
+    XE_REQUIRE(heads / heads_kv == g, "internal: attention group differs from the kernel's");
+    a.hd = hd;
+    a.scale = scale;
+    a.fixed_len = fixed_len;
+    a.q_norm_w = qnw;
+    a.k_norm_w = knw;
+    a.norm_eps = c.eps;
+    a.rope_cos = rope ? d->rope_cos : nullptr;
+    a.rope_sin = rope ? d->rope_sin : nullptr;
+    a.max_splits = ms;
+    P.a.push_back(ph);
+    P.a_labels.push_back(label);
+    P.a_bytes.push_back(fixed_len > 0 ? 4.0 * fixed_len * heads_kv * hd * B : 0.0);
+    fix.push_back({&P.a, P.a.size() - 1, F_ATTN_Q, qv});
+    fix.push_back({&P.a, P.a.size() - 1, F_ATTN_PART, part});
+    ll::Phase mp{};
+    mp.kind = ll::LK_MERGE;
+    mp.u.merge.hq = heads;
+    mp.u.merge.hd = hd;
+    mp.u.merge.max_splits = ms;
+    mp.u.merge.fixed_len = fixed_len;
+    mp.u.merge.div_norm = div_norm;
+    P.a.push_back(mp);
+    P.a_labels.push_back(std::string(label) + "_merge");
+    P.a_bytes.push_back(4.0 * B * heads * hd);
+    fix.push_back({&P.a, P.a.size() - 1, F_MERGE_PART, part});
+    fix.push_back({&P.a, P.a.size() - 1, F_MERGE_OUT, out});
+  };
+  P.a.clear();
+  P.f.clear();
+  P.a_labels.clear();
+  P.f_labels.clear();
+  P.a_bytes.clear();
+  P.f_bytes.clear();
+
+  // Residual updates ride in the prologue of the next GEMV that needs the
+  // residual: A side QKV(L) folds o(L-1) [or xo(L-1)] and down(L-1), Whisper
+  // XQ(L) folds o(L); F side FC1(L) folds down(L-1), o(L) [and xo(L)].  The
+  // tails fold what is left before the lm-head.
+  int p_o = -1, p_xo = -1, p_down = -1;  // previous layer's vectors
+  const float *p_post_attn = nullptr, *p_post_ffn = nullptr;
+  for (int li = 0; li < c.n_layers; li++) {
+    Layer &l = d->L[li];
+    const int v_qkv = vec(nq);
+    const int v_part = vec(hq * ms_self * (hd + 2));
+    const int v_att = vec(hq);
+    const int v_o = vec(D);
+    const int v_ffn = vec(F);
+    const int v_down = vec(D);
+    // ---- A side ----
+    std::vector<PreFold> pre_a;
+    if (li > 0) {
+      if (wh) pre_a.push_back({p_xo, nullptr});
+      else pre_a.push_back({p_o, p_post_attn});
+      pre_a.push_back({p_down, p_post_ffn});
+    }
+    gemv(P.a, n_a, l.qkv, gem ? nullptr : l.qkv_b, -1, norm, l.ln1_w, gem ? nullptr : l.ln1_b, ACT_NONE, v_qkv,
+         "gemv_qkv", pre_a);
+    attn(v_qkv, nq, 0, hq, hq + hk, true, d->kc + d->kv_layer_elems() * li, d->vc + d->kv_layer_elems() * li,
+         static_cast<size_t>(c.n_kv_heads) * c.max_ctx * hd, c.max_ctx, c.n_heads, c.n_kv_heads,
+         opt ? powf(static_cast<float>(hd), -0.5f) : 1.0f / sqrtf(static_cast<float>(hd)), 0,
+         gem ? l.qn : nullptr, gem ? l.kn : nullptr, gem, ms_self, v_part, v_att, opt ? 1 : 0, "attn_self");
+    gemv(P.a, n_a, l.o, gem ? nullptr : l.o_b, v_att, XE_NORM_NONE, nullptr, nullptr, ACT_NONE, v_o, "gemv_o");
+    int v_xo = -1;
+    if (wh) {
+      const int v_xq = vec(D);
+      const int v_xpart = vec(c.n_heads * ms_cross * (hd + 2));
+      const int v_xatt = vec(D);
+      v_xo = vec(D);
+      gemv(P.a, n_a, l.xq, l.xq_b, -1, XE_NORM_LN, l.lnx_w, l.lnx_b, ACT_NONE, v_xq, "gemv_xq", {{v_o, nullptr}});
+      attn(v_xq, D, 0, 0, 0, false, l.ck, l.cv, 0, c.n_cross, c.n_heads, c.n_heads,
+           1.0f / sqrtf(static_cast<float>(hd)), c.n_cross, nullptr, nullptr, false, ms_cross, v_xpart, v_xatt, 0,
+           "attn_cross");
+      gemv(P.a, n_a, l.xo, l.xo_b, v_xatt, XE_NORM_NONE, nullptr, nullptr, ACT_NONE, v_xo, "gemv_xo");
+    }
+    // ---- F side ----
+    std::vector<PreFold> pre_f;
+    if (li > 0) pre_f.push_back({p_down, p_post_ffn});
+    pre_f.push_back({v_o, gem ? l.post_attn : nullptr});
+    if (wh) pre_f.push_back({v_xo, nullptr});
+    gemv(P.f, n_f, l.fc1, gem ? nullptr : l.fc1_b, -1, norm, l.ln2_w, gem ? nullptr : l.ln2_b,
+         gem ? ACT_GEGLU_TANH : (opt ? ACT_RELU : ACT_GELU_ERF), v_ffn, gem ? "gemv_gateup" : "gemv_fc1", pre_f);
+    gemv(P.f, n_f, l.fc2, gem ? nullptr : l.fc2_b, v_ffn, XE_NORM_NONE, nullptr, nullptr, ACT_NONE, v_down,
+         gem ? "gemv_down" : "gemv_fc2");
+    p_o = v_o;
+    p_xo = v_xo;
+    p_down = v_down;
+    p_post_attn = gem ? l.post_attn : nullptr;
+    p_post_ffn = gem ? l.post_ffn : nullptr;
+  }
+  // tails: the last layer's updates before the lm-head
+  if (wh) fold(P.a, p_xo, nullptr, "fold_xo");
+  else fold(P.a, p_o, p_post_attn, "fold_o");
+  fold(P.a, p_down, p_post_ffn, "fold_down");
+  fold(P.f, p_down, p_post_ffn, "fold_down");
+  // argmax partials: [2 parities][B rows][grid * 2]
+  const size_t arg_off = pairs;
+  const int arg_ld = 2 * P.grid;
+  pairs += static_cast<size_t>(2) * B * arg_ld;
+
+  XE_HIP(hipMalloc(reinterpret_cast<void **>(&P.arena), pairs * 8));
+  XE_HIP(hipMemsetAsync(P.arena, 0, pairs * 8, d->s));
+  for (auto &fx : fix) {
+    ll::Vec &v = field_of((*fx.list)[fx.idx], fx.field);
+    v.p = P.arena + vecs[fx.vec].first;
+    v.ld = vecs[fx.vec].second;
+  }
+  P.arg.p = P.arena + arg_off;
+  P.arg.ld = arg_ld;
+  XE_HIP(hipMalloc(reinterpret_cast<void **>(&P.dev_a), std::max<size_t>(1, P.a.size()) * sizeof(ll::Phase)));
+  XE_HIP(hipMalloc(reinterpret_cast<void **>(&P.dev_f), std::max<size_t>(1, P.f.size()) * sizeof(ll::Phase)));
+  XE_HIP(hipMemcpyAsync(P.dev_a, P.a.data(), P.a.size() * sizeof(ll::Phase), hipMemcpyHostToDevice, d->s));
+  XE_HIP(hipMemcpyAsync(P.dev_f, P.f.data(), P.f.size() * sizeof(ll::Phase), hipMemcpyHostToDevice, d->s));
+  XE_HIP(hipStreamSynchronize(d->s));
+
+  ll_tile(c.vocab, P.grid, D, false, c.wdtype, P.head_lpr, P.head_rpl);
+  P.kin = std::max(std::max(D, F), std::max(hq, nq));
+  P.scratch = std::max(std::max(ll::attn_scratch_floats(hd, g), ll::attn_scratch_floats(hd, 1)),
+                       std::max(ll::kMaxSplits * (ll::kDM + 2) + ll::kMaxSplits + 2, P.nb_t * 2 * P.grid)) + 16;
+  P.lds_bytes = sizeof(float) * (static_cast<size_t>(P.nb_t) * D + static_cast<size_t>(P.nb_t) * P.kin + P.scratch);
+  if (P.lds_bytes > 160 * 1024 - 2048) { P.why = "LDS need too large"; return; }
+  P.ok = true;
+}
+
+xe_decoder::LLPlan &ll_plan_for(xe_decoder *d, int B) {
+  auto it = d->ll_plans.find(B);
+  if (it != d->ll_plans.end()) return it->second;
+  xe_decoder::LLPlan &P = d->ll_plans[B];
+  build_ll_plan(d, B, P);
+  return P;
+}
+
+constexpr int kLLChunk = 256;  // decode steps per low-latency launch
+
+// n_steps tokens in one launch.  forced: device [n_forced][B] input tokens of
+// the first steps (prompt feeding); logits: written for every step (the last
+// step's values remain).
+void run_ll(xe_decoder *d, int B, int n_steps, const int32_t *forced, int n_forced, bool want_logits,
+            uint64_t *trace = nullptr) {
+  xe_decoder::LLPlan &P = ll_plan_for(d, B);
+  XE_REQUIRE(P.ok, "low-latency executor unsupported here: " + P.why);
+  const auto &c = d->c;
+  const bool gem = c.family == XE_GEMMA3, opt = c.family == XE_OPT;
+  ll::StepParams sp{};
+  sp.ph_a = P.dev_a;
+  sp.n_a = static_cast<int>(P.a.size());
+  sp.ph_f = P.dev_f;
+  sp.n_f = static_cast<int>(P.f.size());
+  sp.emb = d->emb.w;
+  sp.emb_scale = d->emb.scale;
+  sp.emb_exps = d->emb.exps;
+  sp.pos_emb = d->pos_emb;
+  Spec ps;
+  sp.pos_off = opt ? 2 : 0;
+  sp.pos_rows = tensor_spec(c, XE_T_POS_EMB, -1, ps) ? ps.rows : 1;
+  sp.emb_mul = sqrtf(static_cast<float>(c.d_model));
+  sp.use_mul = gem ? 1 : 0;
+  sp.vocab = c.vocab;
+  sp.d = c.d_model;
+  sp.nb = B;
+  sp.head_norm = gem ? XE_NORM_RMS1P : XE_NORM_LN;
+  sp.head_gamma = d->lnf_w;
+  sp.head_beta = gem ? nullptr : d->lnf_b;
+  sp.head_eps = c.eps;
+  sp.head_lpr = P.head_lpr;
+  sp.head_rpl = P.head_rpl;
+  sp.logits = want_logits ? d->logits : nullptr;
+  sp.arg = P.arg;
+  sp.last_max = opt ? 1 : 0;
+  sp.tokens = d->tokens;
+  sp.pos = d->pos;
+  sp.next = d->next;
+  sp.hist = d->hist;
+  sp.hist_stride = c.max_ctx + 1;
+  sp.forced = forced;
+  sp.n_forced = forced ? n_forced : 0;
+  sp.n_steps = n_steps;
+  sp.ep0 = d->ll_epoch;
+  sp.status = d->step_status;
+  int khz = 0;
+  XE_HIP(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, d->dev->ordinal));
+  sp.limit = static_cast<uint64_t>(khz > 0 ? khz : 100000) * 50;  // 50 ms per wait
+  sp.kin = P.kin;
+  sp.scratch = P.scratch;
+  sp.trace = trace;
+  ll::launch(sp, c.wdtype, P.nb_t, P.hd, P.g, P.lds_bytes, P.grid, d->s);
+  d->ll_epoch += static_cast<unsigned>(n_steps);
+}
+
 // Executor choice: the phases as kernels in one HIP graph per token (the
 // default); XE_STEP=persistent selects the persistent step kernel where the
 // plan allows it (one launch per token, a grid barrier between phases);
@@ -902,7 +1276,20 @@ hipGraphExec_t graph_for(xe_decoder *d, xe_decoder::Plan &plan) {
   return ex;
 }
 
+// The low-latency executor (the default) where its plan supports the model
+// and batch; otherwise, or when XE_STEP / XE_NO_GRAPH name a phase-kernel
+// executor, the phase kernels.
+bool use_ll(xe_decoder *d, int B) {
+  const char *e = getenv("XE_STEP");
+  if (getenv("XE_NO_GRAPH") || (e && *e && std::string(e) != "ll")) return false;
+  return ll_plan_for(d, B).ok;
+}
+
 void run_step(xe_decoder *d, int B, uint64_t *trace = nullptr) {
+  if (!trace && use_ll(d, B)) {
+    run_ll(d, B, 1, nullptr, 0, true);
+    return;
+  }
   xe_decoder::Plan &plan = plan_for(d, B);
   switch (exec_for(plan)) {
     case Exec::Persistent: {
@@ -946,7 +1333,8 @@ void check_step_status(xe_decoder *d) {
   if (st) {
     XE_HIP(hipMemset(d->step_flags, 0, static_cast<size_t>(d->step_grid) * 128));
     XE_HIP(hipMemset(d->step_status, 0, 4));
-    fail("persistent step kernel: a phase barrier timed out (flags re-armed); results are invalid");
+    fail(st == 2u ? "low-latency step kernel: GEMV tile not compiled (host/device tile menus differ); results are invalid"
+                  : "persistent step kernel: a phase barrier timed out (flags re-armed); results are invalid");
   }
 }
 
@@ -1238,6 +1626,16 @@ void feed(xe_decoder *d, const int32_t *prompt, int n_prompt, int batch) {
   int32_t *zpos = h + static_cast<size_t>(n_prompt) * batch;
   for (int b = 0; b < batch; b++) zpos[b] = 0;
   XE_HIP(hipMemcpyAsync(d->pos, zpos, batch * 4, hipMemcpyHostToDevice, d->s));
+  if (use_ll(d, batch)) {  // the whole prompt in one launch, tokens forced
+    XE_HIP(hipMemcpyAsync(d->ll_forced, h, static_cast<size_t>(n_prompt) * batch * 4, hipMemcpyHostToDevice, d->s));
+    XE_HIP(hipMemcpyAsync(d->tokens, h, batch * 4, hipMemcpyHostToDevice, d->s));
+    run_ll(d, batch, n_prompt, d->ll_forced, n_prompt, false);
+    XE_HIP(hipStreamSynchronize(d->s));
+    check_step_status(d);
+    d->fed = n_prompt;
+    d->decoded = 0;
+    return;
+  }
   {
     xe_decoder::Plan &plan = plan_for(d, batch);  // build (and capture) before timing
     if (exec_for(plan) == Exec::Graph) (void)graph_for(d, plan);
@@ -1266,8 +1664,13 @@ void decode(xe_decoder *d, int batch, int n_steps, int32_t *out, double *device_
   hipEvent_t e0, e1;
   XE_HIP(hipEventCreate(&e0));
   XE_HIP(hipEventCreate(&e1));
+  const bool ll_exec = use_ll(d, batch);
   XE_HIP(hipEventRecord(e0, d->s));
-  for (int i = 0; i < n_steps; i++) run_step(d, batch);
+  if (ll_exec) {
+    for (int i = 0; i < n_steps; i += kLLChunk) run_ll(d, batch, std::min(kLLChunk, n_steps - i), nullptr, 0, false);
+  } else {
+    for (int i = 0; i < n_steps; i++) run_step(d, batch);
+  }
   XE_HIP(hipEventRecord(e1, d->s));
   XE_HIP(hipEventSynchronize(e1));
   float ms = 0.f;
@@ -1356,6 +1759,90 @@ int xe_decoder_profile_step(xe_decoder *d, int batch, int max_entries, char *lab
     auto phase_bytes = [&](size_t i) {
       return plan.bytes[i] + (plan.labels[i] == "attn_self" ? kv_bytes : 0.0);
     };
+    if (use_ll(d, batch)) {
+      // One low-latency step with the wall-clock trace: per role, each phase's
+      // time is the advance of that role's latest phase end (the A and F
+      // sides overlap, so the two lists are separate timelines).
+      xe_decoder::LLPlan &P = ll_plan_for(d, batch);
+      const size_t na = P.a.size(), nf = P.f.size(), G = static_cast<size_t>(P.grid);
+      const size_t slots = 2 * (na + nf) + 4 + 3 * (na + nf);
+      uint64_t *tr = nullptr;
+      XE_HIP(hipMalloc(reinterpret_cast<void **>(&tr), slots * G * sizeof(uint64_t)));
+      std::vector<uint64_t> h(slots * G);
+      try {
+        XE_HIP(hipMemsetAsync(tr, 0, slots * G * sizeof(uint64_t), d->s));
+        run_ll(d, batch, 1, nullptr, 0, true, tr);
+        XE_HIP(hipStreamSynchronize(d->s));
+        XE_HIP(hipMemcpy(h.data(), tr, h.size() * sizeof(uint64_t), hipMemcpyDeviceToHost));
+      } catch (...) {
+        (void)hipFree(tr);
+        throw;
+      }
+      (void)hipFree(tr);
+      check_step_status(d);
+      d->decoded += 1;
+      int khz = 0;
+      XE_HIP(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, d->dev->ordinal));
+      XE_REQUIRE(khz > 0, "device wall clock rate unknown");
+      const double us_per_tick = 1000.0 / khz;
+      uint64_t t0 = ~0ull;
+      for (size_t w = 0; w < G; w++) t0 = std::min(t0, h[(na + nf + 3) * G + w]);
+      auto slot_max = [&](size_t sl) {
+        uint64_t m = 0;
+        for (size_t w = 0; w < G; w++) m = std::max(m, h[sl * G + w]);
+        return m;
+      };
+      int n = 0;
+      auto emit = [&](const std::string &label, uint64_t from, uint64_t to, double b) {
+        if (n >= max_entries) return;
+        us[n] = to > from ? (to - from) * us_per_tick : 0.0;
+        bytes[n] = b;
+        std::snprintf(labels + 32 * n, 32, "%s", label.c_str());
+        n++;
+      };
+      // per phase: "wait" = previous end -> input ready (latest over the
+      // role's workgroups), then ready -> end
+      uint64_t prev = t0, a_end = t0, f_end = t0;
+      for (size_t i = 0; i < na; i++) {
+        const uint64_t r = slot_max(na + nf + 4 + i), e = slot_max(i);
+        emit("A:wait:" + P.a_labels[i], prev, std::max(prev, r), 0.0);
+        const bool is_attn = P.a[i].kind == ll::LK_ATTN;
+        if (is_attn) {  // sub-stages: q/k staged, keys done, partials out
+          const size_t sb = 2 * (na + nf) + 4 + 3 * i;
+          const uint64_t s1 = slot_max(sb + 1), s2 = slot_max(sb + 2);
+          emit("A:" + P.a_labels[i] + ".stage", std::max(prev, r), s1, 0.0);
+          emit("A:" + P.a_labels[i] + ".keys", s1, s2, P.a_bytes[i] + (P.a_labels[i] == "attn_self" ? kv_bytes : 0.0));
+          emit("A:" + P.a_labels[i] + ".out", s2, e, 0.0);
+        } else if (P.a[i].kind == ll::LK_GEMV) {  // compute / reduction + epilogue
+          const uint64_t s1 = slot_max(2 * (na + nf) + 4 + 3 * i + 1);
+          emit("A:" + P.a_labels[i] + ".mac", std::max(prev, r), s1, P.a_bytes[i]);
+          emit("A:" + P.a_labels[i] + ".epi", s1, e, 0.0);
+        } else {
+          emit("A:" + P.a_labels[i], std::max(prev, r), e, P.a_bytes[i]);
+        }
+        prev = std::max(prev, e);
+      }
+      a_end = prev;
+      prev = t0;
+      for (size_t i = 0; i < nf; i++) {
+        const uint64_t r = slot_max(2 * na + nf + 4 + i), e = slot_max(na + i);
+        emit("F:wait:" + P.f_labels[i], prev, std::max(prev, r), 0.0);
+        if (P.f[i].kind == ll::LK_GEMV) {
+          const uint64_t s1 = slot_max(2 * (na + nf) + 4 + 3 * (na + i) + 1);
+          emit("F:" + P.f_labels[i] + ".mac", std::max(prev, r), s1, P.f_bytes[i]);
+          emit("F:" + P.f_labels[i] + ".epi", s1, e, 0.0);
+        } else {
+          emit("F:" + P.f_labels[i], std::max(prev, r), e, P.f_bytes[i]);
+        }
+        prev = std::max(prev, e);
+      }
+      f_end = prev;
+      const uint64_t lm = slot_max(na + nf), am = slot_max(na + nf + 1), em = slot_max(na + nf + 2);
+      emit("gemv_lmhead", std::max(a_end, f_end), lm, static_cast<double>(d->emb.bytes()));
+      emit("argmax", lm, am, 16.0 * batch * G);
+      emit("embed", am, em, static_cast<double>(batch) * d->c.d_model * 4);
+      return n;
+    }
     if (exec_for(plan) == Exec::Persistent) {
       // One persistent launch with the wall-clock trace: phase i's time is the
       // advance of the latest publication (critical path), so the entries sum
@@ -1416,6 +1903,21 @@ int xe_decoder_profile_step(xe_decoder *d, int batch, int max_entries, char *lab
     }
     for (auto &e : entries) (void)hipEventDestroy(e.ev);
     return n;
+  }, -1);
+}
+
+int xe_decoder_executor(xe_decoder *d, int batch) {
+  return guard_d([&]() -> int {
+    XE_REQUIRE(d, "null decoder");
+    XE_REQUIRE(batch >= 1 && batch <= d->max_batch, "batch out of range");
+    DeviceGuard dg(d->dev->ordinal);
+    if (use_ll(d, batch)) return XE_EXEC_LL;
+    switch (exec_for(plan_for(d, batch))) {
+      case Exec::Persistent: return XE_EXEC_PERSISTENT;
+      case Exec::Eager: return XE_EXEC_EAGER;
+      case Exec::Graph: break;
+    }
+    return XE_EXEC_GRAPH;
   }, -1);
 }
 

@@ -86,7 +86,7 @@ __device__ __forceinline__ float act_ld(const float *base, int idx) {
     return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(coherent_rsrc(base), idx * 4, 0,
                                                                           kCoherentSc1));
   } else {
-    return base[idx];
+    return gptr(base)[idx];
   }
 }
 
@@ -99,17 +99,19 @@ __device__ __forceinline__ float4 act_ld4(const float *base, int idx) {
         f32x4, __builtin_amdgcn_raw_buffer_load_b128(coherent_rsrc(base), idx * 4, 0, kCoherentSc1));
     return make_float4(v.x, v.y, v.z, v.w);
   } else {
-    return *reinterpret_cast<const float4 *>(base + idx);
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
+    const f32x4 v = *gptr(reinterpret_cast<const f32x4 *>(base + idx));
+    return make_float4(v.x, v.y, v.z, v.w);
   }
 }
 
 template <bool COH>
 __device__ __forceinline__ void act_st(float *p, float v) {
   if constexpr (COH) {
-    __hip_atomic_store(reinterpret_cast<unsigned int *>(p), __float_as_uint(v), __ATOMIC_RELAXED,
+    __hip_atomic_store(gptr_w(reinterpret_cast<unsigned int *>(p)), __float_as_uint(v), __ATOMIC_RELAXED,
                        __HIP_MEMORY_SCOPE_AGENT);
   } else {
-    *p = v;
+    *gptr_w(p) = v;
   }
 }
 
@@ -128,7 +130,7 @@ __device__ __forceinline__ void block_sums(float (&v)[N], float *red, int &slot)
   for (int i = 0; i < N; i++) v[i] = wave_sum(v[i]);
   if constexpr (WPB == 1) return;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  float *r = red + slot * 4 * kMaxWaves;
+  XE_LDS float *r = lptr(red) + slot * 4 * kMaxWaves;
   slot ^= 1;
   if (lane == 0)
 #pragma unroll
@@ -165,7 +167,7 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 // 16-byte streaming load (weights are read once per step: nontemporal).
 __device__ __forceinline__ uint4 ld_nt16(const void *ptr) {
-  const u32x4 v = __builtin_nontemporal_load(static_cast<const u32x4 *>(ptr));
+  const u32x4 v = __builtin_nontemporal_load(gptr(static_cast<const u32x4 *>(ptr)));
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
@@ -186,6 +188,27 @@ struct Chunk<XE_BF16> {
   uint4 lo, hi;
 };
 
+// Zero a chunk's weights unless `keep` (a select, not a branch: a divergent
+// branch around a load or its use makes the compiler wait for every load in
+// flight, which serialises the weight stream).
+__device__ __forceinline__ void mask_u4(uint4 &v, bool keep) {
+  // per component: a select of whole vector objects is lowered through memory
+  v.x = keep ? v.x : 0u;
+  v.y = keep ? v.y : 0u;
+  v.z = keep ? v.z : 0u;
+  v.w = keep ? v.w : 0u;
+}
+
+template <int WT>
+__device__ __forceinline__ void mask_chunk(Chunk<WT> &c, bool keep) {
+  if constexpr (WT == XE_BF16) {
+    mask_u4(c.lo, keep);
+    mask_u4(c.hi, keep);
+  } else {
+    mask_u4(c.q, keep);
+  }
+}
+
 template <int WT>
 __device__ __forceinline__ void load_chunk(const GemvParams &p, int row, int c, Chunk<WT> &out) {
   if constexpr (WT == XE_I8) {
@@ -197,7 +220,7 @@ __device__ __forceinline__ void load_chunk(const GemvParams &p, int row, int c, 
                                                         static_cast<size_t>(row) * p.k);
     out.q = ld_nt16(base + c);
     const uint16_t *eb = reinterpret_cast<const uint16_t *>(p.exps + static_cast<size_t>(row) * (p.k / 8));
-    out.e = eb[c];
+    out.e = gptr(eb)[c];
   } else {
     const uint4 *base = reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(p.w) +
                                                         static_cast<size_t>(row) * p.k);
@@ -435,13 +458,16 @@ __device__ __forceinline__ void gemv_tiles(const GemvParams &p, float4 *xs4, flo
 
     // Load set s covers chunk iterations [s*U, s*U + U).
     Chunk<WT> ca[U][RPL], cb[U][RPL];
+    // Chunk iterations past n_it are skipped (a uniform branch); lanes past
+    // the row's last chunk load a clamped chunk and zero it at use.
     auto load_set = [&](Chunk<WT>(&dst)[U][RPL], int it0) {
 #pragma unroll
       for (int u = 0; u < U; u++) {
-        const int c = (it0 + u) * LPR + kl;
+        if (it0 + u < n_it) {
+          const int c = min((it0 + u) * LPR + kl, nch - 1);
 #pragma unroll
-        for (int i = 0; i < RPL; i++)
-          if (c < nch) load_chunk<WT>(p, row[i], c, dst[u][i]);
+          for (int i = 0; i < RPL; i++) load_chunk<WT>(p, row[i], c, dst[u][i]);
+        }
       }
     };
     load_set(ca, 0);
@@ -474,8 +500,16 @@ __device__ __forceinline__ void gemv_tiles(const GemvParams &p, float4 *xs4, flo
     auto compute_set = [&](const Chunk<WT>(&src)[U][RPL], int it0) {
 #pragma unroll
       for (int u = 0; u < U; u++) {
-        const int c = (it0 + u) * LPR + kl;
-        if (c < nch) compute(src[u], c);
+        if (it0 + u < n_it) {
+          const int c = (it0 + u) * LPR + kl;
+          Chunk<WT> ch[RPL];
+#pragma unroll
+          for (int i = 0; i < RPL; i++) {
+            ch[i] = src[u][i];
+            mask_chunk<WT>(ch[i], c < nch);
+          }
+          compute(ch, min(c, nch - 1));
+        }
       }
     };
     // ping-pong: while one set is consumed the other is in flight
@@ -508,8 +542,8 @@ __device__ __forceinline__ void gemv_tiles(const GemvParams &p, float4 *xs4, flo
 #pragma unroll
         for (int i = 0; i < RPL; i++) {
           float t = acc[b][i];
-          if (WT == XE_I8) t = t * p.scale[row[i]];
-          if (p.bias) t = t + p.bias[row[i]];
+          if (WT == XE_I8) t = t * gptr(p.scale)[row[i]];
+          if (p.bias) t = t + gptr(p.bias)[row[i]];
           v[i] = t;
         }
         if (p.act == ACT_GEGLU_TANH) {

@@ -1,0 +1,8 @@
+// ll_bfp16.hip -- bfp16-weight instantiations of the low-latency step kernel.
+#include "ll_kernel.h"
+
+namespace xe {
+namespace ll {
+StepFn pick_ll_bfp16(int nb, int hd, int g) { return pick_nb<XE_BFP16>(nb, hd, g); }
+}  // namespace ll
+}  // namespace xe

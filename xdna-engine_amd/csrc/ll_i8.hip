@@ -1,0 +1,8 @@
+// ll_i8.hip -- int8-weight instantiations of the low-latency step kernel.
+#include "ll_kernel.h"
+
+namespace xe {
+namespace ll {
+StepFn pick_ll_i8(int nb, int hd, int g) { return pick_nb<XE_I8>(nb, hd, g); }
+}  // namespace ll
+}  // namespace xe

@@ -1,0 +1,330 @@
+// ll_kernel.h -- the low-latency persistent decode step kernel (see ll_dev.h
+// for the exchange protocol and the roles).  One launch runs n_steps tokens
+// for nb <= 4 streams.
+#pragma once
+
+#include "ll_dev.h"
+#include "step_dev.h"
+
+namespace xe {
+namespace ll {
+
+// residual[b] = dequant(E[tok[b]]) (+ P[pos[b] + pos_off]) (* mul); the same
+// arithmetic as sdev::embed_block.
+__device__ __forceinline__ void embed(const StepParams &sp, const int *tok, const int *pos, float *xr) {
+  const int D = sp.d;
+  for (int t = threadIdx.x; t < sp.nb * D; t += kT) {
+    const int b = t / D, j = t % D;
+    int tk = lptr(tok)[b];
+    tk = tk < 0 ? 0 : (tk >= sp.vocab ? sp.vocab - 1 : tk);
+    int prow = lptr(pos)[b] + sp.pos_off;
+    prow = prow < 0 ? 0 : (prow >= sp.pos_rows ? sp.pos_rows - 1 : prow);
+    const size_t i = static_cast<size_t>(tk) * D + j;
+    float v;
+    if (sp.emb_exps)
+      v = ldexpf(static_cast<float>(gptr(static_cast<const int8_t *>(sp.emb))[i]),
+                 static_cast<int>(gptr(sp.emb_exps)[i / 8]) - 133);
+    else if (sp.emb_scale)
+      v = static_cast<float>(gptr(static_cast<const int8_t *>(sp.emb))[i]) * gptr(sp.emb_scale)[tk];
+    else
+      v = __uint_as_float(static_cast<uint32_t>(gptr(static_cast<const uint16_t *>(sp.emb))[i]) << 16);
+    if (sp.pos_emb) v = v + gptr(sp.pos_emb)[static_cast<size_t>(prow) * D + j];
+    if (sp.use_mul) v = v * sp.emb_mul;
+    lptr(xr)[t] = v;
+  }
+}
+
+// The lm-head slice (its own function: its streaming loop needs a different
+// register budget from the per-layer phases).  Arguments by value: a
+// reference to the kernel-argument block or to a caller's private struct would
+// reach the callee as a generic pointer (flat loads).
+struct HeadArgs {
+  const void *w;
+  const float *scale;
+  const uint8_t *exps;
+  const float *gamma, *beta;
+  float *logits;
+  int vocab, d, lpr, rpl, norm, last_max;
+  float eps;
+};
+struct HeadOut {
+  ArgBest best;
+  int ok;
+};
+
+template <int WT, int NB>
+__device__ __noinline__ HeadOut head_gemv(const HeadArgs h, int nb, int r0, int r1, float *xr, float *xin,
+                                          float *red, unsigned ep, const Ctl c) {
+  GemvD hg{};
+  hg.w = h.w;
+  hg.scale = h.scale;
+  hg.exps = h.exps;
+  hg.m = h.vocab;
+  hg.k = h.d;
+  hg.lpr = h.lpr;
+  hg.rpl = h.rpl;
+  HeadOut o;
+#pragma unroll
+  for (int b = 0; b < kMaxNB; b++) {
+    o.best.v[b] = -INFINITY;
+    o.best.i[b] = -1;
+  }
+  auto prep = [&]() -> bool {
+    norm_rows(xr, nb, h.d, h.norm, h.gamma, h.beta, h.eps, xin, red);
+    return true;
+  };
+  o.ok = gemv_any<WT, NB, true>(hg, nb, r0, r1, xin, ep, prep, h.logits, h.vocab, h.last_max, o.best, c, NoSub{}) ? 1 : 0;
+  return o;
+}
+
+template <int WT, int NB, int HD, int G>
+__global__ __launch_bounds__(kT) void ll_step_kernel(StepParams sp) {
+  extern __shared__ float4 lds4[];
+  __shared__ float red[2 * 4 * gdev::kMaxWaves];
+  __shared__ int bad;
+  __shared__ int s_tok[kMaxNB], s_pos[kMaxNB];
+  __shared__ float s_bv[kW][kMaxNB];
+  __shared__ int s_bi[kW][kMaxNB];
+  float *lds = reinterpret_cast<float *>(lds4);
+  const int nb = sp.nb, D = sp.d;
+  float *xr = lds;                                      // residual copy [nb][D]
+  float *xin = lds + static_cast<size_t>(NB) * D;       // GEMV / attention input [nb][kin]
+  float *scr = xin + static_cast<size_t>(NB) * sp.kin;  // scratch
+  const int grid = static_cast<int>(gridDim.x);
+  const bool is_a = blockIdx.x % kRoleStride == 0;
+  const int n_a = (grid + kRoleStride - 1) / kRoleStride;
+  const int rank = is_a ? static_cast<int>(blockIdx.x) / kRoleStride
+                        : static_cast<int>(blockIdx.x) - static_cast<int>(blockIdx.x) / kRoleStride - 1;
+  const int nranks = is_a ? n_a : grid - n_a;
+  const XE_CONST Phase *ph = cptr(is_a ? sp.ph_a : sp.ph_f);
+  const int nph = is_a ? sp.n_a : sp.n_f;
+  if (threadIdx.x == 0) bad = 0;
+  if (threadIdx.x < nb) {
+    const int b = threadIdx.x;
+    s_tok[b] = (sp.forced && sp.n_forced > 0) ? gptr(sp.forced)[b] : gptr(sp.tokens)[b];
+    s_pos[b] = gptr(sp.pos)[b];
+  }
+  __syncthreads();
+  const Ctl c{sp.status, sp.limit, &bad};
+  const int tslots = sp.n_a + sp.n_f;
+  auto mark = [&](int step, int slot) {
+    if (sp.trace && step == 0 && threadIdx.x == 0) gptr_w(sp.trace)[static_cast<size_t>(slot) * grid + blockIdx.x] = wall_clock64();
+  };
+  // input-ready time of phase i (second block of trace slots)
+  auto mark_ready = [&](int step, int i) { mark(step, tslots + 4 + (is_a ? 0 : sp.n_a) + i); };
+  mark(0, tslots + 3);
+  embed(sp, s_tok, s_pos, xr);
+  __syncthreads();
+  ArgBest none;
+
+  for (int step = 0; step < sp.n_steps; step++) {
+    const unsigned ep = sp.ep0 + static_cast<unsigned>(step);
+    bool ok = true;
+    for (int i = 0; i < nph && ok; i++) {
+      const XE_CONST Phase &P = ph[i];
+      switch (P.kind) {
+        case LK_FOLD:
+          ok = fold(P.u.fold, nb, D, xr, xin, red, ep, c);
+          mark_ready(step, i);
+          break;
+        case LK_GEMV: {
+          const XE_CONST GemvD &g = P.u.gemv;
+          // GeGLU rows come in (gate, up) pairs: split on pair boundaries
+          const int unit = g.act == ACT_GEGLU_TANH ? 2 : 1;
+          int r0, r1;
+          rank_rows(g.m / unit, rank, nranks, r0, r1);
+          r0 *= unit;
+          r1 *= unit;
+          auto prep = [&]() -> bool {
+            bool r = true;
+            for (int f = 0; f < g.nfold && r; f++) r = fold(g.folds[f], nb, D, xr, xin, red, ep, c);
+            if (r && g.in_vec) r = get(g.in, nb, g.k, xin, g.k, ep, c);
+            else if (r) norm_rows(xr, nb, g.k, g.norm, g.gamma, g.beta, g.eps, xin, red);
+            mark_ready(step, i);
+            return r;
+          };
+          auto tsub = [&](int sub) { mark(step, tslots + 4 + sp.n_a + sp.n_f + 3 * ((is_a ? 0 : sp.n_a) + i) + sub); };
+          ok = gemv_any<WT, NB, false>(g, nb, r0, r1, xin, ep, prep, nullptr, 0, 0, none, c, tsub);
+          break;
+        }
+        case LK_ATTN: {
+          const XE_CONST AttnD &a = P.u.attn;
+          // the first block's K/V loads overlap the wait for q (prep runs once)
+          bool need_q = true;
+          const int nblk = a.max_splits * a.hkv * nb;
+          for (int vb = rank; vb < nblk && ok; vb += nranks) {
+            const int split = vb % a.max_splits, rest = vb / a.max_splits;
+            const int kvh = rest % a.hkv, b = rest / a.hkv;
+            const int len = a.fixed_len > 0 ? a.fixed_len : s_pos[b] + 1;
+            int chunk, nsplits;
+            ll_split(len, a.max_splits, HD, chunk, nsplits);
+            if (split >= nsplits) continue;
+            auto prep = [&]() -> bool {
+              if (!need_q) return true;
+              need_q = false;
+              const bool r = get(a.q, nb, a.qn, xin, a.qn, ep, c);
+              mark_ready(step, i);
+              return r;
+            };
+            // sub-stage trace: input ready, q/k staged, keys done
+            auto tsub = [&](int sub) { mark(step, tslots + 4 + sp.n_a + sp.n_f + 3 * ((is_a ? 0 : sp.n_a) + i) + sub); };
+            // every attention phase of a plan has group G (host checks)
+            ok = attn_block<HD, G>(a, split, kvh, b, len, xin, scr, ep, prep, tsub);
+          }
+          break;
+        }
+        case LK_MERGE: {
+          const XE_CONST MergeD &mg = P.u.merge;
+          const int per_head = mg.hd / kDM;
+          const int nblk = nb * mg.hq * per_head;
+          for (int vb = rank; vb < nblk && ok; vb += nranks) {
+            const int e0 = (vb % per_head) * kDM, rest = vb / per_head;
+            const int h = rest % mg.hq, b = rest / mg.hq;
+            const int len = mg.fixed_len > 0 ? mg.fixed_len : s_pos[b] + 1;
+            ok = merge_block(mg, b, h, e0, len, scr, ep, c);
+          }
+          break;
+        }
+      }
+      mark(step, (is_a ? 0 : sp.n_a) + i);
+    }
+    if (!ok) break;
+
+    // ---- lm-head slice of this workgroup + its argmax partial ----
+    ArgBest best;
+#pragma unroll
+    for (int b = 0; b < kMaxNB; b++) {
+      best.v[b] = -INFINITY;
+      best.i[b] = -1;
+    }
+    {
+      int r0, r1;
+      rank_rows(sp.vocab, static_cast<int>(blockIdx.x), grid, r0, r1);
+      const HeadArgs ha{sp.emb, sp.emb_scale, sp.emb_exps, sp.head_gamma, sp.head_beta, sp.logits,
+                        sp.vocab, sp.d, sp.head_lpr, sp.head_rpl, sp.head_norm, sp.last_max, sp.head_eps};
+      const HeadOut ho = head_gemv<WT, NB>(ha, nb, r0, r1, xr, xin, red, ep, c);
+      ok = ho.ok != 0;
+      best = ho.best;
+    }
+    if (!ok) break;
+    mark(step, tslots);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+      float v = best.v[b];
+      int idx = best.i[b];
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) {
+        const float ov = __shfl_xor(v, off, 64);
+        const int oi = __shfl_xor(idx, off, 64);
+        if (oi >= 0 && sdev::better(ov, oi, v, idx, sp.last_max)) {
+          v = ov;
+          idx = oi;
+        }
+      }
+      if (lane == 0) {
+        s_bv[wave][b] = v;
+        s_bi[wave][b] = idx;
+      }
+    }
+    __syncthreads();
+    const int parity = static_cast<int>(ep & 1u);
+    const Vec argv{sp.arg.p + static_cast<size_t>(parity) * nb * sp.arg.ld, sp.arg.ld, 0};
+    if (threadIdx.x < nb) {
+      const int b = threadIdx.x;
+      float v = -INFINITY;
+      int idx = -1;
+      for (int w = 0; w < kW; w++)
+        if (s_bi[w][b] >= 0 && sdev::better(s_bv[w][b], s_bi[w][b], v, idx, sp.last_max)) {
+          v = s_bv[w][b];
+          idx = s_bi[w][b];
+        }
+      put(argv, b, 2 * static_cast<int>(blockIdx.x), v, ep);
+      put(argv, b, 2 * static_cast<int>(blockIdx.x) + 1, __int_as_float(idx), ep);
+    }
+    // ---- every workgroup: the same argmax over all partials ----
+    ok = get(argv, nb, 2 * grid, scr, 2 * grid, ep, c);
+    if (!ok) break;
+    mark(step, tslots + 1);
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+      float v = -INFINITY;
+      int idx = -1;
+      if (b < nb)
+        for (int w = threadIdx.x; w < grid; w += kT) {
+          const float pv = lptr(scr)[b * 2 * grid + 2 * w];
+          const int pi = __float_as_int(lptr(scr)[b * 2 * grid + 2 * w + 1]);
+          if (pi >= 0 && sdev::better(pv, pi, v, idx, sp.last_max)) {
+            v = pv;
+            idx = pi;
+          }
+        }
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) {
+        const float ov = __shfl_xor(v, off, 64);
+        const int oi = __shfl_xor(idx, off, 64);
+        if (oi >= 0 && sdev::better(ov, oi, v, idx, sp.last_max)) {
+          v = ov;
+          idx = oi;
+        }
+      }
+      if (lane == 0) {
+        s_bv[wave][b] = v;
+        s_bi[wave][b] = idx;
+      }
+    }
+    __syncthreads();
+    if (threadIdx.x < nb) {
+      const int b = threadIdx.x;
+      float v = -INFINITY;
+      int idx = -1;
+      for (int w = 0; w < kW; w++)
+        if (s_bi[w][b] >= 0 && sdev::better(s_bv[w][b], s_bi[w][b], v, idx, sp.last_max)) {
+          v = s_bv[w][b];
+          idx = s_bi[w][b];
+        }
+      if (idx < 0) idx = 0;
+      const int ps = s_pos[b];
+      const int nxt = (sp.forced && step + 1 < sp.n_forced) ? gptr(sp.forced)[(step + 1) * nb + b] : idx;
+      if (blockIdx.x == 0) {
+        if (ps >= 0 && ps < sp.hist_stride) gptr_w(sp.hist)[static_cast<size_t>(b) * sp.hist_stride + ps] = idx;
+        gptr_w(sp.next)[b] = idx;
+        gptr_w(sp.tokens)[b] = nxt;
+        gptr_w(sp.pos)[b] = ps + 1;
+      }
+      s_tok[b] = nxt;
+      s_pos[b] = ps + 1;
+    }
+    __syncthreads();
+    embed(sp, s_tok, s_pos, xr);
+    __syncthreads();
+    mark(step, tslots + 2);
+  }
+}
+
+using StepFn = void (*)(StepParams);
+
+template <int WT, int NB>
+StepFn pick_head(int hd, int g) {
+  if (hd == 64 && g == 1) return ll_step_kernel<WT, NB, 64, 1>;
+  if (hd == 256 && g == 4) return ll_step_kernel<WT, NB, 256, 4>;
+  return nullptr;
+}
+
+template <int WT>
+StepFn pick_nb(int nb, int hd, int g) {
+  switch (nb) {
+    case 1: return pick_head<WT, 1>(hd, g);
+    case 2: return pick_head<WT, 2>(hd, g);
+    case 4: return pick_head<WT, 4>(hd, g);
+  }
+  return nullptr;
+}
+
+// one translation unit per weight dtype (ll_i8.hip, ll_bf16.hip, ll_bfp16.hip)
+StepFn pick_ll_i8(int nb, int hd, int g);
+StepFn pick_ll_bf16(int nb, int hd, int g);
+StepFn pick_ll_bfp16(int nb, int hd, int g);
+
+}  // namespace ll
+}  // namespace xe

@@ -28,6 +28,7 @@ XE_F32, XE_BF16, XE_I8, XE_BFP16, XE_I32 = 0, 1, 2, 3, 4
 XE_NORM_NONE, XE_NORM_LN, XE_NORM_RMS, XE_NORM_RMS1P = 0, 1, 2, 3
 XE_LAYOUT_MK, XE_LAYOUT_KN = 0, 1
 XE_OPT, XE_WHISPER, XE_GEMMA3 = 0, 1, 2
+EXECUTORS = {0: "graph", 1: "persistent", 2: "eager", 3: "ll"}
 
 EXPORTS = [
     "xe_last_error", "xe_abi_version", "xe_device_count", "xe_device_open", "xe_device_close",
@@ -41,7 +42,7 @@ EXPORTS = [
     "xe_decoder_destroy", "xe_decoder_init_synthetic", "xe_decoder_set_tensor",
     "xe_decoder_get_tensor_q8", "xe_decoder_reset", "xe_decoder_set_cross", "xe_decoder_step",
     "xe_decoder_generate", "xe_decoder_last_step_us", "xe_decoder_weight_bytes",
-    "xe_decoder_feed", "xe_decoder_decode", "xe_decoder_profile_step",
+    "xe_decoder_feed", "xe_decoder_decode", "xe_decoder_profile_step", "xe_decoder_executor",
 ]
 
 
@@ -148,6 +149,7 @@ def lib():
         "xe_decoder_decode": (i, [vp, i, i, vp, C.POINTER(C.c_double)]),
         "xe_decoder_profile_step": (i, [vp, i, i, vp, vp, vp]),
         "xe_decoder_weight_bytes": (u64, [vp]),
+        "xe_decoder_executor": (i, [vp, i]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name, None)
@@ -396,6 +398,7 @@ class Decoder:
 
     def __init__(self, dev, cfg, max_batch=1):
         self.dev, self.cfg, self.max_batch = dev, cfg, max_batch
+        self.batch = None
         self.h = lib().xe_decoder_create(dev.h, C.byref(cfg), max_batch)
         if not self.h:
             raise XdnaError(last_error())
@@ -465,6 +468,11 @@ class Decoder:
         raw = labels.raw
         return [(raw[32 * i:32 * i + 32].split(b"\0")[0].decode(), float(us[i]), float(by[i]))
                 for i in range(n)]
+
+    def executor(self, batch=None):
+        """Name of the executor a step of `batch` streams runs on."""
+        b = batch or self.batch or 1
+        return EXECUTORS[_check(lib().xe_decoder_executor(self.h, b))]
 
     def last_step_us(self):
         return lib().xe_decoder_last_step_us(self.h)
