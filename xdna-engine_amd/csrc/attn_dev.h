@@ -70,10 +70,11 @@ struct AttnParams {
 __device__ __forceinline__ uint16_t f32_to_bf16_rne(float x) {
   // Integer RNE with quiet-NaN, bit-identical to f32_to_bf16_bits
   // (rust/npu-xrt/src/lib.rs:809-817).
-  uint32_t bits = __float_as_uint(x);
-  if ((bits & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((bits >> 16) | 0x0040u);
-  uint32_t bias = 0x00007fffu + ((bits >> 16) & 1u);
-  return static_cast<uint16_t>((bits + bias) >> 16);
+  // Branch-free (a select), so unrolled conversions stay one basic block.
+  const uint32_t bits = __float_as_uint(x);
+  const uint32_t rounded = (bits + 0x00007fffu + ((bits >> 16) & 1u)) >> 16;
+  const uint32_t quiet = (bits >> 16) | 0x0040u;
+  return static_cast<uint16_t>((bits & 0x7fffffffu) > 0x7f800000u ? quiet : rounded);
 }
 
 __device__ __forceinline__ int stream_len(const AttnParams &p, int b) {

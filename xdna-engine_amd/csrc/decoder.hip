@@ -1191,6 +1191,13 @@ constexpr int kLLChunk = 256;  // decode steps per low-latency launch
 // n_steps tokens in one launch.  forced: device [n_forced][B] input tokens of
 // the first steps (prompt feeding); logits: written for every step (the last
 // step's values remain).
+// Trace marks of one traced step: phase ends, 4 step marks, phase
+// input-ready times, kSubSlots sub-stage marks per phase.
+size_t ll_trace_slots(const xe_decoder::LLPlan &P) {
+  const size_t n = P.a.size() + P.f.size();
+  return 2 * n + 4 + ll::kSubSlots * n;
+}
+
 void run_ll(xe_decoder *d, int B, int n_steps, const int32_t *forced, int n_forced, bool want_logits,
             uint64_t *trace = nullptr) {
   xe_decoder::LLPlan &P = ll_plan_for(d, B);
@@ -1239,7 +1246,10 @@ void run_ll(xe_decoder *d, int B, int n_steps, const int32_t *forced, int n_forc
   sp.kin = P.kin;
   sp.scratch = P.scratch;
   sp.trace = trace;
-  ll::launch(sp, c.wdtype, P.nb_t, P.hd, P.g, P.lds_bytes, P.grid, d->s);
+  // a traced launch keeps its marks in LDS behind the scratch area
+  sp.trace_slots = trace ? static_cast<int>(ll_trace_slots(P)) : 0;
+  const size_t lds = P.lds_bytes + (trace ? sizeof(uint64_t) * (sp.trace_slots + 1) : 0);
+  ll::launch(sp, c.wdtype, P.nb_t, P.hd, P.g, lds, P.grid, d->s);
   d->ll_epoch += static_cast<unsigned>(n_steps);
 }
 
@@ -1765,7 +1775,7 @@ int xe_decoder_profile_step(xe_decoder *d, int batch, int max_entries, char *lab
       // sides overlap, so the two lists are separate timelines).
       xe_decoder::LLPlan &P = ll_plan_for(d, batch);
       const size_t na = P.a.size(), nf = P.f.size(), G = static_cast<size_t>(P.grid);
-      const size_t slots = 2 * (na + nf) + 4 + 3 * (na + nf);
+      const size_t slots = ll_trace_slots(P);
       uint64_t *tr = nullptr;
       XE_HIP(hipMalloc(reinterpret_cast<void **>(&tr), slots * G * sizeof(uint64_t)));
       std::vector<uint64_t> h(slots * G);
@@ -1781,6 +1791,15 @@ int xe_decoder_profile_step(xe_decoder *d, int batch, int max_entries, char *lab
       (void)hipFree(tr);
       check_step_status(d);
       d->decoded += 1;
+      if (const char *raw = getenv("XE_LL_TRACE_RAW")) {
+        // diagnostic: the raw per-workgroup trace, [slots][grid] u64 ticks
+        if (FILE *f = std::fopen(raw, "wb")) {
+          const uint64_t dims[4] = {slots, G, na, nf};
+          std::fwrite(dims, sizeof(dims), 1, f);
+          std::fwrite(h.data(), sizeof(uint64_t), h.size(), f);
+          std::fclose(f);
+        }
+      }
       int khz = 0;
       XE_HIP(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, d->dev->ordinal));
       XE_REQUIRE(khz > 0, "device wall clock rate unknown");
@@ -1807,14 +1826,16 @@ int xe_decoder_profile_step(xe_decoder *d, int batch, int max_entries, char *lab
         const uint64_t r = slot_max(na + nf + 4 + i), e = slot_max(i);
         emit("A:wait:" + P.a_labels[i], prev, std::max(prev, r), 0.0);
         const bool is_attn = P.a[i].kind == ll::LK_ATTN;
-        if (is_attn) {  // sub-stages: q/k staged, keys done, partials out
-          const size_t sb = 2 * (na + nf) + 4 + 3 * i;
-          const uint64_t s1 = slot_max(sb + 1), s2 = slot_max(sb + 2);
-          emit("A:" + P.a_labels[i] + ".stage", std::max(prev, r), s1, 0.0);
-          emit("A:" + P.a_labels[i] + ".keys", s1, s2, P.a_bytes[i] + (P.a_labels[i] == "attn_self" ? kv_bytes : 0.0));
-          emit("A:" + P.a_labels[i] + ".out", s2, e, 0.0);
+        if (is_attn) {  // sub-stages: q staged, scores, softmax, P.V, partials out
+          const size_t sb = 2 * (na + nf) + 4 + ll::kSubSlots * i;
+          const uint64_t s0 = slot_max(sb), s1 = slot_max(sb + 1), s2 = slot_max(sb + 2), s3 = slot_max(sb + 3);
+          emit("A:" + P.a_labels[i] + ".stage", std::max(prev, r), s0, 0.0);
+          emit("A:" + P.a_labels[i] + ".qk", s0, s1, P.a_bytes[i] + (P.a_labels[i] == "attn_self" ? kv_bytes : 0.0));
+          emit("A:" + P.a_labels[i] + ".softmax", s1, s2, 0.0);
+          emit("A:" + P.a_labels[i] + ".pv", s2, s3, 0.0);
+          emit("A:" + P.a_labels[i] + ".out", s3, e, 0.0);
         } else if (P.a[i].kind == ll::LK_GEMV) {  // compute / reduction + epilogue
-          const uint64_t s1 = slot_max(2 * (na + nf) + 4 + 3 * i + 1);
+          const uint64_t s1 = slot_max(2 * (na + nf) + 4 + ll::kSubSlots * i + 1);
           emit("A:" + P.a_labels[i] + ".mac", std::max(prev, r), s1, P.a_bytes[i]);
           emit("A:" + P.a_labels[i] + ".epi", s1, e, 0.0);
         } else {
@@ -1828,7 +1849,7 @@ int xe_decoder_profile_step(xe_decoder *d, int batch, int max_entries, char *lab
         const uint64_t r = slot_max(2 * na + nf + 4 + i), e = slot_max(na + i);
         emit("F:wait:" + P.f_labels[i], prev, std::max(prev, r), 0.0);
         if (P.f[i].kind == ll::LK_GEMV) {
-          const uint64_t s1 = slot_max(2 * (na + nf) + 4 + 3 * (na + i) + 1);
+          const uint64_t s1 = slot_max(2 * (na + nf) + 4 + ll::kSubSlots * (na + i) + 1);
           emit("F:" + P.f_labels[i] + ".mac", std::max(prev, r), s1, P.f_bytes[i]);
           emit("F:" + P.f_labels[i] + ".epi", s1, e, 0.0);
         } else {

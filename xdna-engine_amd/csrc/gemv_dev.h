@@ -115,11 +115,80 @@ __device__ __forceinline__ void act_st(float *p, float v) {
   }
 }
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+// Cross-lane butterflies without the LDS crossbar: DPP inside 16-lane rows
+// (quad permutes, then the half-row and row mirrors, which pair the lanes of
+// neighbouring groups once each group is uniform) and gfx950's permlane swaps
+// across rows (permlane16_swap(v, v) hands a lane its neighbouring row's
+// value in one result half and its own in the other).  After the steps for
+// 2^k lanes, every lane of each aligned 2^k group holds op over the group; op
+// must be commutative, which also makes every lane's result bit-identical.
+template <int CTRL>
+__device__ __forceinline__ float dpp_get(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+template <int CTRL>
+__device__ __forceinline__ int dpp_get_i(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, true);
+}
+constexpr int kDppXor1 = 0xB1;    // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;    // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141;
+constexpr int kDppMirror = 0x140;
+
+// op over aligned groups of 2^log2g lanes (log2g wave-uniform, 0..6).
+template <typename Op>
+__device__ __forceinline__ float group_reduce(float v, int log2g, Op op) {
+  if (log2g >= 1) v = op(v, dpp_get<kDppXor1>(v));
+  if (log2g >= 2) v = op(v, dpp_get<kDppXor2>(v));
+  if (log2g >= 3) v = op(v, dpp_get<kDppHalfMirror>(v));
+  if (log2g >= 4) v = op(v, dpp_get<kDppMirror>(v));
+  if (log2g >= 5) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = op(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  }
+  if (log2g >= 6) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = op(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  }
   return v;
 }
+struct OpAdd {
+  __device__ float operator()(float a, float b) const { return a + b; }
+};
+struct OpMax {
+  __device__ float operator()(float a, float b) const { return fmaxf(a, b); }
+};
+__device__ __forceinline__ float group_sum(float v, int log2g) { return group_reduce(v, log2g, OpAdd{}); }
+// N independent group sums, level by level (one uniform branch per level).
+template <int N>
+__device__ __forceinline__ void group_sums(float (&v)[N], int log2g) {
+  if (log2g >= 1)
+#pragma unroll
+    for (int i = 0; i < N; i++) v[i] = v[i] + dpp_get<kDppXor1>(v[i]);
+  if (log2g >= 2)
+#pragma unroll
+    for (int i = 0; i < N; i++) v[i] = v[i] + dpp_get<kDppXor2>(v[i]);
+  if (log2g >= 3)
+#pragma unroll
+    for (int i = 0; i < N; i++) v[i] = v[i] + dpp_get<kDppHalfMirror>(v[i]);
+  if (log2g >= 4)
+#pragma unroll
+    for (int i = 0; i < N; i++) v[i] = v[i] + dpp_get<kDppMirror>(v[i]);
+  if (log2g >= 5)
+#pragma unroll
+    for (int i = 0; i < N; i++) {
+      const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v[i]), __float_as_uint(v[i]), false, false);
+      v[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+  if (log2g >= 6)
+#pragma unroll
+    for (int i = 0; i < N; i++) {
+      const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[i]), __float_as_uint(v[i]), false, false);
+      v[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+}
+__device__ __forceinline__ float wave_sum(float v) { return group_reduce(v, 6, OpAdd{}); }
+__device__ __forceinline__ float wave_max(float v) { return group_reduce(v, 6, OpMax{}); }
 
 // Block-wide sums of N values over WPB waves with one barrier; `slot`
 // alternates so back-to-back reductions never overwrite a slot still being

@@ -49,6 +49,7 @@ constexpr int kMaxNB = 4;     // streams per step
 constexpr int kDM = 16;       // output elements per merge block
 constexpr int kMaxSplits = 64;
 constexpr int kRoleStride = 4;  // blockIdx % 4 == 0: attention side
+constexpr int kSubSlots = 4;    // trace sub-stage marks per phase
 
 // An exchange vector: element (b, i) is pair p[b * ld + i]; ld is even and p
 // 16-byte aligned, so pairs 2j, 2j+1 of a row are one 16-byte load.
@@ -156,9 +157,13 @@ struct StepParams {
   // LDS layout (floats): residual [nb][d] | input [nb][kin] | scratch
   int kin;
   int scratch;
-  // optional wall-clock trace of step 0: [n_a + n_f + 4][grid] phase end
-  // times (A phases, F phases, lm-head, argmax, embed, kernel start)
+  // optional wall-clock trace of step 0: [trace_slots][grid] mark times
+  // (phase ends, lm-head, argmax, embed, kernel start, phase input-ready,
+  // phase sub-stages).  Marks go to LDS (after the scratch area) and are
+  // copied out once at the end of the step, so tracing adds no global store
+  // (whose completion a later poll would wait for) inside the step.
   uint64_t *trace;
+  int trace_slots;
 };
 
 // ---------------------------------------------------------------------------
@@ -371,6 +376,40 @@ struct ArgBest {
   int i[kMaxNB];
 };
 
+// (v, i) <- the better of (v, i) and (ov, oi).  Symmetric (NaN values and
+// negative indices never win), so a butterfly leaves every lane the same pair.
+__device__ __forceinline__ void arg_pick(float &v, int &i, float ov, int oi, int last_max) {
+  const bool a = i >= 0 && v == v, b = oi >= 0 && ov == ov;
+  if (b && (!a || sdev::better(ov, oi, v, i, last_max))) {
+    v = ov;
+    i = oi;
+  }
+}
+
+// Wave-wide argmax of (v, i) pairs (tie rule of sdev::better); every lane
+// ends with the winner, or with i < 0 when no lane holds a valid pair.
+__device__ __forceinline__ void wave_argbest(float &v, int &i, int last_max) {
+  if (!(i >= 0 && v == v)) i = -1;
+  arg_pick(v, i, gdev::dpp_get<gdev::kDppXor1>(v), gdev::dpp_get_i<gdev::kDppXor1>(i), last_max);
+  arg_pick(v, i, gdev::dpp_get<gdev::kDppXor2>(v), gdev::dpp_get_i<gdev::kDppXor2>(i), last_max);
+  arg_pick(v, i, gdev::dpp_get<gdev::kDppHalfMirror>(v), gdev::dpp_get_i<gdev::kDppHalfMirror>(i), last_max);
+  arg_pick(v, i, gdev::dpp_get<gdev::kDppMirror>(v), gdev::dpp_get_i<gdev::kDppMirror>(i), last_max);
+  {
+    const auto rv = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    const auto ri = __builtin_amdgcn_permlane16_swap(static_cast<unsigned>(i), static_cast<unsigned>(i), false, false);
+    v = __uint_as_float(rv[0]);
+    i = static_cast<int>(ri[0]);
+    arg_pick(v, i, __uint_as_float(rv[1]), static_cast<int>(ri[1]), last_max);
+  }
+  {
+    const auto rv = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    const auto ri = __builtin_amdgcn_permlane32_swap(static_cast<unsigned>(i), static_cast<unsigned>(i), false, false);
+    v = __uint_as_float(rv[0]);
+    i = static_cast<int>(ri[0]);
+    arg_pick(v, i, __uint_as_float(rv[1]), static_cast<int>(ri[1]), last_max);
+  }
+}
+
 // One GEMV code path for every phase (code size: the whole step runs from the
 // instruction cache, so each phase kind must stay small and shared).  Tile:
 // lanes per row LPR (runtime: 8/16/32/64) x two rows per lane (a GeGLU
@@ -492,11 +531,17 @@ __device__ __forceinline__ bool gemv_rows(const GD &g, int nb, int r0, int r1, c
     }
     if (!ok) break;
     if (tile == 0) tsub(1);
-    for (int off = LPR >> 1; off >= 1; off >>= 1) {
+    {
+      float flat[NB * RPL];
 #pragma unroll
       for (int b = 0; b < NB; b++)
 #pragma unroll
-        for (int i = 0; i < RPL; i++) acc[b][i] += __shfl_xor(acc[b][i], off, 64);
+        for (int i = 0; i < RPL; i++) flat[b * RPL + i] = acc[b][i];
+      gdev::group_sums<NB * RPL>(flat, lpr_log);
+#pragma unroll
+      for (int b = 0; b < NB; b++)
+#pragma unroll
+        for (int i = 0; i < RPL; i++) acc[b][i] = flat[b * RPL + i];
     }
     if (kl == 0) {
 #pragma unroll
@@ -635,9 +680,11 @@ __device__ __forceinline__ void head_xform(const XE_LDS float *src, XE_LDS float
   }
 }
 
-// Keys one wave round covers: kW waves x (64 / (hd / 8)) keys.  A split is a
-// multiple of it, spread so that every attention-side workgroup gets a share.
-__host__ __device__ constexpr int round_keys(int hd) { return kW * (64 / (hd / 8)); }
+// Attention split blocks.  Keys are taken in 16-key tiles: a split is a
+// multiple of one tile, spread so that every attention-side workgroup gets a
+// share.
+constexpr int kKeyTile = 16;
+__host__ __device__ constexpr int round_keys(int) { return kKeyTile; }
 
 __host__ __device__ __forceinline__ void ll_split(int len, int max_splits, int hd, int &chunk, int &nsplits) {
   const int gran = round_keys(hd);
@@ -647,33 +694,67 @@ __host__ __device__ __forceinline__ void ll_split(int len, int max_splits, int h
   nsplits = (len + chunk - 1) / chunk;
 }
 
+// Keys one round of a block covers (one Q.K tile per wave).
+constexpr int kRoundKeys = kW * kKeyTile;
+
+// LDS scratch of a block (floats): q heads [g][hd] | new key [hd] | new key
+// and value as stored (bf16 pairs) [hd] | scores / probabilities
+// [kRoundKeys][g] | running max, sum, correction [3][16] | Q.K B operands
+// [hd / 32][64 lanes][8 bf16] | per-wave P.V sums [kW][g][hd].
 __host__ __device__ __forceinline__ int attn_scratch_floats(int hd, int g) {
-  return g * hd + kW * g * (hd + 2) + hd;
+  return g * hd + 2 * hd + kRoundKeys * g + 48 + (hd / 32) * 256 + kW * g * hd;
 }
 
-// One split block of (stream b, kv head kvh): keys [split*chunk, ...).
-// The block's first K/V loads and its head-transform constants are issued
-// before `prep` (which waits for the q rows: qin, LDS [nb][a.qn]); scr:
-// attn_scratch_floats.  Returns prep's result.
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ u32x2 ld_kv8(__amdgpu_buffer_rsrc_t rs, int byte_off) {
+  return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rs, byte_off, 0, gdev::kCoherentSc1));
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return static_cast<uint32_t>(adev::f32_to_bf16_rne(lo)) | static_cast<uint32_t>(adev::f32_to_bf16_rne(hi)) << 16;
+}
+
+// One split block of (stream b, kv head kvh): keys [split*chunk, ...), the G
+// query heads of the group at once.
+//   Q.K: per wave one 16-key tile as v_mfma_f32_16x16x32_bf16 steps, K rows
+//   straight from the bf16 cache as the A operand; B column n < G holds
+//   query head n rounded to bf16 and column G + n its rounding remainder, so
+//   C[key][n] + C[key][G + n] is the score with q to ~16 significant bits
+//   (fp32 accumulation).
+//   softmax: scores of the round in LDS, one wave per head (max, exp2, sum),
+//   running max / sum across rounds.
+//   P.V: lanes own 4 dims of a value row (hd / 4 lanes per key), keys spread
+//   over the waves; fp32 FMAs; the waves' sums are added in LDS.
+// The first round's K/V loads and the head-transform constants are issued
+// before `prep` (which waits for the q rows: qin, LDS [nb][a.qn]).  The new
+// key at the last position is not read back from the cache: lanes that hold
+// it take the bf16-rounded values from LDS.  Partial out: (m, l, acc[hd]) per
+// query head, m in log2 units of the scaled score.
 template <int HD, int G, typename AD, typename Prep, typename Sub>
 __device__ __forceinline__ bool attn_block(const AD &a, int split, int kvh, int b, int len, const float *qin,
                                            float *scr, unsigned ep, Prep prep, Sub tsub) {
-  constexpr int EPL = 8;
-  constexpr int L = HD / EPL;
-  constexpr int KPW = 64 / L;
-  constexpr int UK = 4;
-  constexpr int STEP = kW * KPW;
+  static_assert(HD % 32 == 0 && HD <= 256 && 2 * G <= 16, "attention tile shape");
+  constexpr int NJ = HD / 32;                  // MFMA steps per tile
+  constexpr int LPK = HD / 4;                  // P.V lanes per key
+  constexpr int KPI = 64 / LPK;                // keys per P.V load
+  constexpr int PVK = kRoundKeys / (kW * KPI); // P.V loads per wave per round
   XE_LDS float *S = lptr(scr);
   XE_LDS float(*qs)[HD] = reinterpret_cast<XE_LDS float(*)[HD]>(S);
-  XE_LDS float(*red)[G][HD + 2] = reinterpret_cast<XE_LDS float(*)[G][HD + 2]>(S + G * HD);
-  XE_LDS float *kt = S + G * HD + kW * G * (HD + 2);
+  XE_LDS float *kt = S + G * HD;
+  XE_LDS uint32_t *kvb = reinterpret_cast<XE_LDS uint32_t *>(kt + HD);  // k | v, bf16 pairs
+  XE_LDS float *sc = kt + 2 * HD;              // [kRoundKeys][G]
+  XE_LDS float *st = sc + kRoundKeys * G;      // m [16] | l [16] | corr [16]
+  XE_LDS bf16x8_t *bfr = reinterpret_cast<XE_LDS bf16x8_t *>(st + 48);  // [NJ][64]
+  XE_LDS float *red = st + 48 + NJ * 256;      // [kW][G][HD]
   int chunk, nsplits;
   ll_split(len, a.max_splits, HD, chunk, nsplits);
   const int s0 = split * chunk;
   const int s1 = min(len, s0 + chunk);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int posi = len - 1;
-  const int kg = lane / L, kl = lane % L;
 
   uint16_t *kbase = a.kc + a.kv_bstride * b + static_cast<size_t>(kvh) * a.max_ctx * HD;
   uint16_t *vbase = a.vc + a.kv_bstride * b + static_cast<size_t>(kvh) * a.max_ctx * HD;
@@ -681,28 +762,31 @@ __device__ __forceinline__ bool attn_block(const AD &a, int split, int kvh, int 
   const __amdgpu_buffer_rsrc_t vrs = gdev::coherent_rsrc(vbase);
   const bool appender = a.append && split == nsplits - 1;
 
-  // ---- issue the first key block's loads and the transform constants ----
-  // The new key at posi is not read back from the cache: the lane group that
-  // holds it takes the bf16-rounded values from LDS (below), so the cache
-  // stores can drain while the block computes.
-  auto load_keys = [&](int base, u32x4 (&kv)[UK], u32x4 (&vv)[UK], bool (&okk)[UK]) {
+  // lane roles: Q.K row (key) lane & 15, dims 8 (lane >> 4) + 32 j;
+  // P.V key slot lane / LPK, dims 4 (lane % LPK) .. + 4
+  const int qk_row = lane & 15, qk_dim = 8 * (lane >> 4);
+  const int pv_slot = lane / LPK, pv_dim = 4 * (lane % LPK);
+  u32x4 kf[NJ];
+  u32x2 vf[PVK];
+  auto load_round = [&](int rb) {
+    const int kq = rb + wave * kKeyTile + qk_row;
+    const bool kok = kq < s1;
 #pragma unroll
-    for (int u = 0; u < UK; u++) {
-      const int key = base + u * STEP;
-      okk[u] = key < s1;
-      const int off = okk[u] ? (key * HD + kl * EPL) * 2 : kNoRecord;
-      kv[u] = ld_kv(krs, off);
-      vv[u] = ld_kv(vrs, off);
+    for (int j = 0; j < NJ; j++) kf[j] = ld_kv(krs, kok ? (kq * HD + 32 * j + qk_dim) * 2 : kNoRecord);
+#pragma unroll
+    for (int i = 0; i < PVK; i++) {
+      const int kv = rb + (i * kW + wave) * KPI + pv_slot;
+      vf[i] = ld_kv8(vrs, kv < s1 ? (kv * HD + pv_dim) * 2 : kNoRecord);
     }
   };
-  const int base0 = s0 + wave * KPW + kg;
-  u32x4 kv[UK], vv[UK];
-  bool okk[UK];
-  load_keys(base0, kv, vv, okk);
+  load_round(s0);
   HeadConsts<HD> hc;
   load_head_consts<HD>(a, a.fixed_len > 0 ? 0 : posi, hc);
+  if (threadIdx.x < 16) {
+    st[threadIdx.x] = -INFINITY;
+    st[16 + threadIdx.x] = 0.f;
+  }
   if (!prep()) return false;
-  tsub(0);
 
   const XE_LDS float *qrow = lptr(qin) + static_cast<size_t>(b) * a.qn;
   const XE_LDS float *vsrc = qrow + a.v_off + kvh * HD;
@@ -712,168 +796,187 @@ __device__ __forceinline__ bool attn_block(const AD &a, int split, int kvh, int 
   if (appender && wave == kW - 1) {
     head_xform<HD>(qrow + a.k_off + kvh * HD, kt, knorm, hc.kn0, hc.kn1, rope, hc, a.norm_eps);
     __builtin_amdgcn_wave_barrier();
-    for (int j = lane; j < HD; j += 64) {
-      st_bf16_coherent(kbase + static_cast<size_t>(posi) * HD + j, adev::f32_to_bf16_rne(kt[j]));
-      st_bf16_coherent(vbase + static_cast<size_t>(posi) * HD + j, adev::f32_to_bf16_rne(vsrc[j]));
+    // the new row as the cache holds it: one packed copy serves the lanes
+    // that patch it in below and the cache stores at the end
+    for (int j = lane; j < HD / 2; j += 64) {
+      kvb[j] = pack_bf16x2(kt[2 * j], kt[2 * j + 1]);
+      kvb[HD / 2 + j] = pack_bf16x2(vsrc[2 * j], vsrc[2 * j + 1]);
     }
   }
-  __syncthreads();  // q heads and the new k staged in LDS
-  // the new key/value as stored in the cache (bf16, packed pairs)
-  auto pack8 = [&](const XE_LDS float *src) {
-    u32x4 r;
-    r.x = static_cast<uint32_t>(adev::f32_to_bf16_rne(src[0])) | static_cast<uint32_t>(adev::f32_to_bf16_rne(src[1])) << 16;
-    r.y = static_cast<uint32_t>(adev::f32_to_bf16_rne(src[2])) | static_cast<uint32_t>(adev::f32_to_bf16_rne(src[3])) << 16;
-    r.z = static_cast<uint32_t>(adev::f32_to_bf16_rne(src[4])) | static_cast<uint32_t>(adev::f32_to_bf16_rne(src[5])) << 16;
-    r.w = static_cast<uint32_t>(adev::f32_to_bf16_rne(src[6])) | static_cast<uint32_t>(adev::f32_to_bf16_rne(src[7])) << 16;
-    return r;
-  };
-  u32x4 knew = {0u, 0u, 0u, 0u}, vnew = {0u, 0u, 0u, 0u};
-  if (appender) {
-    knew = pack8(kt + kl * EPL);
-    vnew = pack8(vsrc + kl * EPL);
-  }
-  auto substitute = [&](int base, u32x4 (&kv)[UK], u32x4 (&vv)[UK]) {
-    if (!appender) return;
-#pragma unroll
-    for (int u = 0; u < UK; u++) {
-      const bool is_new = base + u * STEP == posi;
-      kv[u].x = is_new ? knew.x : kv[u].x;
-      kv[u].y = is_new ? knew.y : kv[u].y;
-      kv[u].z = is_new ? knew.z : kv[u].z;
-      kv[u].w = is_new ? knew.w : kv[u].w;
-      vv[u].x = is_new ? vnew.x : vv[u].x;
-      vv[u].y = is_new ? vnew.y : vv[u].y;
-      vv[u].z = is_new ? vnew.z : vv[u].z;
-      vv[u].w = is_new ? vnew.w : vv[u].w;
-    }
-  };
-  substitute(base0, kv, vv);
-  tsub(1);
+  __syncthreads();  // q heads and the new k / v staged in LDS
 
-  float qr[G][EPL];
+  // B operands of the Q.K steps, one per 32 dims, built once per block
+  // (column n: head n, or head n - G's remainder; other columns zero)
+  const int col = lane & 15;
+  {
+    const int qh = col < G ? col : col - G;
+    const bool qlive = col < 2 * G;
+    for (int j = wave; j < NJ; j += kW) {
+      const XE_LDS float *src = qs[qlive ? qh : 0] + 32 * j + qk_dim;
+      bf16x8_t f;
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        const float x = qlive ? src[e] : 0.f;
+        const float hi = __uint_as_float(static_cast<uint32_t>(adev::f32_to_bf16_rne(x)) << 16);
+        const float part = col < G ? hi : x - hi;
+        f[e] = __builtin_bit_cast(__bf16, adev::f32_to_bf16_rne(part));
+      }
+      bfr[j * 64 + lane] = f;
+    }
+  }
+  __syncthreads();  // B operands staged
+  tsub(0);
+
+  const float sc2 = a.scale * adev::kLog2e;
+  float acc[G][4];
 #pragma unroll
   for (int gg = 0; gg < G; gg++)
 #pragma unroll
-    for (int e = 0; e < EPL; e++) qr[gg][e] = qs[gg][kl * EPL + e];
-  float m[G], l[G], acc[G][EPL];
+    for (int e = 0; e < 4; e++) acc[gg][e] = 0.f;
+  for (int rb = s0; rb < s1; rb += kRoundKeys) {
+    if (rb != s0) load_round(rb);
+    // ---- Q.K: this wave's 16-key tile ----
+    const int tile0 = rb + wave * kKeyTile;
+    if (appender && posi >= tile0 && posi < tile0 + kKeyTile && tile0 + qk_row == posi) {
 #pragma unroll
-  for (int gg = 0; gg < G; gg++) {
-    m[gg] = -INFINITY;
-    l[gg] = 0.f;
-#pragma unroll
-    for (int e = 0; e < EPL; e++) acc[gg][e] = 0.f;
-  }
-  const float sc2 = a.scale * adev::kLog2e;
-  for (int base = base0; base < s1; base += STEP * UK) {
-    if (base != base0) {
-      load_keys(base, kv, vv, okk);
-      substitute(base, kv, vv);
+      for (int j = 0; j < NJ; j++) kf[j] = *reinterpret_cast<const XE_LDS u32x4 *>(kvb + 16 * j + qk_dim / 2);
     }
-    float s[UK][G];
-    // key slots the whole wave is past (short splits) are skipped: the wave's
-    // first key of slot u is base - kg + u * STEP
-    const int wave_first = base - kg;
+    if (tile0 < s1) {
+      f32x4_t cacc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int u = 0; u < UK; u++) {
-      if (wave_first + u * STEP >= s1) {
-#pragma unroll
-        for (int gg = 0; gg < G; gg++) s[u][gg] = -INFINITY;
-        continue;
-      }
-      const uint32_t w[4] = {kv[u].x, kv[u].y, kv[u].z, kv[u].w};
-      float kf[EPL];
+      for (int j = 0; j < NJ; j++)
+        cacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kf[j]), bfr[j * 64 + lane], cacc, 0, 0, 0);
+      // lane (row group r, column n < G): keys tile0 + 4r + i, head n
 #pragma unroll
       for (int i = 0; i < 4; i++) {
-        kf[2 * i] = __uint_as_float(w[i] << 16);
-        kf[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+        const float rem = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(cacc[i]), 0x100 + G, 0xF, 0xF, true));
+        const int key_l = wave * kKeyTile + 4 * (lane >> 4) + i;
+        if (col < G) sc[key_l * G + col] = tile0 + 4 * (lane >> 4) + i < s1 ? (cacc[i] + rem) * sc2 : -INFINITY;
       }
+    } else if (col < G) {
+#pragma unroll
+      for (int i = 0; i < 4; i++) sc[(wave * kKeyTile + 4 * (lane >> 4) + i) * G + col] = -INFINITY;
+    }
+    __syncthreads();
+    if (rb == s0) tsub(1);
+    // ---- softmax statistics of the round: wave gg handles head gg ----
+    if (wave < G) {
+      const int gg = wave;
+      float sv[kRoundKeys / 64];
+      float mx = -INFINITY;
+#pragma unroll
+      for (int t = 0; t < kRoundKeys / 64; t++) {
+        sv[t] = sc[(lane + 64 * t) * G + gg];
+        mx = fmaxf(mx, sv[t]);
+      }
+      mx = gdev::wave_max(mx);
+      const float m_old = st[gg];
+      const float m_new = fmaxf(m_old, mx);
+      const float corr = m_old == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_old - m_new);
+      float ps = 0.f;
+#pragma unroll
+      for (int t = 0; t < kRoundKeys / 64; t++) {
+        const float p = sv[t] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(sv[t] - m_new);
+        sc[(lane + 64 * t) * G + gg] = p;
+        ps += p;
+      }
+      ps = gdev::wave_sum(ps);
+      if (lane == 0) {
+        st[gg] = m_new;
+        st[16 + gg] = st[16 + gg] * corr + ps;
+        st[32 + gg] = corr;
+      }
+    }
+    __syncthreads();
+    if (rb == s0) tsub(2);
+    // ---- P.V over this wave's keys of the round ----
+    if (rb != s0) {
 #pragma unroll
       for (int gg = 0; gg < G; gg++) {
-        float dd = 0.f;
+        const float corr = st[32 + gg];
 #pragma unroll
-        for (int e = 0; e < EPL; e++) dd = __builtin_fmaf(qr[gg][e], kf[e], dd);
-#pragma unroll
-        for (int off = L / 2; off >= 1; off >>= 1) dd += __shfl_xor(dd, off, 64);
-        s[u][gg] = dd * sc2;
+        for (int e = 0; e < 4; e++) acc[gg][e] *= corr;
       }
     }
 #pragma unroll
-    for (int gg = 0; gg < G; gg++) {
-      float mb = m[gg];
+    for (int i = 0; i < PVK; i++) {
+      if (rb + (i * kW + wave) * KPI >= s1) continue;  // wave-uniform: slots past the split
+      const int key_l = (i * kW + wave) * KPI + pv_slot;
+      u32x2 v = vf[i];
+      if (appender && rb + key_l == posi) v = *reinterpret_cast<const XE_LDS u32x2 *>(kvb + HD / 2 + pv_dim / 2);
+      const float vv[4] = {__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xffff0000u),
+                           __uint_as_float(v.y << 16), __uint_as_float(v.y & 0xffff0000u)};
+      float p[G];
+      if constexpr (G == 4) {
+        const f32x4_t p4 = *reinterpret_cast<const XE_LDS f32x4_t *>(sc + key_l * G);
+        p[0] = p4.x;
+        p[1] = p4.y;
+        p[2] = p4.z;
+        p[3] = p4.w;
+      } else {
 #pragma unroll
-      for (int u = 0; u < UK; u++)
-        if (okk[u]) mb = fmaxf(mb, s[u][gg]);
-      if (mb == -INFINITY) continue;
-      const float corr = __builtin_amdgcn_exp2f(m[gg] - mb);
-      float pu[UK];
-      float psum = 0.f;
-#pragma unroll
-      for (int u = 0; u < UK; u++) {
-        pu[u] = okk[u] ? __builtin_amdgcn_exp2f(s[u][gg] - mb) : 0.f;
-        psum += pu[u];
+        for (int gg = 0; gg < G; gg++) p[gg] = sc[key_l * G + gg];
       }
-      l[gg] = l[gg] * corr + psum;
-      m[gg] = mb;
 #pragma unroll
-      for (int e = 0; e < EPL; e++) acc[gg][e] *= corr;
+      for (int gg = 0; gg < G; gg++)
 #pragma unroll
-      for (int u = 0; u < UK; u++) {
-        if (wave_first + u * STEP >= s1) continue;
-        const uint32_t w[4] = {vv[u].x, vv[u].y, vv[u].z, vv[u].w};
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-          acc[gg][2 * i] = __builtin_fmaf(pu[u], __uint_as_float(w[i] << 16), acc[gg][2 * i]);
-          acc[gg][2 * i + 1] = __builtin_fmaf(pu[u], __uint_as_float(w[i] & 0xffff0000u), acc[gg][2 * i + 1]);
-        }
-      }
+        for (int e = 0; e < 4; e++) acc[gg][e] = __builtin_fmaf(p[gg], vv[e], acc[gg][e]);
     }
+    if (rb + kRoundKeys < s1) __syncthreads();  // scores of the next round overwrite sc
   }
+  tsub(3);
+  // ---- key slots of a wave (KPI > 1), then the waves ----
+  if constexpr (KPI > 1) {
+    float flat[G * 4];
 #pragma unroll
-  for (int off = L; off < 64; off <<= 1) {
+    for (int gg = 0; gg < G; gg++)
 #pragma unroll
-    for (int gg = 0; gg < G; gg++) {
-      const float mo = __shfl_xor(m[gg], off, 64);
-      const float lo = __shfl_xor(l[gg], off, 64);
-      const float mx = fmaxf(m[gg], mo);
-      const float fa = mx == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m[gg] - mx);
-      const float fc = mx == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mo - mx);
-      l[gg] = l[gg] * fa + lo * fc;
+      for (int e = 0; e < 4; e++) flat[gg * 4 + e] = acc[gg][e];
+    // slots are the 16-lane rows (LPK == 16) or row pairs (LPK == 32)
 #pragma unroll
-      for (int e = 0; e < EPL; e++) {
-        const float ao = __shfl_xor(acc[gg][e], off, 64);
-        acc[gg][e] = acc[gg][e] * fa + ao * fc;
+    for (int t = 0; t < G * 4; t++) {
+      if constexpr (LPK == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(flat[t]), __float_as_uint(flat[t]), false, false);
+        flat[t] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
       }
-      m[gg] = mx;
+      const auto r2 = __builtin_amdgcn_permlane32_swap(__float_as_uint(flat[t]), __float_as_uint(flat[t]), false, false);
+      flat[t] = __uint_as_float(r2[0]) + __uint_as_float(r2[1]);
     }
+#pragma unroll
+    for (int gg = 0; gg < G; gg++)
+#pragma unroll
+      for (int e = 0; e < 4; e++) acc[gg][e] = flat[gg * 4 + e];
   }
-  tsub(2);
-  if (kg == 0) {
+  if (lane < LPK) {
 #pragma unroll
     for (int gg = 0; gg < G; gg++) {
-#pragma unroll
-      for (int e = 0; e < EPL; e++) red[wave][gg][2 + kl * EPL + e] = acc[gg][e];
-      if (kl == 0) {
-        red[wave][gg][0] = m[gg];
-        red[wave][gg][1] = l[gg];
-      }
+      f32x4_t v4 = {acc[gg][0], acc[gg][1], acc[gg][2], acc[gg][3]};
+      *reinterpret_cast<XE_LDS f32x4_t *>(red + (wave * G + gg) * HD + pv_dim) = v4;
     }
   }
   __syncthreads();
+  // the new key / value into the cache: read from the next step on (the
+  // step-end fence orders these stores before the argmax hand-off); stored
+  // here so that no wait above includes their completion
+  if (appender && wave == kW - 1) {
+    uint32_t *krow = reinterpret_cast<uint32_t *>(kbase + static_cast<size_t>(posi) * HD);
+    uint32_t *vrow = reinterpret_cast<uint32_t *>(vbase + static_cast<size_t>(posi) * HD);
+    for (int j = lane; j < HD / 2; j += 64) {
+      __hip_atomic_store(gptr_w(krow) + j, kvb[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(gptr_w(vrow) + j, kvb[HD / 2 + j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
   for (int t = threadIdx.x; t < G * (HD + 2); t += kT) {
     const int gg = t / (HD + 2), e = t % (HD + 2);
-    float mx = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < kW; w++) mx = fmaxf(mx, red[w][gg][0]);
-    float v = 0.f;
+    float v;
     if (e == 0) {
-      v = mx;
+      v = st[gg];
+    } else if (e == 1) {
+      v = st[16 + gg];
     } else {
+      v = 0.f;
 #pragma unroll
-      for (int w = 0; w < kW; w++) {
-        const float mw = red[w][gg][0];
-        const float f = mw == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw - mx);
-        v += red[w][gg][e] * f;
-      }
+      for (int w = 0; w < kW; w++) v += red[(w * G + gg) * HD + e - 2];
     }
     put(a.part, b, ((kvh * G + gg) * a.max_splits + split) * (HD + 2) + e, v, ep);
   }
@@ -916,7 +1019,7 @@ __device__ __noinline__ bool merge_block(const XE_CONST MergeD &mg, int b, int h
   if (threadIdx.x < 64) {
     float mx = -INFINITY;
     for (int s = threadIdx.x; s < nsplits; s += 64) mx = fmaxf(mx, tab[s * W]);
-    for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+    mx = gdev::wave_max(mx);
     for (int s = threadIdx.x; s < nsplits; s += 64) {
       const float ms = tab[s * W];
       wts[s] = ms == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ms - mx);

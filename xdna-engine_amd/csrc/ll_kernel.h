@@ -90,6 +90,7 @@ __global__ __launch_bounds__(kT) void ll_step_kernel(StepParams sp) {
   float *xr = lds;                                      // residual copy [nb][D]
   float *xin = lds + static_cast<size_t>(NB) * D;       // GEMV / attention input [nb][kin]
   float *scr = xin + static_cast<size_t>(NB) * sp.kin;  // scratch
+  uint64_t *tlds = reinterpret_cast<uint64_t *>(scr + ((sp.scratch + 1) & ~1));  // trace marks (traced launches)
   const int grid = static_cast<int>(gridDim.x);
   const bool is_a = blockIdx.x % kRoleStride == 0;
   const int n_a = (grid + kRoleStride - 1) / kRoleStride;
@@ -99,6 +100,8 @@ __global__ __launch_bounds__(kT) void ll_step_kernel(StepParams sp) {
   const XE_CONST Phase *ph = cptr(is_a ? sp.ph_a : sp.ph_f);
   const int nph = is_a ? sp.n_a : sp.n_f;
   if (threadIdx.x == 0) bad = 0;
+  if (sp.trace)  // slots a workgroup never marks read as 0
+    for (int t = threadIdx.x; t < sp.trace_slots; t += kT) lptr(tlds)[t] = 0;
   if (threadIdx.x < nb) {
     const int b = threadIdx.x;
     s_tok[b] = (sp.forced && sp.n_forced > 0) ? gptr(sp.forced)[b] : gptr(sp.tokens)[b];
@@ -108,7 +111,7 @@ __global__ __launch_bounds__(kT) void ll_step_kernel(StepParams sp) {
   const Ctl c{sp.status, sp.limit, &bad};
   const int tslots = sp.n_a + sp.n_f;
   auto mark = [&](int step, int slot) {
-    if (sp.trace && step == 0 && threadIdx.x == 0) gptr_w(sp.trace)[static_cast<size_t>(slot) * grid + blockIdx.x] = wall_clock64();
+    if (sp.trace && step == 0 && threadIdx.x == 0) lptr(tlds)[slot] = wall_clock64();
   };
   // input-ready time of phase i (second block of trace slots)
   auto mark_ready = [&](int step, int i) { mark(step, tslots + 4 + (is_a ? 0 : sp.n_a) + i); };
@@ -143,7 +146,7 @@ __global__ __launch_bounds__(kT) void ll_step_kernel(StepParams sp) {
             mark_ready(step, i);
             return r;
           };
-          auto tsub = [&](int sub) { mark(step, tslots + 4 + sp.n_a + sp.n_f + 3 * ((is_a ? 0 : sp.n_a) + i) + sub); };
+          auto tsub = [&](int sub) { mark(step, tslots + 4 + sp.n_a + sp.n_f + kSubSlots * ((is_a ? 0 : sp.n_a) + i) + sub); };
           ok = gemv_any<WT, NB, false>(g, nb, r0, r1, xin, ep, prep, nullptr, 0, 0, none, c, tsub);
           break;
         }
@@ -167,7 +170,7 @@ __global__ __launch_bounds__(kT) void ll_step_kernel(StepParams sp) {
               return r;
             };
             // sub-stage trace: input ready, q/k staged, keys done
-            auto tsub = [&](int sub) { mark(step, tslots + 4 + sp.n_a + sp.n_f + 3 * ((is_a ? 0 : sp.n_a) + i) + sub); };
+            auto tsub = [&](int sub) { mark(step, tslots + 4 + sp.n_a + sp.n_f + kSubSlots * ((is_a ? 0 : sp.n_a) + i) + sub); };
             // every attention phase of a plan has group G (host checks)
             ok = attn_block<HD, G>(a, split, kvh, b, len, xin, scr, ep, prep, tsub);
           }
@@ -213,20 +216,17 @@ __global__ __launch_bounds__(kT) void ll_step_kernel(StepParams sp) {
     for (int b = 0; b < NB; b++) {
       float v = best.v[b];
       int idx = best.i[b];
-#pragma unroll
-      for (int off = 32; off >= 1; off >>= 1) {
-        const float ov = __shfl_xor(v, off, 64);
-        const int oi = __shfl_xor(idx, off, 64);
-        if (oi >= 0 && sdev::better(ov, oi, v, idx, sp.last_max)) {
-          v = ov;
-          idx = oi;
-        }
-      }
+      wave_argbest(v, idx, sp.last_max);
       if (lane == 0) {
         s_bv[wave][b] = v;
         s_bi[wave][b] = idx;
       }
     }
+    // every store of the step (the KV-cache rows above all, which carry no
+    // epoch) has completed before this workgroup's argmax partial is
+    // published: agent-scope (sc1) stores are visible to every XCD once
+    // complete, so a wait for completion suffices (no L2 write-back)
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     const int parity = static_cast<int>(ep & 1u);
     const Vec argv{sp.arg.p + static_cast<size_t>(parity) * nb * sp.arg.ld, sp.arg.ld, 0};
@@ -259,15 +259,7 @@ __global__ __launch_bounds__(kT) void ll_step_kernel(StepParams sp) {
             idx = pi;
           }
         }
-#pragma unroll
-      for (int off = 32; off >= 1; off >>= 1) {
-        const float ov = __shfl_xor(v, off, 64);
-        const int oi = __shfl_xor(idx, off, 64);
-        if (oi >= 0 && sdev::better(ov, oi, v, idx, sp.last_max)) {
-          v = ov;
-          idx = oi;
-        }
-      }
+      wave_argbest(v, idx, sp.last_max);
       if (lane == 0) {
         s_bv[wave][b] = v;
         s_bi[wave][b] = idx;
@@ -299,6 +291,11 @@ __global__ __launch_bounds__(kT) void ll_step_kernel(StepParams sp) {
     embed(sp, s_tok, s_pos, xr);
     __syncthreads();
     mark(step, tslots + 2);
+    if (sp.trace && step == 0) {
+      __syncthreads();
+      for (int t = threadIdx.x; t < sp.trace_slots; t += kT)
+        gptr_w(sp.trace)[static_cast<size_t>(t) * grid + blockIdx.x] = lptr(tlds)[t];
+    }
   }
 }
 
