@@ -175,3 +175,72 @@ def test_whisper_small_short(gpu, xe, executor):
     compare_stream(got, want, margins, "whisper-small")
     dec.close()
     om.close()
+
+
+# ---- batched projections on MFMA (gemm.hip): more than 8 streams ----
+
+@pytest.mark.parametrize("family,wd", CASES)
+def test_tiny_batched_gemm_identity(gpu, xe, family, wd):
+    """20 streams (two MFMA column blocks, the second partial): every
+    projection runs as the bf16x3 MFMA GEMM; greedy streams equal the
+    oracle's fp32 ones."""
+    fam = {"opt": xe.XE_OPT, "whisper": xe.XE_WHISPER, "gemma": xe.XE_GEMMA3}[family]
+    wdtype = {"i8": xe.XE_I8, "bf16": xe.XE_BF16, "bfp16": xe.XE_BFP16}[wd]
+    cfg = tiny(xe, fam, wdtype)
+    batch = 20
+    print("[case] tiny batched %s %s batch %d" % (family, wd, batch), flush=True)
+    dec, om = build(xe, gpu, cfg, seed=13, batch=batch)
+    pr = prompts(cfg, batch, 5, seed=4)
+    got = dec.generate(pr, 24)
+    want, margins = om.generate(pr, 24)
+    compare_stream(got, want, margins, "tiny-b%d-%s-%s" % (batch, family, wd))
+    dec.close()
+    om.close()
+
+
+@pytest.mark.parametrize("family", ["opt", "gemma"])
+def test_tiny_batched_step_logits(gpu, xe, family):
+    """step() logits at 17 streams with per-stream positions vs the oracle."""
+    fam = {"opt": xe.XE_OPT, "gemma": xe.XE_GEMMA3}[family]
+    cfg = tiny(xe, fam, xe.XE_I8)
+    batch = 17
+    dec, om = build(xe, gpu, cfg, seed=3, batch=batch)
+    rng = np.random.default_rng(7)
+    for p in range(6):
+        toks = rng.integers(0, cfg.vocab, batch).astype(np.int32)
+        pos = (np.arange(batch, dtype=np.int32) % 3 + p).astype(np.int32)
+        got, nxt = dec.step(toks, pos)
+        want = om.step(toks, pos)
+        assert np.allclose(got, want, rtol=1e-2, atol=1e-3), np.max(np.abs(got - want))
+        rel = np.linalg.norm(got - want) / np.linalg.norm(want)
+        assert rel < 1e-3, rel
+        for b in range(batch):
+            assert nxt[b] == om.argmax(want[b])
+    dec.close()
+    om.close()
+
+
+def test_tiny_gemma_b64(gpu, xe):
+    """64 streams (the config-5 batch) on the tiny Gemma shape."""
+    cfg = tiny(xe, xe.XE_GEMMA3, xe.XE_I8)
+    dec, om = build(xe, gpu, cfg, seed=2, batch=64)
+    pr = prompts(cfg, 64, 4, seed=9)
+    got = dec.generate(pr, 16)
+    want, margins = om.generate(pr, 16)
+    compare_stream(got, want, margins, "tiny-gemma-b64")
+    dec.close()
+    om.close()
+
+
+def test_gemma3_1b_batched_short(gpu, xe):
+    """Config 5 shape at 16 streams: the MFMA GEMM path on the real sizes
+    (K = 1152 and 6912, GeGLU pairs, the 262144-row lm-head)."""
+    cfg = xe.GEMMA3_1B.replace(max_ctx=64)
+    batch = 16
+    dec, om = build(xe, gpu, cfg, seed=2, batch=batch)
+    pr = prompts(cfg, batch, 3, seed=5)
+    got = dec.generate(pr, 3)
+    want, margins = om.generate(pr, 3)
+    compare_stream(got, want, margins, "gemma3-1b-b16")
+    dec.close()
+    om.close()

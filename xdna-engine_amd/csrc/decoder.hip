@@ -280,6 +280,7 @@ struct xe_decoder {
   // state
   float *xa = nullptr, *xb = nullptr, *qkv = nullptr, *att = nullptr, *sub = nullptr;
   float *ffn = nullptr, *qx = nullptr, *logits = nullptr, *tmp = nullptr;
+  float *xn = nullptr;  // GEMM path: normalised activations [max_batch][max K]
   uint16_t *kc = nullptr, *vc = nullptr;  // [L][B][hkv][max_ctx][hd]
   float *rope_cos = nullptr, *rope_sin = nullptr;
   int32_t *tokens = nullptr, *pos = nullptr, *next = nullptr, *hist = nullptr;
@@ -473,6 +474,7 @@ void alloc_decoder(xe_decoder *d) {
   d->ffn = dalloc<float>(static_cast<size_t>(B) * F, s);
   d->qx = dalloc<float>(static_cast<size_t>(B) * D, s);
   d->logits = dalloc<float>(static_cast<size_t>(B) * c.vocab, s);
+  d->xn = dalloc<float>(static_cast<size_t>(B) * std::max(std::max(D, F), std::max(hq, static_cast<int>(d->nqkv()))), s);
   const size_t kvn = d->kv_layer_elems() * c.n_layers;
   d->kc = dalloc<uint16_t>(kvn, s);
   d->vc = dalloc<uint16_t>(kvn, s);
@@ -556,7 +558,7 @@ void free_decoder(xe_decoder *d) {
                   static_cast<void *>(d->tokens), static_cast<void *>(d->pos),
                   static_cast<void *>(d->next), static_cast<void *>(d->hist),
                   static_cast<void *>(d->arg_v), static_cast<void *>(d->arg_i),
-                  static_cast<void *>(d->attn_work)})
+                  static_cast<void *>(d->attn_work), static_cast<void *>(d->xn)})
     if (p) (void)hipFree(p);
   if (d->host_tok) (void)hipHostFree(d->host_tok);
   if (d->s) (void)hipStreamDestroy(d->s);
@@ -594,14 +596,23 @@ double gemv_bytes(const GemvCall &g, int batch) {
 struct PlanBuilder {
   xe_decoder::Plan &plan;
   int step_nb;
+  float *xn = nullptr;  // GEMM path scratch (null: GEMV only)
   void push(const sdev::Phase &ph, const std::string &label, double bytes, size_t lds) {
     plan.phases.push_back(ph);
     plan.labels.push_back(label);
     plan.bytes.push_back(bytes);
     plan.step_lds = std::max(plan.step_lds, lds);
   }
-  // one GEMV, in chunks of 8 streams (the GEMV tile's batch limit)
+  // One projection over `batch` streams.  Up to 8 streams whose activations
+  // fit the GEMV's LDS staging: the GEMV, in chunks of 8.  Otherwise the MFMA
+  // GEMM (gemm.hip) over all streams, after its prologue when the phase
+  // normalises or adds a residual.
   void gemv(const GemvCall &g, int batch, const std::string &label) {
+    const size_t stage = gdev::gemv_lds_floats(std::min(batch, 8), g.m->cols, g.sub != nullptr) * sizeof(float);
+    if (xn && (batch > 8 || stage > 160 * 1024 - 1024)) {
+      gemm(g, batch, label);
+      return;
+    }
     for (int b0 = 0; b0 < batch; b0 += 8) {
       const int nb = std::min(8, batch - b0);
       GemvLaunch L;
@@ -640,6 +651,52 @@ struct PlanBuilder {
            gdev::gemv_lds_floats(step_nb, L.k, L.sub != nullptr) * sizeof(float));
     }
   }
+  void gemm(const GemvCall &g, int batch, const std::string &label) {
+    GemvLaunch L;
+    L.wdtype = g.m->wdtype;
+    L.w = g.m->w;
+    L.scale = g.m->scale;
+    L.exps = g.m->exps;
+    L.bias = g.bias;
+    L.m = g.m->rows;
+    L.k = g.m->cols;
+    L.x = g.x;
+    L.x_dtype = XE_F32;
+    L.ldx = g.ldx;
+    L.batch = batch;
+    L.sub = g.sub;
+    L.post_w = g.post_w;
+    L.res_out = g.res_out;
+    L.norm = g.norm;
+    L.gamma = g.gamma;
+    L.beta = g.beta;
+    L.eps = g.eps;
+    L.act = g.act;
+    L.y = g.y;
+    L.ldy = g.ldy;
+    XE_REQUIRE(L.k % 16 == 0, "gemm: K must be a multiple of 16");
+    sdev::Phase ph{};
+    ph.variant = L.wdtype;
+    ph.u.gemv = gdev::to_params(L);
+    if (gemm_needs_prologue(ph.u.gemv)) {
+      ph.kind = sdev::PH_GEMM_PRO;
+      ph.nblocks = batch;
+      ph.xn = xn;
+      push(ph, label + "_pro", 4.0 * batch * L.k * (2 + (L.sub ? 1 : 0) + (L.res_out ? 1 : 0)),
+           gdev::gemv_lds_floats(1, L.k, L.sub != nullptr) * sizeof(float));
+      gdev::GemvParams &q = ph.u.gemv;
+      q.x = xn;
+      q.ldx = L.k;
+      q.sub = nullptr;
+      q.post_w = nullptr;
+      q.res_out = nullptr;
+      q.norm = XE_NORM_NONE;
+      ph.xn = nullptr;
+    }
+    ph.kind = sdev::PH_GEMM;
+    ph.nblocks = ((L.m + 63) / 64) * ((batch + 63) / 64);
+    push(ph, label, gemv_bytes(g, batch), 0);
+  }
   void attn(const AttnLaunch &a, const std::string &label, double bytes) {
     sdev::Phase ph{};
     ph.kind = sdev::PH_ATTN;
@@ -666,7 +723,7 @@ void build_plan(xe_decoder *d, int B, xe_decoder::Plan &plan) {
   const int nq = static_cast<int>(d->nqkv());
   const int norm = gem ? XE_NORM_RMS1P : XE_NORM_LN;
   plan.step_nb = B <= 1 ? 1 : B <= 2 ? 2 : 4;
-  PlanBuilder pb{plan, plan.step_nb};
+  PlanBuilder pb{plan, plan.step_nb, d->xn};
 
   // embedding
   {
@@ -878,7 +935,9 @@ void build_plan(xe_decoder *d, int B, xe_decoder::Plan &plan) {
     ph.nblocks = B;
     pb.push(ph, "argmax_final", 8.0 * B * sdev::kArgBlocks, 0);
   }
-  plan.persistent = !getenv("XE_NO_PERSIST") && B <= 4 &&
+  bool gemm_phases = false;
+  for (const auto &ph : plan.phases) gemm_phases |= ph.kind == sdev::PH_GEMM || ph.kind == sdev::PH_GEMM_PRO;
+  plan.persistent = !getenv("XE_NO_PERSIST") && B <= 4 && !gemm_phases &&
                     step_kernel_supported(c.wdtype, plan.step_nb, hd, c.n_heads / c.n_kv_heads) &&
                     plan.step_lds <= 150 * 1024;
 }

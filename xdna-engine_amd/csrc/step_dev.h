@@ -13,7 +13,19 @@
 namespace xe {
 namespace sdev {
 
-enum PhaseKind { PH_EMBED = 0, PH_GEMV = 1, PH_ATTN = 2, PH_MERGE = 3, PH_ARGMAX_PART = 4, PH_ARGMAX_FINAL = 5 };
+// PH_GEMM_PRO / PH_GEMM: a projection over more streams than the GEMV tile
+// holds (gemm.hip): the norm / residual prologue into Phase::xn, then the
+// MFMA GEMM.  Standalone launches only (not in the persistent step kernel).
+enum PhaseKind {
+  PH_EMBED = 0,
+  PH_GEMV = 1,
+  PH_ATTN = 2,
+  PH_MERGE = 3,
+  PH_ARGMAX_PART = 4,
+  PH_ARGMAX_FINAL = 5,
+  PH_GEMM_PRO = 6,
+  PH_GEMM = 7
+};
 
 constexpr int kArgBlocks = 64;
 
@@ -50,6 +62,7 @@ struct Phase {
   int hd, g;
   int nblocks;  // virtual blocks of the phase
   int pad;
+  float *xn;    // PH_GEMM_PRO: normalised activations out [batch][k]
   union {
     gdev::GemvParams gemv;
     adev::AttnParams attn;
@@ -169,6 +182,10 @@ __device__ __forceinline__ void argmax_final_block(const ArgmaxParams &p, int b)
 
 // Standalone execution of one phase (gemv.hip / attn.hip / decoder.hip).
 void launch_phase(const sdev::Phase &ph, hipStream_t s);
+// gemm.hip
+bool gemm_needs_prologue(const gdev::GemvParams &p);
+void launch_gemm_prologue(const gdev::GemvParams &p, float *xn, hipStream_t s);
+void launch_gemm(const gdev::GemvParams &p, int wdtype, hipStream_t s);
 // Persistent execution of a whole step (persist.hip).  phases: device array.
 // flags: one 128-byte slot per workgroup (zeroed at allocation); status[0]
 // becomes non-zero if a barrier wait timed out.
