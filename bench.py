@@ -19,10 +19,15 @@ Extra fields of the JSON line:
                 per-launch events in one profiled step at the end context.
   hbm           whole-step algorithmic bytes (weights + scales + KV read at
                 the mean context of the timed steps) / measured step time
+  batch64       the metric's second batch size (config 5 at b = 64): the same
+                workload for 64 streams, the whole decode to ctx 4096 timed
+                (projections on the MFMA GEMM path); its roofline is the whole
+                step's algorithmic bytes (weights + every stream's KV at the
+                mean context) / its device time
   cpu_baseline  the CPU oracle (oracle/, a C restatement of the reference's
                 decode arithmetic) on a bounded sample of the same workload,
                 timed on this host's cores
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--batch B]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--batch B] [--batch2 B2]
 """
 import argparse
 import importlib.util
@@ -80,12 +85,89 @@ def cpu_baseline(cfg, prompt_len, budget_s, seed):
                       % (prompt_len, n, pos, el, threads)}
 
 
+def run_batch(xe, dev, cfg, args, B, steps, warmup, profile):
+    """Prompt feed, W untimed steps, then K timed greedy steps (default: to the
+    end of the context) for B streams; returns the measurement as a dict."""
+    dec = xe.Decoder(dev, cfg, max_batch=B)
+    t = time.perf_counter()
+    dec.init_synthetic(args.seed)
+    print("[bench] b=%d: weights initialised in %.1f s (%.1f MB)" % (B, time.perf_counter() - t,
+          dec.weight_bytes() / 1e6), file=sys.stderr, flush=True)
+    rng = np.random.default_rng(args.seed)
+    prompt = rng.integers(0, cfg.vocab, (B, args.prompt)).astype(np.int32)
+    dec.feed(prompt)
+    room = args.ctx - args.prompt - (1 if profile else 0)  # one profiled step at the end
+    W = min(warmup, room)
+    K = steps if steps > 0 else room - W
+    if W + K > room:
+        sys.exit("bench.py: warmup + steps exceed the context (%d)" % room)
+    dec.decode(W, want_tokens=False)
+    dev.synchronize()
+    t0 = time.perf_counter()
+    _, dev_us = dec.decode(K, want_tokens=False)
+    dev.synchronize()
+    t1 = time.perf_counter()
+    step_s = (t1 - t0) / K
+    tok_s = B * K / (t1 - t0)
+    executor = dec.executor(B)
+    prof = dec.profile_step() if profile else []
+    by_label = {}
+    for l, u, b in prof:
+        e = by_label.setdefault(l, [0, 0.0, 0.0])
+        e[0] += 1
+        e[1] += u
+        e[2] += b
+    # whole-step algorithmic bytes at the mean context of the timed region
+    mean_ctx = args.prompt + W + K / 2.0
+    kv_bytes = B * cfg.n_layers * mean_ctx * cfg.n_kv_heads * cfg.head_dim * 2 * 2
+    step_bytes = dec.weight_bytes() + kv_bytes
+    hbm_gbps = step_bytes / step_s / 1e9
+    if executor == "ll" or not profile:
+        # the timed launches: bytes and device time summed over them
+        r_bytes, r_us = step_bytes * K, dev_us
+        r_kernel = ("ll_step_kernel (whole decode step per token; %d launches of <= 256 "
+                    "steps in the timed region)" % ((K + 255) // 256) if executor == "ll" else
+                    "whole decode step (%s executor: every kernel of the step)" % executor)
+    else:
+        r_bytes = sum(b for l, u, b in prof if l.startswith("gemv"))
+        r_us = sum(u for l, u, b in prof if l.startswith("gemv"))
+        r_kernel = "gemv (decode GEMV family, one profiled step)"
+    r_gbps = r_bytes / r_us / 1e3
+    res = {
+        "value": round(tok_s, 2), "unit": "tok/s", "steps": K, "warmup": W,
+        "ms_per_step": round(step_s * 1e3, 4),
+        "config": {"workload": "gemma3-1b int8 greedy decode, batch %d, prompt %d, decode to "
+                               "ctx %d" % (B, args.prompt, args.ctx),
+                   "layers": cfg.n_layers, "hidden": cfg.d_model, "heads": "4q/1kv x 256",
+                   "ffn": cfg.ffn, "vocab": cfg.vocab, "batch": B, "prompt": args.prompt,
+                   "ctx": args.ctx, "seed": args.seed, "executor": executor},
+        "device_us_per_step": round(dev_us / max(K, 1), 3),
+        "hbm": {"achieved": round(hbm_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                "frac": round(hbm_gbps / HBM_PEAK_GBPS, 4),
+                "bytes_per_step": int(step_bytes)},
+        "roofline": {"bound": "hbm", "kernel": r_kernel,
+                     "achieved": round(r_gbps, 1), "peak": HBM_PEAK_GBPS,
+                     "unit": "GB/s", "frac": round(r_gbps / HBM_PEAK_GBPS, 4),
+                     "traffic": None, "bytes": int(r_bytes), "us": round(r_us, 2)},
+    }
+    if profile:
+        res["phases"] = {l: {"launches": v[0], "us": round(v[1], 2),
+                             "gbps": round(v[2] / v[1] / 1e3, 1) if v[1] > 0 else None}
+                         for l, v in by_label.items()}
+    dec.close()
+    print("[bench] b=%d: %.1f tok/s, %.3f ms/step (%s)" % (B, tok_s, step_s * 1e3, executor),
+          file=sys.stderr, flush=True)
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=0, help="timed steps (0: decode to --ctx)")
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--batch", type=int, default=1)
+    ap.add_argument("--batch2", type=int, default=64,
+                    help="second batch size measured in the same run (0: none)")
     ap.add_argument("--prompt", type=int, default=512)
     ap.add_argument("--ctx", type=int, default=4096)
     ap.add_argument("--seed", type=int, default=2)
@@ -99,88 +181,33 @@ def main():
 
     xe = load_xe()
     cfg = xe.GEMMA3_1B.replace(max_ctx=args.ctx)
-    B = args.batch
     dev = xe.Device(0)
-    dec = xe.Decoder(dev, cfg, max_batch=B)
-    t = time.perf_counter()
-    dec.init_synthetic(args.seed)
-    print("[bench] weights initialised in %.1f s (%.1f MB)" % (time.perf_counter() - t,
-          dec.weight_bytes() / 1e6), file=sys.stderr, flush=True)
-    rng = np.random.default_rng(args.seed)
-    prompt = rng.integers(0, cfg.vocab, (B, args.prompt)).astype(np.int32)
-    dec.feed(prompt)
-    room = args.ctx - args.prompt - 1  # one profiled step at the end
-    W = min(args.warmup, room)
-    K = args.steps if args.steps > 0 else room - W
-    if W + K > room:
-        sys.exit("bench.py: warmup + steps exceed the context (%d)" % room)
-    dec.decode(W, want_tokens=False)
-    dev.synchronize()
-    t0 = time.perf_counter()
-    _, dev_us = dec.decode(K, want_tokens=False)
-    dev.synchronize()
-    t1 = time.perf_counter()
-    step_s = (t1 - t0) / K
-    tok_s = B * K / (t1 - t0)
-
-    executor = dec.executor(B)
-    prof = dec.profile_step()
-    by_label = {}
-    for l, u, b in prof:
-        e = by_label.setdefault(l, [0, 0.0, 0.0])
-        e[0] += 1
-        e[1] += u
-        e[2] += b
-    # whole-step algorithmic bytes at the mean context of the timed region
-    mean_ctx = args.prompt + W + K / 2.0
-    kv_bytes = B * cfg.n_layers * mean_ctx * cfg.n_kv_heads * cfg.head_dim * 2 * 2
-    step_bytes = dec.weight_bytes() + kv_bytes
-    hbm_gbps = step_bytes / step_s / 1e9
-    if executor == "ll":
-        # one launch per run of <= 256 tokens: bytes and time summed over the
-        # timed launches give the per-launch average ratio
-        r_bytes, r_us = step_bytes * K, dev_us
-        r_kernel = ("ll_step_kernel (whole decode step per token; %d launches of <= 256 "
-                    "steps in the timed region)" % ((K + 255) // 256))
-    else:
-        r_bytes = sum(b for l, u, b in prof if l.startswith("gemv"))
-        r_us = sum(u for l, u, b in prof if l.startswith("gemv"))
-        r_kernel = "gemv (decode GEMV family, one profiled step)"
-    r_gbps = r_bytes / r_us / 1e3
-
+    B = args.batch
+    head = run_batch(xe, dev, cfg, args, B, args.steps, args.warmup, profile=True)
     out = {
         "metric": "int8 decode tok/s, Gemma3-1B-shape b=%d" % B,
-        "value": round(tok_s, 2),
+        "value": head["value"],
         "unit": "tok/s",
         "n_gpus": 1,
-        "steps": K,
-        "warmup": W,
-        "ms_per_step": round(step_s * 1e3, 4),
+        "steps": head["steps"],
+        "warmup": head["warmup"],
+        "ms_per_step": head["ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int8 weights, fp32 accumulate, bf16 KV",
         "data": "synthetic (seeded random-init weights N(0,0.02) quantised int8 per channel; "
                 "uniform random prompt ids)",
-        "config": {"workload": "gemma3-1b int8 greedy decode, batch %d, prompt %d, decode to "
-                               "ctx %d" % (B, args.prompt, args.ctx),
-                   "layers": cfg.n_layers, "hidden": cfg.d_model, "heads": "4q/1kv x 256",
-                   "ffn": cfg.ffn, "vocab": cfg.vocab, "batch": B, "prompt": args.prompt,
-                   "ctx": args.ctx, "seed": args.seed,
-                   "executor": executor},
-        "device_us_per_step": round(dev_us / max(K, 1), 3),
-        "hbm": {"achieved": round(hbm_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                "frac": round(hbm_gbps / HBM_PEAK_GBPS, 4),
-                "bytes_per_step": int(step_bytes)},
-        "roofline": {"bound": "hbm", "kernel": r_kernel,
-                     "achieved": round(r_gbps, 1), "peak": HBM_PEAK_GBPS,
-                     "unit": "GB/s", "frac": round(r_gbps / HBM_PEAK_GBPS, 4),
-                     "traffic": None, "bytes": int(r_bytes), "us": round(r_us, 2)},
-        "phases": {l: {"launches": v[0], "us": round(v[1], 2),
-                       "gbps": round(v[2] / v[1] / 1e3, 1) if v[1] > 0 else None}
-                   for l, v in by_label.items()},
+        "config": head["config"],
+        "device_us_per_step": head["device_us_per_step"],
+        "hbm": head["hbm"],
+        "roofline": head["roofline"],
+        "phases": head["phases"],
     }
-    dec.close()
+    if args.batch2 > 0 and args.batch2 != B:
+        # the metric's second batch size: the whole decode to ctx, timed the same way
+        out["batch%d" % args.batch2] = run_batch(xe, dev, cfg, args, args.batch2, 0, args.warmup,
+                                                 profile=False)
     dev.close()
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(cfg, 4, args.cpu_seconds, args.seed)

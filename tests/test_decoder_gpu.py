@@ -67,14 +67,30 @@ def prompts(cfg, batch, n, seed):
     return rng.integers(0, cfg.vocab, (batch, n)).astype(np.int32)
 
 
+# A greedy step whose two best oracle logits differ by less than this is a
+# tie at fp32 summation-order noise (logits here are O(1) sums of a few
+# hundred to a few thousand fp32 products, each order differing by ~1e-6).
+# A stream may flip there, and only there; it is then not compared further
+# (every later token depends on the flipped one) and the flip is reported.
+TIE_MARGIN = 1e-5
+
+
 def compare_stream(got, want, margins, label):
+    ties = []
     for b in range(got.shape[0]):
         for i in range(got.shape[1]):
             if got[b, i] != want[b, i]:
+                if margins[b, i] < TIE_MARGIN:
+                    ties.append((b, i, float(margins[b, i])))
+                    break
                 pytest.fail("%s stream %d diverges at step %d: gpu %d oracle %d (oracle top-2 "
                             "margin %.3g)" % (label, b, i, got[b, i], want[b, i], margins[b, i]))
-    print("[%s] %d streams x %d tokens identical; min top-2 margin %.3g"
-          % (label, got.shape[0], got.shape[1], float(margins.min())), flush=True)
+    for b, i, m in ties:
+        print("[%s] stream %d flips at an fp32 tie at step %d (oracle top-2 margin %.3g)"
+              % (label, b, i, m), flush=True)
+    assert len(ties) <= max(1, got.shape[0] // 8), "%s: too many tie flips %s" % (label, ties)
+    print("[%s] %d streams x %d tokens identical (%d tie flips); min top-2 margin %.3g"
+          % (label, got.shape[0], got.shape[1], len(ties), float(margins.min())), flush=True)
 
 
 @pytest.mark.parametrize("family", ["opt", "whisper", "gemma"])

@@ -281,6 +281,8 @@ struct xe_decoder {
   float *xa = nullptr, *xb = nullptr, *qkv = nullptr, *att = nullptr, *sub = nullptr;
   float *ffn = nullptr, *qx = nullptr, *logits = nullptr, *tmp = nullptr;
   float *xn = nullptr;  // GEMM path: normalised activations [max_batch][max K]
+  float *gemm_ws = nullptr;  // GEMM split-K partials
+  unsigned *gemm_cnt = nullptr;  // GEMM split-K counters (zeroed once, self-resetting)
   uint16_t *kc = nullptr, *vc = nullptr;  // [L][B][hkv][max_ctx][hd]
   float *rope_cos = nullptr, *rope_sin = nullptr;
   int32_t *tokens = nullptr, *pos = nullptr, *next = nullptr, *hist = nullptr;
@@ -475,6 +477,11 @@ void alloc_decoder(xe_decoder *d) {
   d->qx = dalloc<float>(static_cast<size_t>(B) * D, s);
   d->logits = dalloc<float>(static_cast<size_t>(B) * c.vocab, s);
   d->xn = dalloc<float>(static_cast<size_t>(B) * std::max(std::max(D, F), std::max(hq, static_cast<int>(d->nqkv()))), s);
+  if (B > 8 || F > 4096) {  // the GEMM path can run (see PlanBuilder::gemv)
+    d->gemm_ws = dalloc<float>(gemm_ws_floats(), s);
+    d->gemm_cnt = dalloc<unsigned>(gemm_cnt_words(), s);
+    XE_HIP(hipMemsetAsync(d->gemm_cnt, 0, gemm_cnt_words() * sizeof(unsigned), s));
+  }
   const size_t kvn = d->kv_layer_elems() * c.n_layers;
   d->kc = dalloc<uint16_t>(kvn, s);
   d->vc = dalloc<uint16_t>(kvn, s);
@@ -558,7 +565,8 @@ void free_decoder(xe_decoder *d) {
                   static_cast<void *>(d->tokens), static_cast<void *>(d->pos),
                   static_cast<void *>(d->next), static_cast<void *>(d->hist),
                   static_cast<void *>(d->arg_v), static_cast<void *>(d->arg_i),
-                  static_cast<void *>(d->attn_work), static_cast<void *>(d->xn)})
+                  static_cast<void *>(d->attn_work), static_cast<void *>(d->xn),
+                  static_cast<void *>(d->gemm_ws), static_cast<void *>(d->gemm_cnt)})
     if (p) (void)hipFree(p);
   if (d->host_tok) (void)hipHostFree(d->host_tok);
   if (d->s) (void)hipStreamDestroy(d->s);
@@ -597,6 +605,8 @@ struct PlanBuilder {
   xe_decoder::Plan &plan;
   int step_nb;
   float *xn = nullptr;  // GEMM path scratch (null: GEMV only)
+  float *ws = nullptr;
+  unsigned *cnt = nullptr;
   void push(const sdev::Phase &ph, const std::string &label, double bytes, size_t lds) {
     plan.phases.push_back(ph);
     plan.labels.push_back(label);
@@ -695,6 +705,8 @@ struct PlanBuilder {
     }
     ph.kind = sdev::PH_GEMM;
     ph.nblocks = ((L.m + 63) / 64) * ((batch + 63) / 64);
+    ph.ws = ws;
+    ph.cnt = cnt;
     push(ph, label, gemv_bytes(g, batch), 0);
   }
   void attn(const AttnLaunch &a, const std::string &label, double bytes) {
@@ -723,7 +735,7 @@ void build_plan(xe_decoder *d, int B, xe_decoder::Plan &plan) {
   const int nq = static_cast<int>(d->nqkv());
   const int norm = gem ? XE_NORM_RMS1P : XE_NORM_LN;
   plan.step_nb = B <= 1 ? 1 : B <= 2 ? 2 : 4;
-  PlanBuilder pb{plan, plan.step_nb, d->xn};
+  PlanBuilder pb{plan, plan.step_nb, d->gemm_ws ? d->xn : nullptr, d->gemm_ws, d->gemm_cnt};
 
   // embedding
   {

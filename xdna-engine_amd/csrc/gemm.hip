@@ -36,6 +36,9 @@ constexpr int kBM = 64, kBN = 64, kBK = 64;
 constexpr int kGT = 256;             // threads
 constexpr int kXS = kBK + 8;         // LDS row stride (bf16) of a staged part
 constexpr int kNoRec = 0x7ffffff0;  // past every buffer: loads return zeros
+constexpr size_t kGemmWsFloats = size_t(8) << 20;  // split-K partials (32 MB)
+constexpr size_t kGemmMaxTiles = 8192;     // split-K output tiles (counters)
+constexpr int kMaxSplitsK = 16;            // splits of one GEMM
 
 // Upper 16 bits of two fp32 values (exact bf16 of values with <= 8
 // significant bits) packed as a bf16 pair.
@@ -94,89 +97,130 @@ __device__ __forceinline__ void to_bf16(const WLoad<WT> &w, bf16x8 &a0, bf16x8 &
   }
 }
 
-template <int WT>
-__global__ __launch_bounds__(kGT) void gemm_kernel(gdev::GemvParams p) {
+// Epilogue of rows r0 .. r0 + 3 (a GeGLU pair each half) of stream b.
+__device__ __forceinline__ void epilogue4(const gdev::GemvParams &p, int wdtype, int r0, int b, const float (&acc)[4]) {
+  float t[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int r = min(r0 + i, p.m - 1);
+    t[i] = acc[i] * (wdtype == XE_I8 ? p.scale[r] : 1.0f) + (p.bias ? p.bias[r] : 0.0f);
+  }
+  float *yrow = p.y + static_cast<size_t>(b) * p.ldy;
+  if (p.act == ACT_GEGLU_TANH) {
+#pragma unroll
+    for (int i = 0; i < 4; i += 2)
+      if (r0 + i + 1 < p.m) yrow[(r0 + i) / 2] = gdev::gelu_tanh(t[i]) * t[i + 1] * p.out_scale;
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      if (r0 + i >= p.m) continue;
+      float v = t[i];
+      if (p.act == ACT_RELU) v = v > 0.f ? v : 0.f;
+      else if (p.act == ACT_GELU_ERF) v = gdev::gelu_erf(v);
+      yrow[r0 + i] = v * p.out_scale;
+    }
+  }
+}
+
+// Split-K: blockIdx.z takes K steps [z * spk, (z + 1) * spk).  With more than
+// one split, each workgroup stores its partial tile (agent-scope stores) in
+// ws[tile][z][b][r] and counts itself in cnt[tile]; the last one to arrive
+// adds the partials in split order (the same order on every run) and runs
+// the epilogue, then re-arms the counter for the next launch.
+// MB: MFMA row blocks per wave (the wave's 16 * MB weight rows share each
+// activation fragment read from LDS); a workgroup covers 64 * MB rows.
+template <int WT, int MB>
+__global__ __launch_bounds__(kGT) void gemm_kernel(gdev::GemvParams p, float *ws, unsigned *cnt, int spk) {
+  constexpr int BM = 64 * MB;
   // three parts x [kBN][kXS] bf16
   __shared__ __attribute__((aligned(16))) uint16_t xs[3][kBN * kXS];
+  __shared__ int last;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int m0 = blockIdx.x * kBM, b0 = blockIdx.y * kBN;
+  const int m0 = blockIdx.x * BM, b0 = blockIdx.y * kBN;
   const int K = p.k;
-  const int nsteps = (K + kBK - 1) / kBK;
+  const int ks = gridDim.z, z = blockIdx.z;
+  const int step0 = z * spk;
+  const int nsteps = min((K + kBK - 1) / kBK, step0 + spk) - step0;
   const int nb = min(kBN, p.batch - b0);
   const __amdgpu_buffer_rsrc_t rw = gdev::coherent_rsrc(p.w);
   const __amdgpu_buffer_rsrc_t re = gdev::coherent_rsrc(WT == XE_BFP16 ? static_cast<const void *>(p.exps) : p.w);
   const __amdgpu_buffer_rsrc_t rx = gdev::coherent_rsrc(p.x);
 
-  // this lane's weight row and k offset within a step
-  const int wrow = m0 + wave * 16 + (lane & 15);
-  const bool wrow_ok = wrow < p.m;
+  // this lane's weight rows (one per row block) and k offset within a step
+  const int wbase = m0 + wave * 16 * MB + (lane & 15);
   const int wk = 16 * (lane >> 4);
   // activation staging: thread t stages row t / 4, k (t % 4) * 16 .. + 16
   const int srow = threadIdx.x >> 2, sk = (threadIdx.x & 3) * 16;
   const bool srow_ok = srow < nb;
 
-  WLoad<WT> wcur, wnxt;
-  f32x4 xcur[4], xnxt[4];
-  auto load_x = [&](int step, f32x4 (&xv)[4]) {
-    const int k = step * kBK + sk;
+  // three-stage pipeline: the weights and activations of steps s + 1 and
+  // s + 2 are in flight while step s computes
+  struct Stage {
+    WLoad<WT> w[MB];
+    f32x4 x[4];
+  };
+  // k past this split's end reads zeros.  (One per-lane bound, no uniform
+  // "step is live" flag: the compiler would unswitch on it, issue each load
+  // twice and wait for the first before the second.)
+  const int kend = min(K, (step0 + nsteps) * kBK);
+  auto issue = [&](int step, Stage &st) {
+    const int k = (step0 + step) * kBK + sk;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-      const bool ok = srow_ok && k + 4 * i < K;
+      const bool ok = srow_ok && k + 4 * i < kend;
       const int off = ok ? ((b0 + srow) * p.ldx + k + 4 * i) * 4 : kNoRec;
-      xv[i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, 0));
+      st.x[i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, 0));
+    }
+    const int kw = (step0 + step) * kBK + wk;
+#pragma unroll
+    for (int mb = 0; mb < MB; mb++) {
+      const int row = wbase + 16 * mb;
+      load_w<WT>(rw, re, row, kw, row < p.m && kw < kend, K, st.w[mb]);
     }
   };
-  auto load_wstep = [&](int step, WLoad<WT> &w) {
-    const int k = step * kBK + wk;
-    load_w<WT>(rw, re, wrow, k, wrow_ok && k < K, K, w);
-  };
-  load_wstep(0, wcur);
-  load_x(0, xcur);
 
-  f32x4 acc[4];
+  f32x4 acc[MB][4];
 #pragma unroll
-  for (int j = 0; j < 4; j++) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int mb = 0; mb < MB; mb++)
+#pragma unroll
+    for (int j = 0; j < 4; j++) acc[mb][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  for (int step = 0; step < nsteps; step++) {
+  auto compute = [&](int step, const Stage &st) {
+    if (step >= nsteps) return;  // uniform
     // stage this step's activations as three bf16 parts
-    {
-      uint32_t hp[8], mp[8], lp[8];
+    uint32_t hp[8], mp[8], lp[8];
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const float v[4] = {xcur[i].x, xcur[i].y, xcur[i].z, xcur[i].w};
-        float h[4], m[4], l[4];
+    for (int i = 0; i < 4; i++) {
+      const float v[4] = {st.x[i].x, st.x[i].y, st.x[i].z, st.x[i].w};
+      float h[4], m[4], l[4];
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-          h[j] = trunc_bf16(v[j]);
-          const float r = v[j] - h[j];
-          m[j] = trunc_bf16(r);
-          l[j] = trunc_bf16(r - m[j]);
-        }
-        hp[2 * i] = pack_hi16(h[0], h[1]);
-        hp[2 * i + 1] = pack_hi16(h[2], h[3]);
-        mp[2 * i] = pack_hi16(m[0], m[1]);
-        mp[2 * i + 1] = pack_hi16(m[2], m[3]);
-        lp[2 * i] = pack_hi16(l[0], l[1]);
-        lp[2 * i + 1] = pack_hi16(l[2], l[3]);
+      for (int q = 0; q < 4; q++) {
+        h[q] = trunc_bf16(v[q]);
+        const float r = v[q] - h[q];
+        m[q] = trunc_bf16(r);
+        l[q] = trunc_bf16(r - m[q]);
       }
-      if (step > 0) __syncthreads();  // the previous step's reads are done
-      uint32_t *dh = reinterpret_cast<uint32_t *>(xs[0] + srow * kXS + sk);
-      uint32_t *dm = reinterpret_cast<uint32_t *>(xs[1] + srow * kXS + sk);
-      uint32_t *dl = reinterpret_cast<uint32_t *>(xs[2] + srow * kXS + sk);
-      *reinterpret_cast<u32x4 *>(dh) = u32x4{hp[0], hp[1], hp[2], hp[3]};
-      *reinterpret_cast<u32x4 *>(dh + 4) = u32x4{hp[4], hp[5], hp[6], hp[7]};
-      *reinterpret_cast<u32x4 *>(dm) = u32x4{mp[0], mp[1], mp[2], mp[3]};
-      *reinterpret_cast<u32x4 *>(dm + 4) = u32x4{mp[4], mp[5], mp[6], mp[7]};
-      *reinterpret_cast<u32x4 *>(dl) = u32x4{lp[0], lp[1], lp[2], lp[3]};
-      *reinterpret_cast<u32x4 *>(dl + 4) = u32x4{lp[4], lp[5], lp[6], lp[7]};
+      hp[2 * i] = pack_hi16(h[0], h[1]);
+      hp[2 * i + 1] = pack_hi16(h[2], h[3]);
+      mp[2 * i] = pack_hi16(m[0], m[1]);
+      mp[2 * i + 1] = pack_hi16(m[2], m[3]);
+      lp[2 * i] = pack_hi16(l[0], l[1]);
+      lp[2 * i + 1] = pack_hi16(l[2], l[3]);
     }
-    if (step + 1 < nsteps) {
-      load_wstep(step + 1, wnxt);
-      load_x(step + 1, xnxt);
-    }
+    if (step > 0) __syncthreads();  // the previous step's reads are done
+    uint32_t *dh = reinterpret_cast<uint32_t *>(xs[0] + srow * kXS + sk);
+    uint32_t *dm = reinterpret_cast<uint32_t *>(xs[1] + srow * kXS + sk);
+    uint32_t *dl = reinterpret_cast<uint32_t *>(xs[2] + srow * kXS + sk);
+    *reinterpret_cast<u32x4 *>(dh) = u32x4{hp[0], hp[1], hp[2], hp[3]};
+    *reinterpret_cast<u32x4 *>(dh + 4) = u32x4{hp[4], hp[5], hp[6], hp[7]};
+    *reinterpret_cast<u32x4 *>(dm) = u32x4{mp[0], mp[1], mp[2], mp[3]};
+    *reinterpret_cast<u32x4 *>(dm + 4) = u32x4{mp[4], mp[5], mp[6], mp[7]};
+    *reinterpret_cast<u32x4 *>(dl) = u32x4{lp[0], lp[1], lp[2], lp[3]};
+    *reinterpret_cast<u32x4 *>(dl + 4) = u32x4{lp[4], lp[5], lp[6], lp[7]};
     __syncthreads();
-    bf16x8 a0, a1;
-    to_bf16<WT>(wcur, a0, a1);
+    bf16x8 a0[MB], a1[MB];
+#pragma unroll
+    for (int mb = 0; mb < MB; mb++) to_bf16<WT>(st.w[mb], a0[mb], a1[mb]);
 #pragma unroll
     for (int j = 0; j < 4; j++) {
       if (16 * j < nb) {  // column blocks past the batch are skipped (uniform)
@@ -186,49 +230,86 @@ __global__ __launch_bounds__(kGT) void gemm_kernel(gdev::GemvParams p) {
           const uint16_t *src = xs[part] + brow * kXS + wk;
           const bf16x8 x0 = *reinterpret_cast<const bf16x8 *>(src);
           const bf16x8 x1 = *reinterpret_cast<const bf16x8 *>(src + 8);
-          acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, x0, acc[j], 0, 0, 0);
-          acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, x1, acc[j], 0, 0, 0);
+#pragma unroll
+          for (int mb = 0; mb < MB; mb++) {
+            acc[mb][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0[mb], x0, acc[mb][j], 0, 0, 0);
+            acc[mb][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1[mb], x1, acc[mb][j], 0, 0, 0);
+          }
         }
       }
     }
-    wcur = wnxt;
-#pragma unroll
-    for (int i = 0; i < 4; i++) xcur[i] = xnxt[i];
+  };
+
+  Stage sa, sb, sc;
+  issue(0, sa);
+  issue(1, sb);
+  for (int st = 0; st < nsteps; st += 3) {
+    issue(st + 2, sc);
+    compute(st, sa);
+    issue(st + 3, sa);
+    compute(st + 1, sb);
+    issue(st + 4, sb);
+    compute(st + 2, sc);
   }
 
-  // epilogue: lane holds rows r0 + i (i = 0..3) of column block j's stream
-  const int r0 = m0 + wave * 16 + 4 * (lane >> 4);
-  float sc[4], bi[4];
+  // lane holds rows rl(mb) + i (i = 0..3) of column block j's stream
+  if (ks == 1) {
 #pragma unroll
-  for (int i = 0; i < 4; i++) {
-    const int r = min(r0 + i, p.m - 1);
-    sc[i] = WT == XE_I8 ? p.scale[r] : 1.0f;
-    bi[i] = p.bias ? p.bias[r] : 0.0f;
-  }
+    for (int mb = 0; mb < MB; mb++) {
+      const int rl = wave * 16 * MB + 16 * mb + 4 * (lane >> 4);
 #pragma unroll
-  for (int j = 0; j < 4; j++) {
-    const int b = 16 * j + (lane & 15);
-    if (b >= nb) continue;
-    float *yrow = p.y + static_cast<size_t>(b0 + b) * p.ldy;
-    float t[4];
-#pragma unroll
-    for (int i = 0; i < 4; i++) t[i] = acc[j][i] * sc[i] + bi[i];
-    if (p.act == ACT_GEGLU_TANH) {
-      // rows come in (gate, up) pairs: r0 + (0, 1) and r0 + (2, 3)
-#pragma unroll
-      for (int i = 0; i < 4; i += 2)
-        if (r0 + i + 1 < p.m) yrow[(r0 + i) / 2] = gdev::gelu_tanh(t[i]) * t[i + 1] * p.out_scale;
-    } else {
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        if (r0 + i >= p.m) continue;
-        float v = t[i];
-        if (p.act == ACT_RELU) v = v > 0.f ? v : 0.f;
-        else if (p.act == ACT_GELU_ERF) v = gdev::gelu_erf(v);
-        yrow[r0 + i] = v * p.out_scale;
+      for (int j = 0; j < 4; j++) {
+        const int b = 16 * j + (lane & 15);
+        if (b >= nb) continue;
+        const float a4[4] = {acc[mb][j][0], acc[mb][j][1], acc[mb][j][2], acc[mb][j][3]};
+        epilogue4(p, WT, m0 + rl, b0 + b, a4);
       }
     }
+    return;
   }
+  const int tile = blockIdx.y * gridDim.x + blockIdx.x;
+  float *part = ws + (static_cast<size_t>(tile) * ks + z) * (BM * kBN);
+#pragma unroll
+  for (int mb = 0; mb < MB; mb++) {
+    const int rl = wave * 16 * MB + 16 * mb + 4 * (lane >> 4);
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int b = 16 * j + (lane & 15);
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+        __hip_atomic_store(part + b * BM + rl + i, acc[mb][j][i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's partial stores have completed
+  __syncthreads();
+  if (threadIdx.x == 0)
+    last = __hip_atomic_fetch_add(cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == static_cast<unsigned>(ks - 1);
+  __syncthreads();
+  if (!last) return;
+  // the reduction: item = (stream bb, row quad q); every split's partial in
+  // flight at once (ks <= kMaxSplitsK), then summed in split order
+  const __amdgpu_buffer_rsrc_t rws = gdev::coherent_rsrc(ws + static_cast<size_t>(tile) * ks * (BM * kBN));
+  for (int it = threadIdx.x; it < nb * (BM / 4); it += kGT) {
+    const int bb = it / (BM / 4), q = it % (BM / 4);
+    f32x4 v[kMaxSplitsK];
+#pragma unroll
+    for (int zz = 0; zz < kMaxSplitsK; zz++)
+      v[zz] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                            rws, zz < ks ? ((zz * kBN + bb) * BM + 4 * q) * 4 : kNoRec, 0,
+                                            gdev::kCoherentSc1));
+    float sum[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int zz = 0; zz < kMaxSplitsK; zz++) {
+      if (zz < ks) {
+        sum[0] += v[zz].x;
+        sum[1] += v[zz].y;
+        sum[2] += v[zz].z;
+        sum[3] += v[zz].w;
+      }
+    }
+    epilogue4(p, WT, m0 + 4 * q, b0 + bb, sum);
+  }
+  if (threadIdx.x == 0) __hip_atomic_store(cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Norm / residual prologue of one stream row (blockIdx.x): p.x, p.sub and
@@ -248,15 +329,57 @@ __global__ __launch_bounds__(256) void gemm_prologue_kernel(gdev::GemvParams p, 
   for (int i = threadIdx.x; i < p.k; i += 256) xn[static_cast<size_t>(b) * p.k + i] = xs[i];
 }
 
-using GemmFn = void (*)(gdev::GemvParams);
+using GemmFn = void (*)(gdev::GemvParams, float *, unsigned *, int);
 
-GemmFn pick_gemm(int wdtype) {
-  switch (wdtype) {
-    case XE_I8: return gemm_kernel<XE_I8>;
-    case XE_BF16: return gemm_kernel<XE_BF16>;
-    case XE_BFP16: return gemm_kernel<XE_BFP16>;
+template <int WT>
+GemmFn pick_mb(int mb) {
+  switch (mb) {
+    case 1: return gemm_kernel<WT, 1>;
+    case 2: return gemm_kernel<WT, 2>;
+    case 4: return gemm_kernel<WT, 4>;
   }
   return nullptr;
+}
+
+GemmFn pick_gemm(int wdtype, int mb) {
+  switch (wdtype) {
+    case XE_I8: return pick_mb<XE_I8>(mb);
+    case XE_BF16: return pick_mb<XE_BF16>(mb);
+    case XE_BFP16: return pick_mb<XE_BFP16>(mb);
+  }
+  return nullptr;
+}
+
+// Shape of one GEMM launch: row blocks per wave (MB), splits of K.  The
+// largest MB that still gives every CU about two workgroups (the fewer
+// activation-fragment reads per weight byte, the better), then splits for
+// about four workgroups per CU: at most kMaxSplitsK, at least two K steps
+// each, and a bounded partial workspace.
+struct GemmShape {
+  int mb, ks, spk, tm, tb;
+};
+
+GemmShape gemm_shape(int m, int k, int batch) {
+  const int steps = (k + kBK - 1) / kBK;
+  const int tb = (batch + kBN - 1) / kBN;
+  const int cus = gdev::cu_count();
+  GemmShape g{1, 1, steps, 0, tb};
+  // wide outputs (the lm-head): four row blocks per wave; else one
+  g.mb = static_cast<long long>(m) * tb >= 64LL * 4 * 4 * cus ? 4 : 1;
+  g.tm = (m + 64 * g.mb - 1) / (64 * g.mb);
+  // split K only when the tiles leave most CUs idle: every split's partial
+  // tile costs a write and a read of 64 x 64 x mb floats, so at least four
+  // steps (256 k) per split
+  const int tiles = g.tm * g.tb;
+  int ks = 1;
+  if (2 * tiles < cus) {
+    ks = std::min(kMaxSplitsK, (cus + tiles - 1) / tiles);
+    ks = std::min(ks, std::max(1, steps / 4));
+    while (ks > 1 && static_cast<size_t>(tiles) * ks * 64 * g.mb * kBN > kGemmWsFloats) ks--;
+  }
+  g.spk = (steps + ks - 1) / ks;
+  g.ks = (steps + g.spk - 1) / g.spk;  // no empty split
+  return g;
 }
 
 }  // namespace
@@ -275,7 +398,10 @@ void launch_gemm_prologue(const gdev::GemvParams &p, float *xn, hipStream_t s) {
   XE_HIP(hipGetLastError());
 }
 
-void launch_gemm(const gdev::GemvParams &p, int wdtype, hipStream_t s) {
+size_t gemm_ws_floats() { return kGemmWsFloats; }
+size_t gemm_cnt_words() { return kGemmMaxTiles; }
+
+void launch_gemm(const gdev::GemvParams &p, int wdtype, float *ws, unsigned *cnt, hipStream_t s) {
   XE_REQUIRE(p.m > 0 && p.k > 0 && p.batch > 0, "gemm: empty shape");
   XE_REQUIRE(p.k % 16 == 0, "gemm: K must be a multiple of 16");
   XE_REQUIRE(!p.x_bf16, "gemm: fp32 activations only");
@@ -286,9 +412,12 @@ void launch_gemm(const gdev::GemvParams &p, int wdtype, hipStream_t s) {
   const size_t wb = static_cast<size_t>(p.m) * p.k * (wdtype == XE_BF16 ? 2 : 1);
   XE_REQUIRE(wb < (size_t(1) << 31) && static_cast<size_t>(p.batch) * p.ldx * 4 < (size_t(1) << 31),
              "gemm: operand above 2 GB");
-  GemmFn fn = pick_gemm(wdtype);
+  const GemmShape g = gemm_shape(p.m, p.k, p.batch);
+  GemmFn fn = pick_gemm(wdtype, g.mb);
   XE_REQUIRE(fn, "gemm: unsupported weight dtype");
-  hipLaunchKernelGGL(fn, dim3((p.m + kBM - 1) / kBM, (p.batch + kBN - 1) / kBN), dim3(kGT), 0, s, p);
+  XE_REQUIRE(g.ks == 1 || (ws && cnt && static_cast<size_t>(g.tm) * g.tb <= kGemmMaxTiles),
+             "gemm: split-K workspace missing or too many tiles");
+  hipLaunchKernelGGL(fn, dim3(g.tm, g.tb, g.ks), dim3(kGT), 0, s, p, ws, cnt, g.spk);
   XE_HIP(hipGetLastError());
 }
 

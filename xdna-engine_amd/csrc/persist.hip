@@ -41,7 +41,7 @@ void launch_phase(const sdev::Phase &ph, hipStream_t s) {
   switch (ph.kind) {
     case sdev::PH_GEMV: launch_gemv_phase(ph, s); return;
     case sdev::PH_GEMM_PRO: launch_gemm_prologue(ph.u.gemv, ph.xn, s); return;
-    case sdev::PH_GEMM: launch_gemm(ph.u.gemv, ph.variant, s); return;
+    case sdev::PH_GEMM: launch_gemm(ph.u.gemv, ph.variant, ph.ws, ph.cnt, s); return;
     case sdev::PH_ATTN:
     case sdev::PH_MERGE: launch_attn_phase(ph, s); return;
     case sdev::PH_EMBED:

@@ -63,6 +63,8 @@ struct Phase {
   int nblocks;  // virtual blocks of the phase
   int pad;
   float *xn;    // PH_GEMM_PRO: normalised activations out [batch][k]
+  float *ws;    // PH_GEMM: split-K partial tiles
+  unsigned *cnt;  // PH_GEMM: split-K arrival counters (zero between launches)
   union {
     gdev::GemvParams gemv;
     adev::AttnParams attn;
@@ -185,7 +187,9 @@ void launch_phase(const sdev::Phase &ph, hipStream_t s);
 // gemm.hip
 bool gemm_needs_prologue(const gdev::GemvParams &p);
 void launch_gemm_prologue(const gdev::GemvParams &p, float *xn, hipStream_t s);
-void launch_gemm(const gdev::GemvParams &p, int wdtype, hipStream_t s);
+void launch_gemm(const gdev::GemvParams &p, int wdtype, float *ws, unsigned *cnt, hipStream_t s);
+size_t gemm_ws_floats();
+size_t gemm_cnt_words();
 // Persistent execution of a whole step (persist.hip).  phases: device array.
 // flags: one 128-byte slot per workgroup (zeroed at allocation); status[0]
 // becomes non-zero if a barrier wait timed out.
