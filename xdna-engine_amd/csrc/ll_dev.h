@@ -327,6 +327,46 @@ __device__ __forceinline__ bool fold(const FD &f, int nb, int d, float *xr, floa
   return true;
 }
 
+// The last residual fold of a GEMV's input and its RMS norm in one block
+// reduction (Gemma: t = x + RMSNorm(src)(1 + post_w), then RMS(t)):
+//   sum t^2 = sum x^2 + 2 inv_s sum x s' + inv_s^2 sum s'^2, s' = src (1 + post_w),
+// so sum src^2, sum x^2, sum x s', sum s'^2 come out of one reduction (the
+// same algebra as the phase kernels' prologue).  residual[b] = t,
+// dst[b] = RMS(t) (1 + gamma) (rms1p) or RMS(t) gamma; src is read into dst.
+template <typename FD>
+__device__ __forceinline__ bool fold_rms(const FD &f, int nb, int d, float *xr, float *dst, float *red,
+                                         const float *gamma, float eps, bool rms1p, unsigned ep, const Ctl &c) {
+  if (!get(f.src, nb, d, dst, d, ep, c)) return false;
+  int slot = 0;
+  const XE_GLOBAL float *pw = gptr(f.post_w);
+  const XE_GLOBAL float *gm = gptr(gamma);
+  const float fd = static_cast<float>(d);
+  for (int b = 0; b < nb; b++) {
+    XE_LDS float *x = lptr(xr) + static_cast<size_t>(b) * d;
+    XE_LDS float *h = lptr(dst) + static_cast<size_t>(b) * d;
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int i = threadIdx.x; i < d; i += kT) {
+      const float sv = h[i], xv = x[i];
+      const float spv = sv * (1.0f + pw[i]);
+      acc[0] = __builtin_fmaf(sv, sv, acc[0]);
+      acc[1] = __builtin_fmaf(xv, xv, acc[1]);
+      acc[2] = __builtin_fmaf(xv, spv, acc[2]);
+      acc[3] = __builtin_fmaf(spv, spv, acc[3]);
+    }
+    sums<4>(acc, red, slot);
+    const float inv_s = 1.0f / sqrtf(acc[0] / fd + f.eps);
+    const float st2 = acc[1] + 2.0f * inv_s * acc[2] + inv_s * inv_s * acc[3];
+    const float inv_t = 1.0f / sqrtf(fmaxf(st2, 0.f) / fd + eps);
+    for (int i = threadIdx.x; i < d; i += kT) {
+      const float t = x[i] + h[i] * inv_s * (1.0f + pw[i]);
+      x[i] = t;
+      h[i] = rms1p ? t * inv_t * (1.0f + gm[i]) : t * inv_t * gm[i];
+    }
+  }
+  __syncthreads();
+  return true;
+}
+
 // dst[b] = norm(x[b]) (LayerNorm two-pass / RMS / RMS (1 + w) / copy).
 __device__ __forceinline__ void norm_rows(const float *xr, int nb, int d, int norm, const float *gamma,
                                           const float *beta, float eps, float *dst, float *red) {

@@ -140,8 +140,14 @@ __global__ __launch_bounds__(kT) void ll_step_kernel(StepParams sp) {
           r1 *= unit;
           auto prep = [&]() -> bool {
             bool r = true;
-            for (int f = 0; f < g.nfold && r; f++) r = fold(g.folds[f], nb, D, xr, xin, red, ep, c);
-            if (r && g.in_vec) r = get(g.in, nb, g.k, xin, g.k, ep, c);
+            // the last fold and an RMS norm share one reduction
+            const bool fuse = !g.in_vec && g.nfold > 0 && g.folds[g.nfold - 1].post_w &&
+                              (g.norm == XE_NORM_RMS1P || g.norm == XE_NORM_RMS);
+            const int nplain = fuse ? g.nfold - 1 : g.nfold;
+            for (int f = 0; f < nplain && r; f++) r = fold(g.folds[f], nb, D, xr, xin, red, ep, c);
+            if (r && fuse)
+              r = fold_rms(g.folds[g.nfold - 1], nb, D, xr, xin, red, g.gamma, g.eps, g.norm == XE_NORM_RMS1P, ep, c);
+            else if (r && g.in_vec) r = get(g.in, nb, g.k, xin, g.k, ep, c);
             else if (r) norm_rows(xr, nb, g.k, g.norm, g.gamma, g.beta, g.eps, xin, red);
             mark_ready(step, i);
             return r;
