@@ -303,13 +303,54 @@ __device__ __forceinline__ void sums(float (&v)[N], float *red, int &slot) {
   gdev::block_sums<kW, N>(v, red, slot);
 }
 
+// A d-vector's weights (norm gains), elements threadIdx.x + kT t for t <
+// kPre, read into registers before the poll they follow: the weight stream
+// evicts them from the caches between layers, so a load issued after the
+// input arrives adds a memory round trip to the hand-off.  Elements past
+// kT kPre are read in place.
+constexpr int kPre = 4;
+struct PreW {
+  float v[kPre];
+};
+__device__ __forceinline__ PreW pre_w(const float *w, int d) {
+  PreW r;
+  const XE_GLOBAL float *g = gptr(w);
+#pragma unroll
+  for (int t = 0; t < kPre; t++) {
+    const int i = threadIdx.x + kT * t;
+    r.v[t] = w != nullptr && i < d ? g[i] : 0.f;
+  }
+  return r;
+}
+// body(i, w...) over this thread's elements i of a d-vector, with the
+// preloaded weights of each PreW (or the weight read in place past them).
+template <typename Body>
+__device__ __forceinline__ void each_w(int d, const PreW &a, const float *wa, Body body) {
+#pragma unroll
+  for (int t = 0; t < kPre; t++) {
+    const int i = threadIdx.x + kT * t;
+    if (i < d) body(i, a.v[t]);
+  }
+  for (int i = threadIdx.x + kT * kPre; i < d; i += kT) body(i, gptr(wa)[i]);
+}
+template <typename Body>
+__device__ __forceinline__ void each_w2(int d, const PreW &a, const float *wa, const PreW &b, const float *wb,
+                                        Body body) {
+#pragma unroll
+  for (int t = 0; t < kPre; t++) {
+    const int i = threadIdx.x + kT * t;
+    if (i < d) body(i, a.v[t], b.v[t]);
+  }
+  for (int i = threadIdx.x + kT * kPre; i < d; i += kT) body(i, gptr(wa)[i], gptr(wb)[i]);
+}
+
 // residual[b] += post(src[b]) for b < nb.  tmp: LDS [nb][d].
 template <typename FD>
 __device__ __forceinline__ bool fold(const FD &f, int nb, int d, float *xr, float *tmp, float *red,
                                      unsigned ep, const Ctl &c) {
+  const PreW pw = pre_w(f.post_w, d);
   if (!get(f.src, nb, d, tmp, d, ep, c)) return false;
   int slot = 0;
-  const XE_GLOBAL float *pw = gptr(f.post_w);
   for (int b = 0; b < nb; b++) {
     XE_LDS float *x = lptr(xr) + static_cast<size_t>(b) * d;
     const XE_LDS float *s = lptr(tmp) + static_cast<size_t>(b) * d;
@@ -318,7 +359,7 @@ __device__ __forceinline__ bool fold(const FD &f, int nb, int d, float *xr, floa
       for (int i = threadIdx.x; i < d; i += kT) ss[0] = __builtin_fmaf(s[i], s[i], ss[0]);
       sums<1>(ss, red, slot);
       const float inv = 1.0f / sqrtf(ss[0] / static_cast<float>(d) + f.eps);
-      for (int i = threadIdx.x; i < d; i += kT) x[i] = x[i] + s[i] * inv * (1.0f + pw[i]);
+      each_w(d, pw, f.post_w, [&](int i, float w) { x[i] = x[i] + s[i] * inv * (1.0f + w); });
     } else {
       for (int i = threadIdx.x; i < d; i += kT) x[i] = x[i] + s[i];
     }
@@ -336,43 +377,43 @@ __device__ __forceinline__ bool fold(const FD &f, int nb, int d, float *xr, floa
 template <typename FD>
 __device__ __forceinline__ bool fold_rms(const FD &f, int nb, int d, float *xr, float *dst, float *red,
                                          const float *gamma, float eps, bool rms1p, unsigned ep, const Ctl &c) {
+  const PreW pw = pre_w(f.post_w, d), gm = pre_w(gamma, d);
   if (!get(f.src, nb, d, dst, d, ep, c)) return false;
   int slot = 0;
-  const XE_GLOBAL float *pw = gptr(f.post_w);
-  const XE_GLOBAL float *gm = gptr(gamma);
   const float fd = static_cast<float>(d);
   for (int b = 0; b < nb; b++) {
     XE_LDS float *x = lptr(xr) + static_cast<size_t>(b) * d;
     XE_LDS float *h = lptr(dst) + static_cast<size_t>(b) * d;
     float acc[4] = {0.f, 0.f, 0.f, 0.f};
-    for (int i = threadIdx.x; i < d; i += kT) {
+    each_w(d, pw, f.post_w, [&](int i, float w) {
       const float sv = h[i], xv = x[i];
-      const float spv = sv * (1.0f + pw[i]);
+      const float spv = sv * (1.0f + w);
       acc[0] = __builtin_fmaf(sv, sv, acc[0]);
       acc[1] = __builtin_fmaf(xv, xv, acc[1]);
       acc[2] = __builtin_fmaf(xv, spv, acc[2]);
       acc[3] = __builtin_fmaf(spv, spv, acc[3]);
-    }
+    });
     sums<4>(acc, red, slot);
     const float inv_s = 1.0f / sqrtf(acc[0] / fd + f.eps);
     const float st2 = acc[1] + 2.0f * inv_s * acc[2] + inv_s * inv_s * acc[3];
     const float inv_t = 1.0f / sqrtf(fmaxf(st2, 0.f) / fd + eps);
-    for (int i = threadIdx.x; i < d; i += kT) {
-      const float t = x[i] + h[i] * inv_s * (1.0f + pw[i]);
+    each_w2(d, pw, f.post_w, gm, gamma, [&](int i, float w, float g) {
+      const float t = x[i] + h[i] * inv_s * (1.0f + w);
       x[i] = t;
-      h[i] = rms1p ? t * inv_t * (1.0f + gm[i]) : t * inv_t * gm[i];
-    }
+      h[i] = rms1p ? t * inv_t * (1.0f + g) : t * inv_t * g;
+    });
   }
   __syncthreads();
   return true;
 }
 
-// dst[b] = norm(x[b]) (LayerNorm two-pass / RMS / RMS (1 + w) / copy).
+// dst[b] = norm(x[b]) (LayerNorm two-pass / RMS / RMS (1 + w) / copy); gp,
+// bp: gamma and beta as pre_w read them.
 __device__ __forceinline__ void norm_rows(const float *xr, int nb, int d, int norm, const float *gamma,
-                                          const float *beta, float eps, float *dst, float *red) {
+                                          const float *beta, float eps, float *dst, float *red, const PreW &gp,
+                                          const PreW &bp) {
   int slot = 0;
   const float fd = static_cast<float>(d);
-  const XE_GLOBAL float *gam = gptr(gamma), *bet = gptr(beta);
   for (int b = 0; b < nb; b++) {
     const XE_LDS float *x = lptr(xr) + static_cast<size_t>(b) * d;
     XE_LDS float *h = lptr(dst) + static_cast<size_t>(b) * d;
@@ -388,16 +429,14 @@ __device__ __forceinline__ void norm_rows(const float *xr, int nb, int d, int no
       }
       sums<1>(v2, red, slot);
       const float inv = 1.0f / sqrtf(v2[0] / fd + eps);
-      for (int i = threadIdx.x; i < d; i += kT) h[i] = (x[i] - mean) * inv * gam[i] + bet[i];
+      each_w2(d, gp, gamma, bp, beta, [&](int i, float g, float be) { h[i] = (x[i] - mean) * inv * g + be; });
     } else if (norm == XE_NORM_RMS || norm == XE_NORM_RMS1P) {
       float v1[1] = {0.f};
       for (int i = threadIdx.x; i < d; i += kT) v1[0] = __builtin_fmaf(x[i], x[i], v1[0]);
       sums<1>(v1, red, slot);
       const float inv = 1.0f / sqrtf(v1[0] / fd + eps);
-      if (norm == XE_NORM_RMS1P)
-        for (int i = threadIdx.x; i < d; i += kT) h[i] = x[i] * inv * (1.0f + gam[i]);
-      else
-        for (int i = threadIdx.x; i < d; i += kT) h[i] = x[i] * inv * gam[i];
+      const bool p1 = norm == XE_NORM_RMS1P;
+      each_w(d, gp, gamma, [&](int i, float g) { h[i] = x[i] * inv * (p1 ? 1.0f + g : g); });
     } else {
       for (int i = threadIdx.x; i < d; i += kT) h[i] = x[i];
     }
@@ -677,10 +716,11 @@ __device__ __forceinline__ void load_head_consts(const AD &a, int posi, HeadCons
   }
 }
 
-// Per-head RMSNorm (1 + w) and RoPE of one head vector (LDS src -> LDS dst),
-// one wave; rotate-half pairing (npu-asr-host/src/lib.rs:143-185).
-template <int HD>
-__device__ __forceinline__ void head_xform(const XE_LDS float *src, XE_LDS float *dst, bool norm, const float (&w0)[HeadConsts<HD>::PER],
+// Per-head RMSNorm (1 + w) and RoPE of one head vector (LDS src; out(d, y)
+// takes dim d's result), one wave; rotate-half pairing
+// (npu-asr-host/src/lib.rs:143-185).
+template <int HD, typename Out>
+__device__ __forceinline__ void head_xform(const XE_LDS float *src, Out out, bool norm, const float (&w0)[HeadConsts<HD>::PER],
                                            const float (&w1)[HeadConsts<HD>::PER], bool rope, const HeadConsts<HD> &hc,
                                            float eps) {
   constexpr int HALF = HeadConsts<HD>::HALF, PER = HeadConsts<HD>::PER;
@@ -715,8 +755,8 @@ __device__ __forceinline__ void head_xform(const XE_LDS float *src, XE_LDS float
       y0 = t0;
       y1 = t1;
     }
-    dst[j] = y0;
-    dst[j + HALF] = y1;
+    out(j, y0);
+    out(j + HALF, y1);
   }
 }
 
@@ -737,12 +777,12 @@ __host__ __device__ __forceinline__ void ll_split(int len, int max_splits, int h
 // Keys one round of a block covers (one Q.K tile per wave).
 constexpr int kRoundKeys = kW * kKeyTile;
 
-// LDS scratch of a block (floats): q heads [g][hd] | new key [hd] | new key
-// and value as stored (bf16 pairs) [hd] | scores / probabilities
-// [kRoundKeys][g] | running max, sum, correction [3][16] | Q.K B operands
-// [hd / 32][64 lanes][8 bf16] | per-wave P.V sums [kW][g][hd].
+// LDS scratch of a block (floats): new key [hd] | new key and value as
+// stored (bf16 pairs) [hd] | scores / probabilities [kRoundKeys][g] | running
+// max, sum, correction [3][16] | Q.K B operands [hd / 32][64 lanes][8 bf16] |
+// per-wave P.V sums [kW][g][hd].
 __host__ __device__ __forceinline__ int attn_scratch_floats(int hd, int g) {
-  return g * hd + 2 * hd + kRoundKeys * g + 48 + (hd / 32) * 256 + kW * g * hd;
+  return 2 * hd + kRoundKeys * g + 48 + (hd / 32) * 256 + kW * g * hd;
 }
 
 typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
@@ -760,10 +800,10 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 // One split block of (stream b, kv head kvh): keys [split*chunk, ...), the G
 // query heads of the group at once.
 //   Q.K: per wave one 16-key tile as v_mfma_f32_16x16x32_bf16 steps, K rows
-//   straight from the bf16 cache as the A operand; B column n < G holds
-//   query head n rounded to bf16 and column G + n its rounding remainder, so
-//   C[key][n] + C[key][G + n] is the score with q to ~16 significant bits
-//   (fp32 accumulation).
+//   straight from the bf16 cache as the A operand; B columns n, G + n and
+//   2 G + n hold the three bf16 parts of query head n (q = hi + mid + lo
+//   exactly), so C[key][n] + C[key][G + n] + C[key][2 G + n] is the score
+//   from exact products with fp32 accumulation.
 //   softmax: scores of the round in LDS, one wave per head (max, exp2, sum),
 //   running max / sum across rounds.
 //   P.V: lanes own 4 dims of a value row (hd / 4 lanes per key), keys spread
@@ -776,14 +816,13 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 template <int HD, int G, typename AD, typename Prep, typename Sub>
 __device__ __forceinline__ bool attn_block(const AD &a, int split, int kvh, int b, int len, const float *qin,
                                            float *scr, unsigned ep, Prep prep, Sub tsub) {
-  static_assert(HD % 32 == 0 && HD <= 256 && 2 * G <= 16, "attention tile shape");
+  static_assert(HD % 32 == 0 && HD <= 256 && 3 * G <= 16, "attention tile shape");
   constexpr int NJ = HD / 32;                  // MFMA steps per tile
   constexpr int LPK = HD / 4;                  // P.V lanes per key
   constexpr int KPI = 64 / LPK;                // keys per P.V load
   constexpr int PVK = kRoundKeys / (kW * KPI); // P.V loads per wave per round
   XE_LDS float *S = lptr(scr);
-  XE_LDS float(*qs)[HD] = reinterpret_cast<XE_LDS float(*)[HD]>(S);
-  XE_LDS float *kt = S + G * HD;
+  XE_LDS float *kt = S;
   XE_LDS uint32_t *kvb = reinterpret_cast<XE_LDS uint32_t *>(kt + HD);  // k | v, bf16 pairs
   XE_LDS float *sc = kt + 2 * HD;              // [kRoundKeys][G]
   XE_LDS float *st = sc + kRoundKeys * G;      // m [16] | l [16] | corr [16]
@@ -831,10 +870,29 @@ __device__ __forceinline__ bool attn_block(const AD &a, int split, int kvh, int 
   const XE_LDS float *qrow = lptr(qin) + static_cast<size_t>(b) * a.qn;
   const XE_LDS float *vsrc = qrow + a.v_off + kvh * HD;
   const bool qnorm = a.q_norm_w != nullptr, knorm = a.k_norm_w != nullptr, rope = a.rope_cos != nullptr;
-  for (int gg = wave; gg < G; gg += kW)
-    head_xform<HD>(qrow + a.q_off + (kvh * G + gg) * HD, qs[gg], qnorm, hc.qn0, hc.qn1, rope, hc, a.norm_eps);
+  // B operands of the Q.K steps, written by the q head transforms: step j
+  // (dims 32 j ..) lane (kg, n) holds dims 32 j + 8 kg .. + 8 of column n;
+  // column n + p G (p = 0, 1, 2) is part p of query head n, where q = hi +
+  // mid + lo exactly (truncation: each part takes the next 8 significant
+  // bits), so the three columns' sum is the fp32 score of the bf16 keys.
+  // Columns from 3 G on are never written: their products land in C columns
+  // that nothing reads.
+  XE_LDS uint16_t *bfh = reinterpret_cast<XE_LDS uint16_t *>(bfr);
+  for (int gg = wave; gg < G; gg += kW) {
+    head_xform<HD>(qrow + a.q_off + (kvh * G + gg) * HD, [&](int d, float x) {
+      const uint32_t hi = __float_as_uint(x) & 0xffff0000u;
+      const float r = x - __uint_as_float(hi);
+      const uint32_t mid = __float_as_uint(r) & 0xffff0000u;
+      const uint32_t lo = __float_as_uint(r - __uint_as_float(mid));
+      XE_LDS uint16_t *o = bfh + (((d >> 5) * 64 + ((d & 31) >> 3) * 16 + gg) * 8 + (d & 7));
+      o[0] = static_cast<uint16_t>(hi >> 16);
+      o[8 * G] = static_cast<uint16_t>(mid >> 16);
+      o[16 * G] = static_cast<uint16_t>(lo >> 16);
+    }, qnorm, hc.qn0, hc.qn1, rope, hc, a.norm_eps);
+  }
   if (appender && wave == kW - 1) {
-    head_xform<HD>(qrow + a.k_off + kvh * HD, kt, knorm, hc.kn0, hc.kn1, rope, hc, a.norm_eps);
+    head_xform<HD>(qrow + a.k_off + kvh * HD, [&](int d, float x) { kt[d] = x; }, knorm, hc.kn0, hc.kn1, rope, hc,
+                   a.norm_eps);
     __builtin_amdgcn_wave_barrier();
     // the new row as the cache holds it: one packed copy serves the lanes
     // that patch it in below and the cache stores at the end
@@ -843,29 +901,10 @@ __device__ __forceinline__ bool attn_block(const AD &a, int split, int kvh, int 
       kvb[HD / 2 + j] = pack_bf16x2(vsrc[2 * j], vsrc[2 * j + 1]);
     }
   }
-  __syncthreads();  // q heads and the new k / v staged in LDS
-
-  // B operands of the Q.K steps, one per 32 dims, built once per block
-  // (column n: head n, or head n - G's remainder; other columns zero)
-  const int col = lane & 15;
-  {
-    const int qh = col < G ? col : col - G;
-    const bool qlive = col < 2 * G;
-    for (int j = wave; j < NJ; j += kW) {
-      const XE_LDS float *src = qs[qlive ? qh : 0] + 32 * j + qk_dim;
-      bf16x8_t f;
-#pragma unroll
-      for (int e = 0; e < 8; e++) {
-        const float x = qlive ? src[e] : 0.f;
-        const float hi = __uint_as_float(static_cast<uint32_t>(adev::f32_to_bf16_rne(x)) << 16);
-        const float part = col < G ? hi : x - hi;
-        f[e] = __builtin_bit_cast(__bf16, adev::f32_to_bf16_rne(part));
-      }
-      bfr[j * 64 + lane] = f;
-    }
-  }
-  __syncthreads();  // B operands staged
+  __syncthreads();  // Q.K B operands and the new k / v staged in LDS
   tsub(0);
+
+  const int col = lane & 15;
 
   const float sc2 = a.scale * adev::kLog2e;
   float acc[G][4];
@@ -886,12 +925,14 @@ __device__ __forceinline__ bool attn_block(const AD &a, int split, int kvh, int 
 #pragma unroll
       for (int j = 0; j < NJ; j++)
         cacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kf[j]), bfr[j * 64 + lane], cacc, 0, 0, 0);
-      // lane (row group r, column n < G): keys tile0 + 4r + i, head n
+      // lane (row group r, column n < G): keys tile0 + 4r + i, head n; the
+      // mid and lo parts sit G and 2 G columns to the right (row_shl)
 #pragma unroll
       for (int i = 0; i < 4; i++) {
-        const float rem = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(cacc[i]), 0x100 + G, 0xF, 0xF, true));
+        const float mid = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(cacc[i]), 0x100 + G, 0xF, 0xF, true));
+        const float lo = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(cacc[i]), 0x100 + 2 * G, 0xF, 0xF, true));
         const int key_l = wave * kKeyTile + 4 * (lane >> 4) + i;
-        if (col < G) sc[key_l * G + col] = tile0 + 4 * (lane >> 4) + i < s1 ? (cacc[i] + rem) * sc2 : -INFINITY;
+        if (col < G) sc[key_l * G + col] = tile0 + 4 * (lane >> 4) + i < s1 ? (cacc[i] + mid + lo) * sc2 : -INFINITY;
       }
     } else if (col < G) {
 #pragma unroll

@@ -70,7 +70,7 @@ __device__ __noinline__ HeadOut head_gemv(const HeadArgs h, int nb, int r0, int 
     o.best.i[b] = -1;
   }
   auto prep = [&]() -> bool {
-    norm_rows(xr, nb, h.d, h.norm, h.gamma, h.beta, h.eps, xin, red);
+    norm_rows(xr, nb, h.d, h.norm, h.gamma, h.beta, h.eps, xin, red, pre_w(h.gamma, h.d), pre_w(h.beta, h.d));
     return true;
   };
   o.ok = gemv_any<WT, NB, true>(hg, nb, r0, r1, xin, ep, prep, h.logits, h.vocab, h.last_max, o.best, c, NoSub{}) ? 1 : 0;
@@ -144,11 +144,14 @@ __global__ __launch_bounds__(kT) void ll_step_kernel(StepParams sp) {
             const bool fuse = !g.in_vec && g.nfold > 0 && g.folds[g.nfold - 1].post_w &&
                               (g.norm == XE_NORM_RMS1P || g.norm == XE_NORM_RMS);
             const int nplain = fuse ? g.nfold - 1 : g.nfold;
+            // norm gains read before the folds' polls
+            const bool plain_norm = !fuse && !g.in_vec;
+            const PreW gp = pre_w(plain_norm ? g.gamma : nullptr, g.k), bp = pre_w(plain_norm ? g.beta : nullptr, g.k);
             for (int f = 0; f < nplain && r; f++) r = fold(g.folds[f], nb, D, xr, xin, red, ep, c);
             if (r && fuse)
               r = fold_rms(g.folds[g.nfold - 1], nb, D, xr, xin, red, g.gamma, g.eps, g.norm == XE_NORM_RMS1P, ep, c);
             else if (r && g.in_vec) r = get(g.in, nb, g.k, xin, g.k, ep, c);
-            else if (r) norm_rows(xr, nb, g.k, g.norm, g.gamma, g.beta, g.eps, xin, red);
+            else if (r) norm_rows(xr, nb, g.k, g.norm, g.gamma, g.beta, g.eps, xin, red, gp, bp);
             mark_ready(step, i);
             return r;
           };
