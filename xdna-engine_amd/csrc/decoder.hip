@@ -318,6 +318,7 @@ struct xe_decoder {
     uint64_t *arena = nullptr;  // every exchange vector of the step
     ll::Vec arg{};
     int kin = 0, scratch = 0, nb_t = 1, grid = 0, hd = 64, g = 1;
+    int stage_bytes = 0;  // LDS weight stage (ll::StageLayout), 0: none staged
     size_t lds_bytes = 0;
     int head_lpr = 8, head_rpl = 2;
   };
@@ -991,6 +992,43 @@ void ll_tile(int m, int ranks, int k, bool geglu, int wdtype, int &lpr, int &rpl
   }
 }
 
+
+// Trace marks of one traced step: phase ends, 4 step marks, phase
+// input-ready times, kSubSlots sub-stage marks per phase.
+size_t ll_trace_slots(const xe_decoder::LLPlan &P) {
+  const size_t n = P.a.size() + P.f.size();
+  return 2 * n + 4 + ll::kSubSlots * n;
+}
+
+constexpr size_t kLLLds = 160 * 1024 - 2048;  // dynamic LDS of the step kernel (static LDS aside)
+
+// LDS weight staging (ll::StageLayout).  A GEMV phase whose input is an
+// exchange vector follows another phase of its role directly, so weights
+// it loads at its own start arrive only a memory round trip after that
+// phase: such a phase gets its slice copied into LDS at the start of an
+// earlier phase, the one after the role's previous staged phase (the stage
+// holds one slice at a time).  budget < 0: nothing staged.
+void plan_stage(std::vector<ll::Phase> &list, int ranks, int wt, long budget, int &stage_bytes) {
+  for (auto &ph : list) {
+    ph.issue = -1;
+    if (ph.kind == ll::LK_GEMV) ph.u.gemv.staged = 0;
+  }
+  int last = -1;  // the previous staged phase
+  for (int j = 0; j < static_cast<int>(list.size()); j++) {
+    if (list[j].kind != ll::LK_GEMV) continue;
+    ll::GemvD &g = list[j].u.gemv;
+    const int at = last + 1;
+    if (!g.in_vec || at >= j) continue;  // input from the previous phase; an earlier phase to ride on
+    const int unit = g.act == ACT_GEGLU_TANH ? 2 : 1;
+    const int rows = (g.m / unit + ranks - 1) / ranks * unit;
+    const int need = ll::stage_layout(wt, rows, g.k, g.bias != nullptr).total;
+    if (need > budget) continue;
+    g.staged = 1;
+    list[at].issue = j;
+    last = j;
+    stage_bytes = std::max(stage_bytes, need);
+  }
+}
 void build_ll_plan(xe_decoder *d, int B, xe_decoder::LLPlan &P) {
   const auto &c = d->c;
   const int D = c.d_model, F = c.ffn, hd = c.head_dim;
@@ -1234,18 +1272,33 @@ void build_ll_plan(xe_decoder *d, int B, xe_decoder::LLPlan &P) {
   }
   P.arg.p = P.arena + arg_off;
   P.arg.ld = arg_ld;
+
+  ll_tile(c.vocab, P.grid, D, false, c.wdtype, P.head_lpr, P.head_rpl);
+  // GEMV inputs padded (ll::xstride), attention q rows plain
+  P.kin = std::max(std::max(ll::xstride(D), ll::xstride(F)), std::max(ll::xstride(hq), nq));
+  // scratch: attention blocks, merge tables, argmax partials, and the norm
+  // gains of a GEMV input (up to 3 folds, gamma, beta: 5 regions)
+  P.scratch = std::max(std::max(ll::attn_scratch_floats(hd, g), ll::attn_scratch_floats(hd, 1)),
+                       std::max(ll::kMaxSplits * (ll::kDM + 2) + ll::kMaxSplits + 2, P.nb_t * 2 * P.grid));
+  P.scratch = std::max(P.scratch, 5 * ll::nw_floats(D)) + 16;
+  P.lds_bytes = sizeof(float) * (static_cast<size_t>(P.nb_t) * D + static_cast<size_t>(P.nb_t) * P.kin +
+                                 ((P.scratch + 3) & ~3));
+  if (P.lds_bytes > kLLLds) { P.why = "LDS need too large"; return; }
+  // the weight stage takes what LDS has left, a traced launch's marks kept
+  const long budget = static_cast<long>(kLLLds) - static_cast<long>(P.lds_bytes) -
+                      static_cast<long>(sizeof(uint64_t) * (ll_trace_slots(P) + 1));
+  P.stage_bytes = 0;
+  const char *st_env = std::getenv("XE_LL_STAGE");
+  const bool stage_on = !(st_env && std::string(st_env) == "0");
+  plan_stage(P.a, n_a, c.wdtype, stage_on ? budget : -1, P.stage_bytes);
+  plan_stage(P.f, n_f, c.wdtype, stage_on ? budget : -1, P.stage_bytes);
+  P.lds_bytes += static_cast<size_t>(P.stage_bytes);
+
   XE_HIP(hipMalloc(reinterpret_cast<void **>(&P.dev_a), std::max<size_t>(1, P.a.size()) * sizeof(ll::Phase)));
   XE_HIP(hipMalloc(reinterpret_cast<void **>(&P.dev_f), std::max<size_t>(1, P.f.size()) * sizeof(ll::Phase)));
   XE_HIP(hipMemcpyAsync(P.dev_a, P.a.data(), P.a.size() * sizeof(ll::Phase), hipMemcpyHostToDevice, d->s));
   XE_HIP(hipMemcpyAsync(P.dev_f, P.f.data(), P.f.size() * sizeof(ll::Phase), hipMemcpyHostToDevice, d->s));
   XE_HIP(hipStreamSynchronize(d->s));
-
-  ll_tile(c.vocab, P.grid, D, false, c.wdtype, P.head_lpr, P.head_rpl);
-  P.kin = std::max(std::max(D, F), std::max(hq, nq));
-  P.scratch = std::max(std::max(ll::attn_scratch_floats(hd, g), ll::attn_scratch_floats(hd, 1)),
-                       std::max(ll::kMaxSplits * (ll::kDM + 2) + ll::kMaxSplits + 2, P.nb_t * 2 * P.grid)) + 16;
-  P.lds_bytes = sizeof(float) * (static_cast<size_t>(P.nb_t) * D + static_cast<size_t>(P.nb_t) * P.kin + P.scratch);
-  if (P.lds_bytes > 160 * 1024 - 2048) { P.why = "LDS need too large"; return; }
   P.ok = true;
 }
 
@@ -1262,12 +1315,6 @@ constexpr int kLLChunk = 256;  // decode steps per low-latency launch
 // n_steps tokens in one launch.  forced: device [n_forced][B] input tokens of
 // the first steps (prompt feeding); logits: written for every step (the last
 // step's values remain).
-// Trace marks of one traced step: phase ends, 4 step marks, phase
-// input-ready times, kSubSlots sub-stage marks per phase.
-size_t ll_trace_slots(const xe_decoder::LLPlan &P) {
-  const size_t n = P.a.size() + P.f.size();
-  return 2 * n + 4 + ll::kSubSlots * n;
-}
 
 void run_ll(xe_decoder *d, int B, int n_steps, const int32_t *forced, int n_forced, bool want_logits,
             uint64_t *trace = nullptr) {
@@ -1316,6 +1363,7 @@ void run_ll(xe_decoder *d, int B, int n_steps, const int32_t *forced, int n_forc
   sp.limit = static_cast<uint64_t>(khz > 0 ? khz : 100000) * 50;  // 50 ms per wait
   sp.kin = P.kin;
   sp.scratch = P.scratch;
+  sp.stage_floats = P.stage_bytes / 4;
   sp.trace = trace;
   // a traced launch keeps its marks in LDS behind the scratch area
   sp.trace_slots = trace ? static_cast<int>(ll_trace_slots(P)) : 0;

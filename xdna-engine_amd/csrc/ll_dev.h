@@ -86,6 +86,9 @@ struct GemvD {
   // before the norm: the waits for earlier phases' outputs overlap the loads
   int nfold;
   FoldD folds[3];
+  // 1: this rank's weight slice (and epilogue constants) sits in the LDS
+  // stage area, copied there by an earlier phase (Phase::issue)
+  int staged;
 };
 
 struct AttnD {
@@ -114,7 +117,11 @@ struct MergeD {
 
 struct Phase {
   int kind;
-  int pad[3];
+  // >= 0: at this phase's start, copy the weight slice of GEMV phase `issue`
+  // (same role, staged) into the LDS stage area; its loads then complete
+  // while this phase waits for its input
+  int issue;
+  int pad[2];
   union {
     FoldD fold;
     GemvD gemv;
@@ -154,9 +161,11 @@ struct StepParams {
   unsigned ep0;  // epoch of step 0 (>= 1; buffers start at epoch 0)
   unsigned *status;
   uint64_t limit;  // wall-clock ticks a single wait may take
-  // LDS layout (floats): residual [nb][d] | input [nb][kin] | scratch
+  // LDS layout (floats): residual [nb][d] | input [nb][kin] | scratch |
+  // weight stage [stage_floats] | trace marks
   int kin;
   int scratch;
+  int stage_floats;
   // optional wall-clock trace of step 0: [trace_slots][grid] mark times
   // (phase ends, lm-head, argmax, embed, kernel start, phase input-ready,
   // phase sub-stages).  Marks go to LDS (after the scratch area) and are
@@ -203,12 +212,19 @@ __device__ __forceinline__ u32x4 ld_pairs(__amdgpu_buffer_rsrc_t rs, int off) {
   return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, gdev::kCoherentSc1));
 }
 
+// GEMV inputs in LDS: 16-element chunks at a 20-float stride, so the 16-byte
+// reads of one chunk by consecutive lanes (80 B apart) fall in distinct
+// banks; at the plain 64 B stride every fourth lane collides.
+__host__ __device__ constexpr int xstride(int n) { return n / 16 * 20; }
+__device__ __forceinline__ int xpad(int i) { return i + ((i >> 4) << 2); }
+
 // Read nb rows x n pairs (n even) of v into LDS dst[b * ldd + i], polling until
 // every epoch is ep.  All kT threads; ends with a barrier; WG-uniform result.
-template <typename V>
+// A round holds U 16-byte loads a thread (kT * U * 2 values); the rounds run
+// one after another.  pad: dst rows in the GEMV input layout (xpad).
+template <int U = 4, typename V>
 __device__ __forceinline__ bool get(const V &v, int nb, int n, float *dst, int ldd, unsigned ep,
-                                    const Ctl &c) {
-  constexpr int U = 4;
+                                    const Ctl &c, bool pad = false) {
   const int half = n >> 1;
   const int total = nb * half;
   const __amdgpu_buffer_rsrc_t rs = gdev::coherent_rsrc(v.p);
@@ -225,7 +241,7 @@ __device__ __forceinline__ bool get(const V &v, int nb, int n, float *dst, int l
       const int b = need[u] ? q / half : 0, j = need[u] ? q % half : 0;
       // an offset past the buffer range reads zeros: no divergent branch
       off[u] = need[u] ? (b * v.ld + 2 * j) * 8 : kNoRecord;
-      di[u] = b * ldd + 2 * j;
+      di[u] = b * ldd + (pad ? xpad(2 * j) : 2 * j);  // a pair never straddles a chunk
       val[u] = ld_pairs(rs, off[u]);
     }
     const uint64_t t0 = wall_clock64();
@@ -303,53 +319,52 @@ __device__ __forceinline__ void sums(float (&v)[N], float *red, int &slot) {
   gdev::block_sums<kW, N>(v, red, slot);
 }
 
-// A d-vector's weights (norm gains), elements threadIdx.x + kT t for t <
-// kPre, read into registers before the poll they follow: the weight stream
-// evicts them from the caches between layers, so a load issued after the
-// input arrives adds a memory round trip to the hand-off.  Elements past
-// kT kPre are read in place.
-constexpr int kPre = 4;
-struct PreW {
-  float v[kPre];
-};
-__device__ __forceinline__ PreW pre_w(const float *w, int d) {
-  PreW r;
-  const XE_GLOBAL float *g = gptr(w);
-#pragma unroll
-  for (int t = 0; t < kPre; t++) {
-    const int i = threadIdx.x + kT * t;
-    r.v[t] = w != nullptr && i < d ? g[i] : 0.f;
-  }
-  return r;
-}
-// body(i, w...) over this thread's elements i of a d-vector, with the
-// preloaded weights of each PreW (or the weight read in place past them).
-template <typename Body>
-__device__ __forceinline__ void each_w(int d, const PreW &a, const float *wa, Body body) {
-#pragma unroll
-  for (int t = 0; t < kPre; t++) {
-    const int i = threadIdx.x + kT * t;
-    if (i < d) body(i, a.v[t]);
-  }
-  for (int i = threadIdx.x + kT * kPre; i < d; i += kT) body(i, gptr(wa)[i]);
-}
-template <typename Body>
-__device__ __forceinline__ void each_w2(int d, const PreW &a, const float *wa, const PreW &b, const float *wb,
-                                        Body body) {
-#pragma unroll
-  for (int t = 0; t < kPre; t++) {
-    const int i = threadIdx.x + kT * t;
-    if (i < d) body(i, a.v[t], b.v[t]);
-  }
-  for (int i = threadIdx.x + kT * kPre; i < d; i += kT) body(i, gptr(wa)[i], gptr(wb)[i]);
+constexpr int kNontemporal = 2;  // cache-policy operand: nt (streamed once per step)
+
+// LDS-direct copies: kStageGran bytes a wave per load instruction.
+constexpr int kStageGran = 1024;
+__host__ __device__ inline int stage_pad(int bytes) { return (bytes + kStageGran - 1) / kStageGran * kStageGran; }
+
+// bytes [0, n) of src -> LDS dst, 16 bytes a lane, kStageGran a wave per
+// load; past n the loads return zeros (buffer range), so dst must hold
+// stage_pad(n) bytes.
+__device__ __forceinline__ void lds_copy(const void *src, int n, XE_LDS uint8_t *dst) {
+  const uint64_t a = reinterpret_cast<uint64_t>(src);
+  const uint64_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(a)));
+  const uint64_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(a >> 32)));
+  const __amdgpu_buffer_rsrc_t rs =
+      __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void *>(hi << 32 | lo), static_cast<short>(0), n, 0x00020000);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  for (int off = wave * kStageGran; off < n; off += kW * kStageGran)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, reinterpret_cast<XE_LDS void *>(dst + off), 16, lane * 16 + off, 0,
+                                             0, kNontemporal);
 }
 
+// Norm gains of a d-vector, copied into LDS (nw: stage_pad(4 d) bytes) by
+// LDS-direct loads issued before the poll they follow.  The weight stream
+// evicts them from the caches between layers, and values loaded into
+// registers before a poll are reloaded after it by the compiler (one memory
+// round trip each, on the hand-off's critical path); LDS copies are not.
+// Read them after nw_ready().
+__device__ __forceinline__ void pre_w(const float *w, int d, float *nw) {
+  if (w != nullptr) lds_copy(w, 4 * d, reinterpret_cast<XE_LDS uint8_t *>(lptr(nw)));
+}
+// Every wave's copies have landed (its loads, then the barrier).
+__device__ __forceinline__ void nw_ready() {
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+}
+// LDS floats one pre_w copy of a d-vector takes.
+__host__ __device__ inline int nw_floats(int d) { return stage_pad(4 * d) / 4; }
+
 // residual[b] += post(src[b]) for b < nb.  tmp: LDS [nb][d].
+// nw: the post-norm gain as pre_w copied it (issued by the caller).
 template <typename FD>
 __device__ __forceinline__ bool fold(const FD &f, int nb, int d, float *xr, float *tmp, float *red,
-                                     unsigned ep, const Ctl &c) {
-  const PreW pw = pre_w(f.post_w, d);
+                                     unsigned ep, const Ctl &c, const float *nw) {
   if (!get(f.src, nb, d, tmp, d, ep, c)) return false;
+  if (f.post_w) nw_ready();
+  const XE_LDS float *pw = lptr(nw);
   int slot = 0;
   for (int b = 0; b < nb; b++) {
     XE_LDS float *x = lptr(xr) + static_cast<size_t>(b) * d;
@@ -359,7 +374,7 @@ __device__ __forceinline__ bool fold(const FD &f, int nb, int d, float *xr, floa
       for (int i = threadIdx.x; i < d; i += kT) ss[0] = __builtin_fmaf(s[i], s[i], ss[0]);
       sums<1>(ss, red, slot);
       const float inv = 1.0f / sqrtf(ss[0] / static_cast<float>(d) + f.eps);
-      each_w(d, pw, f.post_w, [&](int i, float w) { x[i] = x[i] + s[i] * inv * (1.0f + w); });
+      for (int i = threadIdx.x; i < d; i += kT) x[i] = x[i] + s[i] * inv * (1.0f + pw[i]);
     } else {
       for (int i = threadIdx.x; i < d; i += kT) x[i] = x[i] + s[i];
     }
@@ -374,49 +389,61 @@ __device__ __forceinline__ bool fold(const FD &f, int nb, int d, float *xr, floa
 // so sum src^2, sum x^2, sum x s', sum s'^2 come out of one reduction (the
 // same algebra as the phase kernels' prologue).  residual[b] = t,
 // dst[b] = RMS(t) (1 + gamma) (rms1p) or RMS(t) gamma; src is read into dst.
+// dst rows are GEMV inputs (xstride / xpad layout).
+// nw: post_w then gamma as pre_w copied them (nw_floats(d) floats apart;
+// issued by the caller).
+__device__ __forceinline__ void fold_rms_rows(int nb, int d, float *xr, float *dst, float *red, float eps_s,
+                                              float eps, bool rms1p, const float *nw);
 template <typename FD>
 __device__ __forceinline__ bool fold_rms(const FD &f, int nb, int d, float *xr, float *dst, float *red,
-                                         const float *gamma, float eps, bool rms1p, unsigned ep, const Ctl &c) {
-  const PreW pw = pre_w(f.post_w, d), gm = pre_w(gamma, d);
-  if (!get(f.src, nb, d, dst, d, ep, c)) return false;
+                                         float eps, bool rms1p, unsigned ep, const Ctl &c, const float *nw) {
+  if (!get(f.src, nb, d, dst, xstride(d), ep, c, true)) return false;
+  nw_ready();
+  fold_rms_rows(nb, d, xr, dst, red, f.eps, eps, rms1p, nw);
+  return true;
+}
+// The arithmetic of fold_rms once src sits in dst (eps_s: the post norm's).
+__device__ __forceinline__ void fold_rms_rows(int nb, int d, float *xr, float *dst, float *red, float eps_s,
+                                              float eps, bool rms1p, const float *nw) {
+  const XE_LDS float *pw = lptr(nw), *gm = lptr(nw) + nw_floats(d);
   int slot = 0;
   const float fd = static_cast<float>(d);
   for (int b = 0; b < nb; b++) {
     XE_LDS float *x = lptr(xr) + static_cast<size_t>(b) * d;
-    XE_LDS float *h = lptr(dst) + static_cast<size_t>(b) * d;
+    XE_LDS float *h = lptr(dst) + static_cast<size_t>(b) * xstride(d);
     float acc[4] = {0.f, 0.f, 0.f, 0.f};
-    each_w(d, pw, f.post_w, [&](int i, float w) {
-      const float sv = h[i], xv = x[i];
-      const float spv = sv * (1.0f + w);
+    for (int i = threadIdx.x; i < d; i += kT) {
+      const float sv = h[xpad(i)], xv = x[i];
+      const float spv = sv * (1.0f + pw[i]);
       acc[0] = __builtin_fmaf(sv, sv, acc[0]);
       acc[1] = __builtin_fmaf(xv, xv, acc[1]);
       acc[2] = __builtin_fmaf(xv, spv, acc[2]);
       acc[3] = __builtin_fmaf(spv, spv, acc[3]);
-    });
+    }
     sums<4>(acc, red, slot);
-    const float inv_s = 1.0f / sqrtf(acc[0] / fd + f.eps);
+    const float inv_s = 1.0f / sqrtf(acc[0] / fd + eps_s);
     const float st2 = acc[1] + 2.0f * inv_s * acc[2] + inv_s * inv_s * acc[3];
     const float inv_t = 1.0f / sqrtf(fmaxf(st2, 0.f) / fd + eps);
-    each_w2(d, pw, f.post_w, gm, gamma, [&](int i, float w, float g) {
-      const float t = x[i] + h[i] * inv_s * (1.0f + w);
+    for (int i = threadIdx.x; i < d; i += kT) {
+      const float t = x[i] + h[xpad(i)] * inv_s * (1.0f + pw[i]);
       x[i] = t;
-      h[i] = rms1p ? t * inv_t * (1.0f + g) : t * inv_t * g;
-    });
+      h[xpad(i)] = rms1p ? t * inv_t * (1.0f + gm[i]) : t * inv_t * gm[i];
+    }
   }
   __syncthreads();
-  return true;
 }
 
-// dst[b] = norm(x[b]) (LayerNorm two-pass / RMS / RMS (1 + w) / copy); gp,
-// bp: gamma and beta as pre_w read them.
-__device__ __forceinline__ void norm_rows(const float *xr, int nb, int d, int norm, const float *gamma,
-                                          const float *beta, float eps, float *dst, float *red, const PreW &gp,
-                                          const PreW &bp) {
+// dst[b] = norm(x[b]) (LayerNorm two-pass / RMS / RMS (1 + w) / copy) as a
+// GEMV input (xstride / xpad layout); nw: gamma and beta as pre_w copied
+// them (2 nw_floats(d)), read after nw_ready().
+__device__ __forceinline__ void norm_rows(const float *xr, int nb, int d, int norm, float eps, float *dst, float *red,
+                                          const float *nw) {
   int slot = 0;
   const float fd = static_cast<float>(d);
+  const XE_LDS float *gam = lptr(nw), *bet = lptr(nw) + nw_floats(d);
   for (int b = 0; b < nb; b++) {
     const XE_LDS float *x = lptr(xr) + static_cast<size_t>(b) * d;
-    XE_LDS float *h = lptr(dst) + static_cast<size_t>(b) * d;
+    XE_LDS float *h = lptr(dst) + static_cast<size_t>(b) * xstride(d);
     if (norm == XE_NORM_LN) {
       float v1[1] = {0.f};
       for (int i = threadIdx.x; i < d; i += kT) v1[0] += x[i];
@@ -429,16 +456,16 @@ __device__ __forceinline__ void norm_rows(const float *xr, int nb, int d, int no
       }
       sums<1>(v2, red, slot);
       const float inv = 1.0f / sqrtf(v2[0] / fd + eps);
-      each_w2(d, gp, gamma, bp, beta, [&](int i, float g, float be) { h[i] = (x[i] - mean) * inv * g + be; });
+      for (int i = threadIdx.x; i < d; i += kT) h[xpad(i)] = (x[i] - mean) * inv * gam[i] + bet[i];
     } else if (norm == XE_NORM_RMS || norm == XE_NORM_RMS1P) {
       float v1[1] = {0.f};
       for (int i = threadIdx.x; i < d; i += kT) v1[0] = __builtin_fmaf(x[i], x[i], v1[0]);
       sums<1>(v1, red, slot);
       const float inv = 1.0f / sqrtf(v1[0] / fd + eps);
       const bool p1 = norm == XE_NORM_RMS1P;
-      each_w(d, gp, gamma, [&](int i, float g) { h[i] = x[i] * inv * (p1 ? 1.0f + g : g); });
+      for (int i = threadIdx.x; i < d; i += kT) h[xpad(i)] = x[i] * inv * (p1 ? 1.0f + gam[i] : gam[i]);
     } else {
-      for (int i = threadIdx.x; i < d; i += kT) h[i] = x[i];
+      for (int i = threadIdx.x; i < d; i += kT) h[xpad(i)] = x[i];
     }
   }
   __syncthreads();
@@ -509,7 +536,6 @@ struct Round {
 struct WRsrc {
   __amdgpu_buffer_rsrc_t w, e;
 };
-constexpr int kNontemporal = 2;  // cache-policy operand: nt (streamed once per step)
 
 template <int WT>
 __device__ __forceinline__ void load_chunk_buf(const WRsrc &rs, int row, int K, int c, bool valid, gdev::Chunk<WT> &out) {
@@ -529,10 +555,72 @@ __device__ __forceinline__ void load_chunk_buf(const WRsrc &rs, int row, int K, 
   }
 }
 
+// ---------------------------------------------------------------------------
+// LDS weight stage.  A staged GEMV phase's slice (this rank's rows [r0, r1))
+// is copied into LDS by LDS-direct buffer loads issued at the start of an
+// earlier phase of the role, so the phase itself finds its weights on chip
+// when its input arrives: its hand-off wait no longer includes a memory round
+// trip for weights issued after the previous phase.  Layout (bytes, each
+// part padded to kStageGran, the span one wave moves per load):
+// zero slot [kStageZero] | weights [rows][row bytes] | bfp16 exponents
+// [rows][k / 8] | scale [rows] | bias [rows].
+// ---------------------------------------------------------------------------
+constexpr int kStageZero = 64;  // zero slot at the stage's start (chunks not valid read it)
+
+struct StageLayout {
+  int w, e, s, b, total;  // byte offsets of the parts and the padded size
+};
+
+
+__host__ __device__ inline StageLayout stage_layout(int wt, int rows, int k, bool bias) {
+  StageLayout L;
+  const int rb = wt == XE_BF16 ? 2 * k : k;
+  L.w = kStageZero;
+  L.e = L.w + stage_pad(rows * rb);
+  L.s = L.e + (wt == XE_BFP16 ? stage_pad(rows * (k / 8)) : 0);
+  L.b = L.s + (wt == XE_I8 ? stage_pad(rows * 4) : 0);
+  L.total = L.b + (bias ? stage_pad(rows * 4) : 0);
+  return L;
+}
+
+// Issue the copies of GEMV g's rows [r0, r1) into the stage area.  The
+// caller has passed a block barrier since the stage's last reader.
+template <int WT, typename GD>
+__device__ __forceinline__ void stage_issue(const GD &g, int r0, int r1, float *stage) {
+  if (r1 <= r0) return;
+  const int rows = r1 - r0;
+  const StageLayout L = stage_layout(WT, rows, g.k, g.bias != nullptr);
+  XE_LDS uint8_t *st = reinterpret_cast<XE_LDS uint8_t *>(lptr(stage));
+  const int rb = WT == XE_BF16 ? 2 * g.k : g.k;
+  lds_copy(static_cast<const uint8_t *>(g.w) + static_cast<size_t>(r0) * rb, rows * rb, st + L.w);
+  if (WT == XE_BFP16) lds_copy(g.exps + static_cast<size_t>(r0) * (g.k / 8), rows * (g.k / 8), st + L.e);
+  if (WT == XE_I8) lds_copy(g.scale + r0, rows * 4, st + L.s);
+  if (g.bias) lds_copy(g.bias + r0, rows * 4, st + L.b);
+}
+
+// One weight chunk from the stage: rw = byte offset of the row's weights
+// (and re = of its exponents) within their parts; a chunk that is not valid
+// reads the stage's zero slot (a select on the address, so the data goes
+// straight into the registers the dot products read).
+template <int WT>
+__device__ __forceinline__ void load_chunk_lds(const XE_LDS uint8_t *st, const StageLayout &L, int rw, int re, int c,
+                                               bool valid, gdev::Chunk<WT> &out) {
+  auto u4 = [](u32x4 v) { return make_uint4(v.x, v.y, v.z, v.w); };
+  if constexpr (WT == XE_BF16) {
+    const XE_LDS u32x4 *p = reinterpret_cast<const XE_LDS u32x4 *>(st + (valid ? L.w + rw + c * 32 : 0));
+    out.lo = u4(p[0]);
+    out.hi = u4(p[1]);
+  } else {
+    out.q = u4(*reinterpret_cast<const XE_LDS u32x4 *>(st + (valid ? L.w + rw + c * 16 : 0)));
+    if constexpr (WT == XE_BFP16)
+      out.e = *reinterpret_cast<const XE_LDS uint16_t *>(st + (valid ? L.e + re + c * 2 : 0));
+  }
+}
+
 template <int WT, int NB, bool HEAD, typename GD, typename Prep, typename Sub>
 __device__ __forceinline__ bool gemv_rows(const GD &g, int nb, int r0, int r1, const float *xs, unsigned ep,
                                           Prep prep, float *logits, int vocab, int last_max, ArgBest &best,
-                                          Sub tsub) {
+                                          Sub tsub, const float *stage, bool staged) {
   using gdev::Chunk;
   using gdev::chunk_dot;
   constexpr int RPL = 2;
@@ -549,8 +637,16 @@ __device__ __forceinline__ bool gemv_rows(const GD &g, int nb, int r0, int r1, c
   WRsrc rs;
   rs.w = gdev::coherent_rsrc(g.w);
   rs.e = gdev::coherent_rsrc(WT == XE_BFP16 ? static_cast<const void *>(g.exps) : g.w);
+  const XE_LDS uint8_t *st = reinterpret_cast<const XE_LDS uint8_t *>(lptr(stage));
+  const StageLayout L = stage_layout(WT, r1 - r0, K, g.bias != nullptr);
   bool ok = true;
   if (ntiles == 0) return prep();
+  if (staged) {
+    ok = prep();
+    // every wave's stage copies have landed (its own loads, then the barrier)
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+  }
   for (int tile = 0; tile < ntiles && ok; tile++) {
     const int row0 = r0 + tile * rows_per_tile + wave * rows_per_wave + rg * RPL;
     bool row_ok[RPL];
@@ -560,6 +656,14 @@ __device__ __forceinline__ bool gemv_rows(const GD &g, int nb, int r0, int r1, c
       row[i] = row0 + i;
       row_ok[i] = row[i] < r1;
     }
+    // stage offsets of the rows (a row past the slice reads row 0, zeroed)
+    int rw[RPL], re[RPL];
+#pragma unroll
+    for (int i = 0; i < RPL; i++) {
+      const int lr = row_ok[i] ? row[i] - r0 : 0;
+      rw[i] = lr * (WT == XE_BF16 ? 2 * K : K);
+      re[i] = lr * (K / 8);
+    }
     float acc[NB][RPL];
     float rscale[RPL], rbias[RPL];
 #pragma unroll
@@ -568,22 +672,39 @@ __device__ __forceinline__ bool gemv_rows(const GD &g, int nb, int r0, int r1, c
       for (int i = 0; i < RPL; i++) acc[b][i] = 0.f;
     for (int it0 = 0; it0 < n_it && ok; it0 += NIT) {
       Chunk<WT> w[NIT][RPL];
+      // one branch around the whole round: inside a branch per chunk the
+      // compiler waits for each chunk's reads before the next
+      if (staged) {
 #pragma unroll
-      for (int u = 0; u < NIT; u++) {
-        const int cc = ((it0 + u) << lpr_log) + kl;
-        const bool valid = it0 + u < n_it && cc < nch;
+        for (int u = 0; u < NIT; u++) {
+          const int cc = ((it0 + u) << lpr_log) + kl;
+          const bool valid = it0 + u < n_it && cc < nch;
 #pragma unroll
-        for (int i = 0; i < RPL; i++) load_chunk_buf<WT>(rs, row[i], K, cc, valid && row_ok[i], w[u][i]);
+          for (int i = 0; i < RPL; i++) load_chunk_lds<WT>(st, L, rw[i], re[i], cc, valid && row_ok[i], w[u][i]);
+        }
+      } else {
+#pragma unroll
+        for (int u = 0; u < NIT; u++) {
+          const int cc = ((it0 + u) << lpr_log) + kl;
+          const bool valid = it0 + u < n_it && cc < nch;
+#pragma unroll
+          for (int i = 0; i < RPL; i++) load_chunk_buf<WT>(rs, row[i], K, cc, valid && row_ok[i], w[u][i]);
+        }
       }
       if (it0 == 0) {  // epilogue constants travel with the first round's loads
 #pragma unroll
         for (int i = 0; i < RPL; i++) {
           const int rr = row_ok[i] ? row[i] : r0;
-          rscale[i] = WT == XE_I8 ? gptr(g.scale)[rr] : 1.0f;
-          rbias[i] = g.bias ? gptr(g.bias)[rr] : 0.0f;
+          if (staged) {
+            rscale[i] = WT == XE_I8 ? reinterpret_cast<const XE_LDS float *>(st + L.s)[rr - r0] : 1.0f;
+            rbias[i] = g.bias ? reinterpret_cast<const XE_LDS float *>(st + L.b)[rr - r0] : 0.0f;
+          } else {
+            rscale[i] = WT == XE_I8 ? gptr(g.scale)[rr] : 1.0f;
+            rbias[i] = g.bias ? gptr(g.bias)[rr] : 0.0f;
+          }
         }
       }
-      if (tile == 0 && it0 == 0) ok = prep();
+      if (tile == 0 && it0 == 0 && !staged) ok = prep();
       if (!ok) break;
 #pragma unroll
       for (int u = 0; u < NIT; u++) {
@@ -595,7 +716,7 @@ __device__ __forceinline__ bool gemv_rows(const GD &g, int nb, int r0, int r1, c
               typedef float f32x4 __attribute__((ext_vector_type(4)));
               float4 xv[4];
               const XE_LDS f32x4 *xr =
-                  reinterpret_cast<const XE_LDS f32x4 *>(lptr(xs) + static_cast<size_t>(b) * K + cx * 16);
+                  reinterpret_cast<const XE_LDS f32x4 *>(lptr(xs) + static_cast<size_t>(b) * xstride(K) + cx * 20);
 #pragma unroll
               for (int j = 0; j < 4; j++) {
                 const f32x4 t = xr[j];
@@ -665,9 +786,10 @@ __device__ __forceinline__ bool gemv_rows(const GD &g, int nb, int r0, int r1, c
 template <int WT, int NB, bool HEAD, typename GD, typename Prep, typename Sub>
 __device__ __forceinline__ bool gemv_any(const GD &g, int nb, int r0, int r1, const float *xs, unsigned ep,
                                          Prep prep, float *logits, int vocab, int last_max, ArgBest &best,
-                                         const Ctl &c, Sub tsub) {
+                                         const Ctl &c, Sub tsub, const float *stage = nullptr,
+                                         bool staged = false) {
   (void)c;
-  return gemv_rows<WT, NB, HEAD>(g, nb, r0, r1, xs, ep, prep, logits, vocab, last_max, best, tsub);
+  return gemv_rows<WT, NB, HEAD>(g, nb, r0, r1, xs, ep, prep, logits, vocab, last_max, best, tsub, stage, staged);
 }
 struct NoSub {
   __device__ void operator()(int) const {}

@@ -54,7 +54,7 @@ struct HeadOut {
 
 template <int WT, int NB>
 __device__ __noinline__ HeadOut head_gemv(const HeadArgs h, int nb, int r0, int r1, float *xr, float *xin,
-                                          float *red, unsigned ep, const Ctl c) {
+                                          float *red, float *nw, unsigned ep, const Ctl c) {
   GemvD hg{};
   hg.w = h.w;
   hg.scale = h.scale;
@@ -69,8 +69,11 @@ __device__ __noinline__ HeadOut head_gemv(const HeadArgs h, int nb, int r0, int 
     o.best.v[b] = -INFINITY;
     o.best.i[b] = -1;
   }
+  pre_w(h.gamma, h.d, nw);
+  pre_w(h.beta, h.d, nw + nw_floats(h.d));
   auto prep = [&]() -> bool {
-    norm_rows(xr, nb, h.d, h.norm, h.gamma, h.beta, h.eps, xin, red, pre_w(h.gamma, h.d), pre_w(h.beta, h.d));
+    nw_ready();
+    norm_rows(xr, nb, h.d, h.norm, h.eps, xin, red, nw);
     return true;
   };
   o.ok = gemv_any<WT, NB, true>(hg, nb, r0, r1, xin, ep, prep, h.logits, h.vocab, h.last_max, o.best, c, NoSub{}) ? 1 : 0;
@@ -90,7 +93,8 @@ __global__ __launch_bounds__(kT) void ll_step_kernel(StepParams sp) {
   float *xr = lds;                                      // residual copy [nb][D]
   float *xin = lds + static_cast<size_t>(NB) * D;       // GEMV / attention input [nb][kin]
   float *scr = xin + static_cast<size_t>(NB) * sp.kin;  // scratch
-  uint64_t *tlds = reinterpret_cast<uint64_t *>(scr + ((sp.scratch + 1) & ~1));  // trace marks (traced launches)
+  float *stage = scr + ((sp.scratch + 3) & ~3);        // staged weight slices (16-byte aligned)
+  uint64_t *tlds = reinterpret_cast<uint64_t *>(stage + sp.stage_floats);  // trace marks (traced launches)
   const int grid = static_cast<int>(gridDim.x);
   const bool is_a = blockIdx.x % kRoleStride == 0;
   const int n_a = (grid + kRoleStride - 1) / kRoleStride;
@@ -100,6 +104,7 @@ __global__ __launch_bounds__(kT) void ll_step_kernel(StepParams sp) {
   const XE_CONST Phase *ph = cptr(is_a ? sp.ph_a : sp.ph_f);
   const int nph = is_a ? sp.n_a : sp.n_f;
   if (threadIdx.x == 0) bad = 0;
+  if (sp.stage_floats > 0 && threadIdx.x < kStageZero / 4) stage[threadIdx.x] = 0.f;  // never copied over
   if (sp.trace)  // slots a workgroup never marks read as 0
     for (int t = threadIdx.x; t < sp.trace_slots; t += kT) lptr(tlds)[t] = 0;
   if (threadIdx.x < nb) {
@@ -125,9 +130,18 @@ __global__ __launch_bounds__(kT) void ll_step_kernel(StepParams sp) {
     bool ok = true;
     for (int i = 0; i < nph && ok; i++) {
       const XE_CONST Phase &P = ph[i];
+      if (P.issue >= 0) {  // a later phase's weight slice into the stage
+        const XE_CONST GemvD &sg = ph[P.issue].u.gemv;
+        const int unit = sg.act == ACT_GEGLU_TANH ? 2 : 1;
+        int s0, s1;
+        rank_rows(sg.m / unit, rank, nranks, s0, s1);
+        __syncthreads();  // the stage's previous reader is done in every wave
+        stage_issue<WT>(sg, s0 * unit, s1 * unit, stage);
+      }
       switch (P.kind) {
         case LK_FOLD:
-          ok = fold(P.u.fold, nb, D, xr, xin, red, ep, c);
+          pre_w(P.u.fold.post_w, D, scr);
+          ok = fold(P.u.fold, nb, D, xr, xin, red, ep, c, scr);
           mark_ready(step, i);
           break;
         case LK_GEMV: {
@@ -144,19 +158,35 @@ __global__ __launch_bounds__(kT) void ll_step_kernel(StepParams sp) {
             const bool fuse = !g.in_vec && g.nfold > 0 && g.folds[g.nfold - 1].post_w &&
                               (g.norm == XE_NORM_RMS1P || g.norm == XE_NORM_RMS);
             const int nplain = fuse ? g.nfold - 1 : g.nfold;
-            // norm gains read before the folds' polls
-            const bool plain_norm = !fuse && !g.in_vec;
-            const PreW gp = pre_w(plain_norm ? g.gamma : nullptr, g.k), bp = pre_w(plain_norm ? g.beta : nullptr, g.k);
-            for (int f = 0; f < nplain && r; f++) r = fold(g.folds[f], nb, D, xr, xin, red, ep, c);
+            // the gains of every fold and of the norm go to LDS before the
+            // first poll: fold f's post gain in region f, then gamma (and
+            // beta) (regions of nw_floats(D) floats in the scratch area)
+            const int nwf = nw_floats(D);
+            for (int f = 0; f < g.nfold; f++) pre_w(g.folds[f].post_w, D, scr + f * nwf);
+            if (!g.in_vec) {
+              pre_w(g.gamma, D, scr + g.nfold * nwf);
+              if (!fuse) pre_w(g.beta, D, scr + (g.nfold + 1) * nwf);
+            }
+            for (int f = 0; f < nplain && r; f++) r = fold(g.folds[f], nb, D, xr, xin, red, ep, c, scr + f * nwf);
             if (r && fuse)
-              r = fold_rms(g.folds[g.nfold - 1], nb, D, xr, xin, red, g.gamma, g.eps, g.norm == XE_NORM_RMS1P, ep, c);
-            else if (r && g.in_vec) r = get(g.in, nb, g.k, xin, g.k, ep, c);
-            else if (r) norm_rows(xr, nb, g.k, g.norm, g.gamma, g.beta, g.eps, xin, red, gp, bp);
+              r = fold_rms(g.folds[g.nfold - 1], nb, D, xr, xin, red, g.eps, g.norm == XE_NORM_RMS1P, ep, c,
+                           scr + (g.nfold - 1) * nwf);
+            else if (r && g.in_vec) {
+              // one round of loads covers the whole input up to kT * 8 pairs
+              // (a second round waits for the first to complete)
+              if (nb * g.k > kT * 8) r = get<8>(g.in, nb, g.k, xin, xstride(g.k), ep, c, true);
+              else r = get(g.in, nb, g.k, xin, xstride(g.k), ep, c, true);
+            }
+            else if (r) {
+              nw_ready();
+              norm_rows(xr, nb, g.k, g.norm, g.eps, xin, red, scr + g.nfold * nwf);
+            }
             mark_ready(step, i);
             return r;
           };
           auto tsub = [&](int sub) { mark(step, tslots + 4 + sp.n_a + sp.n_f + kSubSlots * ((is_a ? 0 : sp.n_a) + i) + sub); };
-          ok = gemv_any<WT, NB, false>(g, nb, r0, r1, xin, ep, prep, nullptr, 0, 0, none, c, tsub);
+          ok = gemv_any<WT, NB, false>(g, nb, r0, r1, xin, ep, prep, nullptr, 0, 0, none, c, tsub, stage,
+                                       g.staged != 0);
           break;
         }
         case LK_ATTN: {
@@ -214,7 +244,7 @@ __global__ __launch_bounds__(kT) void ll_step_kernel(StepParams sp) {
       rank_rows(sp.vocab, static_cast<int>(blockIdx.x), grid, r0, r1);
       const HeadArgs ha{sp.emb, sp.emb_scale, sp.emb_exps, sp.head_gamma, sp.head_beta, sp.logits,
                         sp.vocab, sp.d, sp.head_lpr, sp.head_rpl, sp.head_norm, sp.last_max, sp.head_eps};
-      const HeadOut ho = head_gemv<WT, NB>(ha, nb, r0, r1, xr, xin, red, ep, c);
+      const HeadOut ho = head_gemv<WT, NB>(ha, nb, r0, r1, xr, xin, red, scr, ep, c);
       ok = ho.ok != 0;
       best = ho.best;
     }
