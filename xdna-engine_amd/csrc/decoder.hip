@@ -317,8 +317,9 @@ struct xe_decoder {
     ll::Phase *dev_a = nullptr, *dev_f = nullptr;
     uint64_t *arena = nullptr;  // every exchange vector of the step
     ll::Vec arg{};
-    int kin = 0, scratch = 0, nb_t = 1, grid = 0, hd = 64, g = 1;
-    int stage_bytes = 0;  // LDS weight stage (ll::StageLayout), 0: none staged
+    int kin_a = 0, kin_f = 0, scratch = 0, nb_t = 1, grid = 0, hd = 64, g = 1;
+    int stage_a = 0, stage_f = 0;  // LDS weight stage bytes per role (ll::StageLayout), 0: none staged
+    int kv_floats = 0;             // LDS key/value stage (attention side), 0: none
     size_t lds_bytes = 0;
     int head_lpr = 8, head_rpl = 2;
   };
@@ -1002,6 +1003,30 @@ size_t ll_trace_slots(const xe_decoder::LLPlan &P) {
 
 constexpr size_t kLLLds = 160 * 1024 - 2048;  // dynamic LDS of the step kernel (static LDS aside)
 
+// Key/value staging (ll::kv_stage_issue): each attention phase's blocks of
+// up to kv_cap keys (one round at most) are copied into LDS at the start of
+// the phase before it, which on the attention side waits for its own input
+// long enough for the copies to land.  kv_cap covers the longest block the
+// cache allows, or the most keys budget (bytes, < 0: none) leaves room for
+// (a multiple of the key tile); longer blocks load their keys as before.
+// Returns the stage's floats.
+int plan_kv_stage(std::vector<ll::Phase> &list, int hd, int max_ctx, long budget) {
+  int floats = 0;
+  for (int j = 1; j < static_cast<int>(list.size()); j++) {
+    if (list[j].kind != ll::LK_ATTN) continue;
+    ll::AttnD &a = list[j].u.attn;
+    int chunk, nsplits;
+    ll::ll_split(a.fixed_len > 0 ? a.fixed_len : max_ctx, a.max_splits, hd, chunk, nsplits);
+    int cap = std::min(chunk, ll::kRoundKeys);
+    while (cap > 0 && 4L * ll::kv_stage_floats(hd, cap) > budget) cap -= ll::kKeyTile;
+    a.kv_cap = std::max(cap, 0);
+    if (a.kv_cap == 0) continue;
+    list[j - 1].kv_issue = j;
+    floats = std::max(floats, ll::kv_stage_floats(hd, a.kv_cap));
+  }
+  return floats;
+}
+
 // LDS weight staging (ll::StageLayout).  A GEMV phase whose input is an
 // exchange vector follows another phase of its role directly, so weights
 // it loads at its own start arrive only a memory round trip after that
@@ -1011,7 +1036,9 @@ constexpr size_t kLLLds = 160 * 1024 - 2048;  // dynamic LDS of the step kernel 
 void plan_stage(std::vector<ll::Phase> &list, int ranks, int wt, long budget, int &stage_bytes) {
   for (auto &ph : list) {
     ph.issue = -1;
+    ph.kv_issue = -1;
     if (ph.kind == ll::LK_GEMV) ph.u.gemv.staged = 0;
+    if (ph.kind == ll::LK_ATTN) ph.u.attn.kv_cap = 0;
   }
   int last = -1;  // the previous staged phase
   for (int j = 0; j < static_cast<int>(list.size()); j++) {
@@ -1274,25 +1301,35 @@ void build_ll_plan(xe_decoder *d, int B, xe_decoder::LLPlan &P) {
   P.arg.ld = arg_ld;
 
   ll_tile(c.vocab, P.grid, D, false, c.wdtype, P.head_lpr, P.head_rpl);
-  // GEMV inputs padded (ll::xstride), attention q rows plain
-  P.kin = std::max(std::max(ll::xstride(D), ll::xstride(F)), std::max(ll::xstride(hq), nq));
+  // inputs per role (GEMV inputs padded, ll::xstride; attention q rows and
+  // fold sources plain): A holds QKV / O / cross-attention inputs and q rows,
+  // F the FFN inputs
+  P.kin_a = std::max(std::max(ll::xstride(D), ll::xstride(hq)), std::max(nq, D));
+  P.kin_f = std::max(ll::xstride(D), ll::xstride(F));
   // scratch: attention blocks, merge tables, argmax partials, and the norm
   // gains of a GEMV input (up to 3 folds, gamma, beta: 5 regions)
   P.scratch = std::max(std::max(ll::attn_scratch_floats(hd, g), ll::attn_scratch_floats(hd, 1)),
                        std::max(ll::kMaxSplits * (ll::kDM + 2) + ll::kMaxSplits + 2, P.nb_t * 2 * P.grid));
   P.scratch = std::max(P.scratch, 5 * ll::nw_floats(D)) + 16;
-  P.lds_bytes = sizeof(float) * (static_cast<size_t>(P.nb_t) * D + static_cast<size_t>(P.nb_t) * P.kin +
-                                 ((P.scratch + 3) & ~3));
-  if (P.lds_bytes > kLLLds) { P.why = "LDS need too large"; return; }
-  // the weight stage takes what LDS has left, a traced launch's marks kept
-  const long budget = static_cast<long>(kLLLds) - static_cast<long>(P.lds_bytes) -
-                      static_cast<long>(sizeof(uint64_t) * (ll_trace_slots(P) + 1));
-  P.stage_bytes = 0;
+  auto base = [&](int kin) {
+    return static_cast<long>(sizeof(float)) *
+           (static_cast<long>(P.nb_t) * D + static_cast<long>(P.nb_t) * kin + ((P.scratch + 3) & ~3));
+  };
+  const long base_a = base(P.kin_a), base_f = base(P.kin_f);
+  const long trace_res = static_cast<long>(sizeof(uint64_t) * (ll_trace_slots(P) + 1));  // a traced launch's marks
+  if (std::max(base_a, base_f) + trace_res > static_cast<long>(kLLLds)) { P.why = "LDS need too large"; return; }
+  // the weight stages take what each role's LDS has left
   const char *st_env = std::getenv("XE_LL_STAGE");
   const bool stage_on = !(st_env && std::string(st_env) == "0");
-  plan_stage(P.a, n_a, c.wdtype, stage_on ? budget : -1, P.stage_bytes);
-  plan_stage(P.f, n_f, c.wdtype, stage_on ? budget : -1, P.stage_bytes);
-  P.lds_bytes += static_cast<size_t>(P.stage_bytes);
+  P.stage_a = P.stage_f = 0;
+  plan_stage(P.a, n_a, c.wdtype, stage_on ? static_cast<long>(kLLLds) - base_a - trace_res : -1, P.stage_a);
+  plan_stage(P.f, n_f, c.wdtype, stage_on ? static_cast<long>(kLLLds) - base_f - trace_res : -1, P.stage_f);
+  // then the attention side's key/value stage
+  const char *kv_env = std::getenv("XE_LL_KV");
+  const bool kv_on = !(kv_env && std::string(kv_env) == "0");
+  P.kv_floats = plan_kv_stage(P.a, hd, c.max_ctx,
+                              kv_on ? static_cast<long>(kLLLds) - base_a - P.stage_a - trace_res : -1);
+  P.lds_bytes = static_cast<size_t>(std::max(base_a + P.stage_a + 4L * P.kv_floats, base_f + P.stage_f));
 
   XE_HIP(hipMalloc(reinterpret_cast<void **>(&P.dev_a), std::max<size_t>(1, P.a.size()) * sizeof(ll::Phase)));
   XE_HIP(hipMalloc(reinterpret_cast<void **>(&P.dev_f), std::max<size_t>(1, P.f.size()) * sizeof(ll::Phase)));
@@ -1361,9 +1398,12 @@ void run_ll(xe_decoder *d, int B, int n_steps, const int32_t *forced, int n_forc
   int khz = 0;
   XE_HIP(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, d->dev->ordinal));
   sp.limit = static_cast<uint64_t>(khz > 0 ? khz : 100000) * 50;  // 50 ms per wait
-  sp.kin = P.kin;
+  sp.kin_a = P.kin_a;
+  sp.kin_f = P.kin_f;
   sp.scratch = P.scratch;
-  sp.stage_floats = P.stage_bytes / 4;
+  sp.stage_a = P.stage_a / 4;
+  sp.stage_f = P.stage_f / 4;
+  sp.kv_floats = P.kv_floats;
   sp.trace = trace;
   // a traced launch keeps its marks in LDS behind the scratch area
   sp.trace_slots = trace ? static_cast<int>(ll_trace_slots(P)) : 0;

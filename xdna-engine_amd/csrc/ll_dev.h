@@ -107,6 +107,10 @@ struct AttnD {
   const float *rope_cos, *rope_sin;
   int max_splits;
   Vec part;        // row b: [hq][max_splits][hd + 2] = (m, l, acc[hd])
+  // keys of a block the LDS key/value stage holds (0: none): a block of at
+  // most kv_cap keys has its rows and head constants copied into LDS by the
+  // phase before (Phase::kv_issue)
+  int kv_cap;
 };
 
 struct MergeD {
@@ -121,7 +125,11 @@ struct Phase {
   // (same role, staged) into the LDS stage area; its loads then complete
   // while this phase waits for its input
   int issue;
-  int pad[2];
+  // >= 0: at this phase's start, copy the key/value rows and head constants
+  // of attention phase `kv_issue` (this rank's first block) into the LDS
+  // key/value stage
+  int kv_issue;
+  int pad;
   union {
     FoldD fold;
     GemvD gemv;
@@ -161,11 +169,13 @@ struct StepParams {
   unsigned ep0;  // epoch of step 0 (>= 1; buffers start at epoch 0)
   unsigned *status;
   uint64_t limit;  // wall-clock ticks a single wait may take
-  // LDS layout (floats): residual [nb][d] | input [nb][kin] | scratch |
-  // weight stage [stage_floats] | trace marks
-  int kin;
+  // LDS layout (floats) of a role (A: attention side, F: FFN side):
+  // residual [nb][d] | input [nb][kin] | scratch | weight stage [stage] |
+  // key/value stage [kv_floats] (A) | trace marks
+  int kin_a, kin_f;
   int scratch;
-  int stage_floats;
+  int stage_a, stage_f;
+  int kv_floats;
   // optional wall-clock trace of step 0: [trace_slots][grid] mark times
   // (phase ends, lm-head, argmax, embed, kernel start, phase input-ready,
   // phase sub-stages).  Marks go to LDS (after the scratch area) and are
@@ -838,6 +848,25 @@ __device__ __forceinline__ void load_head_consts(const AD &a, int posi, HeadCons
   }
 }
 
+// The same constants from the key/value stage (after its copies landed).
+template <int HD, typename AD>
+__device__ __forceinline__ void load_head_consts_lds(const AD &a, const float *kvs, HeadConsts<HD> &hc) {
+  constexpr int HALF = HeadConsts<HD>::HALF, PER = HeadConsts<HD>::PER;
+  constexpr int SLOT = kStageGran / 4;
+  const XE_LDS float *k = lptr(kvs);
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int i = 0; i < PER; i++) {
+    const int j = min(lane + 64 * i, HALF - 1);
+    hc.qn0[i] = a.q_norm_w ? k[j] : 0.f;
+    hc.qn1[i] = a.q_norm_w ? k[j + HALF] : 0.f;
+    hc.kn0[i] = a.k_norm_w ? k[SLOT + j] : 0.f;
+    hc.kn1[i] = a.k_norm_w ? k[SLOT + j + HALF] : 0.f;
+    hc.cs[i] = a.rope_cos ? k[2 * SLOT + j] : 1.f;
+    hc.sn[i] = a.rope_sin ? k[3 * SLOT + j] : 0.f;
+  }
+}
+
 // Per-head RMSNorm (1 + w) and RoPE of one head vector (LDS src; out(d, y)
 // takes dim d's result), one wave; rotate-half pairing
 // (npu-asr-host/src/lib.rs:143-185).
@@ -899,6 +928,71 @@ __host__ __device__ __forceinline__ void ll_split(int len, int max_splits, int h
 // Keys one round of a block covers (one Q.K tile per wave).
 constexpr int kRoundKeys = kW * kKeyTile;
 
+// ---------------------------------------------------------------------------
+// Key/value stage (attention side).  The phase before an attention phase
+// copies this rank's block into LDS with LDS-direct loads: q and k norm
+// gains, the RoPE cos / sin rows at the position (one kStageGran slot each),
+// then the block's key rows and value rows, each row padded by 16 bytes so
+// the 16 Q.K lanes of a fragment (16 keys at one offset) fall in distinct
+// banks.  When the attention phase polls for q nothing else is in flight
+// (vector memory completes in issue order, so loads issued at the phase's
+// start would hold the poll back by their memory latency).
+// ---------------------------------------------------------------------------
+__host__ __device__ inline int kv_row_bytes(int hd) { return 2 * hd + 16; }
+__host__ __device__ inline int kv_stage_floats(int hd, int cap) {
+  return (4 * kStageGran + 2 * cap * kv_row_bytes(hd)) / 4;
+}
+
+// Whether block `split` at length len is one the key/value stage holds (the
+// issuing phase and the attention phase decide alike).
+template <typename AD>
+__host__ __device__ inline bool kv_staged(const AD &a, int split, int len) {
+  if (a.kv_cap <= 0) return false;
+  int chunk, nsplits;
+  ll_split(len, a.max_splits, a.hd, chunk, nsplits);
+  return split < nsplits && chunk <= a.kv_cap;
+}
+
+// One row of hd bf16 (row r of src) into LDS dst: lanes below hd / 8 move
+// 16 bytes each.  Wave-uniform row.
+__device__ __forceinline__ void lds_copy_row(__amdgpu_buffer_rsrc_t rs, int src_off, int bytes, XE_LDS uint8_t *dst) {
+  const int lane = threadIdx.x & 63;
+  if (lane * 16 < bytes)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, reinterpret_cast<XE_LDS void *>(dst), 16, src_off + lane * 16, 0, 0,
+                                             gdev::kCoherentSc1);
+}
+
+// Issue the copies of attention block (split, kvh, b) at length len into the
+// key/value stage kvs.  The caller has passed a block barrier since the
+// stage's last reader.  Rows past the cache's current end are copied too
+// (the new row is patched in from LDS; later ones are masked).
+template <int HD, typename AD>
+__device__ __forceinline__ void kv_stage_issue(const AD &a, int split, int kvh, int b, int len, float *kvs) {
+  constexpr int HALF = HD / 2;
+  XE_LDS uint8_t *kb = reinterpret_cast<XE_LDS uint8_t *>(lptr(kvs));
+  const int posi = a.fixed_len > 0 ? 0 : len - 1;
+  if (a.q_norm_w != nullptr) lds_copy(a.q_norm_w, 4 * HD, kb);
+  if (a.k_norm_w != nullptr) lds_copy(a.k_norm_w, 4 * HD, kb + kStageGran);
+  if (a.rope_cos != nullptr) {
+    lds_copy(a.rope_cos + static_cast<size_t>(posi) * HALF, 4 * HALF, kb + 2 * kStageGran);
+    lds_copy(a.rope_sin + static_cast<size_t>(posi) * HALF, 4 * HALF, kb + 3 * kStageGran);
+  }
+  int chunk, nsplits;
+  ll_split(len, a.max_splits, HD, chunk, nsplits);
+  const int s0 = split * chunk, s1 = min(len, s0 + chunk);
+  const uint16_t *kbase = a.kc + a.kv_bstride * b + static_cast<size_t>(kvh) * a.max_ctx * HD;
+  const uint16_t *vbase = a.vc + a.kv_bstride * b + static_cast<size_t>(kvh) * a.max_ctx * HD;
+  const __amdgpu_buffer_rsrc_t krs = gdev::coherent_rsrc(kbase);
+  const __amdgpu_buffer_rsrc_t vrs = gdev::coherent_rsrc(vbase);
+  XE_LDS uint8_t *kk = kb + 4 * kStageGran;
+  XE_LDS uint8_t *vv = kk + a.kv_cap * kv_row_bytes(HD);
+  for (int r = threadIdx.x >> 6; r < s1 - s0; r += kW) {
+    lds_copy_row(krs, (s0 + r) * HD * 2, HD * 2, kk + r * kv_row_bytes(HD));
+    lds_copy_row(vrs, (s0 + r) * HD * 2, HD * 2, vv + r * kv_row_bytes(HD));
+  }
+}
+
+
 // LDS scratch of a block (floats): new key [hd] | new key and value as
 // stored (bf16 pairs) [hd] | scores / probabilities [kRoundKeys][g] | running
 // max, sum, correction [3][16] | Q.K B operands [hd / 32][64 lanes][8 bf16] |
@@ -937,7 +1031,8 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 // query head, m in log2 units of the scaled score.
 template <int HD, int G, typename AD, typename Prep, typename Sub>
 __device__ __forceinline__ bool attn_block(const AD &a, int split, int kvh, int b, int len, const float *qin,
-                                           float *scr, unsigned ep, Prep prep, Sub tsub) {
+                                           float *scr, unsigned ep, Prep prep, Sub tsub, const float *kvs,
+                                           bool staged) {
   static_assert(HD % 32 == 0 && HD <= 256 && 3 * G <= 16, "attention tile shape");
   constexpr int NJ = HD / 32;                  // MFMA steps per tile
   constexpr int LPK = HD / 4;                  // P.V lanes per key
@@ -980,14 +1075,37 @@ __device__ __forceinline__ bool attn_block(const AD &a, int split, int kvh, int 
       vf[i] = ld_kv8(vrs, kv < s1 ? (kv * HD + pv_dim) * 2 : kNoRecord);
     }
   };
-  load_round(s0);
   HeadConsts<HD> hc;
-  load_head_consts<HD>(a, a.fixed_len > 0 ? 0 : posi, hc);
+  if (!staged) {
+    load_round(s0);
+    load_head_consts<HD>(a, a.fixed_len > 0 ? 0 : posi, hc);
+  }
   if (threadIdx.x < 16) {
     st[threadIdx.x] = -INFINITY;
     st[16 + threadIdx.x] = 0.f;
   }
   if (!prep()) return false;
+  if (staged) {
+    // the stage's copies have landed in every wave (its loads, the barrier);
+    // rows past the block read its last row (K: masked scores; V: zeroed)
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    const XE_LDS uint8_t *kk = reinterpret_cast<const XE_LDS uint8_t *>(lptr(kvs)) + 4 * kStageGran;
+    const XE_LDS uint8_t *vv = kk + a.kv_cap * kv_row_bytes(HD);
+    const int last = s1 - s0 - 1;
+    const int kq = min(wave * kKeyTile + qk_row, last);
+#pragma unroll
+    for (int j = 0; j < NJ; j++)
+      kf[j] = *reinterpret_cast<const XE_LDS u32x4 *>(kk + kq * kv_row_bytes(HD) + (32 * j + qk_dim) * 2);
+#pragma unroll
+    for (int i = 0; i < PVK; i++) {
+      const int kv = (i * kW + wave) * KPI + pv_slot;
+      const u32x2 v = *reinterpret_cast<const XE_LDS u32x2 *>(vv + min(kv, last) * kv_row_bytes(HD) + pv_dim * 2);
+      vf[i].x = kv <= last ? v.x : 0u;
+      vf[i].y = kv <= last ? v.y : 0u;
+    }
+    load_head_consts_lds<HD>(a, kvs, hc);
+  }
 
   const XE_LDS float *qrow = lptr(qin) + static_cast<size_t>(b) * a.qn;
   const XE_LDS float *vsrc = qrow + a.v_off + kvh * HD;

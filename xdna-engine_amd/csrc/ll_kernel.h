@@ -90,13 +90,16 @@ __global__ __launch_bounds__(kT) void ll_step_kernel(StepParams sp) {
   __shared__ int s_bi[kW][kMaxNB];
   float *lds = reinterpret_cast<float *>(lds4);
   const int nb = sp.nb, D = sp.d;
-  float *xr = lds;                                      // residual copy [nb][D]
-  float *xin = lds + static_cast<size_t>(NB) * D;       // GEMV / attention input [nb][kin]
-  float *scr = xin + static_cast<size_t>(NB) * sp.kin;  // scratch
-  float *stage = scr + ((sp.scratch + 3) & ~3);        // staged weight slices (16-byte aligned)
-  uint64_t *tlds = reinterpret_cast<uint64_t *>(stage + sp.stage_floats);  // trace marks (traced launches)
   const int grid = static_cast<int>(gridDim.x);
   const bool is_a = blockIdx.x % kRoleStride == 0;
+  // the role's LDS layout (floats; every part 16-byte aligned)
+  const int kin = is_a ? sp.kin_a : sp.kin_f, stage_floats = is_a ? sp.stage_a : sp.stage_f;
+  float *xr = lds;                                     // residual copy [nb][D]
+  float *xin = lds + static_cast<size_t>(NB) * D;      // GEMV / attention input [nb][kin]
+  float *scr = xin + static_cast<size_t>(NB) * kin;    // scratch
+  float *stage = scr + ((sp.scratch + 3) & ~3);       // staged weight slices
+  float *kvs = stage + stage_floats;                   // key/value stage (attention side)
+  uint64_t *tlds = reinterpret_cast<uint64_t *>(kvs + (is_a ? sp.kv_floats : 0));  // trace marks (traced launches)
   const int n_a = (grid + kRoleStride - 1) / kRoleStride;
   const int rank = is_a ? static_cast<int>(blockIdx.x) / kRoleStride
                         : static_cast<int>(blockIdx.x) - static_cast<int>(blockIdx.x) / kRoleStride - 1;
@@ -104,7 +107,7 @@ __global__ __launch_bounds__(kT) void ll_step_kernel(StepParams sp) {
   const XE_CONST Phase *ph = cptr(is_a ? sp.ph_a : sp.ph_f);
   const int nph = is_a ? sp.n_a : sp.n_f;
   if (threadIdx.x == 0) bad = 0;
-  if (sp.stage_floats > 0 && threadIdx.x < kStageZero / 4) stage[threadIdx.x] = 0.f;  // never copied over
+  if (stage_floats > 0 && threadIdx.x < kStageZero / 4) stage[threadIdx.x] = 0.f;  // never copied over
   if (sp.trace)  // slots a workgroup never marks read as 0
     for (int t = threadIdx.x; t < sp.trace_slots; t += kT) lptr(tlds)[t] = 0;
   if (threadIdx.x < nb) {
@@ -130,13 +133,22 @@ __global__ __launch_bounds__(kT) void ll_step_kernel(StepParams sp) {
     bool ok = true;
     for (int i = 0; i < nph && ok; i++) {
       const XE_CONST Phase &P = ph[i];
+      if (P.issue >= 0 || P.kv_issue >= 0) __syncthreads();  // the stages' previous readers are done
       if (P.issue >= 0) {  // a later phase's weight slice into the stage
         const XE_CONST GemvD &sg = ph[P.issue].u.gemv;
         const int unit = sg.act == ACT_GEGLU_TANH ? 2 : 1;
         int s0, s1;
         rank_rows(sg.m / unit, rank, nranks, s0, s1);
-        __syncthreads();  // the stage's previous reader is done in every wave
         stage_issue<WT>(sg, s0 * unit, s1 * unit, stage);
+      }
+      if (P.kv_issue >= 0) {  // the next attention block's keys / values into the key/value stage
+        const XE_CONST AttnD &ka = ph[P.kv_issue].u.attn;
+        const int split = rank % ka.max_splits, rest = rank / ka.max_splits;
+        const int kvh = rest % ka.hkv, b = rest / ka.hkv;
+        if (b < nb) {
+          const int len = ka.fixed_len > 0 ? ka.fixed_len : s_pos[b] + 1;
+          if (kv_staged(ka, split, len)) kv_stage_issue<HD>(ka, split, kvh, b, len, kvs);
+        }
       }
       switch (P.kind) {
         case LK_FOLD:
@@ -211,7 +223,9 @@ __global__ __launch_bounds__(kT) void ll_step_kernel(StepParams sp) {
             // sub-stage trace: input ready, q/k staged, keys done
             auto tsub = [&](int sub) { mark(step, tslots + 4 + sp.n_a + sp.n_f + kSubSlots * ((is_a ? 0 : sp.n_a) + i) + sub); };
             // every attention phase of a plan has group G (host checks)
-            ok = attn_block<HD, G>(a, split, kvh, b, len, xin, scr, ep, prep, tsub);
+            // this rank's first block may sit in the key/value stage
+            const bool staged = vb == rank && kv_staged(a, split, len);
+            ok = attn_block<HD, G>(a, split, kvh, b, len, xin, scr, ep, prep, tsub, kvs, staged);
           }
           break;
         }
