@@ -89,6 +89,9 @@ struct GemvD {
   // 1: this rank's weight slice (and epilogue constants) sits in the LDS
   // stage area, copied there by an earlier phase (Phase::issue)
   int staged;
+  // the waves split K into 1 << ks_log segments (rows the rank holds too few
+  // to keep every wave busy); their partial sums meet in LDS
+  int ks_log;
 };
 
 struct AttnD {
@@ -627,22 +630,70 @@ __device__ __forceinline__ void load_chunk_lds(const XE_LDS uint8_t *st, const S
   }
 }
 
+// a[j] += dot(chunk elements 4 j .. 4 j + 3, x): four independent chains
+// (bfp16: one per exponent half), so consecutive FMAs do not wait on each
+// other.
+template <int WT>
+__device__ __forceinline__ void chunk_dot4(const gdev::Chunk<WT> &ch, const float4 (&xv)[4], float (&a)[4]) {
+  using gdev::sb;
+  if constexpr (WT == XE_I8) {
+    const uint32_t w4[4] = {ch.q.x, ch.q.y, ch.q.z, ch.q.w};
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      a[j] = __builtin_fmaf(xv[j].x, sb(w4[j], 0), a[j]);
+      a[j] = __builtin_fmaf(xv[j].y, sb(w4[j], 1), a[j]);
+      a[j] = __builtin_fmaf(xv[j].z, sb(w4[j], 2), a[j]);
+      a[j] = __builtin_fmaf(xv[j].w, sb(w4[j], 3), a[j]);
+    }
+  } else if constexpr (WT == XE_BFP16) {
+    const uint32_t w4[4] = {ch.q.x, ch.q.y, ch.q.z, ch.q.w};
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      float d = 0.f;
+#pragma unroll
+      for (int i = 2 * h; i < 2 * h + 2; i++) {
+        d = __builtin_fmaf(xv[i].x, sb(w4[i], 0), d);
+        d = __builtin_fmaf(xv[i].y, sb(w4[i], 1), d);
+        d = __builtin_fmaf(xv[i].z, sb(w4[i], 2), d);
+        d = __builtin_fmaf(xv[i].w, sb(w4[i], 3), d);
+      }
+      const int e = static_cast<int>((ch.e >> (8 * h)) & 0xff) - 133;  // e - 127 - 6
+      a[h] += __builtin_ldexpf(d, e);
+    }
+  } else {
+    const uint32_t w8[8] = {ch.lo.x, ch.lo.y, ch.lo.z, ch.lo.w, ch.hi.x, ch.hi.y, ch.hi.z, ch.hi.w};
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const uint32_t p = w8[2 * j], q = w8[2 * j + 1];
+      a[j] = __builtin_fmaf(xv[j].x, __uint_as_float(p << 16), a[j]);
+      a[j] = __builtin_fmaf(xv[j].y, __uint_as_float(p & 0xffff0000u), a[j]);
+      a[j] = __builtin_fmaf(xv[j].z, __uint_as_float(q << 16), a[j]);
+      a[j] = __builtin_fmaf(xv[j].w, __uint_as_float(q & 0xffff0000u), a[j]);
+    }
+  }
+}
+
 template <int WT, int NB, bool HEAD, typename GD, typename Prep, typename Sub>
 __device__ __forceinline__ bool gemv_rows(const GD &g, int nb, int r0, int r1, const float *xs, unsigned ep,
                                           Prep prep, float *logits, int vocab, int last_max, ArgBest &best,
-                                          Sub tsub, const float *stage, bool staged) {
+                                          Sub tsub, const float *stage, bool staged, float *kred) {
   using gdev::Chunk;
-  using gdev::chunk_dot;
   constexpr int RPL = 2;
   constexpr int NIT = Round<WT>::NIT;
   const int lpr_log = __builtin_ctz(static_cast<unsigned>(g.lpr));
   const int LPR = 1 << lpr_log;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int rg = lane >> lpr_log, kl = lane & (LPR - 1);
+  // K segments: wave w takes segment w % S of the chunks for the rows of
+  // its group w / S
+  const int ks_log = HEAD ? 0 : g.ks_log, S = 1 << ks_log;
+  const int seg = wave & (S - 1), wgrp = wave >> ks_log;
   const int rows_per_wave = (64 >> lpr_log) * RPL;
-  const int rows_per_tile = kW * rows_per_wave;
+  const int rows_per_tile = (kW >> ks_log) * rows_per_wave;
   const int K = g.k, nch = K / 16;
-  const int n_it = (nch + LPR - 1) >> lpr_log;
+  const int seg_ch = (nch + S - 1) >> ks_log;
+  const int c_lo = seg * seg_ch, c_hi = min(nch, c_lo + seg_ch);
+  const int n_it = (seg_ch + LPR - 1) >> lpr_log;
   const int ntiles = r1 > r0 ? (r1 - r0 + rows_per_tile - 1) / rows_per_tile : 0;
   WRsrc rs;
   rs.w = gdev::coherent_rsrc(g.w);
@@ -658,7 +709,7 @@ __device__ __forceinline__ bool gemv_rows(const GD &g, int nb, int r0, int r1, c
     __syncthreads();
   }
   for (int tile = 0; tile < ntiles && ok; tile++) {
-    const int row0 = r0 + tile * rows_per_tile + wave * rows_per_wave + rg * RPL;
+    const int row0 = r0 + tile * rows_per_tile + wgrp * rows_per_wave + rg * RPL;
     bool row_ok[RPL];
     int row[RPL];
 #pragma unroll
@@ -674,12 +725,14 @@ __device__ __forceinline__ bool gemv_rows(const GD &g, int nb, int r0, int r1, c
       rw[i] = lr * (WT == XE_BF16 ? 2 * K : K);
       re[i] = lr * (K / 8);
     }
-    float acc[NB][RPL];
+    float acc4[NB][RPL][4];
     float rscale[RPL], rbias[RPL];
 #pragma unroll
     for (int b = 0; b < NB; b++)
 #pragma unroll
-      for (int i = 0; i < RPL; i++) acc[b][i] = 0.f;
+      for (int i = 0; i < RPL; i++)
+#pragma unroll
+        for (int q = 0; q < 4; q++) acc4[b][i][q] = 0.f;
     for (int it0 = 0; it0 < n_it && ok; it0 += NIT) {
       Chunk<WT> w[NIT][RPL];
       // one branch around the whole round: inside a branch per chunk the
@@ -687,16 +740,16 @@ __device__ __forceinline__ bool gemv_rows(const GD &g, int nb, int r0, int r1, c
       if (staged) {
 #pragma unroll
         for (int u = 0; u < NIT; u++) {
-          const int cc = ((it0 + u) << lpr_log) + kl;
-          const bool valid = it0 + u < n_it && cc < nch;
+          const int cc = c_lo + ((it0 + u) << lpr_log) + kl;
+          const bool valid = it0 + u < n_it && cc < c_hi;
 #pragma unroll
           for (int i = 0; i < RPL; i++) load_chunk_lds<WT>(st, L, rw[i], re[i], cc, valid && row_ok[i], w[u][i]);
         }
       } else {
 #pragma unroll
         for (int u = 0; u < NIT; u++) {
-          const int cc = ((it0 + u) << lpr_log) + kl;
-          const bool valid = it0 + u < n_it && cc < nch;
+          const int cc = c_lo + ((it0 + u) << lpr_log) + kl;
+          const bool valid = it0 + u < n_it && cc < c_hi;
 #pragma unroll
           for (int i = 0; i < RPL; i++) load_chunk_buf<WT>(rs, row[i], K, cc, valid && row_ok[i], w[u][i]);
         }
@@ -719,7 +772,7 @@ __device__ __forceinline__ bool gemv_rows(const GD &g, int nb, int r0, int r1, c
 #pragma unroll
       for (int u = 0; u < NIT; u++) {
         if (it0 + u < n_it) {
-          const int cx = min(((it0 + u) << lpr_log) + kl, nch - 1);  // past the row end: zero weights
+          const int cx = min(c_lo + ((it0 + u) << lpr_log) + kl, nch - 1);  // past the segment: zero weights
 #pragma unroll
           for (int b = 0; b < NB; b++) {
             if (b < nb) {
@@ -733,7 +786,7 @@ __device__ __forceinline__ bool gemv_rows(const GD &g, int nb, int r0, int r1, c
                 xv[j] = make_float4(t.x, t.y, t.z, t.w);
               }
 #pragma unroll
-              for (int i = 0; i < RPL; i++) acc[b][i] = chunk_dot<WT>(w[u][i], xv, acc[b][i]);
+              for (int i = 0; i < RPL; i++) chunk_dot4<WT>(w[u][i], xv, acc4[b][i]);
             }
           }
         }
@@ -741,19 +794,41 @@ __device__ __forceinline__ bool gemv_rows(const GD &g, int nb, int r0, int r1, c
     }
     if (!ok) break;
     if (tile == 0) tsub(1);
+    float acc[NB][RPL];
     {
       float flat[NB * RPL];
 #pragma unroll
       for (int b = 0; b < NB; b++)
 #pragma unroll
-        for (int i = 0; i < RPL; i++) flat[b * RPL + i] = acc[b][i];
+        for (int i = 0; i < RPL; i++)
+          flat[b * RPL + i] = (acc4[b][i][0] + acc4[b][i][1]) + (acc4[b][i][2] + acc4[b][i][3]);
       gdev::group_sums<NB * RPL>(flat, lpr_log);
 #pragma unroll
       for (int b = 0; b < NB; b++)
 #pragma unroll
         for (int i = 0; i < RPL; i++) acc[b][i] = flat[b * RPL + i];
     }
-    if (kl == 0) {
+    if (ks_log > 0) {  // segment sums in LDS, added in segment order by the segment-0 waves
+      XE_LDS float *kr = lptr(kred);
+      const int slot = wgrp * rows_per_wave + rg * RPL;
+      if (kl == 0)
+#pragma unroll
+        for (int i = 0; i < RPL; i++)
+#pragma unroll
+          for (int b = 0; b < NB; b++) kr[((seg * rows_per_tile) + slot + i) * NB + b] = acc[b][i];
+      __syncthreads();
+      if (seg == 0 && kl == 0)
+#pragma unroll
+        for (int i = 0; i < RPL; i++)
+#pragma unroll
+          for (int b = 0; b < NB; b++) {
+            float t = kr[(slot + i) * NB + b];
+            for (int sg = 1; sg < S; sg++) t += kr[((sg * rows_per_tile) + slot + i) * NB + b];
+            acc[b][i] = t;
+          }
+      __syncthreads();  // the next tile's sums overwrite these
+    }
+    if (kl == 0 && seg == 0) {
 #pragma unroll
       for (int b = 0; b < NB; b++) {
         if (b >= nb) break;
@@ -789,6 +864,7 @@ __device__ __forceinline__ bool gemv_rows(const GD &g, int nb, int r0, int r1, c
         }
       }
     }
+    if (tile == 0) tsub(2);  // outputs issued
   }
   return ok;
 }
@@ -797,9 +873,10 @@ template <int WT, int NB, bool HEAD, typename GD, typename Prep, typename Sub>
 __device__ __forceinline__ bool gemv_any(const GD &g, int nb, int r0, int r1, const float *xs, unsigned ep,
                                          Prep prep, float *logits, int vocab, int last_max, ArgBest &best,
                                          const Ctl &c, Sub tsub, const float *stage = nullptr,
-                                         bool staged = false) {
+                                         bool staged = false, float *kred = nullptr) {
   (void)c;
-  return gemv_rows<WT, NB, HEAD>(g, nb, r0, r1, xs, ep, prep, logits, vocab, last_max, best, tsub, stage, staged);
+  return gemv_rows<WT, NB, HEAD>(g, nb, r0, r1, xs, ep, prep, logits, vocab, last_max, best, tsub, stage, staged,
+                                 kred);
 }
 struct NoSub {
   __device__ void operator()(int) const {}
@@ -1031,7 +1108,7 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 // query head, m in log2 units of the scaled score.
 template <int HD, int G, typename AD, typename Prep, typename Sub>
 __device__ __forceinline__ bool attn_block(const AD &a, int split, int kvh, int b, int len, const float *qin,
-                                           float *scr, unsigned ep, Prep prep, Sub tsub, const float *kvs,
+                                           float *scr, unsigned ep, Prep prep, Sub tsub, float *kvs,
                                            bool staged) {
   static_assert(HD % 32 == 0 && HD <= 256 && 3 * G <= 16, "attention tile shape");
   constexpr int NJ = HD / 32;                  // MFMA steps per tile
@@ -1085,25 +1162,16 @@ __device__ __forceinline__ bool attn_block(const AD &a, int split, int kvh, int 
     st[16 + threadIdx.x] = 0.f;
   }
   if (!prep()) return false;
+  // staged block: keys / values are read from the stage where they are used
+  // (rows past the block read its last row: K gives masked scores, V is
+  // zeroed), so they hold no registers across the block
+  XE_LDS uint8_t *kk = reinterpret_cast<XE_LDS uint8_t *>(lptr(kvs)) + 4 * kStageGran;
+  XE_LDS uint8_t *vv = kk + a.kv_cap * kv_row_bytes(HD);
+  const int last = s1 - s0 - 1;
   if (staged) {
-    // the stage's copies have landed in every wave (its loads, the barrier);
-    // rows past the block read its last row (K: masked scores; V: zeroed)
+    // the stage's copies have landed in every wave (its loads, the barrier)
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    const XE_LDS uint8_t *kk = reinterpret_cast<const XE_LDS uint8_t *>(lptr(kvs)) + 4 * kStageGran;
-    const XE_LDS uint8_t *vv = kk + a.kv_cap * kv_row_bytes(HD);
-    const int last = s1 - s0 - 1;
-    const int kq = min(wave * kKeyTile + qk_row, last);
-#pragma unroll
-    for (int j = 0; j < NJ; j++)
-      kf[j] = *reinterpret_cast<const XE_LDS u32x4 *>(kk + kq * kv_row_bytes(HD) + (32 * j + qk_dim) * 2);
-#pragma unroll
-    for (int i = 0; i < PVK; i++) {
-      const int kv = (i * kW + wave) * KPI + pv_slot;
-      const u32x2 v = *reinterpret_cast<const XE_LDS u32x2 *>(vv + min(kv, last) * kv_row_bytes(HD) + pv_dim * 2);
-      vf[i].x = kv <= last ? v.x : 0u;
-      vf[i].y = kv <= last ? v.y : 0u;
-    }
     load_head_consts_lds<HD>(a, kvs, hc);
   }
 
@@ -1137,8 +1205,14 @@ __device__ __forceinline__ bool attn_block(const AD &a, int split, int kvh, int 
     // the new row as the cache holds it: one packed copy serves the lanes
     // that patch it in below and the cache stores at the end
     for (int j = lane; j < HD / 2; j += 64) {
-      kvb[j] = pack_bf16x2(kt[2 * j], kt[2 * j + 1]);
-      kvb[HD / 2 + j] = pack_bf16x2(vsrc[2 * j], vsrc[2 * j + 1]);
+      const uint32_t kp = pack_bf16x2(kt[2 * j], kt[2 * j + 1]);
+      const uint32_t vp = pack_bf16x2(vsrc[2 * j], vsrc[2 * j + 1]);
+      kvb[j] = kp;
+      kvb[HD / 2 + j] = vp;
+      if (staged) {  // the staged row of the position (its copy predates this step) takes the new values
+        reinterpret_cast<XE_LDS uint32_t *>(kk + (posi - s0) * kv_row_bytes(HD))[j] = kp;
+        reinterpret_cast<XE_LDS uint32_t *>(vv + (posi - s0) * kv_row_bytes(HD))[j] = vp;
+      }
     }
   }
   __syncthreads();  // Q.K B operands and the new k / v staged in LDS
@@ -1156,7 +1230,13 @@ __device__ __forceinline__ bool attn_block(const AD &a, int split, int kvh, int 
     if (rb != s0) load_round(rb);
     // ---- Q.K: this wave's 16-key tile ----
     const int tile0 = rb + wave * kKeyTile;
-    if (appender && posi >= tile0 && posi < tile0 + kKeyTile && tile0 + qk_row == posi) {
+    if (staged && tile0 < s1) {
+      const int kq = min(wave * kKeyTile + qk_row, last);
+#pragma unroll
+      for (int j = 0; j < NJ; j++)
+        kf[j] = *reinterpret_cast<const XE_LDS u32x4 *>(kk + kq * kv_row_bytes(HD) + (32 * j + qk_dim) * 2);
+    }
+    if (!staged && appender && posi >= tile0 && posi < tile0 + kKeyTile && tile0 + qk_row == posi) {
 #pragma unroll
       for (int j = 0; j < NJ; j++) kf[j] = *reinterpret_cast<const XE_LDS u32x4 *>(kvb + 16 * j + qk_dim / 2);
     }
@@ -1219,29 +1299,60 @@ __device__ __forceinline__ bool attn_block(const AD &a, int split, int kvh, int 
         for (int e = 0; e < 4; e++) acc[gg][e] *= corr;
       }
     }
+    if (staged) {
+      // this wave's key slots (slot i * kW + wave, KPI keys each) hold keys
+      // up to the block's last; four slots' reads are issued together
+      const int nact = wave * KPI <= last ? (last / KPI - wave) / kW + 1 : 0;
+      for (int i0 = 0; i0 < nact; i0 += 4) {
+        u32x2 vq[4];
+        float pq[4][G];
 #pragma unroll
-    for (int i = 0; i < PVK; i++) {
-      if (rb + (i * kW + wave) * KPI >= s1) continue;  // wave-uniform: slots past the split
-      const int key_l = (i * kW + wave) * KPI + pv_slot;
-      u32x2 v = vf[i];
-      if (appender && rb + key_l == posi) v = *reinterpret_cast<const XE_LDS u32x2 *>(kvb + HD / 2 + pv_dim / 2);
-      const float vv[4] = {__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xffff0000u),
-                           __uint_as_float(v.y << 16), __uint_as_float(v.y & 0xffff0000u)};
-      float p[G];
-      if constexpr (G == 4) {
-        const f32x4_t p4 = *reinterpret_cast<const XE_LDS f32x4_t *>(sc + key_l * G);
-        p[0] = p4.x;
-        p[1] = p4.y;
-        p[2] = p4.z;
-        p[3] = p4.w;
-      } else {
+        for (int q = 0; q < 4; q++) {
+          const int key_l = ((i0 + q) * kW + wave) * KPI + pv_slot;
+          const int kr = min(key_l, last);
+          vq[q] = *reinterpret_cast<const XE_LDS u32x2 *>(vv + kr * kv_row_bytes(HD) + pv_dim * 2);
 #pragma unroll
-        for (int gg = 0; gg < G; gg++) p[gg] = sc[key_l * G + gg];
+          for (int gg = 0; gg < G; gg++) pq[q][gg] = sc[kr * G + gg];
+        }
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          const int key_l = ((i0 + q) * kW + wave) * KPI + pv_slot;
+          const bool in = i0 + q < nact && key_l <= last;
+          const float vv4[4] = {__uint_as_float(vq[q].x << 16), __uint_as_float(vq[q].x & 0xffff0000u),
+                                __uint_as_float(vq[q].y << 16), __uint_as_float(vq[q].y & 0xffff0000u)};
+#pragma unroll
+          for (int gg = 0; gg < G; gg++) {
+            const float p = in ? pq[q][gg] : 0.f;
+#pragma unroll
+            for (int e = 0; e < 4; e++) acc[gg][e] = __builtin_fmaf(p, vv4[e], acc[gg][e]);
+          }
+        }
       }
-#pragma unroll
-      for (int gg = 0; gg < G; gg++)
-#pragma unroll
-        for (int e = 0; e < 4; e++) acc[gg][e] = __builtin_fmaf(p[gg], vv[e], acc[gg][e]);
+    } else {
+  #pragma unroll
+      for (int i = 0; i < PVK; i++) {
+        if (rb + (i * kW + wave) * KPI >= s1) continue;  // wave-uniform: slots past the split
+        const int key_l = (i * kW + wave) * KPI + pv_slot;
+        u32x2 v = vf[i];
+        if (appender && rb + key_l == posi) v = *reinterpret_cast<const XE_LDS u32x2 *>(kvb + HD / 2 + pv_dim / 2);
+        const float vv[4] = {__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xffff0000u),
+                             __uint_as_float(v.y << 16), __uint_as_float(v.y & 0xffff0000u)};
+        float p[G];
+        if constexpr (G == 4) {
+          const f32x4_t p4 = *reinterpret_cast<const XE_LDS f32x4_t *>(sc + key_l * G);
+          p[0] = p4.x;
+          p[1] = p4.y;
+          p[2] = p4.z;
+          p[3] = p4.w;
+        } else {
+  #pragma unroll
+          for (int gg = 0; gg < G; gg++) p[gg] = sc[key_l * G + gg];
+        }
+  #pragma unroll
+        for (int gg = 0; gg < G; gg++)
+  #pragma unroll
+          for (int e = 0; e < 4; e++) acc[gg][e] = __builtin_fmaf(p[gg], vv[e], acc[gg][e]);
+      }
     }
     if (rb + kRoundKeys < s1) __syncthreads();  // scores of the next round overwrite sc
   }
@@ -1287,18 +1398,24 @@ __device__ __forceinline__ bool attn_block(const AD &a, int split, int kvh, int 
       __hip_atomic_store(gptr_w(vrow) + j, kvb[HD / 2 + j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
+  // the waves' sums, four dims a thread (16-byte reads), into LDS (the Q.K
+  // operand area, free by now); then the partials go out with consecutive
+  // lanes on consecutive pairs (a store instruction covers whole lines)
+  XE_LDS float *outb = reinterpret_cast<XE_LDS float *>(bfr);  // [G][HD]
+  for (int t = threadIdx.x; t < G * HD / 4; t += kT) {
+    const int gg = t / (HD / 4), e4 = 4 * (t % (HD / 4));
+    f32x4_t v4[kW];
+#pragma unroll
+    for (int w = 0; w < kW; w++) v4[w] = *reinterpret_cast<const XE_LDS f32x4_t *>(red + (w * G + gg) * HD + e4);
+    f32x4_t sum = v4[0];
+#pragma unroll
+    for (int w = 1; w < kW; w++) sum += v4[w];
+    *reinterpret_cast<XE_LDS f32x4_t *>(outb + gg * HD + e4) = sum;
+  }
+  __syncthreads();
   for (int t = threadIdx.x; t < G * (HD + 2); t += kT) {
     const int gg = t / (HD + 2), e = t % (HD + 2);
-    float v;
-    if (e == 0) {
-      v = st[gg];
-    } else if (e == 1) {
-      v = st[16 + gg];
-    } else {
-      v = 0.f;
-#pragma unroll
-      for (int w = 0; w < kW; w++) v += red[(w * G + gg) * HD + e - 2];
-    }
+    const float v = e == 0 ? st[gg] : (e == 1 ? st[16 + gg] : outb[gg * HD + e - 2]);
     put(a.part, b, ((kvh * G + gg) * a.max_splits + split) * (HD + 2) + e, v, ep);
   }
   __syncthreads();  // scratch is reused by the next block

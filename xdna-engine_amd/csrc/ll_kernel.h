@@ -197,8 +197,9 @@ __global__ __launch_bounds__(kT) void ll_step_kernel(StepParams sp) {
             return r;
           };
           auto tsub = [&](int sub) { mark(step, tslots + 4 + sp.n_a + sp.n_f + kSubSlots * ((is_a ? 0 : sp.n_a) + i) + sub); };
+          // K-segment sums go to the scratch area (its norm gains are read by then)
           ok = gemv_any<WT, NB, false>(g, nb, r0, r1, xin, ep, prep, nullptr, 0, 0, none, c, tsub, stage,
-                                       g.staged != 0);
+                                       g.staged != 0, scr);
           break;
         }
         case LK_ATTN: {
