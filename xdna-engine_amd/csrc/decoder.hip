@@ -1309,7 +1309,7 @@ void build_ll_plan(xe_decoder *d, int B, xe_decoder::LLPlan &P) {
   // scratch: attention blocks, merge tables, argmax partials, and the norm
   // gains of a GEMV input (up to 3 folds, gamma, beta: 5 regions)
   P.scratch = std::max(std::max(ll::attn_scratch_floats(hd, g), ll::attn_scratch_floats(hd, 1)),
-                       std::max(ll::kMaxSplits * (ll::kDM + 2) + ll::kMaxSplits + 2, P.nb_t * 2 * P.grid));
+                       std::max(ll::kMaxSplits * (ll::kDM + 2) + ll::kMaxSplits + ll::kW * (ll::kDM + 1), P.nb_t * 2 * P.grid));
   P.scratch = std::max(P.scratch, 5 * ll::nw_floats(D)) + 16;
   auto base = [&](int kin) {
     return static_cast<long>(sizeof(float)) *

@@ -1423,7 +1423,8 @@ __device__ __forceinline__ bool attn_block(const AD &a, int split, int kvh, int 
 }
 
 // Merge block: stream b, q head h, outputs [e0, e0 + kDM) of the head.
-// tab: LDS scratch >= kMaxSplits * (kDM + 2) + kMaxSplits + 2 floats.
+// tab: LDS scratch >= kMaxSplits * (kDM + 2) + kMaxSplits + kW * (kDM + 1)
+// floats.
 __device__ __noinline__ bool merge_block(const XE_CONST MergeD &mg, int b, int h, int e0, int len, float *tab_,
                                             unsigned ep, const Ctl c) {
   const int HD = mg.hd;
@@ -1464,12 +1465,40 @@ __device__ __noinline__ bool merge_block(const XE_CONST MergeD &mg, int b, int h
     }
   }
   __syncthreads();
+  // weighted sums over the splits: lane (group, e) of all kT threads takes
+  // splits group, group + kT / kDM, ...; the 64 / kDM groups of a wave meet
+  // by lane swaps, the waves' sums in LDS (fixed order throughout)
+  static_assert(kDM == 16, "merge lanes: 16 outputs a block");
+  XE_LDS float *wsum = wts + kMaxSplits;  // [kW][kDM + 1]
+  {
+    const int e = threadIdx.x & (kDM - 1), grp = threadIdx.x >> 4;
+    float ls = 0.f, at = 0.f;
+    for (int s = grp; s < nsplits; s += kT / kDM) {
+      const float w = wts[s];
+      ls = __builtin_fmaf(tab[s * W + 1], w, ls);
+      at = __builtin_fmaf(tab[s * W + 2 + e], w, at);
+    }
+    auto swap_add = [](float v, bool half32) {
+      const auto r = half32 ? __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false)
+                            : __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+      return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    };
+    at = swap_add(swap_add(at, false), true);
+    ls = swap_add(swap_add(ls, false), true);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane < kDM) {
+      wsum[wave * (kDM + 1) + lane] = at;
+      if (lane == 0) wsum[wave * (kDM + 1) + kDM] = ls;
+    }
+  }
+  __syncthreads();
   if (threadIdx.x < kDM) {
     const int e = threadIdx.x;
     float ls = 0.f, at = 0.f;
-    for (int s = 0; s < nsplits; s++) {
-      ls += tab[s * W + 1] * wts[s];
-      at += tab[s * W + 2 + e] * wts[s];
+#pragma unroll
+    for (int w = 0; w < kW; w++) {
+      at += wsum[w * (kDM + 1) + e];
+      ls += wsum[w * (kDM + 1) + kDM];
     }
     const float o = mg.div_norm ? at / ls : at * (1.0f / ls);
     put(mg.out, b, h * HD + e0 + e, o, ep);
