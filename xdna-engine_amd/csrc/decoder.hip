@@ -203,6 +203,24 @@ bool tensor_spec(const xe_model_config &c, int kind, int layer, Spec &s) {
   }
 }
 
+// src [rows][cols] -> dst [cols / 4][rows][4]: element (r, c) at
+// (c / 4 * rows + r) * 4 + c % 4 (cols a multiple of 4); 32 x 32 tiles
+// through LDS.
+template <typename T>
+__global__ void transpose4_kernel(const T *src, T *dst, int rows, int cols) {
+  __shared__ T tile[32][33];
+  const int c0 = blockIdx.x * 32, r0 = blockIdx.y * 32;
+  for (int i = threadIdx.y; i < 32; i += 8) {
+    const int r = r0 + i, c = c0 + threadIdx.x;
+    if (r < rows && c < cols) tile[i][threadIdx.x] = src[static_cast<size_t>(r) * cols + c];
+  }
+  __syncthreads();
+  for (int i = threadIdx.y; i < 32; i += 8) {
+    const int c = c0 + i, r = r0 + threadIdx.x;
+    if (c < cols && r < rows) dst[(static_cast<size_t>(c / 4) * rows + r) * 4 + c % 4] = tile[threadIdx.x][i];
+  }
+}
+
 size_t wbytes(int wdtype, size_t n) {
   return wdtype == XE_BF16 ? 2 * n : wdtype == XE_BFP16 ? n + n / 8 : n;
 }
@@ -324,6 +342,10 @@ struct xe_decoder {
     int head_lpr = 8, head_rpl = 2;
   };
   std::map<int, LLPlan> ll_plans;
+  // FFN output projections transposed ([ffn / 4][d_model][4] per layer) for the
+  // low-latency executor's split FFN output (ll::DpartD); empty until a plan
+  // uses them, refreshed when a layer's projection is set
+  std::vector<void *> ll_fc2t;
   unsigned ll_epoch = 1;           // epoch of the next step (exchange buffers start at 0)
   int32_t *ll_forced = nullptr;    // device [max_ctx + 1][max_batch] prompt tokens
   double last_step_us = 0.0;
@@ -539,6 +561,8 @@ void free_decoder(xe_decoder *d) {
     if (kv.second.dev_f) (void)hipFree(kv.second.dev_f);
     if (kv.second.arena) (void)hipFree(kv.second.arena);
   }
+  for (void *p : d->ll_fc2t)
+    if (p) (void)hipFree(p);
   if (d->ll_forced) (void)hipFree(d->ll_forced);
   if (d->step_status) (void)hipFree(d->step_status);
   d->emb.release();
@@ -1033,7 +1057,10 @@ int plan_kv_stage(std::vector<ll::Phase> &list, int hd, int max_ctx, long budget
 // phase: such a phase gets its slice copied into LDS at the start of an
 // earlier phase, the one after the role's previous staged phase (the stage
 // holds one slice at a time).  budget < 0: nothing staged.
-void plan_stage(std::vector<ll::Phase> &list, int ranks, int wt, long budget, int &stage_bytes) {
+// dpart_need: the stage bytes of a split FFN output phase (ll::LK_DPART),
+// which is always staged, by the phase right before it.
+void plan_stage(std::vector<ll::Phase> &list, int ranks, int wt, long budget, int &stage_bytes,
+                int dpart_need = 0) {
   for (auto &ph : list) {
     ph.issue = -1;
     ph.kv_issue = -1;
@@ -1042,6 +1069,12 @@ void plan_stage(std::vector<ll::Phase> &list, int ranks, int wt, long budget, in
   }
   int last = -1;  // the previous staged phase
   for (int j = 0; j < static_cast<int>(list.size()); j++) {
+    if (list[j].kind == ll::LK_DPART && j > 0) {  // the GEMV before never reads the stage itself
+      list[j - 1].issue = j;
+      last = j;
+      stage_bytes = std::max(stage_bytes, dpart_need);
+      continue;
+    }
     if (list[j].kind != ll::LK_GEMV) continue;
     ll::GemvD &g = list[j].u.gemv;
     const int at = last + 1;
@@ -1056,6 +1089,31 @@ void plan_stage(std::vector<ll::Phase> &list, int ranks, int wt, long budget, in
     stage_bytes = std::max(stage_bytes, need);
   }
 }
+// Transposed FFN output projection of one layer (int8 / bf16 weights):
+// ll_fc2t[layer] = fc2.w^T with four hidden rows interleaved,
+// [ffn / 4][d_model][4] (ll::DpartD), on the decoder's stream.
+void ll_fc2t_layer(xe_decoder *d, int layer) {
+  const Mat &m = d->L[layer].fc2;
+  const dim3 grid((m.cols + 31) / 32, (m.rows + 31) / 32), block(32, 8);
+  if (m.wdtype == XE_BF16)
+    transpose4_kernel<uint16_t><<<grid, block, 0, d->s>>>(static_cast<const uint16_t *>(m.w),
+                                                         static_cast<uint16_t *>(d->ll_fc2t[layer]), m.rows, m.cols);
+  else
+    transpose4_kernel<int8_t><<<grid, block, 0, d->s>>>(static_cast<const int8_t *>(m.w),
+                                                       static_cast<int8_t *>(d->ll_fc2t[layer]), m.rows, m.cols);
+  XE_HIP(hipGetLastError());
+}
+
+void ll_fc2t_ensure(xe_decoder *d) {
+  if (!d->ll_fc2t.empty()) return;
+  d->ll_fc2t.assign(d->c.n_layers, nullptr);
+  for (int li = 0; li < d->c.n_layers; li++) {
+    const Mat &m = d->L[li].fc2;
+    XE_HIP(hipMalloc(&d->ll_fc2t[li], wbytes(m.wdtype, static_cast<size_t>(m.rows) * m.cols)));
+    ll_fc2t_layer(d, li);
+  }
+}
+
 void build_ll_plan(xe_decoder *d, int B, xe_decoder::LLPlan &P) {
   const auto &c = d->c;
   const int D = c.d_model, F = c.ffn, hd = c.head_dim;
@@ -1087,7 +1145,7 @@ void build_ll_plan(xe_decoder *d, int B, xe_decoder::LLPlan &P) {
   };
   // phases refer to vectors by index until the arena exists: (list, phase, field) -> vec
   enum Field { F_GEMV_IN, F_GEMV_OUT, F_FOLD_SRC, F_ATTN_Q, F_ATTN_PART, F_MERGE_PART, F_MERGE_OUT,
-               F_GEMV_FOLD0, F_GEMV_FOLD1, F_GEMV_FOLD2 };
+               F_GEMV_FOLD0, F_GEMV_FOLD1, F_GEMV_FOLD2, F_DPART_PART, F_REDUCE_PART, F_REDUCE_OUT };
   struct Fix {
     std::vector<ll::Phase> *list;
     size_t idx;
@@ -1106,6 +1164,9 @@ void build_ll_plan(xe_decoder *d, int B, xe_decoder::LLPlan &P) {
       case F_GEMV_FOLD0: return ph.u.gemv.folds[0].src;
       case F_GEMV_FOLD1: return ph.u.gemv.folds[1].src;
       case F_GEMV_FOLD2: return ph.u.gemv.folds[2].src;
+      case F_DPART_PART: return ph.u.dpart.part;
+      case F_REDUCE_PART: return ph.u.reduce.part;
+      case F_REDUCE_OUT: return ph.u.reduce.out;
       default: return ph.u.merge.out;
     }
   };
@@ -1130,7 +1191,7 @@ void build_ll_plan(xe_decoder *d, int B, xe_decoder::LLPlan &P) {
   };
   auto gemv = [&](std::vector<ll::Phase> &list, int ranks, const Mat &m, const float *bias, int in_vec,
                   int norm_kind, const float *gamma, const float *beta, int act, int out_vec, const char *label,
-                  std::vector<PreFold> pre = {}) {
+                  std::vector<PreFold> pre = {}, int out_lds = 0) {
     ll::Phase ph{};
     ph.kind = ll::LK_GEMV;
     ll::GemvD &gd = ph.u.gemv;
@@ -1160,7 +1221,8 @@ void build_ll_plan(xe_decoder *d, int B, xe_decoder::LLPlan &P) {
     for (size_t f = 0; f < pre.size(); f++)
       fix.push_back({&list, list.size() - 1, static_cast<Field>(F_GEMV_FOLD0 + f), pre[f].vec});
     if (in_vec >= 0) fix.push_back({&list, list.size() - 1, F_GEMV_IN, in_vec});
-    fix.push_back({&list, list.size() - 1, F_GEMV_OUT, out_vec});
+    if (out_lds > 0) list.back().u.gemv.out_lds = out_lds;
+    else fix.push_back({&list, list.size() - 1, F_GEMV_OUT, out_vec});
   };
   auto fold = [&](std::vector<ll::Phase> &list, int src, const float *post_w, const char *label) {
     ll::Phase ph{};
@@ -1218,6 +1280,14 @@ void build_ll_plan(xe_decoder *d, int B, xe_decoder::LLPlan &P) {
     fix.push_back({&P.a, P.a.size() - 1, F_MERGE_PART, part});
     fix.push_back({&P.a, P.a.size() - 1, F_MERGE_OUT, out});
   };
+  // FFN output split: int8 / bf16 weights, at most kRedRows outputs per
+  // F rank to sum, kRedParts ranks (XE_LL_FFN_SPLIT=0: the plain GEMV pair)
+  const char *fs_env = std::getenv("XE_LL_FFN_SPLIT");
+  const bool ffn_split = !(fs_env && std::string(fs_env) == "0") &&
+                         (c.wdtype == XE_I8 || c.wdtype == XE_BF16) && D % 4 == 0 &&
+                         (D + n_f - 1) / n_f <= ll::kRedRows && n_f <= ll::kRedParts;
+  const int ffn_kn = 4 * ((F / 4 + n_f - 1) / n_f);  // hidden slice of an F rank (at most; multiples of 4)
+  if (ffn_split) ll_fc2t_ensure(d);
   P.a.clear();
   P.f.clear();
   P.a_labels.clear();
@@ -1270,10 +1340,42 @@ void build_ll_plan(xe_decoder *d, int B, xe_decoder::LLPlan &P) {
     if (li > 0) pre_f.push_back({p_down, p_post_ffn});
     pre_f.push_back({v_o, gem ? l.post_attn : nullptr});
     if (wh) pre_f.push_back({v_xo, nullptr});
-    gemv(P.f, n_f, l.fc1, gem ? nullptr : l.fc1_b, -1, norm, l.ln2_w, gem ? nullptr : l.ln2_b,
-         gem ? ACT_GEGLU_TANH : (opt ? ACT_RELU : ACT_GELU_ERF), v_ffn, gem ? "gemv_gateup" : "gemv_fc1", pre_f);
-    gemv(P.f, n_f, l.fc2, gem ? nullptr : l.fc2_b, v_ffn, XE_NORM_NONE, nullptr, nullptr, ACT_NONE, v_down,
-         gem ? "gemv_down" : "gemv_fc2");
+    const int act = gem ? ACT_GEGLU_TANH : (opt ? ACT_RELU : ACT_GELU_ERF);
+    if (ffn_split) {
+      // FFN output split (ll::DpartD / ReduceD): the hidden slice stays in
+      // LDS, partials for every output cross over, each rank sums its share
+      gemv(P.f, n_f, l.fc1, gem ? nullptr : l.fc1_b, -1, norm, l.ln2_w, gem ? nullptr : l.ln2_b, act, -1,
+           gem ? "gemv_gateup" : "gemv_fc1", pre_f, ll::xstride(D));
+      const int v_dpart = vec(n_f * D);
+      ll::Phase dp{};
+      dp.kind = ll::LK_DPART;
+      dp.u.dpart.wt = d->ll_fc2t[li];
+      dp.u.dpart.d = D;
+      dp.u.dpart.k = F;
+      dp.u.dpart.unit = gem ? 2 : 1;
+      dp.u.dpart.m_prev = l.fc1.rows;
+      dp.u.dpart.act_off = ll::xstride(D);
+      P.f.push_back(dp);
+      P.f_labels.push_back(gem ? "ffn_down_part" : "ffn_fc2_part");
+      P.f_bytes.push_back(static_cast<double>(l.fc2.bytes()) + 8.0 * B * n_f * D);
+      fix.push_back({&P.f, P.f.size() - 1, F_DPART_PART, v_dpart});
+      ll::Phase rp{};
+      rp.kind = ll::LK_REDUCE;
+      rp.u.reduce.d = D;
+      rp.u.reduce.nparts = n_f;
+      rp.u.reduce.scale = l.fc2.scale;
+      rp.u.reduce.bias = gem ? nullptr : l.fc2_b;
+      P.f.push_back(rp);
+      P.f_labels.push_back(gem ? "ffn_down_reduce" : "ffn_fc2_reduce");
+      P.f_bytes.push_back(8.0 * B * n_f * D);
+      fix.push_back({&P.f, P.f.size() - 1, F_REDUCE_PART, v_dpart});
+      fix.push_back({&P.f, P.f.size() - 1, F_REDUCE_OUT, v_down});
+    } else {
+      gemv(P.f, n_f, l.fc1, gem ? nullptr : l.fc1_b, -1, norm, l.ln2_w, gem ? nullptr : l.ln2_b, act, v_ffn,
+           gem ? "gemv_gateup" : "gemv_fc1", pre_f);
+      gemv(P.f, n_f, l.fc2, gem ? nullptr : l.fc2_b, v_ffn, XE_NORM_NONE, nullptr, nullptr, ACT_NONE, v_down,
+           gem ? "gemv_down" : "gemv_fc2");
+    }
     p_o = v_o;
     p_xo = v_xo;
     p_down = v_down;
@@ -1305,12 +1407,16 @@ void build_ll_plan(xe_decoder *d, int B, xe_decoder::LLPlan &P) {
   // fold sources plain): A holds QKV / O / cross-attention inputs and q rows,
   // F the FFN inputs
   P.kin_a = std::max(std::max(ll::xstride(D), ll::xstride(hq)), std::max(nq, D));
-  P.kin_f = std::max(ll::xstride(D), ll::xstride(F));
+  // F: the GEMV inputs, or (split FFN output) the FFN input and the hidden slice
+  P.kin_f = ffn_split ? ll::xstride(D) + (ffn_kn + 3) / 4 * 4 : std::max(ll::xstride(D), ll::xstride(F));
   // scratch: attention blocks, merge tables, argmax partials, and the norm
   // gains of a GEMV input (up to 3 folds, gamma, beta: 5 regions)
   P.scratch = std::max(std::max(ll::attn_scratch_floats(hd, g), ll::attn_scratch_floats(hd, 1)),
                        std::max(ll::kMaxSplits * (ll::kDM + 2) + ll::kMaxSplits + ll::kW * (ll::kDM + 1), P.nb_t * 2 * P.grid));
-  P.scratch = std::max(P.scratch, 5 * ll::nw_floats(D)) + 16;
+  P.scratch = std::max(P.scratch, 5 * ll::nw_floats(D));
+  if (ffn_split)  // the partials' staging and the reduce tables
+    P.scratch = std::max(P.scratch, std::max(ll::dpart_obuf_floats(P.nb_t, D), ll::kW * P.nb_t * ll::kRedRows + 512));
+  P.scratch += 16;
   auto base = [&](int kin) {
     return static_cast<long>(sizeof(float)) *
            (static_cast<long>(P.nb_t) * D + static_cast<long>(P.nb_t) * kin + ((P.scratch + 3) & ~3));
@@ -1323,7 +1429,11 @@ void build_ll_plan(xe_decoder *d, int B, xe_decoder::LLPlan &P) {
   const bool stage_on = !(st_env && std::string(st_env) == "0");
   P.stage_a = P.stage_f = 0;
   plan_stage(P.a, n_a, c.wdtype, stage_on ? static_cast<long>(kLLLds) - base_a - trace_res : -1, P.stage_a);
-  plan_stage(P.f, n_f, c.wdtype, stage_on ? static_cast<long>(kLLLds) - base_f - trace_res : -1, P.stage_f);
+  // the split FFN output's projection slice goes to the stage during the GEMV before it
+  const int dpart_need = ffn_split ? ll::kStageZero + ll::stage_pad(ffn_kn * D * (c.wdtype == XE_BF16 ? 2 : 1)) : 0;
+  if (dpart_need > static_cast<long>(kLLLds) - base_f - trace_res) { P.why = "LDS need too large (FFN split)"; return; }
+  plan_stage(P.f, n_f, c.wdtype, stage_on ? static_cast<long>(kLLLds) - base_f - trace_res : -1, P.stage_f,
+             dpart_need);
   // then the attention side's key/value stage
   const char *kv_env = std::getenv("XE_LL_KV");
   const bool kv_on = !(kv_env && std::string(kv_env) == "0");
@@ -1656,6 +1766,7 @@ int xe_decoder_init_synthetic(xe_decoder *d, uint64_t seed) {
           synth_vector(d, seed, kind, layer, sp, p.vec, kind == XE_T_ENC_OUT);
         }
       }
+    for (size_t li = 0; li < d->ll_fc2t.size(); li++) ll_fc2t_layer(d, static_cast<int>(li));
     XE_HIP(hipStreamSynchronize(d->s));
     d->cross_ready = false;
     if (d->c.family == XE_WHISPER) precompute_cross(d);
@@ -1675,6 +1786,7 @@ int xe_decoder_set_tensor(xe_decoder *d, int kind, int layer, const float *data,
     Place p = d->place(kind, layer);
     if (sp.quant) {
       upload_matrix(d, sp, p, data);
+      if (kind == XE_T_FC2_W && !d->ll_fc2t.empty()) ll_fc2t_layer(d, layer);
     } else {
       std::vector<float> tmp(data, data + count);
       if (kind == XE_T_ENC_OUT)

@@ -59,7 +59,7 @@ struct Vec {
   int pad;
 };
 
-enum Kind { LK_FOLD = 0, LK_GEMV = 1, LK_ATTN = 2, LK_MERGE = 3 };
+enum Kind { LK_FOLD = 0, LK_GEMV = 1, LK_ATTN = 2, LK_MERGE = 3, LK_DPART = 4, LK_REDUCE = 5 };
 
 // residual += post(src): plain add, or Gemma's RMSNorm (1 + w) of src first.
 struct FoldD {
@@ -92,6 +92,10 @@ struct GemvD {
   // the waves split K into 1 << ks_log segments (rows the rank holds too few
   // to keep every wave busy); their partial sums meet in LDS
   int ks_log;
+  // > 0: the activations stay in this workgroup's LDS (its slice of the
+  // FFN's hidden vector, read by the next phase, LK_DPART) instead of `out`,
+  // at this float offset into each input row
+  int out_lds;
 };
 
 struct AttnD {
@@ -122,6 +126,30 @@ struct MergeD {
   int hq, hd, max_splits, fixed_len, div_norm;
 };
 
+// FFN output, first half: this rank's slice of the hidden vector (the
+// previous phase's activations, in LDS) times the matching rows of the
+// output projection stored transposed, four hidden rows interleaved (wt:
+// [k / 4][d][4], element (k, j) at (k / 4 * d + j) * 4 + k % 4), giving
+// partial sums for all d outputs: part row b = [ranks][d].  Slices start
+// on multiples of four hidden rows.
+struct DpartD {
+  const void *wt;  // [k / 4][d][4] int8 or bf16
+  int d, k;        // outputs, hidden size
+  int unit;        // projection rows per hidden element of the previous GEMV (2: GeGLU pairs)
+  int m_prev;      // rows of the previous GEMV (its rank split fixes this rank's k slice)
+  int act_off;     // float offset of the slice in each LDS input row (the previous GEMV's out_lds)
+  Vec part;
+};
+
+// FFN output, second half: rows [r0, r1) of d (this rank's share) summed
+// over the ranks' partials (in a fixed order), then scale (int8) and bias.
+struct ReduceD {
+  Vec part;        // [ranks][d] per row b
+  int d, nparts;
+  const float *scale, *bias;
+  Vec out;
+};
+
 struct Phase {
   int kind;
   // >= 0: at this phase's start, copy the weight slice of GEMV phase `issue`
@@ -138,6 +166,8 @@ struct Phase {
     GemvD gemv;
     AttnD attn;
     MergeD merge;
+    DpartD dpart;
+    ReduceD reduce;
   } u;
 };
 
@@ -192,6 +222,7 @@ struct StepParams {
 // exchange primitives
 // ---------------------------------------------------------------------------
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
 
 template <typename V>
 __device__ __forceinline__ void put(const V &v, int b, int i, float x, unsigned ep) {
@@ -291,8 +322,7 @@ __device__ __forceinline__ bool get(const V &v, int nb, int n, float *dst, int l
 template <int NI>
 __device__ __forceinline__ bool get_scattered(const uint64_t *base, const int (&idx)[NI], const bool (&need_in)[NI],
                                               float (&out)[NI], unsigned ep, const Ctl &c) {
-  typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
-  const __amdgpu_buffer_rsrc_t rs = gdev::coherent_rsrc(base);
+    const __amdgpu_buffer_rsrc_t rs = gdev::coherent_rsrc(base);
   bool need[NI];
   u32x2 val[NI];
 #pragma unroll
@@ -676,7 +706,8 @@ __device__ __forceinline__ void chunk_dot4(const gdev::Chunk<WT> &ch, const floa
 template <int WT, int NB, bool HEAD, typename GD, typename Prep, typename Sub>
 __device__ __forceinline__ bool gemv_rows(const GD &g, int nb, int r0, int r1, const float *xs, unsigned ep,
                                           Prep prep, float *logits, int vocab, int last_max, ArgBest &best,
-                                          Sub tsub, const float *stage, bool staged, float *kred) {
+                                          Sub tsub, const float *stage, bool staged, float *kred, float *lout,
+                                          int lout_ld) {
   using gdev::Chunk;
   constexpr int RPL = 2;
   constexpr int NIT = Round<WT>::NIT;
@@ -769,25 +800,25 @@ __device__ __forceinline__ bool gemv_rows(const GD &g, int nb, int r0, int r1, c
       }
       if (tile == 0 && it0 == 0 && !staged) ok = prep();
       if (!ok) break;
+      // every row of the NB tile (rows past nb hold unused values): a
+      // branch on nb per chunk costs more than the FMAs it would skip
 #pragma unroll
       for (int u = 0; u < NIT; u++) {
         if (it0 + u < n_it) {
           const int cx = min(c_lo + ((it0 + u) << lpr_log) + kl, nch - 1);  // past the segment: zero weights
 #pragma unroll
           for (int b = 0; b < NB; b++) {
-            if (b < nb) {
-              typedef float f32x4 __attribute__((ext_vector_type(4)));
-              float4 xv[4];
-              const XE_LDS f32x4 *xr =
-                  reinterpret_cast<const XE_LDS f32x4 *>(lptr(xs) + static_cast<size_t>(b) * xstride(K) + cx * 20);
+            typedef float f32x4 __attribute__((ext_vector_type(4)));
+            float4 xv[4];
+            const XE_LDS f32x4 *xr =
+                reinterpret_cast<const XE_LDS f32x4 *>(lptr(xs) + static_cast<size_t>(b) * xstride(K) + cx * 20);
 #pragma unroll
-              for (int j = 0; j < 4; j++) {
-                const f32x4 t = xr[j];
-                xv[j] = make_float4(t.x, t.y, t.z, t.w);
-              }
-#pragma unroll
-              for (int i = 0; i < RPL; i++) chunk_dot4<WT>(w[u][i], xv, acc4[b][i]);
+            for (int j = 0; j < 4; j++) {
+              const f32x4 t = xr[j];
+              xv[j] = make_float4(t.x, t.y, t.z, t.w);
             }
+#pragma unroll
+            for (int i = 0; i < RPL; i++) chunk_dot4<WT>(w[u][i], xv, acc4[b][i]);
           }
         }
       }
@@ -851,7 +882,11 @@ __device__ __forceinline__ bool gemv_rows(const GD &g, int nb, int r0, int r1, c
             }
           }
         } else if (g.act == ACT_GEGLU_TANH) {
-          if (row_ok[0]) put(g.out, b, row[0] / 2, gdev::gelu_tanh(v[0]) * v[1], ep);
+          const float t = gdev::gelu_tanh(v[0]) * v[1];
+          if (row_ok[0]) {
+            if (g.out_lds) lptr(lout)[b * lout_ld + (row[0] - r0) / 2] = t;
+            else put(g.out, b, row[0] / 2, t, ep);
+          }
         } else {
 #pragma unroll
           for (int i = 0; i < RPL; i++) {
@@ -859,7 +894,8 @@ __device__ __forceinline__ bool gemv_rows(const GD &g, int nb, int r0, int r1, c
             float t = v[i];
             if (g.act == ACT_RELU) t = t > 0.f ? t : 0.f;
             else if (g.act == ACT_GELU_ERF) t = gdev::gelu_erf(t);
-            put(g.out, b, row[i], t, ep);
+            if (g.out_lds) lptr(lout)[b * lout_ld + row[i] - r0] = t;
+            else put(g.out, b, row[i], t, ep);
           }
         }
       }
@@ -873,10 +909,11 @@ template <int WT, int NB, bool HEAD, typename GD, typename Prep, typename Sub>
 __device__ __forceinline__ bool gemv_any(const GD &g, int nb, int r0, int r1, const float *xs, unsigned ep,
                                          Prep prep, float *logits, int vocab, int last_max, ArgBest &best,
                                          const Ctl &c, Sub tsub, const float *stage = nullptr,
-                                         bool staged = false, float *kred = nullptr) {
+                                         bool staged = false, float *kred = nullptr, float *lout = nullptr,
+                                         int lout_ld = 0) {
   (void)c;
   return gemv_rows<WT, NB, HEAD>(g, nb, r0, r1, xs, ep, prep, logits, vocab, last_max, best, tsub, stage, staged,
-                                 kred);
+                                 kred, lout, lout_ld);
 }
 struct NoSub {
   __device__ void operator()(int) const {}
@@ -886,6 +923,245 @@ struct NoSub {
 __device__ __forceinline__ void rank_rows(int m, int r, int n, int &r0, int &r1) {
   r0 = static_cast<int>((static_cast<long long>(m) * r) / n);
   r1 = static_cast<int>((static_cast<long long>(m) * (r + 1)) / n);
+}
+
+// ---------------------------------------------------------------------------
+// FFN output in two phases (LK_DPART, LK_REDUCE): each rank multiplies its
+// slice of the hidden vector, left in LDS by the GEMV before, by the
+// matching rows of the transposed output projection, and puts partial sums
+// for every output; the ranks then sum those partials for their own share of
+// the outputs.  The exchange between the two carries one value per output
+// and rank instead of the whole hidden vector to every rank.
+// ---------------------------------------------------------------------------
+// The hidden slice [k0, k1) of this rank (the previous GEMV's rows / unit).
+template <typename DD>
+__device__ __forceinline__ void dpart_slice(const DD &dp, int rank, int nranks, int &k0, int &k1) {
+  rank_rows(dp.m_prev / (dp.unit * 4), rank, nranks, k0, k1);
+  k0 *= 4;
+  k1 *= 4;
+}
+
+// Copy rows [k0, k1) of wt into the stage (after kStageZero).
+template <int WT, typename DD>
+__device__ __forceinline__ void dpart_stage_issue(const DD &dp, int k0, int k1, float *stage) {
+  if (k1 <= k0) return;
+  const int rb = (WT == XE_BF16 ? 2 : 1) * dp.d;
+  lds_copy(static_cast<const uint8_t *>(dp.wt) + static_cast<size_t>(k0) * rb, (k1 - k0) * rb,
+           reinterpret_cast<XE_LDS uint8_t *>(lptr(stage)) + kStageZero);
+}
+
+// partial[b][r] = sum over k < kn of wt[k0 + k][r] act[b][k] (act: LDS,
+// 16-byte aligned, row stride act_ld a multiple of 4; kn a multiple of 4).
+// A lane takes four consecutive outputs, four k at a time: one 16-byte
+// (int8) or 32-byte (bf16) read of the interleaved stage and one broadcast
+// read of the activations, the next group's reads issued before this
+// group's FMAs.  The results go through LDS (obuf) so the puts run
+// consecutive lanes over consecutive outputs.
+template <int WT>
+struct DpW {
+  u32x4 a, b;  // b: bf16 only
+};
+template <int WT>
+__device__ __forceinline__ void dpart_ld(const XE_LDS uint8_t *w, int elem, DpW<WT> &o) {
+  const XE_LDS u32x4 *p = reinterpret_cast<const XE_LDS u32x4 *>(w + elem * (WT == XE_BF16 ? 2 : 1));
+  o.a = p[0];
+  if constexpr (WT == XE_BF16) o.b = p[1];
+}
+// weight of output e (of the lane's four), hidden row kk (of the group's four)
+template <int WT>
+__device__ __forceinline__ float dpart_wv(const DpW<WT> &v, int e, int kk) {
+  if constexpr (WT == XE_BF16) {
+    const int idx = e * 4 + kk;
+    const uint32_t d = idx < 8 ? v.a[idx / 2] : v.b[(idx - 8) / 2];
+    return __uint_as_float(idx & 1 ? d & 0xffff0000u : d << 16);
+  } else {
+    return gdev::sb(v.a[e], kk);
+  }
+}
+
+// Lanes per SIMD: waves w and w + 4 share SIMD w % 4, so work is balanced
+// across SIMDs when threads [0, 256) and [256, 512) carry equal shares.  The
+// first quads go 256 to a pass over all kn (threads t and t + 256 alike
+// after an even number of passes); the remaining tq < 256 quads are split
+// into S segments of the k groups over the threads with one pass fewer, each
+// segment's partial summed in segment order before the put.
+struct DpartMap {
+  int hq, tq, tb, S;
+};
+__device__ __forceinline__ DpartMap dpart_map(int d, int kn) {
+  DpartMap m;
+  const int nq = d / 4, ng = kn / 4;
+  m.hq = nq / 256 * 256;
+  m.tq = nq - m.hq;
+  const int L = (m.hq / 256) % 2 ? kT - 256 : kT;
+  m.tb = kT - L;
+  m.S = m.tq > 0 ? max(1, min(L / m.tq, ng)) : 1;
+  return m;
+}
+__host__ __device__ inline int dpart_obuf_floats(int nb, int d) { return nb * (d + 4 * kT); }
+
+// acc[b][e] += sum over groups [g0, g1) (quad q), two groups a step with
+// the next group's reads in flight during each group's FMAs.  Every row of
+// the NB tile is computed (rows past nb hold unused values): a branch on nb
+// inside the loop costs more than the FMAs it would skip.
+template <int WT, int NB>
+__device__ __forceinline__ void dpart_groups(const XE_LDS uint8_t *w, const XE_LDS float *a, int act_ld, int D,
+                                             int q, int g0, int g1, float (&acc)[NB][4]) {
+  typedef float f4 __attribute__((ext_vector_type(4)));
+  auto ld = [&](int g, DpW<WT> &wv, f4 (&xv)[NB]) {
+    dpart_ld<WT>(w, (g * D + 4 * q) * 4, wv);
+#pragma unroll
+    for (int b = 0; b < NB; b++) xv[b] = *reinterpret_cast<const XE_LDS f4 *>(a + b * act_ld + 4 * g);
+  };
+  auto comp = [&](const DpW<WT> &wv, const f4 (&xv)[NB]) {
+#pragma unroll
+    for (int kk = 0; kk < 4; kk++) {
+      float wf[4];
+#pragma unroll
+      for (int e = 0; e < 4; e++) wf[e] = dpart_wv<WT>(wv, e, kk);
+#pragma unroll
+      for (int b = 0; b < NB; b++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) acc[b][e] = __builtin_fmaf(wf[e], xv[b][kk], acc[b][e]);
+    }
+  };
+  if (g1 <= g0) return;
+  DpW<WT> wa, wb;
+  f4 xa[NB], xb[NB];
+  ld(g0, wa, xa);
+  int g = g0;
+  for (; g + 2 <= g1; g += 2) {
+    ld(g + 1, wb, xb);
+    comp(wa, xa);
+    if (g + 2 < g1) ld(g + 2, wa, xa);
+    comp(wb, xb);
+  }
+  if (g < g1) comp(wa, xa);
+}
+
+template <int WT, int NB, typename DD, typename TS>
+__device__ __forceinline__ void dpart_block(const DD &dp, int nb, int kn, const float *act, int act_ld,
+                                            const float *stage, float *obuf, int rank, unsigned ep, TS &&tsub) {
+  typedef float f4 __attribute__((ext_vector_type(4)));
+  const XE_LDS uint8_t *w = reinterpret_cast<const XE_LDS uint8_t *>(lptr(stage)) + kStageZero;
+  const XE_LDS float *a = lptr(act);
+  XE_LDS float *o = lptr(obuf);
+  const int D = dp.d, ng = kn / 4;
+  const DpartMap m = dpart_map(D, kn);
+  XE_LDS float *tp = o + nb * D;  // tail partials [S][nb][tq][4]
+  for (int q = threadIdx.x; q < m.hq; q += kT) {
+    float acc[NB][4];
+#pragma unroll
+    for (int b = 0; b < NB; b++)
+#pragma unroll
+      for (int e = 0; e < 4; e++) acc[b][e] = 0.f;
+    dpart_groups<WT, NB>(w, a, act_ld, D, q, 0, ng, acc);
+#pragma unroll
+    for (int b = 0; b < NB; b++)
+      if (b < nb) *reinterpret_cast<XE_LDS f4 *>(o + b * D + 4 * q) = f4{acc[b][0], acc[b][1], acc[b][2], acc[b][3]};
+  }
+  {
+    const int it = static_cast<int>(threadIdx.x) - m.tb;
+    if (it >= 0 && it < m.tq * m.S) {
+      const int qi = it % m.tq, sg = it / m.tq;
+      float acc[NB][4];
+#pragma unroll
+      for (int b = 0; b < NB; b++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) acc[b][e] = 0.f;
+      dpart_groups<WT, NB>(w, a, act_ld, D, m.hq + qi, sg * ng / m.S, (sg + 1) * ng / m.S, acc);
+#pragma unroll
+      for (int b = 0; b < NB; b++)
+        if (b < nb)
+          *reinterpret_cast<XE_LDS f4 *>(tp + ((sg * nb + b) * m.tq + qi) * 4) =
+              f4{acc[b][0], acc[b][1], acc[b][2], acc[b][3]};
+    }
+  }
+  tsub(1);
+  __syncthreads();
+  tsub(2);
+  for (int t = threadIdx.x; t < nb * D; t += kT) {
+    const int b = t / D, r = t - b * D;
+    float v;
+    if (r < 4 * m.hq) {
+      v = o[t];
+    } else {
+      const int ri = r - 4 * m.hq;
+      v = tp[(b * m.tq) * 4 + ri];
+      for (int sg = 1; sg < m.S; sg++) v += tp[((sg * nb + b) * m.tq) * 4 + ri];
+    }
+    put(dp.part, b, rank * D + r, v, ep);
+  }
+}
+
+// Rows [r0, r1) of the FFN output: the nparts ranks' partials summed, times
+// scale (int8 weights), plus bias.  Lane t polls parts p = t / kRedRows + i
+// * (kT / kRedRows) of row j = t % kRedRows and adds them in i order; the
+// lanes of a row meet by lane swaps (fixed pattern), the waves in LDS (wave
+// order).  tab: LDS >= kW * NB * kRedRows + 2 * 256 floats.
+constexpr int kRedRows = 8;      // output rows a rank sums (at most)
+constexpr int kRedParts = 256;   // partials per output (at most)
+template <int NB, typename RD, typename TS>
+__device__ __forceinline__ bool reduce_block(const RD &rd, int nb, int r0, int r1, float *tab_, unsigned ep,
+                                             const Ctl &c, TS &&tsub) {
+  XE_LDS float *wsum = lptr(tab_);                    // [kW][NB][kRedRows]
+  XE_LDS float *sb_ = wsum + kW * NB * kRedRows;      // scale | bias (aligned blocks)
+  const int nr = r1 - r0, np = rd.nparts;
+  // scale / bias of the rows: the 16-byte blocks holding them, copied into
+  // LDS ahead of the poll
+  const int a0 = r0 & ~3;
+  if (rd.scale != nullptr) lds_copy(rd.scale + a0, (r1 - a0) * 4, reinterpret_cast<XE_LDS uint8_t *>(sb_));
+  if (rd.bias != nullptr) lds_copy(rd.bias + a0, (r1 - a0) * 4, reinterpret_cast<XE_LDS uint8_t *>(sb_ + 256));
+  constexpr int PI = kRedParts * kRedRows / kT;  // polls per lane and batch row
+  constexpr int NI = NB * PI;
+  const int j = threadIdx.x & (kRedRows - 1), p0 = threadIdx.x / kRedRows;
+  int idx[NI];
+  bool need[NI];
+  float got[NI];
+#pragma unroll
+  for (int b = 0; b < NB; b++)
+#pragma unroll
+    for (int i = 0; i < PI; i++) {
+      const int p = p0 + i * (kT / kRedRows);
+      need[b * PI + i] = j < nr && p < np && b < nb;
+      idx[b * PI + i] = need[b * PI + i] ? b * rd.part.ld + p * rd.d + r0 + j : 0;
+      got[b * PI + i] = 0.f;
+    }
+  const bool okp = get_scattered<NI>(rd.part.p, idx, need, got, ep, c);
+  if (!okp) raise_stop(c);
+  tsub(1);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int b = 0; b < NB; b++) {
+    if (b >= nb) break;
+    float v = got[b * PI];
+#pragma unroll
+    for (int i = 1; i < PI; i++) v += got[b * PI + i];
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, true));  // row_ror:8
+    auto swap_add = [](float x, bool half32) {
+      const auto r = half32 ? __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false)
+                            : __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+      return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    };
+    v = swap_add(swap_add(v, false), true);
+    if (lane < kRedRows) wsum[(wave * NB + b) * kRedRows + lane] = v;
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // the scale / bias copies (and every wave's, after the barrier)
+  __syncthreads();
+  if (*lptr(c.bad)) return false;
+  if (threadIdx.x < nb * kRedRows) {
+    const int b = threadIdx.x / kRedRows, jj = threadIdx.x % kRedRows;
+    if (jj < nr) {
+      float t = 0.f;
+#pragma unroll
+      for (int w = 0; w < kW; w++) t += wsum[(w * NB + b) * kRedRows + jj];
+      if (rd.scale != nullptr) t *= sb_[r0 - a0 + jj];
+      if (rd.bias != nullptr) t += sb_[256 + r0 - a0 + jj];
+      put(rd.out, b, r0 + jj, t, ep);
+    }
+  }
+  __syncthreads();
+  return true;
 }
 
 // ---------------------------------------------------------------------------

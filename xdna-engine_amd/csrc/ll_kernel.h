@@ -94,8 +94,10 @@ __global__ __launch_bounds__(kT) void ll_step_kernel(StepParams sp) {
   const bool is_a = blockIdx.x % kRoleStride == 0;
   // the role's LDS layout (floats; every part 16-byte aligned)
   const int kin = is_a ? sp.kin_a : sp.kin_f, stage_floats = is_a ? sp.stage_a : sp.stage_f;
+  const int nph = is_a ? sp.n_a : sp.n_f;
+  const XE_CONST Phase *ph = cptr(is_a ? sp.ph_a : sp.ph_f);
   float *xr = lds;                                     // residual copy [nb][D]
-  float *xin = lds + static_cast<size_t>(NB) * D;      // GEMV / attention input [nb][kin]
+  float *xin = xr + static_cast<size_t>(NB) * D;       // GEMV / attention input [nb][kin]
   float *scr = xin + static_cast<size_t>(NB) * kin;    // scratch
   float *stage = scr + ((sp.scratch + 3) & ~3);       // staged weight slices
   float *kvs = stage + stage_floats;                   // key/value stage (attention side)
@@ -104,8 +106,6 @@ __global__ __launch_bounds__(kT) void ll_step_kernel(StepParams sp) {
   const int rank = is_a ? static_cast<int>(blockIdx.x) / kRoleStride
                         : static_cast<int>(blockIdx.x) - static_cast<int>(blockIdx.x) / kRoleStride - 1;
   const int nranks = is_a ? n_a : grid - n_a;
-  const XE_CONST Phase *ph = cptr(is_a ? sp.ph_a : sp.ph_f);
-  const int nph = is_a ? sp.n_a : sp.n_f;
   if (threadIdx.x == 0) bad = 0;
   if (stage_floats > 0 && threadIdx.x < kStageZero / 4) stage[threadIdx.x] = 0.f;  // never copied over
   if (sp.trace)  // slots a workgroup never marks read as 0
@@ -132,17 +132,24 @@ __global__ __launch_bounds__(kT) void ll_step_kernel(StepParams sp) {
     const unsigned ep = sp.ep0 + static_cast<unsigned>(step);
     bool ok = true;
     for (int i = 0; i < nph && ok; i++) {
-      const XE_CONST Phase &P = ph[i];
-      if (P.issue >= 0 || P.kv_issue >= 0) __syncthreads();  // the stages' previous readers are done
-      if (P.issue >= 0) {  // a later phase's weight slice into the stage
-        const XE_CONST GemvD &sg = ph[P.issue].u.gemv;
-        const int unit = sg.act == ACT_GEGLU_TANH ? 2 : 1;
-        int s0, s1;
-        rank_rows(sg.m / unit, rank, nranks, s0, s1);
-        stage_issue<WT>(sg, s0 * unit, s1 * unit, stage);
+      const int kind = ph[i].kind, issue = ph[i].issue, kv_issue = ph[i].kv_issue;
+      if (issue >= 0 || kv_issue >= 0) __syncthreads();  // the stages' previous readers are done
+      if (issue >= 0) {  // a later phase's weight slice into the stage
+        if (ph[issue].kind == LK_DPART) {
+          const XE_CONST DpartD &sd = ph[issue].u.dpart;
+          int k0, k1;
+          dpart_slice(sd, rank, nranks, k0, k1);
+          dpart_stage_issue<WT>(sd, k0, k1, stage);
+        } else {
+          const XE_CONST GemvD &sg = ph[issue].u.gemv;
+          const int unit = (sg.act == ACT_GEGLU_TANH ? 2 : 1) * (sg.out_lds ? 4 : 1);
+          int s0, s1;
+          rank_rows(sg.m / unit, rank, nranks, s0, s1);
+          stage_issue<WT>(sg, s0 * unit, s1 * unit, stage);
+        }
       }
-      if (P.kv_issue >= 0) {  // the next attention block's keys / values into the key/value stage
-        const XE_CONST AttnD &ka = ph[P.kv_issue].u.attn;
+      if (kv_issue >= 0) {  // the next attention block's keys / values into the key/value stage
+        const XE_CONST AttnD &ka = ph[kv_issue].u.attn;
         const int split = rank % ka.max_splits, rest = rank / ka.max_splits;
         const int kvh = rest % ka.hkv, b = rest / ka.hkv;
         if (b < nb) {
@@ -150,16 +157,20 @@ __global__ __launch_bounds__(kT) void ll_step_kernel(StepParams sp) {
           if (kv_staged(ka, split, len)) kv_stage_issue<HD>(ka, split, kvh, b, len, kvs);
         }
       }
-      switch (P.kind) {
-        case LK_FOLD:
-          pre_w(P.u.fold.post_w, D, scr);
-          ok = fold(P.u.fold, nb, D, xr, xin, red, ep, c, scr);
+      switch (kind) {
+        case LK_FOLD: {
+          const XE_CONST FoldD &fd = ph[i].u.fold;
+          pre_w(fd.post_w, D, scr);
+          ok = fold(fd, nb, D, xr, xin, red, ep, c, scr);
           mark_ready(step, i);
           break;
+        }
         case LK_GEMV: {
-          const XE_CONST GemvD &g = P.u.gemv;
-          // GeGLU rows come in (gate, up) pairs: split on pair boundaries
-          const int unit = g.act == ACT_GEGLU_TANH ? 2 : 1;
+          const XE_CONST GemvD &g = ph[i].u.gemv;
+          const XE_CONST FoldD *gf = g.folds;
+          // GeGLU rows come in (gate, up) pairs: split on pair boundaries;
+          // activations kept for LK_DPART: on multiples of four of them
+          const int unit = (g.act == ACT_GEGLU_TANH ? 2 : 1) * (g.out_lds ? 4 : 1);
           int r0, r1;
           rank_rows(g.m / unit, rank, nranks, r0, r1);
           r0 *= unit;
@@ -167,21 +178,21 @@ __global__ __launch_bounds__(kT) void ll_step_kernel(StepParams sp) {
           auto prep = [&]() -> bool {
             bool r = true;
             // the last fold and an RMS norm share one reduction
-            const bool fuse = !g.in_vec && g.nfold > 0 && g.folds[g.nfold - 1].post_w &&
+            const bool fuse = !g.in_vec && g.nfold > 0 && gf[g.nfold - 1].post_w &&
                               (g.norm == XE_NORM_RMS1P || g.norm == XE_NORM_RMS);
             const int nplain = fuse ? g.nfold - 1 : g.nfold;
             // the gains of every fold and of the norm go to LDS before the
             // first poll: fold f's post gain in region f, then gamma (and
             // beta) (regions of nw_floats(D) floats in the scratch area)
             const int nwf = nw_floats(D);
-            for (int f = 0; f < g.nfold; f++) pre_w(g.folds[f].post_w, D, scr + f * nwf);
+            for (int f = 0; f < g.nfold; f++) pre_w(gf[f].post_w, D, scr + f * nwf);
             if (!g.in_vec) {
               pre_w(g.gamma, D, scr + g.nfold * nwf);
               if (!fuse) pre_w(g.beta, D, scr + (g.nfold + 1) * nwf);
             }
-            for (int f = 0; f < nplain && r; f++) r = fold(g.folds[f], nb, D, xr, xin, red, ep, c, scr + f * nwf);
+            for (int f = 0; f < nplain && r; f++) r = fold(gf[f], nb, D, xr, xin, red, ep, c, scr + f * nwf);
             if (r && fuse)
-              r = fold_rms(g.folds[g.nfold - 1], nb, D, xr, xin, red, g.eps, g.norm == XE_NORM_RMS1P, ep, c,
+              r = fold_rms(gf[g.nfold - 1], nb, D, xr, xin, red, g.eps, g.norm == XE_NORM_RMS1P, ep, c,
                            scr + (g.nfold - 1) * nwf);
             else if (r && g.in_vec) {
               // one round of loads covers the whole input up to kT * 8 pairs
@@ -199,11 +210,11 @@ __global__ __launch_bounds__(kT) void ll_step_kernel(StepParams sp) {
           auto tsub = [&](int sub) { mark(step, tslots + 4 + sp.n_a + sp.n_f + kSubSlots * ((is_a ? 0 : sp.n_a) + i) + sub); };
           // K-segment sums go to the scratch area (its norm gains are read by then)
           ok = gemv_any<WT, NB, false>(g, nb, r0, r1, xin, ep, prep, nullptr, 0, 0, none, c, tsub, stage,
-                                       g.staged != 0, scr);
+                                       g.staged != 0, scr, xin + g.out_lds, kin);
           break;
         }
         case LK_ATTN: {
-          const XE_CONST AttnD &a = P.u.attn;
+          const XE_CONST AttnD &a = ph[i].u.attn;
           // the first block's K/V loads overlap the wait for q (prep runs once)
           bool need_q = true;
           const int nblk = a.max_splits * a.hkv * nb;
@@ -230,8 +241,30 @@ __global__ __launch_bounds__(kT) void ll_step_kernel(StepParams sp) {
           }
           break;
         }
+        case LK_DPART: {  // this rank's share of the FFN output projection, as partials
+          const XE_CONST DpartD &dp = ph[i].u.dpart;
+          int k0, k1;
+          dpart_slice(dp, rank, nranks, k0, k1);
+          auto tsub = [&](int sub) { mark(step, tslots + 4 + sp.n_a + sp.n_f + kSubSlots * ((is_a ? 0 : sp.n_a) + i) + sub); };
+          // the stage copies (issued by the phase before) have landed in every wave
+          __builtin_amdgcn_s_waitcnt(0);
+          tsub(0);
+          __syncthreads();
+          mark_ready(step, i);
+          dpart_block<WT, NB>(dp, nb, k1 - k0, xin + dp.act_off, kin, stage, scr, rank, ep, tsub);
+          break;
+        }
+        case LK_REDUCE: {  // the partials summed for this rank's outputs
+          const XE_CONST ReduceD &rd = ph[i].u.reduce;
+          int r0, r1;
+          rank_rows(rd.d, rank, nranks, r0, r1);
+          auto tsub = [&](int sub) { mark(step, tslots + 4 + sp.n_a + sp.n_f + kSubSlots * ((is_a ? 0 : sp.n_a) + i) + sub); };
+          mark_ready(step, i);
+          ok = reduce_block<NB>(rd, nb, r0, r1, scr, ep, c, tsub);
+          break;
+        }
         case LK_MERGE: {
-          const XE_CONST MergeD &mg = P.u.merge;
+          const XE_CONST MergeD &mg = ph[i].u.merge;
           const int per_head = mg.hd / kDM;
           const int nblk = nb * mg.hq * per_head;
           for (int vb = rank; vb < nblk && ok; vb += nranks) {
