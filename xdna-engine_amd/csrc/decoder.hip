@@ -1132,6 +1132,8 @@ void build_ll_plan(xe_decoder *d, int B, xe_decoder::LLPlan &P) {
   for (int k : {D, F, hq}) if (k % 16) { P.why = "K not a multiple of 16"; return; }
   P.grid = d->dev->num_cus > 0 ? d->dev->num_cus : 256;
   const int n_a = (P.grid + ll::kRoleStride - 1) / ll::kRoleStride, n_f = P.grid - n_a;
+  const char *tail_env = std::getenv("XE_LL_TAIL");
+  const int tail_mode = tail_env ? std::atoi(tail_env) : 1;
 
   // exchange arena: offsets first, one allocation after
   size_t pairs = 0;
@@ -1202,6 +1204,7 @@ void build_ll_plan(xe_decoder *d, int B, xe_decoder::LLPlan &P) {
     gd.m = m.rows;
     gd.k = m.cols;
     ll_tile(m.rows, ranks, m.cols, act == ACT_GEGLU_TANH, m.wdtype, gd.lpr, gd.rpl);
+    gd.tail_split = tail_mode == 2 || (tail_mode == 1 && out_lds > 0) ? 1 : 0;
     gd.in_vec = in_vec >= 0 ? 1 : 0;
     gd.norm = norm_kind;
     gd.gamma = gamma;

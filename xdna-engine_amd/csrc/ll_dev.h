@@ -92,6 +92,9 @@ struct GemvD {
   // the waves split K into 1 << ks_log segments (rows the rank holds too few
   // to keep every wave busy); their partial sums meet in LDS
   int ks_log;
+  // 1: one tile's row groups past the fourth are K-split over waves 4..7
+  // (waves w and w + 4 share a SIMD; see gemv_rows)
+  int tail_split;
   // > 0: the activations stay in this workgroup's LDS (its slice of the
   // FFN's hidden vector, read by the next phase, LK_DPART) instead of `out`,
   // at this float offset into each input row
@@ -717,15 +720,29 @@ __device__ __forceinline__ bool gemv_rows(const GD &g, int nb, int r0, int r1, c
   const int rg = lane >> lpr_log, kl = lane & (LPR - 1);
   // K segments: wave w takes segment w % S of the chunks for the rows of
   // its group w / S
-  const int ks_log = HEAD ? 0 : g.ks_log, S = 1 << ks_log;
-  const int seg = wave & (S - 1), wgrp = wave >> ks_log;
+  const int ks_log = HEAD ? 0 : g.ks_log;
+  int S = 1 << ks_log;
+  int seg = wave & (S - 1), wgrp = wave >> ks_log;
   const int rows_per_wave = (64 >> lpr_log) * RPL;
   const int rows_per_tile = (kW >> ks_log) * rows_per_wave;
+  // Tail split: waves w and w + 4 share SIMD w % 4 (the older wave issues
+  // first), so in one tile of 5 or 6 row groups (one a wave) the waves past
+  // the fourth finish last, with their SIMD's other wave's work on top.
+  // Waves 0..3 keep groups 0..3; waves 4..7 share the rest, each taking a K
+  // segment (one group: quarters, two: halves); the segment sums meet in LDS.
+  const int nrg = (r1 - r0 + rows_per_wave - 1) / rows_per_wave;
+  const int tail = (!HEAD && g.tail_split && ks_log == 0 && (nrg == 5 || nrg == 6)) ? nrg - 4 : 0;
+  if (tail > 0 && wave >= 4) {
+    S = tail == 1 ? 4 : 2;
+    seg = (wave - 4) % S;
+    wgrp = 4 + (wave - 4) / S;
+  }
   const int K = g.k, nch = K / 16;
-  const int seg_ch = (nch + S - 1) >> ks_log;
+  const int seg_ch = (nch + S - 1) / S;
   const int c_lo = seg * seg_ch, c_hi = min(nch, c_lo + seg_ch);
   const int n_it = (seg_ch + LPR - 1) >> lpr_log;
   const int ntiles = r1 > r0 ? (r1 - r0 + rows_per_tile - 1) / rows_per_tile : 0;
+  const bool ksum = ks_log > 0 || tail > 0;  // some wave holds a K segment
   WRsrc rs;
   rs.w = gdev::coherent_rsrc(g.w);
   rs.e = gdev::coherent_rsrc(WT == XE_BFP16 ? static_cast<const void *>(g.exps) : g.w);
@@ -839,7 +856,7 @@ __device__ __forceinline__ bool gemv_rows(const GD &g, int nb, int r0, int r1, c
 #pragma unroll
         for (int i = 0; i < RPL; i++) acc[b][i] = flat[b * RPL + i];
     }
-    if (ks_log > 0) {  // segment sums in LDS, added in segment order by the segment-0 waves
+    if (ksum) {  // segment sums in LDS, added in segment order by the segment-0 waves
       XE_LDS float *kr = lptr(kred);
       const int slot = wgrp * rows_per_wave + rg * RPL;
       if (kl == 0)
