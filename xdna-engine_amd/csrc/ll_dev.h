@@ -367,6 +367,18 @@ __device__ __forceinline__ void sums(float (&v)[N], float *red, int &slot) {
 
 constexpr int kNontemporal = 2;  // cache-policy operand: nt (streamed once per step)
 
+// A workgroup barrier for LDS hand-offs only: this wave's LDS accesses are
+// complete, then s_barrier.  __syncthreads() also waits for the wave's
+// global stores (its workgroup-scope fence), which after the exchange puts
+// of a phase costs their write latency (~0.5 us) before anyone moves on;
+// exchange data never needs that wait (readers poll epochs).
+__device__ __forceinline__ void lds_barrier() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt, expcnt unconstrained
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
 // LDS-direct copies: kStageGran bytes a wave per load instruction.
 constexpr int kStageGran = 1024;
 __host__ __device__ inline int stage_pad(int bytes) { return (bytes + kStageGran - 1) / kStageGran * kStageGran; }
@@ -1177,7 +1189,7 @@ __device__ __forceinline__ bool reduce_block(const RD &rd, int nb, int r0, int r
       put(rd.out, b, r0 + jj, t, ep);
     }
   }
-  __syncthreads();
+  lds_barrier();
   return true;
 }
 
@@ -1691,27 +1703,22 @@ __device__ __forceinline__ bool attn_block(const AD &a, int split, int kvh, int 
       __hip_atomic_store(gptr_w(vrow) + j, kvb[HD / 2 + j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
-  // the waves' sums, four dims a thread (16-byte reads), into LDS (the Q.K
-  // operand area, free by now); then the partials go out with consecutive
-  // lanes on consecutive pairs (a store instruction covers whole lines)
-  XE_LDS float *outb = reinterpret_cast<XE_LDS float *>(bfr);  // [G][HD]
-  for (int t = threadIdx.x; t < G * HD / 4; t += kT) {
-    const int gg = t / (HD / 4), e4 = 4 * (t % (HD / 4));
-    f32x4_t v4[kW];
-#pragma unroll
-    for (int w = 0; w < kW; w++) v4[w] = *reinterpret_cast<const XE_LDS f32x4_t *>(red + (w * G + gg) * HD + e4);
-    f32x4_t sum = v4[0];
-#pragma unroll
-    for (int w = 1; w < kW; w++) sum += v4[w];
-    *reinterpret_cast<XE_LDS f32x4_t *>(outb + gg * HD + e4) = sum;
-  }
-  __syncthreads();
+  // the partials go out with consecutive lanes on consecutive pairs (a
+  // store instruction covers whole lines); each acc value is the waves' sum
+  // (wave order), read straight from the per-wave sums
   for (int t = threadIdx.x; t < G * (HD + 2); t += kT) {
     const int gg = t / (HD + 2), e = t % (HD + 2);
-    const float v = e == 0 ? st[gg] : (e == 1 ? st[16 + gg] : outb[gg * HD + e - 2]);
+    float v;
+    if (e < 2) {
+      v = st[16 * e + gg];
+    } else {
+      v = red[gg * HD + e - 2];
+#pragma unroll
+      for (int w = 1; w < kW; w++) v += red[(w * G + gg) * HD + e - 2];
+    }
     put(a.part, b, ((kvh * G + gg) * a.max_splits + split) * (HD + 2) + e, v, ep);
   }
-  __syncthreads();  // scratch is reused by the next block
+  lds_barrier();  // scratch is reused by the next block
   return true;
 }
 
@@ -1796,7 +1803,7 @@ __device__ __noinline__ bool merge_block(const XE_CONST MergeD &mg, int b, int h
     const float o = mg.div_norm ? at / ls : at * (1.0f / ls);
     put(mg.out, b, h * HD + e0 + e, o, ep);
   }
-  __syncthreads();
+  lds_barrier();
   return true;
 }
 

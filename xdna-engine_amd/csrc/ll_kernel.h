@@ -133,7 +133,7 @@ __global__ __launch_bounds__(kT) void ll_step_kernel(StepParams sp) {
     bool ok = true;
     for (int i = 0; i < nph && ok; i++) {
       const int kind = ph[i].kind, issue = ph[i].issue, kv_issue = ph[i].kv_issue;
-      if (issue >= 0 || kv_issue >= 0) __syncthreads();  // the stages' previous readers are done
+      if (issue >= 0 || kv_issue >= 0) lds_barrier();  // the stages' previous readers are done
       if (issue >= 0) {  // a later phase's weight slice into the stage
         if (ph[issue].kind == LK_DPART) {
           const XE_CONST DpartD &sd = ph[issue].u.dpart;
