@@ -1692,17 +1692,6 @@ __device__ __forceinline__ bool attn_block(const AD &a, int split, int kvh, int 
     }
   }
   __syncthreads();
-  // the new key / value into the cache: read from the next step on (the
-  // step-end fence orders these stores before the argmax hand-off); stored
-  // here so that no wait above includes their completion
-  if (appender && wave == kW - 1) {
-    uint32_t *krow = reinterpret_cast<uint32_t *>(kbase + static_cast<size_t>(posi) * HD);
-    uint32_t *vrow = reinterpret_cast<uint32_t *>(vbase + static_cast<size_t>(posi) * HD);
-    for (int j = lane; j < HD / 2; j += 64) {
-      __hip_atomic_store(gptr_w(krow) + j, kvb[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(gptr_w(vrow) + j, kvb[HD / 2 + j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-  }
   // the partials go out with consecutive lanes on consecutive pairs (a
   // store instruction covers whole lines); each acc value is the waves' sum
   // (wave order), read straight from the per-wave sums
@@ -1717,6 +1706,19 @@ __device__ __forceinline__ bool attn_block(const AD &a, int split, int kvh, int 
       for (int w = 1; w < kW; w++) v += red[(w * G + gg) * HD + e - 2];
     }
     put(a.part, b, ((kvh * G + gg) * a.max_splits + split) * (HD + 2) + e, v, ep);
+  }
+  // the new key / value into the cache: read from the next step on (the
+  // step-end fence orders these stores before the argmax hand-off); stored
+  // last so that no wait above includes their completion (the compiler
+  // waits for every vector-memory operation before an LDS read that an
+  // LDS-direct copy might still be writing)
+  if (appender && wave == kW - 1) {
+    uint32_t *krow = reinterpret_cast<uint32_t *>(kbase + static_cast<size_t>(posi) * HD);
+    uint32_t *vrow = reinterpret_cast<uint32_t *>(vbase + static_cast<size_t>(posi) * HD);
+    for (int j = lane; j < HD / 2; j += 64) {
+      __hip_atomic_store(gptr_w(krow) + j, kvb[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(gptr_w(vrow) + j, kvb[HD / 2 + j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
   }
   lds_barrier();  // scratch is reused by the next block
   return true;
