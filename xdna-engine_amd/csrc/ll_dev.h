@@ -1181,9 +1181,12 @@ __device__ __forceinline__ bool reduce_block(const RD &rd, int nb, int r0, int r
   if (threadIdx.x < nb * kRedRows) {
     const int b = threadIdx.x / kRedRows, jj = threadIdx.x % kRedRows;
     if (jj < nr) {
+      float ws[kW];  // every wave's read first, then the sum in wave order
+#pragma unroll
+      for (int w = 0; w < kW; w++) ws[w] = wsum[(w * NB + b) * kRedRows + jj];
       float t = 0.f;
 #pragma unroll
-      for (int w = 0; w < kW; w++) t += wsum[(w * NB + b) * kRedRows + jj];
+      for (int w = 0; w < kW; w++) t += ws[w];
       if (rd.scale != nullptr) t *= sb_[r0 - a0 + jj];
       if (rd.bias != nullptr) t += sb_[256 + r0 - a0 + jj];
       put(rd.out, b, r0 + jj, t, ep);
@@ -1701,9 +1704,13 @@ __device__ __forceinline__ bool attn_block(const AD &a, int split, int kvh, int 
     if (e < 2) {
       v = st[16 * e + gg];
     } else {
-      v = red[gg * HD + e - 2];
+      // all the waves' reads first, then the sum in wave order
+      float rv[kW];
 #pragma unroll
-      for (int w = 1; w < kW; w++) v += red[(w * G + gg) * HD + e - 2];
+      for (int w = 0; w < kW; w++) rv[w] = red[(w * G + gg) * HD + e - 2];
+      v = rv[0];
+#pragma unroll
+      for (int w = 1; w < kW; w++) v += rv[w];
     }
     put(a.part, b, ((kvh * G + gg) * a.max_splits + split) * (HD + 2) + e, v, ep);
   }
@@ -1796,11 +1803,16 @@ __device__ __noinline__ bool merge_block(const XE_CONST MergeD &mg, int b, int h
   __syncthreads();
   if (threadIdx.x < kDM) {
     const int e = threadIdx.x;
-    float ls = 0.f, at = 0.f;
+    float ls = 0.f, at = 0.f, wa[kW], wl[kW];  // every wave's reads first, then the sums in wave order
 #pragma unroll
     for (int w = 0; w < kW; w++) {
-      at += wsum[w * (kDM + 1) + e];
-      ls += wsum[w * (kDM + 1) + kDM];
+      wa[w] = wsum[w * (kDM + 1) + e];
+      wl[w] = wsum[w * (kDM + 1) + kDM];
+    }
+#pragma unroll
+    for (int w = 0; w < kW; w++) {
+      at += wa[w];
+      ls += wl[w];
     }
     const float o = mg.div_norm ? at / ls : at * (1.0f / ls);
     put(mg.out, b, h * HD + e0 + e, o, ep);
