@@ -1550,9 +1550,13 @@ __device__ __forceinline__ bool attn_block(const AD &a, int split, int kvh, int 
     }
     if (tile0 < s1) {
       f32x4_t cacc = {0.f, 0.f, 0.f, 0.f};
+      bf16x8_t bq[NJ];  // every B operand read first (one LDS latency, not NJ)
+#pragma unroll
+      for (int j = 0; j < NJ; j++) bq[j] = bfr[j * 64 + lane];
+      __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of the chain
 #pragma unroll
       for (int j = 0; j < NJ; j++)
-        cacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kf[j]), bfr[j * 64 + lane], cacc, 0, 0, 0);
+        cacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kf[j]), bq[j], cacc, 0, 0, 0);
       // lane (row group r, column n < G): keys tile0 + 4r + i, head n; the
       // mid and lo parts sit G and 2 G columns to the right (row_shl)
 #pragma unroll
