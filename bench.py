@@ -40,6 +40,13 @@ import numpy as np
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 HBM_PEAK_GBPS = 8000.0
+# HBM bytes per step of the low-latency step kernel at the default workload
+# (b = 1, prompt 512, decode to ctx 4096): rocprofv3 --pmc FETCH_SIZE and
+# WRITE_SIZE per dispatch over the timed region, each scaled by what the same
+# counter reads for a 1 GiB device copy (bench.py --copy-probe); commands and
+# numbers in profiles/ll_traffic_gemma3_1b_b1.md.  Measured offline (counters
+# need their own profiler run); null for any other workload.
+LL_TRAFFIC_BYTES_PER_STEP = 1345337816
 
 
 def load_xe():
@@ -148,7 +155,10 @@ def run_batch(xe, dev, cfg, args, B, steps, warmup, profile):
         "roofline": {"bound": "hbm", "kernel": r_kernel,
                      "achieved": round(r_gbps, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(r_gbps / HBM_PEAK_GBPS, 4),
-                     "traffic": None, "bytes": int(r_bytes), "us": round(r_us, 2)},
+                     "traffic": (LL_TRAFFIC_BYTES_PER_STEP if executor == "ll" and B == 1 and
+                                 args.prompt == 512 and args.ctx == 4096 and args.steps == 0 else None),
+                     "traffic_unit": "bytes per step",
+                     "bytes": int(r_bytes), "us": round(r_us, 2)},
     }
     if profile:
         res["phases"] = {l: {"launches": v[0], "us": round(v[1], 2),
@@ -173,7 +183,20 @@ def main():
     ap.add_argument("--seed", type=int, default=2)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="only copy MIB MiB device to device (torch), three times: the plain "
+                         "copy kernel that scales rocprofv3's FETCH_SIZE / WRITE_SIZE counters")
     args = ap.parse_args()
+    if args.copy_probe > 0:
+        import torch
+        n = args.copy_probe * (1 << 20) // 4
+        x = torch.ones(n, dtype=torch.float32, device="cuda:0")
+        y = torch.empty_like(x)
+        for _ in range(3):
+            y.copy_(x)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_probe_bytes": n * 4, "copies": 3}), flush=True)
+        return
     if args.gpus != 1:
         print("bench.py: this build runs on one GPU only (every GPU box here has one); "
               "--gpus %d is not supported" % args.gpus, file=sys.stderr)
