@@ -260,6 +260,105 @@ void xo_gemv_i8(const float *x, int b, int k, int m, const int8_t *q,
   }
 }
 
+/* xo_gemv_i8 over a copy of q stored in blocks of eight rows, k-major
+ * (qb[(blk * K + j) * 8 + i] = q[blk * 8 + i, j]; rows past M are zero).
+ * Each output still accumulates x[j] * q[r, j] for j = 0..K-1 in order in
+ * its own fp32 accumulator (a separate multiply and add, as in the scalar
+ * loop): the eight lanes of a block, and the blocks, are independent sums,
+ * so the AVX2 form computes exactly what the scalar form does. */
+static void xo_dot8_i8_scalar(const float *xb, int k, const int8_t *tq, int nb, float *out) {
+  for (int bl = 0; bl < nb; bl++) {
+    const int8_t *t = tq + (size_t)bl * k * 8;
+    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int j = 0; j < k; j++) {
+      float xj = xb[j];
+      for (int i = 0; i < 8; i++) acc[i] += xj * (float)t[(size_t)j * 8 + i];
+    }
+    for (int i = 0; i < 8; i++) out[bl * 8 + i] = acc[i];
+  }
+}
+
+#if defined(__x86_64__)
+#include <immintrin.h>
+/* Four blocks (32 rows) per pass: four independent accumulator vectors. */
+__attribute__((target("avx2")))
+static void xo_dot8_i8_avx2(const float *xb, int k, const int8_t *tq, int nb, float *out) {
+  int bl = 0;
+  for (; bl + 4 <= nb; bl += 4) {
+    const int8_t *t0 = tq + (size_t)bl * k * 8;
+    const int8_t *t1 = t0 + (size_t)k * 8, *t2 = t1 + (size_t)k * 8, *t3 = t2 + (size_t)k * 8;
+    __m256 a0 = _mm256_setzero_ps(), a1 = _mm256_setzero_ps();
+    __m256 a2 = _mm256_setzero_ps(), a3 = _mm256_setzero_ps();
+    for (int j = 0; j < k; j++) {
+      __m256 xj = _mm256_broadcast_ss(xb + j);
+      __m256 w0 = _mm256_cvtepi32_ps(_mm256_cvtepi8_epi32(_mm_loadl_epi64((const __m128i *)(t0 + (size_t)j * 8))));
+      __m256 w1 = _mm256_cvtepi32_ps(_mm256_cvtepi8_epi32(_mm_loadl_epi64((const __m128i *)(t1 + (size_t)j * 8))));
+      __m256 w2 = _mm256_cvtepi32_ps(_mm256_cvtepi8_epi32(_mm_loadl_epi64((const __m128i *)(t2 + (size_t)j * 8))));
+      __m256 w3 = _mm256_cvtepi32_ps(_mm256_cvtepi8_epi32(_mm_loadl_epi64((const __m128i *)(t3 + (size_t)j * 8))));
+      a0 = _mm256_add_ps(a0, _mm256_mul_ps(xj, w0));
+      a1 = _mm256_add_ps(a1, _mm256_mul_ps(xj, w1));
+      a2 = _mm256_add_ps(a2, _mm256_mul_ps(xj, w2));
+      a3 = _mm256_add_ps(a3, _mm256_mul_ps(xj, w3));
+    }
+    _mm256_storeu_ps(out + bl * 8, a0);
+    _mm256_storeu_ps(out + bl * 8 + 8, a1);
+    _mm256_storeu_ps(out + bl * 8 + 16, a2);
+    _mm256_storeu_ps(out + bl * 8 + 24, a3);
+  }
+  if (bl < nb) xo_dot8_i8_scalar(xb, k, tq + (size_t)bl * k * 8, nb - bl, out + bl * 8);
+}
+#endif
+
+static void xo_dot8_i8(const float *xb, int k, const int8_t *tq, int nb, float *out) {
+#if defined(__x86_64__)
+  if (__builtin_cpu_supports("avx2")) {
+    xo_dot8_i8_avx2(xb, k, tq, nb, out);
+    return;
+  }
+#endif
+  xo_dot8_i8_scalar(xb, k, tq, nb, out);
+}
+
+static int8_t *xo_block8_i8(const int8_t *q, int m, int k) {
+  int nblk = (m + 7) / 8;
+  int8_t *qb = (int8_t *)calloc((size_t)nblk * k * 8, 1);
+#pragma omp parallel for schedule(static)
+  for (int blk = 0; blk < nblk; blk++)
+    for (int i = 0; i < 8 && blk * 8 + i < m; i++) {
+      const int8_t *row = q + (size_t)(blk * 8 + i) * k;
+      int8_t *dst = qb + (size_t)blk * k * 8 + i;
+      for (int j = 0; j < k; j++) dst[(size_t)j * 8] = row[j];
+    }
+  return qb;
+}
+
+static void xo_gemv_i8_blocked(const float *xb, int k, int m, const int8_t *qb,
+                               const float *s, const float *bias, float *y) {
+  int nblk = (m + 7) / 8, ngrp = (nblk + 3) / 4;
+#pragma omp parallel for schedule(static)
+  for (int g = 0; g < ngrp; g++) {
+    int b0 = g * 4, nb = nblk - b0 < 4 ? nblk - b0 : 4;
+    float acc[32];
+    xo_dot8_i8(xb, k, qb + (size_t)b0 * k * 8, nb, acc);
+    for (int i = 0; i < nb * 8 && b0 * 8 + i < m; i++) {
+      int r = b0 * 8 + i;
+      float v = acc[i] * s[r];
+      y[r] = bias ? v + bias[r] : v;
+    }
+  }
+}
+
+/* xo_gemv_i8 through the row-blocked copy the decoder models use
+ * (xo_block8_i8 + xo_gemv_i8_blocked).  Pins: equal to xo_gemv_i8 bit for
+ * bit on ragged shapes (tests/test_oracle.py). */
+void xo_gemv_i8_rowblocked(const float *x, int b, int k, int m, const int8_t *q,
+                           const float *s, const float *bias, float *y) {
+  int8_t *qb = xo_block8_i8(q, m, k);
+  for (int bi = 0; bi < b; bi++)
+    xo_gemv_i8_blocked(x + (size_t)bi * k, k, m, qb, s, bias, y + (size_t)bi * m);
+  free(qb);
+}
+
 /* Lin::fwd int8 verbatim loop shape: W [K,N], k-outer (opt125m_decode.rs:
  * 106-125).  Kept to pin xo_gemv_i8 against the reference's own layout. */
 void xo_lin_fwd_i8_kn(const float *x, int b, int k, int n, const int8_t *q_kn,
@@ -631,6 +730,15 @@ float xo_synth_value(uint64_t base, uint64_t idx, float mean, float stdv) {
   return v + mean;
 }
 
+/* Elements [start, start + n) of a synthetic stream (the product's
+ * xe_buf_fill_synthetic, before its storage rounding). */
+void xo_synth_fill_range(uint64_t seed, uint32_t tensor, float mean, float stdv,
+                         uint64_t start, float *out, size_t n) {
+  uint64_t base = xo_synth_base(seed, tensor);
+#pragma omp parallel for schedule(static)
+  for (size_t i = 0; i < n; i++) out[i] = xo_synth_value(base, start + i, mean, stdv);
+}
+
 void xo_synth_fill(uint64_t seed, uint32_t tensor, float mean, float stdv,
                    float *out, size_t n) {
   uint64_t base = xo_synth_base(seed, tensor);
@@ -649,6 +757,7 @@ typedef struct {
   float mean, stdv;
   float *f32;       /* unquantised tensors */
   int8_t *q;        /* XE_I8 */
+  int8_t *qb;       /* XE_I8 copy in blocks of 8 rows, k-major (xo_block8_i8) */
   float *s;
   uint16_t *bf;     /* XE_BF16 */
   int8_t *mant;     /* XE_BFP16 */
@@ -663,6 +772,12 @@ struct xo_model {
   uint16_t *kc, *vc;           /* [L][batch][hkv][max_ctx][hd] bf16 */
   uint16_t *xk, *xv;           /* Whisper cross K/V [L][h][n_cross][hd] */
   float *rope_cos, *rope_sin;  /* [max_ctx][hd/2] */
+  /* fp32 K/V caches (self and cross), used instead of the bf16 ones when
+   * kv_f32 is set: the reference CPU paths keep their caches in f32
+   * (opt125m_decode.rs:263-268, whisper_decoder.rs:458, 472). */
+  int kv_f32;
+  float *kcf, *vcf, *xkf, *xvf;
+  int mutation; /* XO_MUT_*: a planted composition mistake (tests only) */
 };
 
 /* Shape + init law of every tensor a family has.  Linear weights, biases and
@@ -735,6 +850,7 @@ static void xo_tensor_build(xo_model *m, int kind, int layer) {
     t->q = (int8_t *)malloc(n);
     t->s = (float *)malloc((size_t)R * 4);
     xo_quant_rows_i8(w, R, C, t->q, t->s);
+    t->qb = xo_block8_i8(t->q, R, C);
   } else if (m->c.wdtype == XE_BF16) {
     t->bf = (uint16_t *)malloc(n * 2);
     xo_pack_bf16(w, t->bf, n);
@@ -756,7 +872,8 @@ static void xo_rope_table(xo_model *m) {
   for (int p = 0; p < T; p++)
     for (int i = 0; i < half; i++) {
       float e = (float)(2 * i) / (float)hd;
-      float inv = 1.0f / powf(m->c.rope_theta, e);
+      float theta = m->mutation == XO_MUT_ROPE_THETA ? 10000.0f : m->c.rope_theta;
+      float inv = 1.0f / powf(theta, e);
       float ang = (float)p * inv;
       float cv = cosf(ang), sv = sinf(ang);
       m->rope_cos[(size_t)p * hd + i] = cv;
@@ -788,9 +905,10 @@ void xo_model_free(xo_model *m) {
   for (int k = 0; k < XE_T_COUNT; k++)
     for (int l = 0; l < 65; l++) {
       xo_tensor *t = &m->t[k][l];
-      free(t->f32); free(t->q); free(t->s); free(t->bf); free(t->mant); free(t->exps);
+      free(t->f32); free(t->q); free(t->qb); free(t->s); free(t->bf); free(t->mant); free(t->exps);
     }
   free(m->kc); free(m->vc); free(m->xk); free(m->xv);
+  free(m->kcf); free(m->vcf); free(m->xkf); free(m->xvf);
   free(m->rope_cos); free(m->rope_sin);
   free(m);
 }
@@ -799,6 +917,30 @@ void xo_model_reset(xo_model *m) {
   size_t kv = (size_t)m->c.n_layers * m->batch * m->c.n_kv_heads * m->c.max_ctx * m->c.head_dim;
   memset(m->kc, 0, kv * 2);
   memset(m->vc, 0, kv * 2);
+  if (m->kcf) {
+    memset(m->kcf, 0, kv * 4);
+    memset(m->vcf, 0, kv * 4);
+  }
+}
+
+/* Keep the K/V caches (self and, after the next set_cross, cross) in fp32
+ * instead of rounding them to bf16: the reference CPU decoders' own choice
+ * (opt125m_decode.rs:263-268, whisper_decoder.rs:458, 472).  The product
+ * rounds K/V to bf16, so the bf16 caches are the
+ * default; the fp32 mode exists to compare the oracle's decoder composition
+ * with independent fp32 implementations.  Clears the caches. */
+int xo_model_set_kv_f32(xo_model *m, int on) {
+  size_t kv = (size_t)m->c.n_layers * m->batch * m->c.n_kv_heads * m->c.max_ctx * m->c.head_dim;
+  free(m->kcf); free(m->vcf); free(m->xkf); free(m->xvf);
+  m->kcf = m->vcf = m->xkf = m->xvf = NULL;
+  m->kv_f32 = on ? 1 : 0;
+  if (on) {
+    m->kcf = (float *)calloc(kv, 4);
+    m->vcf = (float *)calloc(kv, 4);
+    if (!m->kcf || !m->vcf) return -1;
+  }
+  xo_model_reset(m);
+  return 0;
 }
 
 static const xo_tensor *T(const xo_model *m, int kind, int layer) {
@@ -813,7 +955,7 @@ static void xo_lin(const xo_model *m, int kind, int layer, int bias_kind,
   const xo_tensor *b = bias_kind >= 0 ? T(m, bias_kind, layer) : NULL;
   const float *bias = b ? b->f32 : NULL;
   if (m->c.wdtype == XE_I8)
-    xo_gemv_i8(x, 1, w->cols, w->rows, w->q, w->s, bias, y);
+    xo_gemv_i8_blocked(x, w->cols, w->rows, w->qb, w->s, bias, y);
   else if (m->c.wdtype == XE_BF16)
     xo_gemv_bf16w(x, 1, w->cols, w->rows, w->bf, bias, y);
   else
@@ -835,15 +977,33 @@ static void xo_embed_row(const xo_model *m, int tok, float *x) {
   }
 }
 
+/* Plant one composition mistake (XO_MUT_*; 0 restores the faithful step).
+ * Test infrastructure: the HF cross-check fixtures must catch every one of
+ * them, which shows the fixtures pin the composition. */
+int xo_model_set_mutation(xo_model *m, int code) {
+  m->mutation = code;
+  if (m->c.family == XE_GEMMA3) {
+    free(m->rope_cos);
+    free(m->rope_sin);
+    xo_rope_table(m);
+  }
+  return 0;
+}
+
 int xo_model_set_cross(xo_model *m, const float *enc) {
   if (m->c.family != XE_WHISPER) return -1;
   int Tn = m->c.n_cross, D = m->c.d_model, H = m->c.n_heads, hd = m->c.head_dim, L = m->c.n_layers;
   const float *src = enc ? enc : T(m, XE_T_ENC_OUT, -1)->f32;
   float *e = (float *)malloc((size_t)Tn * D * 4);
   for (size_t i = 0; i < (size_t)Tn * D; i++) e[i] = xo_bf16_round(src[i]);
-  free(m->xk); free(m->xv);
+  free(m->xk); free(m->xv); free(m->xkf); free(m->xvf);
+  m->xkf = m->xvf = NULL;
   m->xk = (uint16_t *)malloc((size_t)L * Tn * D * 2);
   m->xv = (uint16_t *)malloc((size_t)L * Tn * D * 2);
+  if (m->kv_f32) {
+    m->xkf = (float *)malloc((size_t)L * Tn * D * 4);
+    m->xvf = (float *)malloc((size_t)L * Tn * D * 4);
+  }
   /* precompute_cross (whisper_decoder.rs:1143-1232 / host path :388-397):
    * K = enc . cross_k (no bias), V = enc . cross_v + b, stored bf16 in the
    * head-major [h][t][hd] layout of the fused path (:1167-1186). */
@@ -857,6 +1017,10 @@ int xo_model_set_cross(xo_model *m, const float *enc) {
         for (int j = 0; j < hd; j++) {
           size_t o = (((size_t)l * H + h) * Tn + t) * hd + j;
           m->xk[o] = xo_f32_to_bf16_bits(kr[h * hd + j]);
+          if (m->xkf) {
+            m->xkf[o] = kr[h * hd + j];
+            m->xvf[o] = vr[h * hd + j];
+          }
           m->xv[o] = xo_f32_to_bf16_bits(vr[h * hd + j]);
         }
     }
@@ -870,6 +1034,104 @@ static void xo_rope_apply(const xo_model *m, float *v, int pos) {
   float tmp[1024];
   xo_rope(v, 1, 1, hd, m->rope_cos + (size_t)pos * hd, m->rope_sin + (size_t)pos * hd, tmp);
   memcpy(v, tmp, (size_t)hd * 4);
+}
+
+/* Scores of keys [j0, min(j0 + 8, len)): sc[j] = (sum over t = 0..hd-1 in
+ * order of q[t] * k[j][t]) * scale, each key its own sequential f32 sum.
+ * The AVX2 form runs the eight keys in the eight lanes (gathering k[j][t]
+ * across keys), which leaves every key's arithmetic the scalar loop's. */
+static void xo_scores8_scalar(const float *qh, const uint16_t *kb, const float *kf, int j0,
+                              int len, int hd, float scale, float *sc) {
+  for (int j = j0; j < len && j < j0 + 8; j++) {
+    float dot = 0.f;
+    if (kf)
+      for (int t = 0; t < hd; t++) dot += qh[t] * kf[(size_t)j * hd + t];
+    else
+      for (int t = 0; t < hd; t++) dot += qh[t] * xo_bf16_bits_to_f32(kb[(size_t)j * hd + t]);
+    sc[j] = dot * scale;
+  }
+}
+
+#if defined(__x86_64__)
+__attribute__((target("avx2")))
+static void xo_scores8_avx2(const float *qh, const uint16_t *kb, const float *kf, int j0,
+                            int hd, float scale, float *sc) {
+  __m256 acc = _mm256_setzero_ps();
+  if (kf) {
+    const __m256i idx = _mm256_mullo_epi32(_mm256_setr_epi32(0, 1, 2, 3, 4, 5, 6, 7),
+                                           _mm256_set1_epi32(hd));
+    const float *base = kf + (size_t)j0 * hd;
+    for (int t = 0; t < hd; t++) {
+      __m256 kv = _mm256_i32gather_ps(base + t, idx, 4);
+      acc = _mm256_add_ps(acc, _mm256_mul_ps(_mm256_set1_ps(qh[t]), kv));
+    }
+  } else {
+    /* 32-bit words holding elements t (low half) and t + 1 (high half) */
+    const __m256i idx = _mm256_mullo_epi32(_mm256_setr_epi32(0, 1, 2, 3, 4, 5, 6, 7),
+                                           _mm256_set1_epi32(hd * 2));
+    const char *base = (const char *)(kb + (size_t)j0 * hd);
+    const __m256i hi_mask = _mm256_set1_epi32((int)0xffff0000u);
+    for (int t = 0; t < hd; t += 2) {
+      __m256i w = _mm256_i32gather_epi32((const int *)(base + 2 * t), idx, 1);
+      __m256 k0 = _mm256_castsi256_ps(_mm256_slli_epi32(w, 16));
+      __m256 k1 = _mm256_castsi256_ps(_mm256_and_si256(w, hi_mask));
+      acc = _mm256_add_ps(acc, _mm256_mul_ps(_mm256_set1_ps(qh[t]), k0));
+      acc = _mm256_add_ps(acc, _mm256_mul_ps(_mm256_set1_ps(qh[t + 1]), k1));
+    }
+  }
+  _mm256_storeu_ps(sc + j0, _mm256_mul_ps(acc, _mm256_set1_ps(scale)));
+}
+#endif
+
+static void xo_scores8(const float *qh, const uint16_t *kb, const float *kf, int j0, int len,
+                       int hd, float scale, float *sc) {
+#if defined(__x86_64__)
+  if (j0 + 8 <= len && hd % 2 == 0 && __builtin_cpu_supports("avx2")) {
+    xo_scores8_avx2(qh, kb, kf, j0, hd, scale, sc);
+    return;
+  }
+#endif
+  xo_scores8_scalar(qh, kb, kf, j0, len, hd, scale, sc);
+}
+
+/* One query head against `len` cached rows: attend_one per head
+ * (whisper_decoder.rs:242-278): scores (q . k) * scale in f32, max, exp and
+ * a sequential sum, then ctx += p * v over the keys in order.  OPT divides
+ * each probability by the sum (opt125m_decode.rs:277-280, div_by_sum);
+ * attend_one multiplies by 1/sum (:266-270).  Rows come from the bf16 cache
+ * (kb, vb) or the fp32 one (kf, vf).  The OpenMP splits are over keys (each
+ * score is its own dot product) and over output dimensions (each keeps the
+ * key order), so every value is the sequential computation. */
+static void xo_head_attend(const float *qh, const uint16_t *kb, const uint16_t *vb,
+                           const float *kf, const float *vf, int len, int hd, float scale,
+                           int div_by_sum, float *sc, float *oh) {
+  int nk8 = (len + 7) / 8;
+#pragma omp parallel for schedule(static) if (len >= 256)
+  for (int j8 = 0; j8 < nk8; j8++) xo_scores8(qh, kb, kf, j8 * 8, len, hd, scale, sc);
+  float mx = -INFINITY;
+  for (int j = 0; j < len; j++) mx = fmaxf(mx, sc[j]);
+  float sum = 0.f;
+  for (int j = 0; j < len; j++) {
+    sc[j] = expf(sc[j] - mx);
+    sum += sc[j];
+  }
+  float inv = 1.0f / sum;
+  for (int j = 0; j < len; j++) sc[j] = div_by_sum ? sc[j] / sum : sc[j] * inv;
+  int nblk = (hd + 15) / 16;
+#pragma omp parallel for schedule(static) if (len >= 256)
+  for (int tb = 0; tb < nblk; tb++) {
+    int t0 = tb * 16, t1 = t0 + 16 < hd ? t0 + 16 : hd;
+    float acc[16];
+    for (int t = t0; t < t1; t++) acc[t - t0] = 0.f;
+    for (int j = 0; j < len; j++) {
+      float p = sc[j];
+      if (vf)
+        for (int t = t0; t < t1; t++) acc[t - t0] += p * vf[(size_t)j * hd + t];
+      else
+        for (int t = t0; t < t1; t++) acc[t - t0] += p * xo_bf16_bits_to_f32(vb[(size_t)j * hd + t]);
+    }
+    for (int t = t0; t < t1; t++) oh[t] = acc[t - t0];
+  }
 }
 
 /* One stream's decode step.  OPT: Opt::step (opt125m_decode.rs:252-293).
@@ -897,10 +1159,10 @@ static void xo_step_one(xo_model *m, int b, int tok, int pos, float *logits) {
   xo_embed_row(m, tok, x);
   if (fam == XE_OPT || fam == XE_WHISPER) {
     const xo_tensor *pe = T(m, XE_T_POS_EMB, -1);
-    int prow = fam == XE_OPT ? pos + 2 : pos;
+    int prow = fam == XE_OPT ? pos + (m->mutation == XO_MUT_OPT_POS_OFFSET ? 1 : 2) : pos;
     for (int d = 0; d < D; d++) x[d] = x[d] + pe->f32[(size_t)prow * D + d];
   } else {
-    float nrm = sqrtf((float)D);
+    float nrm = m->mutation == XO_MUT_GEMMA_NO_EMB_SCALE ? 1.0f : sqrtf((float)D);
     for (int d = 0; d < D; d++) x[d] = x[d] * nrm;
   }
 
@@ -915,7 +1177,7 @@ static void xo_step_one(xo_model *m, int b, int tok, int pos, float *logits) {
     xo_lin(m, XE_T_V_W, l, XE_T_V_B, h, v);
     float scale;
     if (fam == XE_OPT) {
-      float s = powf((float)hd, -0.5f);
+      float s = m->mutation == XO_MUT_OPT_NO_Q_SCALE ? 1.0f : powf((float)hd, -0.5f);
       for (int i = 0; i < hq; i++) q[i] = q[i] * s;
       scale = 1.0f;
     } else if (fam == XE_WHISPER) {
@@ -937,40 +1199,28 @@ static void xo_step_one(xo_model *m, int b, int tok, int pos, float *logits) {
     for (int hh = 0; hh < Hk; hh++)
       for (int j = 0; j < hd; j++) {
         size_t off = ((lb + hh) * MC + pos) * hd + j;
-        m->kc[off] = xo_f32_to_bf16_bits(k[hh * hd + j]);
-        m->vc[off] = xo_f32_to_bf16_bits(v[hh * hd + j]);
+        if (m->kv_f32) {
+          m->kcf[off] = k[hh * hd + j];
+          m->vcf[off] = v[hh * hd + j];
+        } else {
+          m->kc[off] = xo_f32_to_bf16_bits(k[hh * hd + j]);
+          m->vc[off] = xo_f32_to_bf16_bits(v[hh * hd + j]);
+        }
       }
     int len = pos + 1;
     for (int hh = 0; hh < H; hh++) {
-      int kvh = hh / group;
-      const uint16_t *kh = m->kc + (lb + kvh) * MC * hd;
-      const uint16_t *vh = m->vc + (lb + kvh) * MC * hd;
-      const float *qh = q + hh * hd;
-      for (int j = 0; j < len; j++) {
-        float dot = 0.f;
-        for (int t = 0; t < hd; t++) dot += qh[t] * xo_bf16_bits_to_f32(kh[(size_t)j * hd + t]);
-        sc[j] = dot * scale;
-      }
-      float mx = -INFINITY;
-      for (int j = 0; j < len; j++) mx = fmaxf(mx, sc[j]);
-      float sum = 0.f;
-      for (int j = 0; j < len; j++) {
-        sc[j] = expf(sc[j] - mx);
-        sum += sc[j];
-      }
-      float inv = 1.0f / sum;
-      float *oh = ctx + hh * hd;
-      for (int t = 0; t < hd; t++) oh[t] = 0.f;
-      for (int j = 0; j < len; j++) {
-        /* OPT divides each prob by the sum (opt125m_decode.rs:280); attend_one
-         * multiplies by 1/sum (whisper_decoder.rs:266-270). */
-        float p = fam == XE_OPT ? sc[j] / sum : sc[j] * inv;
-        for (int t = 0; t < hd; t++) oh[t] += p * xo_bf16_bits_to_f32(vh[(size_t)j * hd + t]);
-      }
+      size_t base = (lb + hh / group) * MC * hd;
+      if (m->kv_f32)
+        xo_head_attend(q + hh * hd, NULL, NULL, m->kcf + base, m->vcf + base, len, hd, scale,
+                       fam == XE_OPT, sc, ctx + hh * hd);
+      else
+        xo_head_attend(q + hh * hd, m->kc + base, m->vc + base, NULL, NULL, len, hd, scale,
+                       fam == XE_OPT, sc, ctx + hh * hd);
     }
     xo_lin(m, XE_T_O_W, l, XE_T_O_B, ctx, o);
     if (fam == XE_GEMMA3) {
-      xo_rmsnorm(o, D, T(m, XE_T_POST_ATTN_W, l)->f32, eps, h);
+      xo_rmsnorm(o, D, T(m, m->mutation == XO_MUT_GEMMA_SWAP_POST_NORMS ? XE_T_POST_FFN_W : XE_T_POST_ATTN_W, l)->f32,
+                 eps, h);
       for (int d = 0; d < D; d++) x[d] = x[d] + h[d];
     } else {
       for (int d = 0; d < D; d++) x[d] = x[d] + o[d];
@@ -981,29 +1231,15 @@ static void xo_step_one(xo_model *m, int b, int tok, int pos, float *logits) {
       int Tn = c->n_cross;
       xo_layer_norm(x, 1, D, T(m, XE_T_LNX_W, l)->f32, T(m, XE_T_LNX_B, l)->f32, eps, h);
       xo_lin(m, XE_T_XQ_W, l, XE_T_XQ_B, h, q);
+      float xscale = m->mutation == XO_MUT_WHISPER_CROSS_SCALE ? 1.0f : scale;
       for (int hh = 0; hh < H; hh++) {
-        const uint16_t *kh = m->xk + ((size_t)l * H + hh) * Tn * hd;
-        const uint16_t *vh = m->xv + ((size_t)l * H + hh) * Tn * hd;
-        const float *qh = q + hh * hd;
-        for (int j = 0; j < Tn; j++) {
-          float dot = 0.f;
-          for (int t = 0; t < hd; t++) dot += qh[t] * xo_bf16_bits_to_f32(kh[(size_t)j * hd + t]);
-          sc[j] = dot * scale;
-        }
-        float mx = -INFINITY;
-        for (int j = 0; j < Tn; j++) mx = fmaxf(mx, sc[j]);
-        float sum = 0.f;
-        for (int j = 0; j < Tn; j++) {
-          sc[j] = expf(sc[j] - mx);
-          sum += sc[j];
-        }
-        float inv = 1.0f / sum;
-        float *oh = ctx + hh * hd;
-        for (int t = 0; t < hd; t++) oh[t] = 0.f;
-        for (int j = 0; j < Tn; j++) {
-          float p = sc[j] * inv;
-          for (int t = 0; t < hd; t++) oh[t] += p * xo_bf16_bits_to_f32(vh[(size_t)j * hd + t]);
-        }
+        size_t base = ((size_t)l * H + hh) * Tn * hd;
+        if (m->kv_f32)
+          xo_head_attend(q + hh * hd, NULL, NULL, m->xkf + base, m->xvf + base, Tn, hd, xscale, 0,
+                         sc, ctx + hh * hd);
+        else
+          xo_head_attend(q + hh * hd, m->xk + base, m->xv + base, NULL, NULL, Tn, hd, xscale, 0,
+                         sc, ctx + hh * hd);
       }
       xo_lin(m, XE_T_XO_W, l, XE_T_XO_B, ctx, o);
       for (int d = 0; d < D; d++) x[d] = x[d] + o[d];
@@ -1041,7 +1277,15 @@ static void xo_step_one(xo_model *m, int b, int tok, int pos, float *logits) {
   free(x); free(h); free(q); free(k); free(v); free(ctx); free(o); free(f1); free(f2); free(sc);
 }
 
+/* Streams are independent (own K/V rows, own outputs, read-only weights):
+ * with more than one, each thread takes whole streams and the OpenMP regions
+ * inside a step run on that thread alone (nested regions are inactive). */
 void xo_model_step(xo_model *m, const int *tokens, const int *pos, int batch, float *logits) {
+  if (batch == 1) { /* no enclosing region: the step's own regions use every thread */
+    xo_step_one(m, 0, tokens[0], pos[0], logits);
+    return;
+  }
+#pragma omp parallel for schedule(dynamic, 1)
   for (int b = 0; b < batch; b++)
     xo_step_one(m, b, tokens[b], pos[b], logits + (size_t)b * m->c.vocab);
 }
@@ -1059,24 +1303,35 @@ static float xo_margin(const float *v, int n, int best) {
 }
 
 /* Opt::generate (opt125m_decode.rs:296-315) for every stream. */
+/* One stream of xo_model_generate. */
+static void xo_generate_one(xo_model *m, int b, const int *prompt, int n_prompt, int n_new,
+                            int *out, float *margins) {
+  int V = m->c.vocab;
+  float *logits = (float *)malloc((size_t)V * 4);
+  for (int p = 0; p < n_prompt; p++) xo_step_one(m, b, prompt[p], p, logits);
+  int pos = n_prompt;
+  for (int i = 0; i < n_new; i++) {
+    int next = xo_model_argmax(m, logits);
+    out[i] = next;
+    if (margins) margins[i] = xo_margin(logits, V, next);
+    if (i + 1 == n_new) break;
+    xo_step_one(m, b, next, pos, logits);
+    pos++;
+  }
+  free(logits);
+}
+
 int xo_model_generate(xo_model *m, const int *prompt, int n_prompt, int batch,
                       int n_new, int *out, float *margins) {
   if (batch > m->batch || n_prompt < 1 || n_prompt + n_new > m->c.max_ctx + 1) return -1;
-  int V = m->c.vocab;
-  float *logits = (float *)malloc((size_t)V * 4);
-  for (int b = 0; b < batch; b++) {
-    for (int p = 0; p < n_prompt; p++) xo_step_one(m, b, prompt[(size_t)b * n_prompt + p], p, logits);
-    int pos = n_prompt;
-    for (int i = 0; i < n_new; i++) {
-      int next = xo_model_argmax(m, logits);
-      out[(size_t)b * n_new + i] = next;
-      if (margins) margins[(size_t)b * n_new + i] = xo_margin(logits, V, next);
-      if (i + 1 == n_new) break;
-      xo_step_one(m, b, next, pos, logits);
-      pos++;
-    }
+  if (batch == 1) {
+    xo_generate_one(m, 0, prompt, n_prompt, n_new, out, margins);
+    return 0;
   }
-  free(logits);
+#pragma omp parallel for schedule(dynamic, 1)
+  for (int b = 0; b < batch; b++)
+    xo_generate_one(m, b, prompt + (size_t)b * n_prompt, n_prompt, n_new, out + (size_t)b * n_new,
+                    margins ? margins + (size_t)b * n_new : NULL);
   return 0;
 }
 

@@ -61,6 +61,10 @@ void xo_dequant_epi(const int32_t *acc, int mp, int n, float scale_a,
 /* ---- weight-only GEMV / linear (opt125m_decode.rs:106-125) ---- */
 void xo_gemv_i8(const float *x, int b, int k, int m, const int8_t *q,
                 const float *s, const float *bias, float *y);
+/* xo_gemv_i8 computed from a k-major copy in blocks of 8 rows (the form
+ * the decoder models use); bit-identical to xo_gemv_i8. */
+void xo_gemv_i8_rowblocked(const float *x, int b, int k, int m, const int8_t *q,
+                           const float *s, const float *bias, float *y);
 void xo_lin_fwd_i8_kn(const float *x, int b, int k, int n, const int8_t *q_kn,
                       const float *s, const float *bias, float *y);
 void xo_gemv_f32(const float *x, int b, int k, int m, const float *w,
@@ -112,6 +116,8 @@ uint64_t xo_synth_base(uint64_t seed, uint32_t tensor);
 float xo_synth_value(uint64_t base, uint64_t idx, float mean, float stdv);
 void xo_synth_fill(uint64_t seed, uint32_t tensor, float mean, float stdv,
                    float *out, size_t n);
+void xo_synth_fill_range(uint64_t seed, uint32_t tensor, float mean, float stdv,
+                         uint64_t start, float *out, size_t n);
 
 /* ---- decoder models (configs 1, 4, 5) ----
  * The config struct and tensor kinds are the public ones of
@@ -121,6 +127,21 @@ xo_model *xo_model_create(const xe_model_config *cfg, uint64_t seed,
                           int batch);
 void xo_model_free(xo_model *m);
 void xo_model_reset(xo_model *m);
+/* fp32 K/V caches instead of bf16 (the reference CPU decoders' choice);
+ * clears them.  Used to compare the composition with fp32 implementations. */
+int xo_model_set_kv_f32(xo_model *m, int on);
+/* Planted composition mistakes, for tests that show the decoder fixtures
+ * catch them (0 = none). */
+enum {
+  XO_MUT_NONE = 0,
+  XO_MUT_OPT_POS_OFFSET = 1,       /* OPT position row pos + 1, not pos + 2 */
+  XO_MUT_GEMMA_SWAP_POST_NORMS = 2,/* post-attention norm with the post-FFN weight */
+  XO_MUT_GEMMA_NO_EMB_SCALE = 3,   /* no sqrt(d) embedding scale */
+  XO_MUT_ROPE_THETA = 4,           /* RoPE theta 1e4 instead of the config's */
+  XO_MUT_WHISPER_CROSS_SCALE = 5,  /* cross-attention scores without 1/sqrt(hd) */
+  XO_MUT_OPT_NO_Q_SCALE = 6        /* OPT q not scaled by hd^-0.5 */
+};
+int xo_model_set_mutation(xo_model *m, int code);
 /* enc [n_cross, d]; NULL = the synthetic XE_T_ENC_OUT tensor. */
 int xo_model_set_cross(xo_model *m, const float *enc);
 /* One step for every stream b < batch: tokens[b] at pos[b]. */

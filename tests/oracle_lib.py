@@ -60,6 +60,7 @@ def lib():
         "xo_quant_cols_i8": (None, [f32p, C.c_int, C.c_int, i8p, f32p]),
         "xo_dequant_epi": (None, [i32p, C.c_int, C.c_int, C.c_float, f32p, C.c_void_p, f32p]),
         "xo_gemv_i8": (None, [f32p, C.c_int, C.c_int, C.c_int, i8p, f32p, C.c_void_p, f32p]),
+        "xo_gemv_i8_rowblocked": (None, [f32p, C.c_int, C.c_int, C.c_int, i8p, f32p, C.c_void_p, f32p]),
         "xo_lin_fwd_i8_kn": (None, [f32p, C.c_int, C.c_int, C.c_int, i8p, f32p, C.c_void_p, f32p]),
         "xo_gemv_f32": (None, [f32p, C.c_int, C.c_int, C.c_int, f32p, C.c_void_p, f32p]),
         "xo_gemv_bf16w": (None, [f32p, C.c_int, C.c_int, C.c_int, u16p, C.c_void_p, f32p]),
@@ -81,9 +82,13 @@ def lib():
         "xo_synth_base": (C.c_uint64, [C.c_uint64, C.c_uint32]),
         "xo_synth_value": (C.c_float, [C.c_uint64, C.c_uint64, C.c_float, C.c_float]),
         "xo_synth_fill": (None, [C.c_uint64, C.c_uint32, C.c_float, C.c_float, f32p, C.c_size_t]),
+        "xo_synth_fill_range": (None, [C.c_uint64, C.c_uint32, C.c_float, C.c_float, C.c_uint64,
+                                       f32p, C.c_size_t]),
         "xo_model_create": (C.c_void_p, [C.POINTER(ModelConfig), C.c_uint64, C.c_int]),
         "xo_model_free": (None, [C.c_void_p]),
         "xo_model_reset": (None, [C.c_void_p]),
+        "xo_model_set_kv_f32": (C.c_int, [C.c_void_p, C.c_int]),
+        "xo_model_set_mutation": (C.c_int, [C.c_void_p, C.c_int]),
         "xo_model_set_cross": (C.c_int, [C.c_void_p, C.c_void_p]),
         "xo_model_step": (None, [C.c_void_p, i32p, i32p, C.c_int, f32p]),
         "xo_model_argmax": (C.c_int, [C.c_void_p, f32p]),
@@ -207,6 +212,20 @@ def synth_fill(seed, tensor, mean, std, n):
     return out
 
 
+def synth_range(seed, tensor, mean, std, start, n):
+    """Elements [start, start+n) of a synthetic stream, fp32."""
+    out = np.empty(n, np.float32)
+    lib().xo_synth_fill_range(seed, tensor, mean, std, start, out, n)
+    return out
+
+
+def round_half_away_i8(v):
+    """roundf + clamp(+-127) of fp32 values, as int8."""
+    v = np.asarray(v, np.float64)
+    r = np.sign(v) * np.floor(np.abs(v) + 0.5)
+    return np.clip(r, -127, 127).astype(np.int8)
+
+
 class OracleModel:
     """The oracle decoder (configs 1, 4, 5)."""
 
@@ -226,6 +245,14 @@ class OracleModel:
 
     def reset(self):
         lib().xo_model_reset(self.h)
+
+    def set_mutation(self, code):
+        """Plant a composition mistake (oracle XO_MUT_*), 0 for none."""
+        assert lib().xo_model_set_mutation(self.h, code) == 0
+
+    def set_kv_f32(self, on=True):
+        """fp32 K/V caches (the reference CPU decoders' choice) instead of bf16."""
+        assert lib().xo_model_set_kv_f32(self.h, 1 if on else 0) == 0
 
     def set_cross(self, enc=None):
         e = None if enc is None else np.ascontiguousarray(enc, np.float32)

@@ -199,6 +199,21 @@ def test_gemv_i8_matches_reference_kn_loop_bitwise():
     assert np.array_equal(y_kn.view(np.uint32), y_mk.view(np.uint32))
 
 
+@pytest.mark.parametrize("m,k", [(1, 7), (8, 64), (37, 96), (97, 200), (257, 1152)])
+def test_gemv_i8_rowblocked_equals_scalar_bitwise(m, k):
+    """The decoder models' GEMV (row blocks of 8, k-major, vector code) is
+    the scalar k-ordered loop bit for bit, ragged row counts included."""
+    rng = np.random.default_rng(m * 1000 + k)
+    q = rng.integers(-127, 128, (m, k)).astype(np.int8)
+    s = rng.uniform(0.001, 0.02, m).astype(np.float32)
+    bias = rng.standard_normal(m).astype(np.float32)
+    x = rng.standard_normal((2, k)).astype(np.float32)
+    want = O.gemv_i8(x, q, s, bias)
+    got = np.empty((2, m), np.float32)
+    L().xo_gemv_i8_rowblocked(x, 2, k, m, q, s, O.ptr(bias), got)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
 def test_gemv_i8_integer_inputs_exact():
     rng = np.random.default_rng(2)
     q = rng.integers(-127, 128, (33, 64)).astype(np.int8)

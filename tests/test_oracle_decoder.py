@@ -1,0 +1,108 @@
+"""The oracle's decoder composition (xo_step_one, oracle/xe_oracle.c) against
+Hugging Face's OPT, Whisper-decoder and Gemma-3 implementations.
+
+tests/golden/hf_decoder_*.npz hold HF's fp32 logits at every position of a
+prompt + greedy stream, computed on the oracle's own weights (int8 q * scale,
+fp32 vectors) by tests/golden/gen_hf_decoder_vectors.py; the reference builds
+its goldens with the same library (scripts/opt125m_reference.py:7-9,
+scripts/gemma_ref_generate.py:42-47).  The oracle keeps its K/V in fp32 here,
+as the reference CPU decoders do (opt125m_decode.rs:263-268,
+whisper_decoder.rs:458, 472); the product and its default oracle round K/V
+to bf16, checked below as a bounded deviation.
+
+What this pins: OPT's position offset (+2) and q scaling, pre-LN order and
+ReLU; Whisper's cross attention (no k bias), three pre-norms and exact GELU;
+Gemma-3's sandwich norms, (1 + w) RMSNorm, per-head q/k norms, RoPE
+(rotate-half, theta from the config), sqrt(d) embedding scale, GeGLU-tanh
+and the 1/sqrt(query_pre_attn_scalar) score scale; the tied head.  Each
+planted mistake (oracle XO_MUT_*) must break the match.
+"""
+import os
+
+import numpy as np
+import pytest
+
+import oracle_lib as O
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+FAMILIES = ["opt", "whisper", "gemma3"]
+
+
+def fixture(name):
+    return np.load(os.path.join(HERE, "golden", "hf_decoder_%s.npz" % name), allow_pickle=False)
+
+
+def oracle_model(fx, kv_f32=True):
+    c = O.ModelConfig()
+    for k, v in zip(fx["cfg_names"], fx["cfg_values"]):
+        k = str(k)
+        setattr(c, k, float(v) if k in ("eps", "rope_theta") else int(round(float(v))))
+    om = O.OracleModel(c, int(fx["seed"]), 1)
+    if kv_f32:
+        om.set_kv_f32(True)
+    if c.family == 1:
+        om.set_cross(None)
+    return om
+
+
+def oracle_logits(om, tokens, n):
+    return np.stack([om.step(np.array([tokens[p]], np.int32), np.array([p], np.int32))[0]
+                     for p in range(n)])
+
+
+def rel_l2(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return np.linalg.norm(a - b, axis=-1) / np.linalg.norm(b, axis=-1)
+
+
+@pytest.mark.parametrize("name", FAMILIES)
+def test_oracle_decoder_matches_hf(name):
+    fx = fixture(name)
+    want = fx["logits"]
+    toks = fx["tokens"]
+    om = oracle_model(fx)
+    got = oracle_logits(om, toks, want.shape[0])
+    err = rel_l2(got, want)
+    # fp32 on both sides; only summation order and libm differ (measured
+    # <= 9.3e-7 rel-L2, 5.1e-7 max abs; every planted mistake >= 1.6e-2)
+    assert err.max() <= 5e-6, err
+    assert np.max(np.abs(got - want)) <= 5e-6
+    # the greedy continuation: the oracle's argmax (its family tie rule) is
+    # HF's token at every generated position
+    n_prompt = int(fx["n_prompt"])
+    for p in range(n_prompt - 1, want.shape[0]):
+        assert om.argmax(got[p]) == toks[p + 1], p
+    om.close()
+
+
+CASES = [("opt", 1), ("opt", 6), ("whisper", 5), ("gemma3", 2), ("gemma3", 3), ("gemma3", 4)]
+NAMES = {1: "OPT position offset +1", 2: "Gemma post-norms swapped", 3: "no sqrt(d) embedding scale",
+         4: "RoPE theta 1e4", 5: "Whisper cross scores without 1/sqrt(hd)",
+         6: "OPT q without hd^-0.5"}
+
+
+@pytest.mark.parametrize("name,mutation", CASES)
+def test_planted_composition_mistake_is_caught(name, mutation):
+    """The fixtures pin the composition: each planted mistake moves the
+    logits far outside the tolerance above."""
+    fx = fixture(name)
+    want = fx["logits"]
+    om = oracle_model(fx)
+    om.set_mutation(mutation)
+    got = oracle_logits(om, fx["tokens"], want.shape[0])
+    om.close()
+    assert rel_l2(got, want).max() > 1e-2, NAMES[mutation]
+
+
+@pytest.mark.parametrize("name", FAMILIES)
+def test_bf16_kv_oracle_deviation_is_bounded(name):
+    """The default oracle (bf16 K/V cache, the product's numerics) stays
+    within bf16 rounding of HF's fp32-cache logits on these tiny models."""
+    fx = fixture(name)
+    want = fx["logits"]
+    om = oracle_model(fx, kv_f32=False)
+    got = oracle_logits(om, fx["tokens"], want.shape[0])
+    om.close()
+    err = rel_l2(got, want)
+    assert err.max() <= 1e-2, err   # measured 1.3e-3 (OPT, Whisper), 4.1e-3 (Gemma-3)
