@@ -91,6 +91,17 @@ int xe_buf_read(xe_buf *buf, void *dst, size_t nbytes, size_t offset);
 /* Device address of the buffer (for the *_dev entry points). */
 void *xe_buf_device_ptr(xe_buf *buf);
 size_t xe_buf_size(xe_buf *buf);
+/* Fill count elements at byte offset of buf with elements [start, start +
+ * count) of the counter-based synthetic stream (seed, stream) that
+ * xe_decoder_init_synthetic uses for weights: value = mean + stdv * z, z an
+ * Irwin-Hall (n=4) approximately normal variate; stored as XE_F32, XE_BF16
+ * (RNE) or XE_I8 (rounded half away from zero, clamped to +-127).
+ * Deterministic and bit-identical to the CPU generator, so multi-GB test and
+ * benchmark inputs are made in HBM without a host copy.  No counterpart in
+ * the reference (its inputs come from files). */
+int xe_buf_fill_synthetic(xe_buf *buf, size_t offset, int dtype, uint64_t seed,
+                          uint32_t stream, uint64_t start, float mean,
+                          float stdv, size_t count);
 
 /* ------------------------------------------------------------------------ */
 /* op layer (CtxDecode, ctx_decode.rs:142-694)                              */
@@ -133,14 +144,18 @@ void xe_weight_free(xe_weight *w);
 int xe_weight_shape(const xe_weight *w, int *m, int *k, int *wdtype);
 
 /* CtxDecode::gemv (ctx_decode.rs:325-366), batched: y[b,m] = W x[b,k]
- * (+ bias), fp32 out.  x_dtype XE_F32 or XE_BF16 (host pointer). */
+ * (+ bias), fp32 out.  x_dtype XE_F32 or XE_BF16 (host pointer).  batch
+ * 1..512 (the reference's batched tiles go to Mp = 512, ctx2.rs:46-55): up
+ * to 8 rows run the bandwidth GEMV, more the MFMA GEMM (bf16-split fp32
+ * activations, fp32 accumulate). */
 int xe_gemv(xe_ctx *ctx, const xe_weight *w, const void *x, int x_dtype,
             int batch, float *y);
 /* CtxDecode::fused_norm_gemv (ctx_decode.rs:617-643). */
 int xe_fused_norm_gemv(xe_ctx *ctx, const xe_weight *w, const void *x,
                        int x_dtype, int batch, float *y);
 /* Device-pointer form of xe_gemv / xe_fused_norm_gemv (no host copies; the
- * weight's pre-norm, if any, is applied).  Asynchronous on the ctx stream. */
+ * weight's pre-norm, if any, is applied).  Asynchronous on the ctx stream.
+ * More than 8 rows need XE_F32 x. */
 int xe_gemv_dev(xe_ctx *ctx, const xe_weight *w, const void *x_dev,
                 int x_dtype, int batch, float *y_dev);
 

@@ -246,3 +246,24 @@ def test_registration_rejects_bad_k(gpu, xe):
     dev, ctx = gpu
     with pytest.raises(xe.XdnaError, match="multiple of 16"):
         ctx.register_weight_q8(np.zeros((4, 20), np.int8), np.ones(4, np.float32))
+
+
+# ---- more than 8 rows: the MFMA GEMM behind the same op-layer entry ----
+
+@pytest.mark.parametrize("m,k", [(6912, 1152), (1152, 6912), (3072, 768)])
+@pytest.mark.parametrize("b", [16, 64, 200])
+def test_norm_gemm_int8_batched(gpu, xe, m, k, b):
+    """xe_fused_norm_gemv at 16..200 rows (MFMA GEMM, bf16 three-part split
+    of the fp32 activations, fp32 accumulate) against the oracle GEMV."""
+    dev, ctx = gpu
+    print("[case] int8 LN+GEMM m=%d k=%d b=%d" % (m, k, b), flush=True)
+    x, gamma, beta, q, s = config2_inputs(m, k, b, seed=m + k + b)
+    w = ctx.register_weight_q8(q, s)
+    ctx.set_norm(w, xe.Norm.Ln(gamma, beta, 1e-5))
+    got = ctx.fused_norm_gemv(w, x)
+    want = O.gemv_i8(oracle_ln(x, gamma, beta), q, s)
+    w.free()
+    err = np.linalg.norm(got - want) / np.linalg.norm(want)
+    print("[gemm] m=%d k=%d b=%d rel-L2 %.3g max abs %.3g" % (m, k, b, err,
+                                                            np.max(np.abs(got - want))), flush=True)
+    close(got, want)

@@ -90,6 +90,21 @@ void xe_ctx::ensure_attn(size_t work_floats) {
   }
 }
 
+void xe_ctx::ensure_gemm(size_t xn_floats) {
+  if (!gemm_ws) {
+    XE_HIP(hipMalloc(&gemm_ws, gemm_op_ws_floats() * sizeof(float)));
+    XE_HIP(hipMalloc(&gemm_cnt, gemm_op_cnt_words() * sizeof(unsigned)));
+    XE_HIP(hipMemsetAsync(gemm_cnt, 0, gemm_op_cnt_words() * sizeof(unsigned), dev->stream));
+  }
+  if (xn_floats > gemm_xn_floats) {
+    if (gemm_xn) XE_HIP(hipFree(gemm_xn));
+    gemm_xn = nullptr;
+    gemm_xn_floats = 0;
+    XE_HIP(hipMalloc(&gemm_xn, xn_floats * sizeof(float)));
+    gemm_xn_floats = xn_floats;
+  }
+}
+
 namespace {
 
 template <typename T>
@@ -207,21 +222,47 @@ GemvLaunch gemv_args(const xe_weight *w, const void *x, int x_dtype, int batch, 
   return g;
 }
 
+// Up to 8 rows: the GEMV kernels; 9..kMaxOpBatch: the MFMA GEMM (fp32 x).
+constexpr int kMaxOpBatch = 512;  // the reference's largest batched tile (Mp <= 512, ctx2.rs)
+
+void launch_linear(xe_ctx *ctx, const xe_weight *w, const void *x, int x_dtype, int batch,
+                   float *y, hipStream_t s) {
+  if (batch <= 8) {
+    launch_gemv(gemv_args(w, x, x_dtype, batch, y), s);
+  } else {
+    XE_REQUIRE(x_dtype == XE_F32, "more than 8 rows need fp32 x");
+    ctx->ensure_gemm(w->norm != XE_NORM_NONE ? static_cast<size_t>(batch) * w->k : 0);
+    launch_gemm_op(gemv_args(w, x, x_dtype, batch, y), ctx->gemm_xn, ctx->gemm_ws, ctx->gemm_cnt, s);
+  }
+  ctx->dispatches++;
+}
+
 int run_gemv_host(xe_ctx *ctx, const xe_weight *w, const void *x, int x_dtype, int batch,
                   float *y) {
   XE_REQUIRE(ctx && w && x && y, "null argument");
   XE_REQUIRE(x_dtype == XE_F32 || x_dtype == XE_BF16, "x dtype must be XE_F32 or XE_BF16");
-  XE_REQUIRE(batch >= 1 && batch <= 8, "gemv batch must be 1..8");
+  XE_REQUIRE(batch >= 1 && batch <= kMaxOpBatch, "gemv batch must be 1..512");
   DeviceGuard dg(ctx->dev->ordinal);
   hipStream_t s = ctx->dev->stream;
+  // more than 8 rows run on the GEMM, which reads fp32: widen bf16 here
+  std::vector<float> widened;
+  if (batch > 8 && x_dtype == XE_BF16) {
+    const uint16_t *xb = static_cast<const uint16_t *>(x);
+    widened.resize(static_cast<size_t>(batch) * w->k);
+    for (size_t i = 0; i < widened.size(); i++) {
+      const uint32_t u = static_cast<uint32_t>(xb[i]) << 16;
+      std::memcpy(&widened[i], &u, 4);
+    }
+    x = widened.data();
+    x_dtype = XE_F32;
+  }
   const size_t xbytes = static_cast<size_t>(batch) * w->k * (x_dtype == XE_F32 ? 4 : 2);
   const size_t ybytes = static_cast<size_t>(batch) * w->m * 4;
   char *d = static_cast<char *>(ctx->ensure_scratch(xbytes + ybytes + 256));
   void *dx = d;
   float *dy = reinterpret_cast<float *>(d + ((xbytes + 255) / 256) * 256);
   XE_HIP(hipMemcpyAsync(dx, x, xbytes, hipMemcpyHostToDevice, s));
-  launch_gemv(gemv_args(w, dx, x_dtype, batch, dy), s);
-  ctx->dispatches++;
+  launch_linear(ctx, w, dx, x_dtype, batch, dy, s);
   XE_HIP(hipMemcpyAsync(y, dy, ybytes, hipMemcpyDeviceToHost, s));
   XE_HIP(hipStreamSynchronize(s));
   return 0;
@@ -365,6 +406,9 @@ void xe_ctx_destroy(xe_ctx *ctx) {
     if (ctx->scratch) (void)hipFree(ctx->scratch);
     if (ctx->host_pinned) (void)hipHostFree(ctx->host_pinned);
     if (ctx->attn_work) (void)hipFree(ctx->attn_work);
+    if (ctx->gemm_ws) (void)hipFree(ctx->gemm_ws);
+    if (ctx->gemm_cnt) (void)hipFree(ctx->gemm_cnt);
+    if (ctx->gemm_xn) (void)hipFree(ctx->gemm_xn);
     delete ctx;
     return 0;
   }, -1);
@@ -509,10 +553,9 @@ int xe_gemv_dev(xe_ctx *ctx, const xe_weight *w, const void *x_dev, int x_dtype,
   return guard([&]() -> int {
     XE_REQUIRE(ctx && w && x_dev && y_dev, "null argument");
     XE_REQUIRE(x_dtype == XE_F32 || x_dtype == XE_BF16, "x dtype must be XE_F32 or XE_BF16");
-    XE_REQUIRE(batch >= 1 && batch <= 8, "gemv batch must be 1..8");
+    XE_REQUIRE(batch >= 1 && batch <= kMaxOpBatch, "gemv batch must be 1..512");
     DeviceGuard dg(ctx->dev->ordinal);
-    launch_gemv(gemv_args(w, x_dev, x_dtype, batch, y_dev), ctx->dev->stream);
-    ctx->dispatches++;
+    launch_linear(ctx, w, x_dev, x_dtype, batch, y_dev, ctx->dev->stream);
     return 0;
   }, -1);
 }

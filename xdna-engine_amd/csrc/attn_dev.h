@@ -77,10 +77,13 @@ __device__ __forceinline__ uint16_t f32_to_bf16_rne(float x) {
   return static_cast<uint16_t>((bits & 0x7fffffffu) > 0x7f800000u ? quiet : rounded);
 }
 
+// Filled length of stream b.  A length outside [1, max_ctx] (a device-side
+// length array the host cannot check, or a position past the cache) makes
+// the stream's blocks return at once: no K/V row is appended or read past
+// the cache, and the stream's output is left as it was.
 __device__ __forceinline__ int stream_len(const AttnParams &p, int b) {
-  if (p.lens) return p.lens[b];
-  if (p.pos) return p.pos[b] + 1;
-  return p.fixed_len;
+  const int len = p.lens ? p.lens[b] : p.pos ? p.pos[b] + 1 : p.fixed_len;
+  return len > p.max_ctx ? 0 : len;
 }
 
 __host__ __device__ __forceinline__ void split_range(int len, int max_splits, int &chunk, int &nsplits) {

@@ -88,7 +88,14 @@ struct xe_ctx {
   // split-K attention workspace (partials)
   float *attn_work = nullptr;
   size_t attn_work_floats = 0;
+  // batched GEMM (more than 8 rows): split-K partials, arrival counters
+  // (zeroed once, self-resetting) and the prologue's normalised rows
+  float *gemm_ws = nullptr;
+  unsigned *gemm_cnt = nullptr;
+  float *gemm_xn = nullptr;
+  size_t gemm_xn_floats = 0;
   void *ensure_scratch(size_t n);
+  void ensure_gemm(size_t xn_floats);
   void *ensure_pinned(size_t n);
   void ensure_attn(size_t work_floats);
 };
@@ -131,6 +138,13 @@ struct GemvLaunch {
 };
 
 void launch_gemv(const GemvLaunch &p, hipStream_t s);
+// More than 8 rows: the MFMA GEMM (gemm.hip), after a prologue kernel into xn
+// [batch, k] when the launch has a norm or residual prologue.  fp32 x only.
+// ws / cnt: split-K workspace (gemm_op_ws_floats() floats) and per-tile
+// arrival counters (gemm_op_cnt_words(), zeroed once; they re-arm).
+void launch_gemm_op(const GemvLaunch &L, float *xn, float *ws, unsigned *cnt, hipStream_t s);
+size_t gemm_op_ws_floats();
+size_t gemm_op_cnt_words();
 // int8 activations x int8 weights -> int32 (exact).
 void launch_gemv_i8act(const int8_t *q, const int8_t *xq, int m, int k, int batch,
                        int32_t *acc, hipStream_t s);

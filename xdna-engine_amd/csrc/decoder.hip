@@ -128,6 +128,23 @@ __global__ void synth_vec_kernel(uint64_t base, float mean, float k, size_t n, f
   }
 }
 
+// Elements [start, start + n) of a synthetic stream into dst[0, n): fp32,
+// bf16 bits (RNE) or int8 (the Irwin-Hall integer sum scaled by k and
+// rounded half away from zero, clamped to +-127: uniform-ish int8 codes).
+__global__ void synth_fill_kernel(uint64_t base, float mean, float k, uint64_t start, size_t n,
+                                  void *dst, int dtype) {
+  for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < n;
+       i += static_cast<size_t>(gridDim.x) * blockDim.x) {
+    const float v = synth_value(base, start + i, mean, k);
+    if (dtype == XE_BF16)
+      static_cast<uint16_t *>(dst)[i] = bf16_bits_dev(v);
+    else if (dtype == XE_I8)
+      static_cast<int8_t *>(dst)[i] = static_cast<int8_t>(fminf(fmaxf(roundf(v), -127.0f), 127.0f));
+    else
+      static_cast<float *>(dst)[i] = v;
+  }
+}
+
 // --------------------------------------------------------------------------
 // step kernels
 // --------------------------------------------------------------------------
@@ -350,8 +367,23 @@ struct xe_decoder {
   int32_t *ll_forced = nullptr;    // device [max_ctx + 1][max_batch] prompt tokens
   double last_step_us = 0.0;
   bool cross_ready = false;
-  int fed = 0;      // prompt length of the current streams
-  int decoded = 0;  // steps decoded after the prompt
+  // Host copy of every stream's next position (the one the kernels append
+  // the K/V row at and read the RoPE / position row of): feed() sets it to
+  // the prompt length, step() to pos + 1, decode() and profile_step()
+  // advance it.  live = streams whose device token / position state was set
+  // by feed() or step() since the last reset; decode(batch) needs batch <= live.
+  std::vector<int> hpos;
+  int live = 0;
+  // bound every position a run of n_steps from the host positions would
+  // process: the K/V rows and position rows of streams b < batch
+  void require_room(int batch, int n_steps) const {
+    XE_REQUIRE(batch <= live, "decode batch exceeds the streams fed or stepped since the last reset");
+    for (int b = 0; b < batch; b++) {
+      XE_REQUIRE(static_cast<long>(hpos[b]) + n_steps <= c.max_ctx, "decode would run past max_ctx");
+      if (c.family != XE_GEMMA3)
+        XE_REQUIRE(static_cast<long>(hpos[b]) + n_steps <= c.max_pos, "decode would run past the position table");
+    }
+  }
   // per-launch profiling (xe_decoder_profile_step): an event after each
   // launch on the decoder stream, with the launch's algorithmic bytes
   struct ProfEntry {
@@ -1721,6 +1753,27 @@ auto guard_d(F &&f, decltype(f()) on_error) -> decltype(f()) {
 
 extern "C" {
 
+int xe_buf_fill_synthetic(xe_buf *buf, size_t offset, int dtype, uint64_t seed, uint32_t stream,
+                          uint64_t start, float mean, float stdv, size_t count) {
+  return guard_d([&]() -> int {
+    XE_REQUIRE(buf && buf->ptr, "null buffer");
+    XE_REQUIRE(dtype == XE_F32 || dtype == XE_BF16 || dtype == XE_I8, "dtype must be XE_F32, XE_BF16 or XE_I8");
+    const size_t es = dtype == XE_F32 ? 4 : dtype == XE_BF16 ? 2 : 1;
+    XE_REQUIRE(offset % es == 0, "offset not aligned to the element size");
+    XE_REQUIRE(count <= (buf->size - std::min(offset, buf->size)) / es, "fill runs past the buffer");
+    if (count == 0) return 0;
+    DeviceGuard dg(buf->dev->ordinal);
+    hipStream_t st = buf->dev->stream;
+    const size_t blocks = std::min<size_t>((count + 255) / 256, 8192);
+    synth_fill_kernel<<<static_cast<unsigned>(blocks), 256, 0, st>>>(
+        synth_base(seed, stream), mean, stdv * kIh4InvStd, start, count,
+        static_cast<char *>(buf->ptr) + offset, dtype);
+    XE_HIP(hipGetLastError());
+    XE_HIP(hipStreamSynchronize(st));
+    return 0;
+  }, -1);
+}
+
 xe_decoder *xe_decoder_create(xe_device *dev, const xe_model_config *cfg, int max_batch) {
   return guard_d([&]() -> xe_decoder * {
     XE_REQUIRE(dev && cfg, "null argument");
@@ -1730,6 +1783,7 @@ xe_decoder *xe_decoder_create(xe_device *dev, const xe_model_config *cfg, int ma
     d->dev = dev;
     d->c = *cfg;
     d->max_batch = max_batch;
+    d->hpos.assign(max_batch, 0);
     try {
       XE_HIP(hipStreamCreateWithFlags(&d->s, hipStreamNonBlocking));
       alloc_decoder(d);
@@ -1833,6 +1887,8 @@ int xe_decoder_reset(xe_decoder *d) {
     XE_HIP(hipMemsetAsync(d->kc, 0, kvn * 2, d->s));
     XE_HIP(hipMemsetAsync(d->vc, 0, kvn * 2, d->s));
     XE_HIP(hipStreamSynchronize(d->s));
+    d->hpos.assign(d->max_batch, 0);
+    d->live = 0;
     return 0;
   }, -1);
 }
@@ -1879,6 +1935,8 @@ int xe_decoder_step(xe_decoder *d, const int32_t *tokens, const int32_t *pos, in
     if (next) XE_HIP(hipMemcpyAsync(next, d->next, batch * 4, hipMemcpyDeviceToHost, d->s));
     XE_HIP(hipStreamSynchronize(d->s));
     check_step_status(d);
+    for (int b = 0; b < batch; b++) d->hpos[b] = pos[b] + 1;
+    d->live = std::max(d->live, batch);
     return 0;
   }, -1);
 }
@@ -1916,8 +1974,8 @@ void feed(xe_decoder *d, const int32_t *prompt, int n_prompt, int batch) {
     run_ll(d, batch, n_prompt, d->ll_forced, n_prompt, false);
     XE_HIP(hipStreamSynchronize(d->s));
     check_step_status(d);
-    d->fed = n_prompt;
-    d->decoded = 0;
+    for (int b = 0; b < batch; b++) d->hpos[b] = n_prompt;
+    d->live = batch;
     return;
   }
   {
@@ -1931,20 +1989,18 @@ void feed(xe_decoder *d, const int32_t *prompt, int n_prompt, int batch) {
   }
   XE_HIP(hipStreamSynchronize(d->s));
   check_step_status(d);
-  d->fed = n_prompt;
-  d->decoded = 0;
+  for (int b = 0; b < batch; b++) d->hpos[b] = n_prompt;
+  d->live = batch;
 }
 
 // n_steps further greedy steps from the device state; out [batch, n_steps]
 // receives the tokens those steps emit (may be NULL).
 void decode(xe_decoder *d, int batch, int n_steps, int32_t *out, double *device_us) {
   check_ready(d, batch);
-  XE_REQUIRE(d->fed > 0, "feed a prompt first");
+  XE_REQUIRE(d->live > 0, "feed a prompt first");
   XE_REQUIRE(n_steps >= 0, "negative step count");
-  const int first_pos = d->fed + d->decoded;  // position the next step processes
-  XE_REQUIRE(first_pos + n_steps <= d->c.max_ctx, "decode would run past max_ctx");
-  if (d->c.family != XE_GEMMA3)
-    XE_REQUIRE(first_pos + n_steps <= d->c.max_pos, "decode would run past the position table");
+  d->require_room(batch, n_steps);
+  const std::vector<int> first_pos(d->hpos.begin(), d->hpos.begin() + batch);  // positions the next step processes
   hipEvent_t e0, e1;
   XE_HIP(hipEventCreate(&e0));
   XE_HIP(hipEventCreate(&e1));
@@ -1964,14 +2020,14 @@ void decode(xe_decoder *d, int batch, int n_steps, int32_t *out, double *device_
   check_step_status(d);
   if (n_steps > 0) d->last_step_us = 1000.0 * ms / n_steps;
   if (device_us) *device_us = 1000.0 * ms;
-  d->decoded += n_steps;
+  for (int b = 0; b < batch; b++) d->hpos[b] += n_steps;
   if (out && n_steps > 0) {
     std::vector<int32_t> hist(static_cast<size_t>(batch) * (d->c.max_ctx + 1));
     XE_HIP(hipMemcpy(hist.data(), d->hist, hist.size() * 4, hipMemcpyDeviceToHost));
     for (int b = 0; b < batch; b++)
       for (int i = 0; i < n_steps; i++)
         out[static_cast<size_t>(b) * n_steps + i] =
-            hist[static_cast<size_t>(b) * (d->c.max_ctx + 1) + first_pos + i];
+            hist[static_cast<size_t>(b) * (d->c.max_ctx + 1) + first_pos[b] + i];
   }
 }
 
@@ -2028,8 +2084,8 @@ int xe_decoder_profile_step(xe_decoder *d, int batch, int max_entries, char *lab
   return guard_d([&]() -> int {
     XE_REQUIRE(d && labels && us && bytes, "null argument");
     check_ready(d, batch);
-    XE_REQUIRE(d->fed > 0, "feed a prompt first");
-    XE_REQUIRE(d->fed + d->decoded < d->c.max_ctx, "no room for another step");
+    XE_REQUIRE(d->live > 0, "feed a prompt first");
+    d->require_room(batch, 1);
     DeviceGuard dg(d->dev->ordinal);
     XE_HIP(hipStreamSynchronize(d->s));
     d->prof_pos.assign(batch, 0);
@@ -2064,7 +2120,7 @@ int xe_decoder_profile_step(xe_decoder *d, int batch, int max_entries, char *lab
       }
       (void)hipFree(tr);
       check_step_status(d);
-      d->decoded += 1;
+      for (int b = 0; b < batch; b++) d->hpos[b] += 1;
       if (const char *raw = getenv("XE_LL_TRACE_RAW")) {
         // diagnostic: the raw per-workgroup trace, [slots][grid] u64 ticks
         if (FILE *f = std::fopen(raw, "wb")) {
@@ -2156,7 +2212,7 @@ int xe_decoder_profile_step(xe_decoder *d, int batch, int max_entries, char *lab
       }
       (void)hipFree(tr);
       check_step_status(d);
-      d->decoded += 1;
+      for (int b = 0; b < batch; b++) d->hpos[b] += 1;
       int khz = 0;
       XE_HIP(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, d->dev->ordinal));
       XE_REQUIRE(khz > 0, "device wall clock rate unknown");
@@ -2187,7 +2243,7 @@ int xe_decoder_profile_step(xe_decoder *d, int batch, int max_entries, char *lab
     }
     d->prof = nullptr;
     XE_HIP(hipStreamSynchronize(d->s));
-    d->decoded += 1;
+    for (int b = 0; b < batch; b++) d->hpos[b] += 1;
     int n = 0;
     for (size_t i = 1; i < entries.size() && n < max_entries; i++, n++) {
       float ms = 0.f;

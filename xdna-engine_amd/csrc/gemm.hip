@@ -421,4 +421,23 @@ void launch_gemm(const gdev::GemvParams &p, int wdtype, float *ws, unsigned *cnt
   XE_HIP(hipGetLastError());
 }
 
+size_t gemm_op_ws_floats() { return kGemmWsFloats; }
+size_t gemm_op_cnt_words() { return kGemmMaxTiles; }
+
+void launch_gemm_op(const GemvLaunch &L, float *xn, float *ws, unsigned *cnt, hipStream_t s) {
+  XE_REQUIRE(L.x_dtype == XE_F32, "gemm: fp32 activations only");
+  gdev::GemvParams p = gdev::to_params(L);
+  if (gemm_needs_prologue(p)) {
+    XE_REQUIRE(xn, "gemm: prologue without a row buffer");
+    launch_gemm_prologue(p, xn, s);
+    p.x = xn;
+    p.ldx = p.k;
+    p.sub = nullptr;
+    p.post_w = nullptr;
+    p.res_out = nullptr;
+    p.norm = XE_NORM_NONE;
+  }
+  launch_gemm(p, L.wdtype, ws, cnt, s);
+}
+
 }  // namespace xe

@@ -33,7 +33,8 @@ EXECUTORS = {0: "graph", 1: "persistent", 2: "eager", 3: "ll"}
 EXPORTS = [
     "xe_last_error", "xe_abi_version", "xe_device_count", "xe_device_open", "xe_device_close",
     "xe_device_synchronize", "xe_device_name", "xe_buf_alloc", "xe_buf_free", "xe_buf_write",
-    "xe_buf_read", "xe_buf_device_ptr", "xe_buf_size", "xe_ctx_create", "xe_ctx_destroy",
+    "xe_buf_read", "xe_buf_device_ptr", "xe_buf_size", "xe_buf_fill_synthetic", "xe_ctx_create",
+    "xe_ctx_destroy",
     "xe_ctx_dispatches", "xe_ctx_reset_dispatches", "xe_register_weight",
     "xe_register_weight_q8", "xe_register_weight_bfp16", "xe_register_weight_bf16",
     "xe_register_fused", "xe_weight_set_norm", "xe_weight_free", "xe_weight_shape", "xe_gemv",
@@ -114,6 +115,7 @@ def lib():
         "xe_buf_read": (i, [vp, vp, sz, sz]),
         "xe_buf_device_ptr": (vp, [vp]),
         "xe_buf_size": (sz, [vp]),
+        "xe_buf_fill_synthetic": (i, [vp, sz, i, u64, C.c_uint32, u64, f, f, sz]),
         "xe_ctx_create": (vp, [vp]),
         "xe_ctx_destroy": (None, [vp]),
         "xe_ctx_dispatches": (u64, [vp]),
@@ -234,6 +236,12 @@ class Buf:
         out = np.empty(count, dtype)
         _check(lib().xe_buf_read(self.h, _p(out), out.nbytes, offset))
         return out
+
+    def fill_synthetic(self, dtype, seed, stream, count, mean=0.0, std=1.0, start=0, offset=0):
+        """Elements [start, start+count) of the synthetic stream (seed, stream)
+        written at byte offset, as XE_F32 / XE_BF16 / XE_I8 (on the device)."""
+        _check(lib().xe_buf_fill_synthetic(self.h, offset, dtype, seed, stream, start, mean, std,
+                                           count))
 
     def free(self):
         if self.h:
