@@ -186,6 +186,19 @@ int xe_attn_decode_dev(xe_ctx *ctx, const float *q_dev, const uint16_t *kc_dev,
                        const uint16_t *vc_dev, const int32_t *lens_dev,
                        int batch, int hq, int hkv, int hd, int max_ctx,
                        float scale, float *out_dev);
+/* xe_attn_decode_dev without any allocation.  No counterpart in the
+ * reference: for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).  The
+ * split partials go to a static per-GPU workspace of 4 Mi floats (16 MB)
+ * instead of the ctx's own; a call needing more (batch * hq * splits *
+ * (hd + 2) floats, splits <= 64) fails with -1.  Same kernels and results
+ * as xe_attn_decode_dev.  Calls that overlap on one GPU (any ctx, any
+ * thread) share the workspace and race: serialise them. */
+int xe_attn_decode_dev_static(xe_ctx *ctx, const float *q_dev,
+                              const uint16_t *kc_dev, const uint16_t *vc_dev,
+                              const int32_t *lens_dev, int batch, int hq,
+                              int hkv, int hd, int max_ctx, float scale,
+                              float *out_dev);
 
 /* Wait for the ctx stream; returns 0 or -1. */
 int xe_ctx_synchronize(xe_ctx *ctx);

@@ -301,6 +301,8 @@ xe_device *xe_device_open(int ordinal) {
     d->max_lds = prop.sharedMemPerBlock;
     // default priority: other priorities have hung on this hardware pool
     XE_HIP(hipStreamCreateWithFlags(&d->stream, hipStreamNonBlocking));
+    // the static attention workspace's device address, once per device
+    (void)attn_static_scratch(ordinal);
     return d;
   }, nullptr);
 }
@@ -621,9 +623,22 @@ int xe_w8a8_linear(xe_ctx *ctx, const xe_weight *w, const float *x, int batch, f
   }, -1);
 }
 
+// Splits per (stream, kv head): about four workgroups per CU in total, at
+// most one per 64 cache rows and at most 64.
+static int attn_splits(const xe_ctx *ctx, int batch, int hkv, int max_ctx) {
+  const int target = 4 * ctx->dev->num_cus;
+  int ms = target / (batch * hkv);
+  const int cap = (max_ctx + 63) / 64;
+  ms = ms < 1 ? 1 : ms;
+  ms = ms > cap ? cap : ms;
+  return ms > 64 ? 64 : ms;
+}
+
+// work: the split partials (attn_work_floats(batch, hq, hd, splits) floats);
+// null = the ctx's own workspace, grown on demand.
 static int attn_impl(xe_ctx *ctx, const float *q, const uint16_t *kc, const uint16_t *vc,
                      const int32_t *lens, int batch, int hq, int hkv, int hd, int max_ctx,
-                     float scale, float *out) {
+                     float scale, float *out, float *work = nullptr) {
   AttnLaunch a;
   a.q = q;
   a.kc = const_cast<uint16_t *>(kc);
@@ -637,15 +652,13 @@ static int attn_impl(xe_ctx *ctx, const float *q, const uint16_t *kc, const uint
   a.scale = scale;
   a.lens = lens;
   a.out = out;
-  const int target = 4 * ctx->dev->num_cus;
-  int ms = target / (batch * hkv);
-  const int cap = (max_ctx + 63) / 64;
-  ms = ms < 1 ? 1 : ms;
-  ms = ms > cap ? cap : ms;
-  ms = ms > 64 ? 64 : ms;
-  a.max_splits = ms;
-  ctx->ensure_attn(attn_work_floats(batch, hq, hd, ms));
-  a.work = ctx->attn_work;
+  a.max_splits = attn_splits(ctx, batch, hkv, max_ctx);
+  if (work) {
+    a.work = work;
+  } else {
+    ctx->ensure_attn(attn_work_floats(batch, hq, hd, a.max_splits));
+    a.work = ctx->attn_work;
+  }
   launch_attn(a, ctx->dev->stream);
   ctx->dispatches++;
   return 0;
@@ -660,6 +673,24 @@ int xe_attn_decode_dev(xe_ctx *ctx, const float *q_dev, const uint16_t *kc_dev,
     DeviceGuard dg(ctx->dev->ordinal);
     return attn_impl(ctx, q_dev, kc_dev, vc_dev, lens_dev, batch, hq, hkv, hd, max_ctx, scale,
                      out_dev);
+  }, -1);
+}
+
+int xe_attn_decode_dev_static(xe_ctx *ctx, const float *q_dev, const uint16_t *kc_dev,
+                              const uint16_t *vc_dev, const int32_t *lens_dev, int batch, int hq,
+                              int hkv, int hd, int max_ctx, float scale, float *out_dev) {
+  return guard([&]() -> int {
+    XE_REQUIRE(ctx && q_dev && kc_dev && vc_dev && lens_dev && out_dev, "null argument");
+    XE_REQUIRE(batch > 0 && hq > 0 && hkv > 0 && hd > 0, "bad shape");
+    DeviceGuard dg(ctx->dev->ordinal);
+    const size_t need = attn_work_floats(batch, hq, hd, attn_splits(ctx, batch, hkv, max_ctx));
+    XE_REQUIRE(need <= attn_static_floats(),
+               "xe_attn_decode_dev_static: " + std::to_string(need) + " partial floats needed, the static "
+               "workspace holds " + std::to_string(attn_static_floats()) +
+               " (fewer streams or query heads per call)");
+    float *work = static_cast<float *>(attn_static_scratch(ctx->dev->ordinal));
+    return attn_impl(ctx, q_dev, kc_dev, vc_dev, lens_dev, batch, hq, hkv, hd, max_ctx, scale,
+                     out_dev, work);
   }, -1);
 }
 

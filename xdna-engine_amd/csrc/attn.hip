@@ -1,6 +1,8 @@
 // attn.hip -- split-K flash-decode attention kernels for gfx950 (device code
 // in attn_dev.h): a partial launch over (split, kv head, stream) and a merge
 // launch over (element block, kv head, stream).
+#include <mutex>
+
 #include "step_dev.h"
 
 namespace xe {
@@ -97,6 +99,37 @@ void launch_attn_phase(const sdev::Phase &ph, hipStream_t s) {
 
 size_t attn_work_floats(int batch, int hq, int hd, int max_splits) {
   return static_cast<size_t>(batch) * hq * max_splits * (hd + 2);
+}
+
+// ---------------------------------------------------------------------------
+// Workspace of the allocation-free entry point (xe_attn_decode_dev_static):
+// the split partials live in this file-scope device array, one copy per GPU
+// for the life of the process.  In host code `scratch` is only a stand-in
+// symbol: its device address comes from hipGetSymbolAddress, resolved once
+// per device with that device current, and only that address is ever passed
+// to kernels.
+// ---------------------------------------------------------------------------
+namespace {
+constexpr size_t kStaticAttnFloats = size_t(4) << 20;  // 16 MB of partials
+__device__ __align__(256) float scratch[kStaticAttnFloats];
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices] = {};
+}  // namespace
+
+size_t attn_static_floats() { return kStaticAttnFloats; }
+
+void *attn_static_scratch(int ordinal) {
+  XE_REQUIRE(ordinal >= 0 && ordinal < kMaxDevices, "device ordinal out of range for the static workspace");
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[ordinal]) {
+    DeviceGuard dg(ordinal);
+    void *ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    XE_REQUIRE(e == hipSuccess && ptr, std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
+    g_scratch_ptr[ordinal] = ptr;
+  }
+  return g_scratch_ptr[ordinal];
 }
 
 void launch_attn(const AttnLaunch &L, hipStream_t s) {

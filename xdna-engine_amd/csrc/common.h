@@ -184,6 +184,10 @@ struct AttnLaunch {
 };
 
 size_t attn_work_floats(int batch, int hq, int hd, int max_splits);
+// Device address (resolved once per device) and capacity in floats of the
+// static split-partial workspace used by xe_attn_decode_dev_static.
+void *attn_static_scratch(int ordinal);
+size_t attn_static_floats();
 void launch_attn(const AttnLaunch &p, hipStream_t s);
 
 // ---------------------------------------------------------------------------

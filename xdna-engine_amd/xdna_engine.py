@@ -39,7 +39,7 @@ EXPORTS = [
     "xe_register_weight_q8", "xe_register_weight_bfp16", "xe_register_weight_bf16",
     "xe_register_fused", "xe_weight_set_norm", "xe_weight_free", "xe_weight_shape", "xe_gemv",
     "xe_fused_norm_gemv", "xe_gemv_dev", "xe_gemv_i8act", "xe_gemv_i8act_dev", "xe_w8a8_linear",
-    "xe_attn_decode", "xe_attn_decode_dev", "xe_ctx_synchronize", "xe_decoder_create",
+    "xe_attn_decode", "xe_attn_decode_dev", "xe_attn_decode_dev_static", "xe_ctx_synchronize", "xe_decoder_create",
     "xe_decoder_destroy", "xe_decoder_init_synthetic", "xe_decoder_set_tensor",
     "xe_decoder_get_tensor_q8", "xe_decoder_reset", "xe_decoder_set_cross", "xe_decoder_step",
     "xe_decoder_generate", "xe_decoder_last_step_us", "xe_decoder_weight_bytes",
@@ -137,6 +137,7 @@ def lib():
         "xe_w8a8_linear": (i, [vp, vp, vp, i, vp, C.POINTER(f)]),
         "xe_attn_decode": (i, [vp, vp, vp, vp, vp, i, i, i, i, i, f, vp]),
         "xe_attn_decode_dev": (i, [vp, vp, vp, vp, vp, i, i, i, i, i, f, vp]),
+        "xe_attn_decode_dev_static": (i, [vp, vp, vp, vp, vp, i, i, i, i, i, f, vp]),
         "xe_decoder_create": (vp, [vp, C.POINTER(ModelConfig), i]),
         "xe_decoder_destroy": (None, [vp]),
         "xe_decoder_init_synthetic": (i, [vp, u64]),
