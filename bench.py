@@ -25,9 +25,19 @@ Extra fields of the JSON line:
                 step's algorithmic bytes (weights + every stream's KV at the
                 mean context) / its device time
   cpu_baseline  the CPU oracle (oracle/, a C restatement of the reference's
-                decode arithmetic) on a bounded sample of the same workload,
-                timed on this host's cores
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--batch B] [--batch2 B2]
+                decode arithmetic) on a bounded sample of the same workload
+                at the mean context of the GPU's timed steps (cache primed
+                with synthetic rows), timed on this host's cores with OpenMP
+                (value), plus the reference-shaped single-thread form (k-outer
+                [K, N] linears, opt125m_decode.rs:106-125) and single-thread
+                Lin::fwd / attend_one kernels on config-2/3 inputs
+Modes:
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--batch B] [--batch2 B2]
+  python bench.py --kernels      isolated config-2 GEMVs (int8 / bfp16 / bf16,
+                                 b 1/4/8, >= 512 MB of rotating weight copies)
+                                 and config-3 mha_decode, GB/s per kernel
+  python bench.py --copy-probe MIB   a plain MIB MiB device copy, three times
+                                 (scales rocprofv3's FETCH_SIZE / WRITE_SIZE)
 """
 import argparse
 import importlib.util
@@ -58,24 +68,12 @@ def load_xe():
     return mod
 
 
-def cpu_baseline(cfg, prompt_len, budget_s, seed):
-    """Oracle decode on the host: feed a short prompt, then time greedy steps
-    until ~budget_s of CPU work (bounded sample of the same workload)."""
-    sys.path.insert(0, os.path.join(ROOT, "tests"))
-    import oracle_lib as O
-    oc = O.ModelConfig()
-    for name, _ in O.ModelConfig._fields_:
-        setattr(oc, name, getattr(cfg, name))
-    oc.max_ctx = 2048
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or (os.cpu_count() or 1)
-    O.lib().xo_set_threads(threads)
-    om = O.OracleModel(oc, seed, 1)
-    rng = np.random.default_rng(seed)
-    toks = rng.integers(0, cfg.vocab, prompt_len).astype(np.int32)
-    for p in range(prompt_len):
-        logits = om.step(toks[p:p + 1], np.array([p], np.int32))
-    tok = om.argmax(logits[0])
-    n, pos = 0, prompt_len
+def _time_decode(om, O, vocab, ctx0, budget_s, max_steps):
+    """Greedy steps of stream 0 from position ctx0 (cache primed) for about
+    budget_s seconds; returns (steps, seconds)."""
+    rng = np.random.default_rng(ctx0)
+    tok = int(rng.integers(0, vocab))
+    n, pos = 0, ctx0
     t0 = time.perf_counter()
     while True:
         logits = om.step(np.array([tok], np.int32), np.array([pos], np.int32))
@@ -83,13 +81,78 @@ def cpu_baseline(cfg, prompt_len, budget_s, seed):
         n += 1
         pos += 1
         el = time.perf_counter() - t0
-        if el >= budget_s or pos >= oc.max_ctx - 1:
-            break
+        if el >= budget_s or n >= max_steps:
+            return n, el
+
+
+def cpu_baseline(cfg, ctx_mean, budget_s, seed):
+    """The CPU restatement on this host (bounded samples of the same work):
+    value = OpenMP oracle decode of Gemma-3-1B int8 at the GPU line's mean
+    context; single_thread = the reference's loop shape (k-outer [K, N]
+    linears, scalar attention, one thread); kernels = single-thread Lin::fwd
+    int8 and attend_one on config-2/3 inputs."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle_lib as O
+    oc = O.ModelConfig()
+    for name, _ in O.ModelConfig._fields_:
+        setattr(oc, name, getattr(cfg, name))
+    ctx0 = int(min(ctx_mean, cfg.max_ctx - 64))
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or (os.cpu_count() or 1)
+    L = O.lib()
+    L.xo_set_threads(threads)
+    t = time.perf_counter()
+    om = O.OracleModel(oc, seed, 1)
+    om.prime_kv(0, ctx0, seed)
+    setup = time.perf_counter() - t
+    n, el = _time_decode(om, O, cfg.vocab, ctx0, budget_s * 0.5, 10 ** 6)
+    res = {"value": round(n / el, 3), "unit": "tok/s", "cores": threads, "kind": "port",
+           "nproc": os.cpu_count(),
+           "sample": "oracle Gemma-3-1B int8 greedy decode (C restatement, row-blocked AVX2 "
+                     "linears), %d steps from ctx %d (the GPU line's mean context; cache primed "
+                     "with synthetic bf16 rows), %.1f s, OpenMP %d threads (setup %.1f s)"
+                     % (n, ctx0, el, threads, setup)}
+    # the reference's own loop shape, one thread
+    L.xo_set_threads(1)
+    om.set_kouter(True)
+    n1, el1 = _time_decode(om, O, cfg.vocab, ctx0, budget_s * 0.3, 10 ** 6)
+    res["single_thread"] = {"value": round(n1 / el1, 3), "unit": "tok/s", "cores": 1,
+                            "sample": "%d steps from ctx %d, %.1f s: k-outer [K, N] int8 linears "
+                                      "(opt125m_decode.rs:106-125 loop shape), one thread"
+                                      % (n1, ctx0, el1)}
     om.close()
-    return {"value": n / el, "unit": "tok/s", "cores": threads, "kind": "port",
-            "sample": "oracle Gemma-3-1B int8 decode (C restatement), %d-token prompt then %d "
-                      "greedy steps at ctx <= %d, %.1f s, OpenMP %d threads"
-                      % (prompt_len, n, pos, el, threads)}
+    # kernels: Lin::fwd int8 (k-outer) and attention, one thread
+    rng = np.random.default_rng(0)
+    kern = []
+    t_end = time.perf_counter() + budget_s * 0.2
+    for (m, k) in [(3072, 768), (6912, 1152), (4096, 4096)]:
+        q = rng.integers(-127, 128, (k, m)).astype(np.int8)
+        sc = rng.uniform(0.001, 0.02, m).astype(np.float32)
+        x = rng.standard_normal((1, k)).astype(np.float32)
+        y = np.empty((1, m), np.float32)
+        reps, t0 = 0, time.perf_counter()
+        while reps < 3 or (time.perf_counter() - t0 < 0.5 and time.perf_counter() < t_end):
+            L.xo_lin_fwd_i8_kn(x, 1, k, m, q, sc, None, y)
+            reps += 1
+        us = (time.perf_counter() - t0) / reps * 1e6
+        by = m * k + 4 * m + 4 * k + 4 * m
+        kern.append({"kernel": "Lin::fwd int8 %dx%d b=1" % (m, k), "us": round(us, 1),
+                     "gbps": round(by / us / 1e3, 2)})
+    for (hq, hkv, hd, ctx) in [(12, 12, 64, 4096), (4, 1, 256, 4096)]:
+        qv = rng.standard_normal((1, hq, hd)).astype(np.float32)
+        kc = O.bf16_bits(rng.standard_normal((1, hkv, ctx, hd)).astype(np.float32))
+        vc = O.bf16_bits(rng.standard_normal((1, hkv, ctx, hd)).astype(np.float32))
+        lens = np.array([ctx], np.int32)
+        reps, t0 = 0, time.perf_counter()
+        while reps < 3 or (time.perf_counter() - t0 < 0.5 and time.perf_counter() < t_end):
+            O.attn_decode(qv, kc, vc, lens, 1.0 / hd ** 0.5)
+            reps += 1
+        us = (time.perf_counter() - t0) / reps * 1e6
+        by = ctx * hkv * hd * 4
+        kern.append({"kernel": "attend_one %dq/%dkv x %d ctx %d b=1" % (hq, hkv, hd, ctx),
+                     "us": round(us, 1), "gbps": round(by / us / 1e3, 2)})
+    res["kernels"] = kern
+    L.xo_set_threads(threads)
+    return res
 
 
 def run_batch(xe, dev, cfg, args, B, steps, warmup, profile):
@@ -124,8 +187,11 @@ def run_batch(xe, dev, cfg, args, B, steps, warmup, profile):
         e[0] += 1
         e[1] += u
         e[2] += b
-    # whole-step algorithmic bytes at the mean context of the timed region
-    mean_ctx = args.prompt + W + K / 2.0
+    # whole-step algorithmic bytes at the mean context of the timed region:
+    # the timed steps process positions first..last
+    first = args.prompt + W
+    last = first + K - 1
+    mean_ctx = (first + last) / 2.0 + 1
     kv_bytes = B * cfg.n_layers * mean_ctx * cfg.n_kv_heads * cfg.head_dim * 2 * 2
     step_bytes = dec.weight_bytes() + kv_bytes
     hbm_gbps = step_bytes / step_s / 1e9
@@ -143,8 +209,10 @@ def run_batch(xe, dev, cfg, args, B, steps, warmup, profile):
     res = {
         "value": round(tok_s, 2), "unit": "tok/s", "steps": K, "warmup": W,
         "ms_per_step": round(step_s * 1e3, 4),
-        "config": {"workload": "gemma3-1b int8 greedy decode, batch %d, prompt %d, decode to "
-                               "ctx %d" % (B, args.prompt, args.ctx),
+        "config": {"workload": "gemma3-1b int8 greedy decode, batch %d, prompt %d, timed steps "
+                               "at positions %d..%d (context %d..%d)"
+                               % (B, args.prompt, first, last, first + 1, last + 1),
+                   "timed_positions": [first, last],
                    "layers": cfg.n_layers, "hidden": cfg.d_model, "heads": "4q/1kv x 256",
                    "ffn": cfg.ffn, "vocab": cfg.vocab, "batch": B, "prompt": args.prompt,
                    "ctx": args.ctx, "seed": args.seed, "executor": executor},
@@ -161,13 +229,117 @@ def run_batch(xe, dev, cfg, args, B, steps, warmup, profile):
                      "bytes": int(r_bytes), "us": round(r_us, 2)},
     }
     if profile:
-        res["phases"] = {l: {"launches": v[0], "us": round(v[1], 2),
-                             "gbps": round(v[2] / v[1] / 1e3, 1) if v[1] > 0 else None}
+        # per-phase device time of one traced step at the end context (the
+        # low-latency kernel's phases overlap loads staged by earlier phases,
+        # so no per-phase bandwidth is derived from them)
+        res["phases"] = {l: {"launches": v[0], "us": round(v[1], 2)}
                          for l, v in by_label.items()}
     dec.close()
     print("[bench] b=%d: %.1f tok/s, %.3f ms/step (%s)" % (B, tok_s, step_s * 1e3, executor),
           file=sys.stderr, flush=True)
     return res
+
+
+# ---- isolated kernels (BASELINE configs 2 and 3) ----
+
+GEMV_SHAPES = [(3072, 768), (768, 3072), (6912, 1152), (4096, 4096), (14336, 4096)]
+ROTATE_BYTES = 512 << 20   # weight copies per shape: >= 2x the 256 MB last-level cache
+
+
+def gemv_case(xe, dev, ctx, wd, m, k, batches, seed):
+    """Config 2: LayerNorm(x) then W x for one weight format and shape, over
+    enough device-resident copies of W (synthetic) to stream >= 512 MB per
+    rotation; returns one record per batch size."""
+    es = {xe.XE_I8: 1.0, xe.XE_BFP16: 1.125, xe.XE_BF16: 2.0}[wd]
+    per = int(m * k * es) + (4 * m if wd == xe.XE_I8 else 0)
+    n = max(2, min(256, -(-ROTATE_BYTES // per)))
+    esz = 2 if wd == xe.XE_BF16 else 1
+    wb = xe.Buf(dev, n * m * k * esz)
+    wb.fill_synthetic(xe.XE_BF16 if wd == xe.XE_BF16 else xe.XE_I8, seed, 1, n * m * k,
+                      std=0.02 if wd == xe.XE_BF16 else 60.0)
+    sb = eb = None
+    if wd == xe.XE_I8:
+        sb = xe.Buf(dev, n * m * 4)
+        sb.fill_synthetic(xe.XE_F32, seed, 2, n * m, mean=0.0105, std=0.003)
+    if wd == xe.XE_BFP16:
+        eb = xe.Buf(dev, n * m * k // 8)
+        eb.fill_synthetic(xe.XE_I8, seed, 3, n * m * k // 8, mean=118.0, std=2.0)
+    rng = np.random.default_rng(seed)
+    gamma = rng.normal(1.0, 0.1, k).astype(np.float32)
+    beta = rng.normal(0.0, 0.1, k).astype(np.float32)
+    views = []
+    for i in range(n):
+        w = ctx.register_weight_view(wd, m, k, wb.ptr + i * m * k * esz,
+                                     sb.ptr + i * m * 4 if sb else None,
+                                     eb.ptr + i * m * k // 8 if eb else None)
+        ctx.set_norm(w, xe.Norm.Ln(gamma, beta, 1e-5))
+        views.append(w)
+    xb = xe.Buf(dev, 8 * k * 2)
+    xb.fill_synthetic(xe.XE_BF16, seed, 4, 8 * k)
+    yb = xe.Buf(dev, 8 * m * 4)
+    out = []
+    name = {xe.XE_I8: "int8", xe.XE_BFP16: "bfp16", xe.XE_BF16: "bf16"}[wd]
+    for b in batches:
+        est_us = per / 5e6
+        reps = int(max(3, min(400, 3e5 / (n * est_us))))
+        us = ctx.probe_gemv(views, xb.ptr, xe.XE_BF16, b, yb.ptr, reps)
+        by = per + b * k * 2 + b * m * 4 + 8 * k
+        out.append({"kernel": "LN+GEMV %s %dx%d b=%d" % (name, m, k, b), "us": round(us, 3),
+                    "bytes": by, "gbps": round(by / us / 1e3, 1),
+                    "frac": round(by / us / 1e3 / HBM_PEAK_GBPS, 4), "copies": n,
+                    "rotation_mb": round(n * per / 1e6, 1)})
+        print("[kernels] %s" % out[-1], file=sys.stderr, flush=True)
+    for w in views:
+        w.free()
+    for buf in (wb, sb, eb, xb, yb):
+        if buf:
+            buf.free()
+    return out
+
+
+def attn_case(xe, dev, ctx, hq, hkv, hd, mc, b, seed):
+    """Config 3: one query per stream over a bf16 cache, lengths U[mc/2, mc]."""
+    rng = np.random.default_rng(seed)
+    lens = rng.integers(mc // 2, mc + 1, b).astype(np.int32)
+    nkv = b * hkv * mc * hd
+    kb, vb = xe.Buf(dev, nkv * 2), xe.Buf(dev, nkv * 2)
+    kb.fill_synthetic(xe.XE_BF16, seed, 11, nkv)
+    vb.fill_synthetic(xe.XE_BF16, seed, 12, nkv)
+    qb = xe.Buf(dev, b * hq * hd * 4)
+    qb.fill_synthetic(xe.XE_F32, seed, 13, b * hq * hd)
+    lb = xe.Buf.from_array(dev, lens)
+    ob = xe.Buf(dev, b * hq * hd * 4)
+    by = int(lens.astype(np.int64).sum()) * hkv * hd * 4 + b * hq * hd * 8
+    reps = int(max(3, min(200, 2e5 / max(by / 5e6, 1.0))))
+    us = ctx.probe_attn(qb.ptr, kb.ptr, vb.ptr, lb.ptr, b, hq, hkv, hd, mc, 1.0 / hd ** 0.5,
+                        ob.ptr, reps)
+    for buf in (kb, vb, qb, lb, ob):
+        buf.free()
+    rec = {"kernel": "mha_decode %dq/%dkv x %d ctx %d b=%d" % (hq, hkv, hd, mc, b),
+           "us": round(us, 2), "bytes": by, "gbps": round(by / us / 1e3, 1),
+           "frac": round(by / us / 1e3 / HBM_PEAK_GBPS, 4)}
+    print("[kernels] %s" % rec, file=sys.stderr, flush=True)
+    return rec
+
+
+def run_kernels(args):
+    xe = load_xe()
+    dev = xe.Device(0)
+    ctx = xe.CtxDecode(dev)
+    recs = []
+    for wd in (xe.XE_I8, xe.XE_BFP16, xe.XE_BF16):
+        for (m, k) in GEMV_SHAPES:
+            recs += gemv_case(xe, dev, ctx, wd, m, k, (1, 4, 8), args.seed + m + k)
+    for (hq, hkv, hd) in ((12, 12, 64), (4, 1, 256)):
+        for mc in (128, 1024, 4096, 32768):
+            for b in (1, 16, 64):
+                recs.append(attn_case(xe, dev, ctx, hq, hkv, hd, mc, b, args.seed + mc + b))
+    ctx.close()
+    dev.close()
+    return {"metric": "isolated kernel HBM GB/s (BASELINE configs 2 and 3)", "unit": "GB/s",
+            "peak": HBM_PEAK_GBPS, "timing": "HIP events around graph replays of the launches "
+            "(xe_probe_gemv / xe_probe_attn), weights rotated over >= 512 MB of copies",
+            "kernels": recs}
 
 
 def main():
@@ -184,23 +356,32 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
-                    help="only copy MIB MiB device to device (torch), three times: the plain "
-                         "copy kernel that scales rocprofv3's FETCH_SIZE / WRITE_SIZE counters")
+                    help="only copy MIB MiB device to device (the library's streaming copy "
+                         "kernel), three times: the plain copy that scales rocprofv3's "
+                         "FETCH_SIZE / WRITE_SIZE counters")
+    ap.add_argument("--kernels", action="store_true",
+                    help="only the isolated kernels: config-2 GEMVs and config-3 mha_decode")
     args = ap.parse_args()
-    if args.copy_probe > 0:
-        import torch
-        n = args.copy_probe * (1 << 20) // 4
-        x = torch.ones(n, dtype=torch.float32, device="cuda:0")
-        y = torch.empty_like(x)
-        for _ in range(3):
-            y.copy_(x)
-        torch.cuda.synchronize()
-        print(json.dumps({"copy_probe_bytes": n * 4, "copies": 3}), flush=True)
-        return
     if args.gpus != 1:
         print("bench.py: this build runs on one GPU only (every GPU box here has one); "
               "--gpus %d is not supported" % args.gpus, file=sys.stderr)
         sys.exit(2)
+    if args.copy_probe > 0:
+        xe = load_xe()
+        dev = xe.Device(0)
+        n = args.copy_probe * (1 << 20)
+        a, b = xe.Buf(dev, n), xe.Buf(dev, n)
+        a.fill_synthetic(xe.XE_I8, 1, 1, n)
+        for _ in range(3):
+            b.copy_from(a, n)
+        a.free()
+        b.free()
+        dev.close()
+        print(json.dumps({"copy_probe_bytes": n, "copies": 3, "kernel": "copy16_kernel"}), flush=True)
+        return
+    if args.kernels:
+        print(json.dumps(run_kernels(args)), flush=True)
+        return
 
     xe = load_xe()
     cfg = xe.GEMMA3_1B.replace(max_ctx=args.ctx)
@@ -233,7 +414,8 @@ def main():
                                                  profile=False)
     dev.close()
     if not args.no_cpu:
-        out["cpu_baseline"] = cpu_baseline(cfg, 4, args.cpu_seconds, args.seed)
+        first, last = head["config"]["timed_positions"]
+        out["cpu_baseline"] = cpu_baseline(cfg, (first + last) // 2, args.cpu_seconds, args.seed)
     print(json.dumps(out), flush=True)
 
 

@@ -102,6 +102,11 @@ size_t xe_buf_size(xe_buf *buf);
 int xe_buf_fill_synthetic(xe_buf *buf, size_t offset, int dtype, uint64_t seed,
                           uint32_t stream, uint64_t start, float mean,
                           float stdv, size_t count);
+/* Device-to-device copy by a streaming kernel (one read, one write per
+ * byte); sizes and offsets multiples of 16 bytes.  Also the known-size copy
+ * that calibrates the HBM byte counters. */
+int xe_buf_copy(xe_buf *dst, size_t dst_off, const xe_buf *src, size_t src_off,
+                size_t nbytes);
 
 /* ------------------------------------------------------------------------ */
 /* op layer (CtxDecode, ctx_decode.rs:142-694)                              */
@@ -130,6 +135,16 @@ xe_weight *xe_register_weight_bfp16(xe_ctx *ctx, int m, int k,
 /* Pre-rounded bf16 weight: bits [m,k]. */
 xe_weight *xe_register_weight_bf16(xe_ctx *ctx, int m, int k,
                                    const uint16_t *bits, const float *bias);
+/* A weight over device memory the caller owns (no copy; freeing the view
+ * leaves the memory alone): w_dev in the layout of the dtype above,
+ * scale_dev [m] fp32 (XE_I8), exps_dev [m, k/8] (XE_BFP16), bias_dev [m] or
+ * NULL.  The register-once form of DecodeWeight (ctx_decode.rs:82-140) for
+ * weights already resident, e.g. in a loaded arena (npu-weights/src/
+ * arena.rs:14-99). */
+xe_weight *xe_register_weight_view(xe_ctx *ctx, int wdtype, int m, int k,
+                                   const void *w_dev, const float *scale_dev,
+                                   const uint8_t *exps_dev,
+                                   const float *bias_dev);
 /* CtxDecode::register_fused (ctx_decode.rs:566-612): a weight plus a pre-norm
  * (enum xe_norm) applied to x on the device before the GEMV.  gamma/beta have
  * k elements (beta only for XE_NORM_LN). */
@@ -202,6 +217,20 @@ int xe_attn_decode_dev_static(xe_ctx *ctx, const float *q_dev,
 
 /* Wait for the ctx stream; returns 0 or -1. */
 int xe_ctx_synchronize(xe_ctx *ctx);
+
+/* Kernel probes (the reference's decode_gemv_probe.rs / mha_decode_probe.rs
+ * timing runs): the launches of one xe_gemv_dev per weight in ws (same
+ * shape; rotating copies defeat the 256 MB last-level cache) or of one
+ * xe_attn_decode_dev call are captured in a HIP graph and replayed reps
+ * times; the device time of the replays (HIP events on the ctx stream) per
+ * launch / per call is returned in microseconds. */
+int xe_probe_gemv(xe_ctx *ctx, const xe_weight *const *ws, int n_weights,
+                  const void *x_dev, int x_dtype, int batch, float *y_dev,
+                  int reps, double *us_per_launch);
+int xe_probe_attn(xe_ctx *ctx, const float *q_dev, const uint16_t *kc_dev,
+                  const uint16_t *vc_dev, const int32_t *lens_dev, int batch,
+                  int hq, int hkv, int hd, int max_ctx, float scale,
+                  float *out_dev, int reps, double *us_per_call);
 
 /* ------------------------------------------------------------------------ */
 /* decoder layer (decode-backend contract)                                  */

@@ -758,6 +758,7 @@ typedef struct {
   float *f32;       /* unquantised tensors */
   int8_t *q;        /* XE_I8 */
   int8_t *qb;       /* XE_I8 copy in blocks of 8 rows, k-major (xo_block8_i8) */
+  int8_t *qkn;      /* XE_I8 copy in the reference's [K, N] layout (k-outer mode) */
   float *s;
   uint16_t *bf;     /* XE_BF16 */
   int8_t *mant;     /* XE_BFP16 */
@@ -778,6 +779,7 @@ struct xo_model {
   int kv_f32;
   float *kcf, *vcf, *xkf, *xvf;
   int mutation; /* XO_MUT_*: a planted composition mistake (tests only) */
+  int kouter;   /* int8 linears through the reference's k-outer [K, N] loop */
 };
 
 /* Shape + init law of every tensor a family has.  Linear weights, biases and
@@ -905,7 +907,7 @@ void xo_model_free(xo_model *m) {
   for (int k = 0; k < XE_T_COUNT; k++)
     for (int l = 0; l < 65; l++) {
       xo_tensor *t = &m->t[k][l];
-      free(t->f32); free(t->q); free(t->qb); free(t->s); free(t->bf); free(t->mant); free(t->exps);
+      free(t->f32); free(t->q); free(t->qb); free(t->qkn); free(t->s); free(t->bf); free(t->mant); free(t->exps);
     }
   free(m->kc); free(m->vc); free(m->xk); free(m->xv);
   free(m->kcf); free(m->vcf); free(m->xkf); free(m->xvf);
@@ -954,7 +956,9 @@ static void xo_lin(const xo_model *m, int kind, int layer, int bias_kind,
   const xo_tensor *w = T(m, kind, layer);
   const xo_tensor *b = bias_kind >= 0 ? T(m, bias_kind, layer) : NULL;
   const float *bias = b ? b->f32 : NULL;
-  if (m->c.wdtype == XE_I8)
+  if (m->c.wdtype == XE_I8 && m->kouter)
+    xo_lin_fwd_i8_kn(x, 1, w->cols, w->rows, w->qkn, w->s, bias, y);
+  else if (m->c.wdtype == XE_I8)
     xo_gemv_i8_blocked(x, w->cols, w->rows, w->qb, w->s, bias, y);
   else if (m->c.wdtype == XE_BF16)
     xo_gemv_bf16w(x, 1, w->cols, w->rows, w->bf, bias, y);
@@ -987,6 +991,55 @@ int xo_model_set_mutation(xo_model *m, int code) {
     free(m->rope_sin);
     xo_rope_table(m);
   }
+  return 0;
+}
+
+/* int8 linears through the reference's own loop shape: W in [K, N], k
+ * outer, one f32 accumulator per output updated in k order
+ * (opt125m_decode.rs:106-125, xo_lin_fwd_i8_kn) -- the same values as the
+ * default row-blocked form, with the reference's memory traffic.  For the
+ * reference-shaped CPU timing. */
+int xo_model_set_kouter(xo_model *m, int on) {
+  m->kouter = 0;
+  if (!on) return 0;
+  if (m->c.wdtype != XE_I8) return -1;
+  for (int kind = 0; kind < XE_T_COUNT; kind++)
+    for (int l = 0; l < 65; l++) {
+      xo_tensor *t = &m->t[kind][l];
+      if (!t->present || !t->q || t->qkn) continue;
+      t->qkn = (int8_t *)malloc((size_t)t->rows * t->cols);
+      if (!t->qkn) return -1;
+#pragma omp parallel for schedule(static)
+      for (int r = 0; r < t->rows; r++)
+        for (int c = 0; c < t->cols; c++) t->qkn[(size_t)c * t->rows + r] = t->q[(size_t)r * t->cols + c];
+    }
+  m->kouter = 1;
+  return 0;
+}
+
+/* Fill stream b's K/V rows [0, n_pos) of every layer with synthetic bf16
+ * values (N(0,1) from the counter generator): a cache of a given length
+ * without feeding a prompt, for timing steps at long contexts. */
+int xo_model_prime_kv(xo_model *m, int b, int n_pos, uint64_t seed) {
+  if (b < 0 || b >= m->batch || n_pos < 0 || n_pos > m->c.max_ctx) return -1;
+  int Hk = m->c.n_kv_heads, hd = m->c.head_dim, MC = m->c.max_ctx;
+  for (int l = 0; l < m->c.n_layers; l++)
+    for (int h = 0; h < Hk; h++) {
+      size_t base = ((((size_t)l * m->batch + b) * Hk + h) * MC) * hd;
+      uint64_t kb = xo_synth_base(seed, (uint32_t)(2 * (l * Hk + h)));
+      uint64_t vb = xo_synth_base(seed, (uint32_t)(2 * (l * Hk + h) + 1));
+#pragma omp parallel for schedule(static)
+      for (size_t i = 0; i < (size_t)n_pos * hd; i++) {
+        float kv = xo_synth_value(kb, i, 0.0f, 1.0f), vv = xo_synth_value(vb, i, 0.0f, 1.0f);
+        if (m->kv_f32) {
+          m->kcf[base + i] = xo_bf16_round(kv);
+          m->vcf[base + i] = xo_bf16_round(vv);
+        } else {
+          m->kc[base + i] = xo_f32_to_bf16_bits(kv);
+          m->vc[base + i] = xo_f32_to_bf16_bits(vv);
+        }
+      }
+    }
   return 0;
 }
 

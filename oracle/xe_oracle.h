@@ -142,6 +142,10 @@ enum {
   XO_MUT_OPT_NO_Q_SCALE = 6        /* OPT q not scaled by hd^-0.5 */
 };
 int xo_model_set_mutation(xo_model *m, int code);
+/* int8 linears through the reference's k-outer [K, N] loop (same values). */
+int xo_model_set_kouter(xo_model *m, int on);
+/* Synthetic bf16 K/V rows [0, n_pos) for stream b (timing at long contexts). */
+int xo_model_prime_kv(xo_model *m, int b, int n_pos, uint64_t seed);
 /* enc [n_cross, d]; NULL = the synthetic XE_T_ENC_OUT tensor. */
 int xo_model_set_cross(xo_model *m, const float *enc);
 /* One step for every stream b < batch: tokens[b] at pos[b]. */

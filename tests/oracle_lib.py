@@ -89,6 +89,8 @@ def lib():
         "xo_model_reset": (None, [C.c_void_p]),
         "xo_model_set_kv_f32": (C.c_int, [C.c_void_p, C.c_int]),
         "xo_model_set_mutation": (C.c_int, [C.c_void_p, C.c_int]),
+        "xo_model_set_kouter": (C.c_int, [C.c_void_p, C.c_int]),
+        "xo_model_prime_kv": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_uint64]),
         "xo_model_set_cross": (C.c_int, [C.c_void_p, C.c_void_p]),
         "xo_model_step": (None, [C.c_void_p, i32p, i32p, C.c_int, f32p]),
         "xo_model_argmax": (C.c_int, [C.c_void_p, f32p]),
@@ -249,6 +251,14 @@ class OracleModel:
     def set_mutation(self, code):
         """Plant a composition mistake (oracle XO_MUT_*), 0 for none."""
         assert lib().xo_model_set_mutation(self.h, code) == 0
+
+    def set_kouter(self, on=True):
+        """int8 linears through the reference's k-outer [K, N] loop."""
+        assert lib().xo_model_set_kouter(self.h, 1 if on else 0) == 0
+
+    def prime_kv(self, b, n_pos, seed=0):
+        """Synthetic K/V rows [0, n_pos) of stream b (timing at long contexts)."""
+        assert lib().xo_model_prime_kv(self.h, b, n_pos, seed) == 0
 
     def set_kv_f32(self, on=True):
         """fp32 K/V caches (the reference CPU decoders' choice) instead of bf16."""

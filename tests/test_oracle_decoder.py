@@ -106,3 +106,18 @@ def test_bf16_kv_oracle_deviation_is_bounded(name):
     om.close()
     err = rel_l2(got, want)
     assert err.max() <= 1e-2, err   # measured 1.3e-3 (OPT, Whisper), 4.1e-3 (Gemma-3)
+
+
+def test_kouter_mode_is_bit_identical():
+    """The reference-shaped k-outer linears ([K, N], opt125m_decode.rs:106-125)
+    used for the CPU timing compute exactly the default form's values."""
+    fx = fixture("gemma3")
+    a = oracle_model(fx, kv_f32=False)
+    b = oracle_model(fx, kv_f32=False)
+    b.set_kouter(True)
+    toks = fx["tokens"]
+    la = oracle_logits(a, toks, 12)
+    lb = oracle_logits(b, toks, 12)
+    assert np.array_equal(la.view(np.uint32), lb.view(np.uint32))
+    a.close()
+    b.close()

@@ -118,6 +118,8 @@ T *dev_upload(const T *src, size_t n, hipStream_t s) {
   return d;
 }
 
+// The matrix, scales, exponents and bias belong to the weight unless it is a
+// view (xe_register_weight_view); a pre-norm's gamma / beta always do.
 void free_weight(xe_weight *w) {
   if (!w) return;
   if (w->owns) {
@@ -125,9 +127,9 @@ void free_weight(xe_weight *w) {
     (void)hipFree(w->scale);
     (void)hipFree(w->exps);
     (void)hipFree(w->bias);
-    (void)hipFree(w->gamma);
-    (void)hipFree(w->beta);
   }
+  (void)hipFree(w->gamma);
+  (void)hipFree(w->beta);
   delete w;
 }
 
@@ -184,10 +186,8 @@ void fill_weight_from_f32(xe_weight *wt, const float *w_mk, const float *bias) {
 void set_norm(xe_weight *w, int norm, const float *gamma, const float *beta, float eps) {
   XE_REQUIRE(norm >= XE_NORM_NONE && norm <= XE_NORM_RMS1P, "unknown norm kind");
   hipStream_t s = w->ctx->dev->stream;
-  if (w->owns) {
-    (void)hipFree(w->gamma);
-    (void)hipFree(w->beta);
-  }
+  (void)hipFree(w->gamma);
+  (void)hipFree(w->beta);
   w->gamma = w->beta = nullptr;
   w->norm = norm;
   w->eps = eps;
@@ -488,6 +488,25 @@ xe_weight *xe_register_weight_bf16(xe_ctx *ctx, int m, int k, const uint16_t *bi
   }, nullptr);
 }
 
+xe_weight *xe_register_weight_view(xe_ctx *ctx, int wdtype, int m, int k, const void *w_dev,
+                                   const float *scale_dev, const uint8_t *exps_dev,
+                                   const float *bias_dev) {
+  return guard([&]() -> xe_weight * {
+    XE_REQUIRE(w_dev, "null weight pointer");
+    XE_REQUIRE(wdtype == XE_I8 || wdtype == XE_BF16 || wdtype == XE_BFP16, "unknown weight dtype");
+    XE_REQUIRE(wdtype != XE_I8 || scale_dev, "int8 weight view needs scales");
+    XE_REQUIRE(wdtype != XE_BFP16 || exps_dev, "bfp16 weight view needs exponents");
+    DeviceGuard dg(ctx ? ctx->dev->ordinal : 0);
+    xe_weight *wt = new_weight(ctx, wdtype, m, k);
+    wt->owns = false;
+    wt->w = const_cast<void *>(w_dev);
+    wt->scale = const_cast<float *>(scale_dev);
+    wt->exps = const_cast<uint8_t *>(exps_dev);
+    wt->bias = const_cast<float *>(bias_dev);
+    return wt;
+  }, nullptr);
+}
+
 xe_weight *xe_register_fused(xe_ctx *ctx, int wdtype, int m, int k, const float *w, int layout,
                              int norm, const float *gamma, const float *beta, float eps,
                              const float *bias) {
@@ -727,6 +746,96 @@ int xe_attn_decode(xe_ctx *ctx, const float *q, const uint16_t *kc, const uint16
     attn_impl(ctx, dq, dk, dv, dl, batch, hq, hkv, hd, max_ctx, scale, dout);
     XE_HIP(hipMemcpyAsync(out, dout, qn * 4, hipMemcpyDeviceToHost, s));
     XE_HIP(hipStreamSynchronize(s));
+    return 0;
+  }, -1);
+}
+
+}  // extern "C"
+
+namespace {
+
+// Replay a captured sequence of launches `reps` times on the ctx stream and
+// return the device microseconds per replay (HIP events around the replays).
+template <typename F>
+double time_captured(xe_ctx *ctx, int reps, F &&enqueue) {
+  hipStream_t s = ctx->dev->stream;
+  XE_HIP(hipStreamSynchronize(s));
+  hipGraph_t g = nullptr;
+  XE_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeRelaxed));
+  try {
+    enqueue();
+  } catch (...) {
+    hipGraph_t junk = nullptr;
+    (void)hipStreamEndCapture(s, &junk);
+    if (junk) (void)hipGraphDestroy(junk);
+    throw;
+  }
+  XE_HIP(hipStreamEndCapture(s, &g));
+  hipGraphExec_t ex = nullptr;
+  const hipError_t ie = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(g);
+  XE_HIP(ie);
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  double us = 0.0;
+  try {
+    XE_HIP(hipGraphLaunch(ex, s));  // warm-up replay
+    XE_HIP(hipEventCreate(&e0));
+    XE_HIP(hipEventCreate(&e1));
+    XE_HIP(hipEventRecord(e0, s));
+    for (int r = 0; r < reps; r++) XE_HIP(hipGraphLaunch(ex, s));
+    XE_HIP(hipEventRecord(e1, s));
+    XE_HIP(hipEventSynchronize(e1));
+    float ms = 0.f;
+    XE_HIP(hipEventElapsedTime(&ms, e0, e1));
+    us = 1000.0 * ms / reps;
+  } catch (...) {
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    (void)hipGraphExecDestroy(ex);
+    throw;
+  }
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  (void)hipGraphExecDestroy(ex);
+  return us;
+}
+
+}  // namespace
+
+extern "C" {
+
+int xe_probe_gemv(xe_ctx *ctx, const xe_weight *const *ws, int n_weights, const void *x_dev,
+                  int x_dtype, int batch, float *y_dev, int reps, double *us_per_launch) {
+  return guard([&]() -> int {
+    XE_REQUIRE(ctx && ws && n_weights > 0 && x_dev && y_dev && us_per_launch, "null argument");
+    XE_REQUIRE(reps > 0, "reps must be positive");
+    XE_REQUIRE(batch >= 1 && batch <= kMaxOpBatch, "gemv batch must be 1..512");
+    for (int i = 0; i < n_weights; i++) {
+      XE_REQUIRE(ws[i], "null weight");
+      XE_REQUIRE(ws[i]->m == ws[0]->m && ws[i]->k == ws[0]->k, "probe weights differ in shape");
+    }
+    DeviceGuard dg(ctx->dev->ordinal);
+    if (batch > 8) ctx->ensure_gemm(static_cast<size_t>(batch) * ws[0]->k);  // no allocation under capture
+    const double us = time_captured(ctx, reps, [&]() {
+      for (int i = 0; i < n_weights; i++)
+        launch_linear(ctx, ws[i], x_dev, x_dtype, batch, y_dev, ctx->dev->stream);
+    });
+    *us_per_launch = us / n_weights;
+    return 0;
+  }, -1);
+}
+
+int xe_probe_attn(xe_ctx *ctx, const float *q_dev, const uint16_t *kc_dev, const uint16_t *vc_dev,
+                  const int32_t *lens_dev, int batch, int hq, int hkv, int hd, int max_ctx,
+                  float scale, float *out_dev, int reps, double *us_per_call) {
+  return guard([&]() -> int {
+    XE_REQUIRE(ctx && q_dev && kc_dev && vc_dev && lens_dev && out_dev && us_per_call, "null argument");
+    XE_REQUIRE(batch > 0 && hq > 0 && hkv > 0 && hd > 0 && reps > 0, "bad shape");
+    DeviceGuard dg(ctx->dev->ordinal);
+    ctx->ensure_attn(attn_work_floats(batch, hq, hd, attn_splits(ctx, batch, hkv, max_ctx)));
+    *us_per_call = time_captured(ctx, reps, [&]() {
+      attn_impl(ctx, q_dev, kc_dev, vc_dev, lens_dev, batch, hq, hkv, hd, max_ctx, scale, out_dev);
+    });
     return 0;
   }, -1);
 }

@@ -145,6 +145,14 @@ __global__ void synth_fill_kernel(uint64_t base, float mean, float k, uint64_t s
   }
 }
 
+// dst[i] = src[i] over n 16-byte words (a plain streaming copy: one read and
+// one write per byte).
+__global__ void copy16_kernel(const uint4 *src, uint4 *dst, size_t n) {
+  for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < n;
+       i += static_cast<size_t>(gridDim.x) * blockDim.x)
+    dst[i] = src[i];
+}
+
 // --------------------------------------------------------------------------
 // step kernels
 // --------------------------------------------------------------------------
@@ -1768,6 +1776,28 @@ int xe_buf_fill_synthetic(xe_buf *buf, size_t offset, int dtype, uint64_t seed, 
     synth_fill_kernel<<<static_cast<unsigned>(blocks), 256, 0, st>>>(
         synth_base(seed, stream), mean, stdv * kIh4InvStd, start, count,
         static_cast<char *>(buf->ptr) + offset, dtype);
+    XE_HIP(hipGetLastError());
+    XE_HIP(hipStreamSynchronize(st));
+    return 0;
+  }, -1);
+}
+
+int xe_buf_copy(xe_buf *dst, size_t dst_off, const xe_buf *src, size_t src_off, size_t nbytes) {
+  return guard_d([&]() -> int {
+    XE_REQUIRE(dst && src && dst->ptr && src->ptr, "null buffer");
+    XE_REQUIRE(dst->dev == src->dev, "buffers on different devices");
+    XE_REQUIRE(nbytes % 16 == 0 && dst_off % 16 == 0 && src_off % 16 == 0,
+               "copy sizes and offsets must be multiples of 16 bytes");
+    XE_REQUIRE(dst_off <= dst->size && nbytes <= dst->size - dst_off, "copy runs past the destination");
+    XE_REQUIRE(src_off <= src->size && nbytes <= src->size - src_off, "copy runs past the source");
+    if (nbytes == 0) return 0;
+    DeviceGuard dg(dst->dev->ordinal);
+    hipStream_t st = dst->dev->stream;
+    const size_t n = nbytes / 16;
+    const size_t blocks = std::min<size_t>((n + 255) / 256, 16384);
+    copy16_kernel<<<static_cast<unsigned>(blocks), 256, 0, st>>>(
+        reinterpret_cast<const uint4 *>(static_cast<const char *>(src->ptr) + src_off),
+        reinterpret_cast<uint4 *>(static_cast<char *>(dst->ptr) + dst_off), n);
     XE_HIP(hipGetLastError());
     XE_HIP(hipStreamSynchronize(st));
     return 0;

@@ -33,7 +33,8 @@ EXECUTORS = {0: "graph", 1: "persistent", 2: "eager", 3: "ll"}
 EXPORTS = [
     "xe_last_error", "xe_abi_version", "xe_device_count", "xe_device_open", "xe_device_close",
     "xe_device_synchronize", "xe_device_name", "xe_buf_alloc", "xe_buf_free", "xe_buf_write",
-    "xe_buf_read", "xe_buf_device_ptr", "xe_buf_size", "xe_buf_fill_synthetic", "xe_ctx_create",
+    "xe_buf_read", "xe_buf_device_ptr", "xe_buf_size", "xe_buf_fill_synthetic", "xe_buf_copy", "xe_register_weight_view", "xe_probe_gemv",
+    "xe_probe_attn", "xe_ctx_create",
     "xe_ctx_destroy",
     "xe_ctx_dispatches", "xe_ctx_reset_dispatches", "xe_register_weight",
     "xe_register_weight_q8", "xe_register_weight_bfp16", "xe_register_weight_bf16",
@@ -116,6 +117,10 @@ def lib():
         "xe_buf_device_ptr": (vp, [vp]),
         "xe_buf_size": (sz, [vp]),
         "xe_buf_fill_synthetic": (i, [vp, sz, i, u64, C.c_uint32, u64, f, f, sz]),
+        "xe_buf_copy": (i, [vp, sz, vp, sz, sz]),
+        "xe_register_weight_view": (vp, [vp, i, i, i, vp, vp, vp, vp]),
+        "xe_probe_gemv": (i, [vp, vp, i, vp, i, i, vp, i, C.POINTER(C.c_double)]),
+        "xe_probe_attn": (i, [vp, vp, vp, vp, vp, i, i, i, i, i, f, vp, i, C.POINTER(C.c_double)]),
         "xe_ctx_create": (vp, [vp]),
         "xe_ctx_destroy": (None, [vp]),
         "xe_ctx_dispatches": (u64, [vp]),
@@ -238,6 +243,10 @@ class Buf:
         _check(lib().xe_buf_read(self.h, _p(out), out.nbytes, offset))
         return out
 
+    def copy_from(self, src, nbytes, dst_off=0, src_off=0):
+        """Device-to-device copy by the library's streaming copy kernel."""
+        _check(lib().xe_buf_copy(self.h, dst_off, src.h, src_off, nbytes))
+
     def fill_synthetic(self, dtype, seed, stream, count, mean=0.0, std=1.0, start=0, offset=0):
         """Elements [start, start+count) of the synthetic stream (seed, stream)
         written at byte offset, as XE_F32 / XE_BF16 / XE_I8 (on the device)."""
@@ -344,6 +353,28 @@ class CtxDecode:
     def set_norm(self, weight, norm):
         _check(lib().xe_weight_set_norm(weight.h, norm.kind, _p(norm.gamma), _p(norm.beta),
                                         norm.eps))
+
+    def register_weight_view(self, wdtype, m, k, w_ptr, scale_ptr=None, exps_ptr=None,
+                             bias_ptr=None):
+        """A weight over device memory (Buf.ptr + offset); no copy."""
+        return Weight(lib().xe_register_weight_view(self.h, wdtype, m, k, w_ptr, scale_ptr,
+                                                    exps_ptr, bias_ptr))
+
+    def probe_gemv(self, weights, x_ptr, x_dtype, batch, y_ptr, reps):
+        """Device microseconds per launch of xe_gemv_dev rotating over weights."""
+        arr = (C.c_void_p * len(weights))(*[w.h for w in weights])
+        us = C.c_double()
+        _check(lib().xe_probe_gemv(self.h, arr, len(weights), x_ptr, x_dtype, batch, y_ptr, reps,
+                                   C.byref(us)))
+        return us.value
+
+    def probe_attn(self, q_ptr, k_ptr, v_ptr, lens_ptr, b, hq, hkv, hd, max_ctx, scale, out_ptr,
+                   reps):
+        """Device microseconds per xe_attn_decode_dev call."""
+        us = C.c_double()
+        _check(lib().xe_probe_attn(self.h, q_ptr, k_ptr, v_ptr, lens_ptr, b, hq, hkv, hd, max_ctx,
+                                   scale, out_ptr, reps, C.byref(us)))
+        return us.value
 
     # -- execution (ctx_decode.rs:325-366, 617-643) --
     def _run(self, fn, weight, x):
