@@ -246,7 +246,7 @@ GEMV_SHAPES = [(3072, 768), (768, 3072), (6912, 1152), (4096, 4096), (14336, 409
 ROTATE_BYTES = 512 << 20   # weight copies per shape: >= 2x the 256 MB last-level cache
 
 
-def gemv_case(xe, dev, ctx, wd, m, k, batches, seed):
+def gemv_case(xe, dev, ctx, wd, m, k, batches, seed, eager):
     """Config 2: LayerNorm(x) then W x for one weight format and shape, over
     enough device-resident copies of W (synthetic) to stream >= 512 MB per
     rotation; returns one record per batch size."""
@@ -282,7 +282,7 @@ def gemv_case(xe, dev, ctx, wd, m, k, batches, seed):
     for b in batches:
         est_us = per / 5e6
         reps = int(max(3, min(400, 3e5 / (n * est_us))))
-        us = ctx.probe_gemv(views, xb.ptr, xe.XE_BF16, b, yb.ptr, reps)
+        us = ctx.probe_gemv(views, xb.ptr, xe.XE_BF16, b, yb.ptr, reps, eager)
         by = per + b * k * 2 + b * m * 4 + 8 * k
         out.append({"kernel": "LN+GEMV %s %dx%d b=%d" % (name, m, k, b), "us": round(us, 3),
                     "bytes": by, "gbps": round(by / us / 1e3, 1),
@@ -297,7 +297,7 @@ def gemv_case(xe, dev, ctx, wd, m, k, batches, seed):
     return out
 
 
-def attn_case(xe, dev, ctx, hq, hkv, hd, mc, b, seed):
+def attn_case(xe, dev, ctx, hq, hkv, hd, mc, b, seed, eager):
     """Config 3: one query per stream over a bf16 cache, lengths U[mc/2, mc]."""
     rng = np.random.default_rng(seed)
     lens = rng.integers(mc // 2, mc + 1, b).astype(np.int32)
@@ -312,7 +312,7 @@ def attn_case(xe, dev, ctx, hq, hkv, hd, mc, b, seed):
     by = int(lens.astype(np.int64).sum()) * hkv * hd * 4 + b * hq * hd * 8
     reps = int(max(3, min(200, 2e5 / max(by / 5e6, 1.0))))
     us = ctx.probe_attn(qb.ptr, kb.ptr, vb.ptr, lb.ptr, b, hq, hkv, hd, mc, 1.0 / hd ** 0.5,
-                        ob.ptr, reps)
+                        ob.ptr, reps, eager)
     for buf in (kb, vb, qb, lb, ob):
         buf.free()
     rec = {"kernel": "mha_decode %dq/%dkv x %d ctx %d b=%d" % (hq, hkv, hd, mc, b),
@@ -329,16 +329,19 @@ def run_kernels(args):
     recs = []
     for wd in (xe.XE_I8, xe.XE_BFP16, xe.XE_BF16):
         for (m, k) in GEMV_SHAPES:
-            recs += gemv_case(xe, dev, ctx, wd, m, k, (1, 4, 8), args.seed + m + k)
+            recs += gemv_case(xe, dev, ctx, wd, m, k, (1, 4, 8), args.seed + m + k, args.eager)
     for (hq, hkv, hd) in ((12, 12, 64), (4, 1, 256)):
         for mc in (128, 1024, 4096, 32768):
             for b in (1, 16, 64):
-                recs.append(attn_case(xe, dev, ctx, hq, hkv, hd, mc, b, args.seed + mc + b))
+                recs.append(attn_case(xe, dev, ctx, hq, hkv, hd, mc, b, args.seed + mc + b,
+                                      args.eager))
     ctx.close()
     dev.close()
     return {"metric": "isolated kernel HBM GB/s (BASELINE configs 2 and 3)", "unit": "GB/s",
-            "peak": HBM_PEAK_GBPS, "timing": "HIP events around graph replays of the launches "
-            "(xe_probe_gemv / xe_probe_attn), weights rotated over >= 512 MB of copies",
+            "peak": HBM_PEAK_GBPS,
+            "timing": ("HIP events around plain back-to-back launches" if args.eager else
+                       "HIP events around graph replays of the launches") +
+                      " (xe_probe_gemv / xe_probe_attn), weights rotated over >= 512 MB of copies",
             "kernels": recs}
 
 
@@ -361,6 +364,9 @@ def main():
                          "FETCH_SIZE / WRITE_SIZE counters")
     ap.add_argument("--kernels", action="store_true",
                     help="only the isolated kernels: config-2 GEMVs and config-3 mha_decode")
+    ap.add_argument("--eager", action="store_true",
+                    help="--kernels with plain launches instead of graph replays (for runs under "
+                         "rocprofv3's kernel trace, which has crashed on graph launches here)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build runs on one GPU only (every GPU box here has one); "

@@ -221,16 +221,19 @@ int xe_ctx_synchronize(xe_ctx *ctx);
 /* Kernel probes (the reference's decode_gemv_probe.rs / mha_decode_probe.rs
  * timing runs): the launches of one xe_gemv_dev per weight in ws (same
  * shape; rotating copies defeat the 256 MB last-level cache) or of one
- * xe_attn_decode_dev call are captured in a HIP graph and replayed reps
- * times; the device time of the replays (HIP events on the ctx stream) per
- * launch / per call is returned in microseconds. */
+ * xe_attn_decode_dev call, repeated reps times; the device time (HIP events
+ * on the ctx stream) per launch / per call is returned in microseconds.
+ * flags 0: the launches are captured in a HIP graph and the graph replayed
+ * (no host gaps); XE_PROBE_EAGER: plain launches (for runs under a kernel
+ * tracer, which reports the kernel durations itself). */
+enum { XE_PROBE_EAGER = 1 };
 int xe_probe_gemv(xe_ctx *ctx, const xe_weight *const *ws, int n_weights,
                   const void *x_dev, int x_dtype, int batch, float *y_dev,
-                  int reps, double *us_per_launch);
+                  int reps, int flags, double *us_per_launch);
 int xe_probe_attn(xe_ctx *ctx, const float *q_dev, const uint16_t *kc_dev,
                   const uint16_t *vc_dev, const int32_t *lens_dev, int batch,
                   int hq, int hkv, int hd, int max_ctx, float scale,
-                  float *out_dev, int reps, double *us_per_call);
+                  float *out_dev, int reps, int flags, double *us_per_call);
 
 /* ------------------------------------------------------------------------ */
 /* decoder layer (decode-backend contract)                                  */

@@ -754,10 +754,45 @@ int xe_attn_decode(xe_ctx *ctx, const float *q, const uint16_t *kc, const uint16
 
 namespace {
 
-// Replay a captured sequence of launches `reps` times on the ctx stream and
-// return the device microseconds per replay (HIP events around the replays).
+// Device microseconds per repetition of `enqueue` (HIP events on the ctx
+// stream around the repetitions).  XE_PROBE_EAGER: plain launches, so the
+// time includes any host gaps between short kernels (a profiler's per-kernel
+// trace then gives the kernel durations; graph launches under a kernel
+// tracer have crashed in the HIP runtime on this image).  Otherwise the
+// launches are captured once in a HIP graph and the graph is replayed.
 template <typename F>
-double time_captured(xe_ctx *ctx, int reps, F &&enqueue) {
+double time_eager(xe_ctx *ctx, int reps, F &&enqueue) {
+  hipStream_t s = ctx->dev->stream;
+  enqueue();  // warm-up
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  XE_HIP(hipEventCreate(&e0));
+  const hipError_t ce = hipEventCreate(&e1);
+  if (ce != hipSuccess) {
+    (void)hipEventDestroy(e0);
+    XE_HIP(ce);
+  }
+  double us = 0.0;
+  try {
+    XE_HIP(hipEventRecord(e0, s));
+    for (int r = 0; r < reps; r++) enqueue();
+    XE_HIP(hipEventRecord(e1, s));
+    XE_HIP(hipEventSynchronize(e1));
+    float ms = 0.f;
+    XE_HIP(hipEventElapsedTime(&ms, e0, e1));
+    us = 1000.0 * ms / reps;
+  } catch (...) {
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    throw;
+  }
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  return us;
+}
+
+template <typename F>
+double time_captured(xe_ctx *ctx, int reps, int flags, F &&enqueue) {
+  if (flags & XE_PROBE_EAGER) return time_eager(ctx, reps, enqueue);
   hipStream_t s = ctx->dev->stream;
   XE_HIP(hipStreamSynchronize(s));
   hipGraph_t g = nullptr;
@@ -805,7 +840,8 @@ double time_captured(xe_ctx *ctx, int reps, F &&enqueue) {
 extern "C" {
 
 int xe_probe_gemv(xe_ctx *ctx, const xe_weight *const *ws, int n_weights, const void *x_dev,
-                  int x_dtype, int batch, float *y_dev, int reps, double *us_per_launch) {
+                  int x_dtype, int batch, float *y_dev, int reps, int flags,
+                  double *us_per_launch) {
   return guard([&]() -> int {
     XE_REQUIRE(ctx && ws && n_weights > 0 && x_dev && y_dev && us_per_launch, "null argument");
     XE_REQUIRE(reps > 0, "reps must be positive");
@@ -816,7 +852,7 @@ int xe_probe_gemv(xe_ctx *ctx, const xe_weight *const *ws, int n_weights, const 
     }
     DeviceGuard dg(ctx->dev->ordinal);
     if (batch > 8) ctx->ensure_gemm(static_cast<size_t>(batch) * ws[0]->k);  // no allocation under capture
-    const double us = time_captured(ctx, reps, [&]() {
+    const double us = time_captured(ctx, reps, flags, [&]() {
       for (int i = 0; i < n_weights; i++)
         launch_linear(ctx, ws[i], x_dev, x_dtype, batch, y_dev, ctx->dev->stream);
     });
@@ -827,13 +863,13 @@ int xe_probe_gemv(xe_ctx *ctx, const xe_weight *const *ws, int n_weights, const 
 
 int xe_probe_attn(xe_ctx *ctx, const float *q_dev, const uint16_t *kc_dev, const uint16_t *vc_dev,
                   const int32_t *lens_dev, int batch, int hq, int hkv, int hd, int max_ctx,
-                  float scale, float *out_dev, int reps, double *us_per_call) {
+                  float scale, float *out_dev, int reps, int flags, double *us_per_call) {
   return guard([&]() -> int {
     XE_REQUIRE(ctx && q_dev && kc_dev && vc_dev && lens_dev && out_dev && us_per_call, "null argument");
     XE_REQUIRE(batch > 0 && hq > 0 && hkv > 0 && hd > 0 && reps > 0, "bad shape");
     DeviceGuard dg(ctx->dev->ordinal);
     ctx->ensure_attn(attn_work_floats(batch, hq, hd, attn_splits(ctx, batch, hkv, max_ctx)));
-    *us_per_call = time_captured(ctx, reps, [&]() {
+    *us_per_call = time_captured(ctx, reps, flags, [&]() {
       attn_impl(ctx, q_dev, kc_dev, vc_dev, lens_dev, batch, hq, hkv, hd, max_ctx, scale, out_dev);
     });
     return 0;

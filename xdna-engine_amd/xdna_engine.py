@@ -119,8 +119,8 @@ def lib():
         "xe_buf_fill_synthetic": (i, [vp, sz, i, u64, C.c_uint32, u64, f, f, sz]),
         "xe_buf_copy": (i, [vp, sz, vp, sz, sz]),
         "xe_register_weight_view": (vp, [vp, i, i, i, vp, vp, vp, vp]),
-        "xe_probe_gemv": (i, [vp, vp, i, vp, i, i, vp, i, C.POINTER(C.c_double)]),
-        "xe_probe_attn": (i, [vp, vp, vp, vp, vp, i, i, i, i, i, f, vp, i, C.POINTER(C.c_double)]),
+        "xe_probe_gemv": (i, [vp, vp, i, vp, i, i, vp, i, i, C.POINTER(C.c_double)]),
+        "xe_probe_attn": (i, [vp, vp, vp, vp, vp, i, i, i, i, i, f, vp, i, i, C.POINTER(C.c_double)]),
         "xe_ctx_create": (vp, [vp]),
         "xe_ctx_destroy": (None, [vp]),
         "xe_ctx_dispatches": (u64, [vp]),
@@ -360,20 +360,21 @@ class CtxDecode:
         return Weight(lib().xe_register_weight_view(self.h, wdtype, m, k, w_ptr, scale_ptr,
                                                     exps_ptr, bias_ptr))
 
-    def probe_gemv(self, weights, x_ptr, x_dtype, batch, y_ptr, reps):
-        """Device microseconds per launch of xe_gemv_dev rotating over weights."""
+    def probe_gemv(self, weights, x_ptr, x_dtype, batch, y_ptr, reps, eager=False):
+        """Device microseconds per launch of xe_gemv_dev rotating over weights
+        (graph replays; eager: plain launches)."""
         arr = (C.c_void_p * len(weights))(*[w.h for w in weights])
         us = C.c_double()
         _check(lib().xe_probe_gemv(self.h, arr, len(weights), x_ptr, x_dtype, batch, y_ptr, reps,
-                                   C.byref(us)))
+                                   1 if eager else 0, C.byref(us)))
         return us.value
 
     def probe_attn(self, q_ptr, k_ptr, v_ptr, lens_ptr, b, hq, hkv, hd, max_ctx, scale, out_ptr,
-                   reps):
+                   reps, eager=False):
         """Device microseconds per xe_attn_decode_dev call."""
         us = C.c_double()
         _check(lib().xe_probe_attn(self.h, q_ptr, k_ptr, v_ptr, lens_ptr, b, hq, hkv, hd, max_ctx,
-                                   scale, out_ptr, reps, C.byref(us)))
+                                   scale, out_ptr, reps, 1 if eager else 0, C.byref(us)))
         return us.value
 
     # -- execution (ctx_decode.rs:325-366, 617-643) --
