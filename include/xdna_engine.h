@@ -43,7 +43,9 @@ enum xe_dtype {
   XE_BF16 = 1,
   XE_I8 = 2,    /* int8 symmetric, per-output-row fp32 scale */
   XE_BFP16 = 3, /* 8 int8 mantissas per block + one biased 8-bit exponent */
-  XE_I32 = 4
+  XE_I32 = 4,
+  XE_I4 = 5     /* int4 symmetric (+-7), per-output-row fp32 scale; two
+                   nibbles a byte along k (k = 2j low, 2j+1 high) */
 };
 
 /* pre-norm of the fused norm+GEMV (ctx_decode.rs:74-79 Norm) */
@@ -122,12 +124,25 @@ void xe_ctx_reset_dispatches(xe_ctx *ctx);
 /* CtxDecode::register_weight (ctx_decode.rs:269-317): copy W (fp32, layout
  * MK [m,k] or KN [k,m]) to the device, quantised to wdtype (XE_I8: per-row
  * symmetric int8, scale = amax/127, round half away from zero, clamp +-127 --
- * opt125m_decode.rs:45-62; XE_BFP16; XE_BF16 RNE).  bias may be NULL. */
+ * opt125m_decode.rs:45-62; XE_I4: scale = amax/7, clamp +-7 --
+ * opt125m_decode.rs:63-79; XE_BFP16; XE_BF16 RNE).  bias may be NULL. */
 xe_weight *xe_register_weight(xe_ctx *ctx, int wdtype, int m, int k,
                               const float *w, int layout, const float *bias);
 /* Pre-quantised int8 weight: q [m,k] row-major, scales [m] (fp32). */
 xe_weight *xe_register_weight_q8(xe_ctx *ctx, int m, int k, const int8_t *q,
                                  const float *scales, const float *bias);
+/* Pre-quantised int4 weight (Lin int4 branch, opt125m_decode.rs:63-105):
+ * packed uint8 [m, k/2], byte j of row r holding k = 2j in the low nibble
+ * and k = 2j+1 in the high one (two's complement, -7..7), scales [m] fp32.
+ * The reference's own packing ([K, N/2], two output columns a byte) is taken
+ * by xe_register_weight_q4_kn. */
+xe_weight *xe_register_weight_q4(xe_ctx *ctx, int m, int k, const uint8_t *packed,
+                                 const float *scales, const float *bias);
+/* The reference's int4 layout as Lin::load builds it: packed_kn [k, m/2]
+ * (row r = input k, byte c2 = output columns 2*c2 (low) and 2*c2+1 (high)),
+ * scales [m]; repacked along k at registration.  m even. */
+xe_weight *xe_register_weight_q4_kn(xe_ctx *ctx, int m, int k, const uint8_t *packed_kn,
+                                    const float *scales, const float *bias);
 /* Pre-encoded bfp16 weight: mant [m,k] int8, exps [m,k/8] biased (e+127). */
 xe_weight *xe_register_weight_bfp16(xe_ctx *ctx, int m, int k,
                                     const int8_t *mant, const uint8_t *exps,
@@ -175,16 +190,30 @@ int xe_gemv_dev(xe_ctx *ctx, const xe_weight *w, const void *x_dev,
                 int x_dtype, int batch, float *y_dev);
 
 /* int8 activations x int8 weights -> int32 (ctx2.rs:771-830 device part):
- * acc[b,m] = sum_k xq[b,k] * q[m,k], exact.  w must be XE_I8. */
+ * acc[b,m] = sum_k xq[b,k] * q[m,k], exact.  w must be XE_I8; batch 1..512
+ * (<= 8 rows an sdot4 GEMV, more the int8 MFMA GEMM). */
 int xe_gemv_i8act(xe_ctx *ctx, const xe_weight *w, const int8_t *xq,
                   int batch, int32_t *acc);
 int xe_gemv_i8act_dev(xe_ctx *ctx, const xe_weight *w, const int8_t *xq_dev,
                       int batch, int32_t *acc_dev);
 /* W8A8 dynamic linear (ctx2.rs:771-830, 1352-1435): per-tensor activation
- * scale amax/127, int8 x int8 -> i32 on the device, dequant in the order
- * (acc * scale_a) * ws[c] + bias[c].  scale_a_out may be NULL. */
+ * scale amax/127, int8 x int8 -> i32, dequant in the order
+ * (acc * scale_a) * ws[c] (+ bias[c]) -- all on the device; batch 1..512
+ * (<= 8 rows an sdot4 GEMV, more the int8 MFMA GEMM).  Epi::Bias when the
+ * weight has a bias, Epi::None otherwise.  scale_a_out may be NULL. */
 int xe_w8a8_linear(xe_ctx *ctx, const xe_weight *w, const float *x,
                    int batch, float *y, float *scale_a_out);
+/* dequant epilogues of the reference's Epi (ctx2.rs:1386-1435). */
+enum xe_epi {
+  XE_EPI_NONE = 0,      /* (acc * scale_a) * ws[c] */
+  XE_EPI_BIAS = 1,      /* ... + bias[c] */
+  XE_EPI_SILU_BIAS = 2  /* z = ... + bias[c]; z * fast_sigmoid(z) (:1338-1348) */
+};
+/* Device-pointer form (asynchronous on the ctx stream): x_dev fp32
+ * [batch, k], y_dev fp32 [batch, m], scale_a_dev (a device float, may be
+ * NULL) receives scale_a.  epi is enum xe_epi. */
+int xe_w8a8_linear_dev(xe_ctx *ctx, const xe_weight *w, const float *x_dev,
+                       int batch, int epi, float *y_dev, float *scale_a_dev);
 
 /* Single-query attention over a bf16 KV cache (CtxDecode::attn,
  * ctx_decode.rs:468-555; mha_decode.cc:90-175), generalised to GQA,

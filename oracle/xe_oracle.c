@@ -178,6 +178,7 @@ float xo_fast_exp_nonpos(float x) {
  * -0.5 -> -1, 2.5 -> 3), clamp. */
 int8_t xo_quant_i8(float x, float scale) {
   float v = roundf(x / scale);
+  if (v != v) return 0; /* Rust's saturating `as i8` maps NaN to 0 */
   if (v < -127.0f) v = -127.0f;
   if (v > 127.0f) v = 127.0f;
   return (int8_t)v;
@@ -375,6 +376,112 @@ void xo_lin_fwd_i8_kn(const float *x, int b, int k, int n, const int8_t *q_kn,
   }
 }
 
+/* ------------------------------------------------------------------------ */
+/* int4 weights (OPT_INT4, opt125m_decode.rs:63-105)                        */
+/* ------------------------------------------------------------------------ */
+
+/* Nibble sign extension `((v as i32) ^ 0x8) - 0x8` (opt125m_decode.rs:87). */
+static inline int xo_sext4(unsigned v) { return (int)((v & 0xFu) ^ 0x8u) - 0x8; }
+
+/* Lin::load int4 branch (opt125m_decode.rs:63-79) in the reference's own
+ * layout: W [K,N]; s[c] = max_r |W[r,c]| / 7 (1.0 if 0); q = round(W/s)
+ * (half away from zero) clamped to +-7; packed [K, N/2], the even column in
+ * the low nibble, the odd one in the high nibble.  N even. */
+void xo_quant_cols_i4(const float *w_kn, int k, int n, uint8_t *packed_kn, float *s) {
+  for (int c = 0; c < n; c++) {
+    float amax = 0.f;
+    for (int r = 0; r < k; r++) {
+      float v = fabsf(w_kn[(size_t)r * n + c]);
+      amax = v > amax ? v : amax;
+    }
+    s[c] = amax > 0.0f ? amax / 7.0f : 1.0f;
+  }
+  for (int r = 0; r < k; r++)
+    for (int c2 = 0; c2 < n / 2; c2++) {
+      unsigned nib[2];
+      for (int h = 0; h < 2; h++) {
+        int c = 2 * c2 + h;
+        float v = roundf(w_kn[(size_t)r * n + c] / s[c]);
+        if (v != v) v = 0.0f; /* saturating `as i32` maps NaN to 0 */
+        if (v < -7.0f) v = -7.0f;
+        if (v > 7.0f) v = 7.0f;
+        nib[h] = (unsigned)((int)v & 0x0F);
+      }
+      packed_kn[(size_t)r * (n / 2) + c2] = (uint8_t)(nib[0] | (nib[1] << 4));
+    }
+}
+
+/* Lin::fwd int4 branch verbatim loop shape (opt125m_decode.rs:83-105): k
+ * outer, y[2j] += a * sext(lo), y[2j+1] += a * sext(hi) in k order (f32),
+ * then y * s + b. */
+void xo_lin_fwd_i4_kn(const float *x, int b, int k, int n, const uint8_t *packed_kn,
+                      const float *s, const float *bias, float *y) {
+  const int nh = n / 2;
+  for (int mi = 0; mi < b; mi++) {
+    float *yr = y + (size_t)mi * n;
+    for (int ni = 0; ni < n; ni++) yr[ni] = 0.f;
+    for (int ki = 0; ki < k; ki++) {
+      float a = x[(size_t)mi * k + ki];
+      const uint8_t *row = packed_kn + (size_t)ki * nh;
+      for (int nj = 0; nj < nh; nj++) {
+        uint8_t byte = row[nj];
+        yr[2 * nj] += a * (float)xo_sext4(byte & 0x0F);
+        yr[2 * nj + 1] += a * (float)xo_sext4(byte >> 4);
+      }
+    }
+    for (int ni = 0; ni < n; ni++) yr[ni] = yr[ni] * s[ni] + (bias ? bias[ni] : 0.0f);
+  }
+}
+
+/* The same quantisation in the build's [M,K] layout (out-major rows): row r
+ * is output channel r, s[r] = max_k |W[r,k]| / 7, and the row's K values are
+ * packed along K: byte j holds k = 2j (low nibble) and k = 2j+1 (high).  K
+ * even.  Same q and s as xo_quant_cols_i4 on the transpose. */
+void xo_quant_rows_i4(const float *w, int m, int k, uint8_t *packed, float *s) {
+  for (int r = 0; r < m; r++) {
+    const float *row = w + (size_t)r * k;
+    float amax = 0.f;
+    for (int j = 0; j < k; j++) {
+      float v = fabsf(row[j]);
+      amax = v > amax ? v : amax;
+    }
+    float sc = amax > 0.0f ? amax / 7.0f : 1.0f;
+    s[r] = sc;
+    for (int j2 = 0; j2 < k / 2; j2++) {
+      unsigned nib[2];
+      for (int h = 0; h < 2; h++) {
+        float v = roundf(row[2 * j2 + h] / sc);
+        if (v != v) v = 0.0f;
+        if (v < -7.0f) v = -7.0f;
+        if (v > 7.0f) v = 7.0f;
+        nib[h] = (unsigned)((int)v & 0x0F);
+      }
+      packed[(size_t)r * (k / 2) + j2] = (uint8_t)(nib[0] | (nib[1] << 4));
+    }
+  }
+}
+
+/* Lin::fwd int4 in [M,K] layout: y[r] = sum over k in order of
+ * x[k] * sext(q[r,k]), then y * s[r] + b[r] (the per-output sum of
+ * xo_lin_fwd_i4_kn, in the same k order, so the two agree bit for bit). */
+void xo_gemv_i4(const float *x, int b, int k, int m, const uint8_t *packed,
+                const float *s, const float *bias, float *y) {
+  for (int bi = 0; bi < b; bi++) {
+    const float *xb = x + (size_t)bi * k;
+#pragma omp parallel for schedule(static)
+    for (int r = 0; r < m; r++) {
+      const uint8_t *row = packed + (size_t)r * (k / 2);
+      float acc = 0.f;
+      for (int j = 0; j < k; j++) {
+        uint8_t byte = row[j / 2];
+        acc += xb[j] * (float)xo_sext4((j & 1) ? (unsigned)(byte >> 4) : (unsigned)byte);
+      }
+      float v = acc * s[r];
+      y[(size_t)bi * m + r] = bias ? v + bias[r] : v;
+    }
+  }
+}
+
 /* linear_row (whisper_decoder.rs:215-230) semantics with an [M,K] f32
  * weight: bias first, then += x[k] * w in k order. */
 void xo_gemv_f32(const float *x, int b, int k, int m, const float *w,
@@ -493,12 +600,39 @@ void xo_gemm_i8i8_i32(const int8_t *a, int mp, int k, const int8_t *w, int m,
 void xo_w8a8_linear(const float *a, int mp, int k, const int8_t *wq,
                     const float *ws, int m, const float *bias, float *out,
                     float *scale_a_out) {
+  xo_w8a8_linear_epi(a, mp, k, wq, ws, m, bias, bias ? XO_EPI_BIAS : XO_EPI_NONE, out,
+                     scale_a_out);
+}
+
+/* fast_sigmoid (ctx2.rs:1338-1348): stable sigmoid on fast_exp_nonpos. */
+float xo_fast_sigmoid(float x) {
+  if (x >= 0.0f) return 1.0f / (1.0f + xo_fast_exp_nonpos(-x));
+  float e = xo_fast_exp_nonpos(x);
+  return e / (1.0f + e);
+}
+
+/* forward_view_int8 with the op's epilogue (dequant_epi, ctx2.rs:1386-1435):
+ * v = (acc as f32 * scale_a) * ws[c]; Epi::None -> v; Epi::Bias -> v + b[c];
+ * Epi::SiluBias -> z = v + b[c], z * fast_sigmoid(z). */
+void xo_w8a8_linear_epi(const float *a, int mp, int k, const int8_t *wq,
+                        const float *ws, int m, const float *bias, int epi, float *out,
+                        float *scale_a_out) {
   float scale_a = xo_quant_scale(a, (size_t)mp * k);
   int8_t *aq = (int8_t *)malloc((size_t)mp * k);
   int32_t *acc = (int32_t *)malloc((size_t)mp * m * 4);
   for (size_t i = 0; i < (size_t)mp * k; i++) aq[i] = xo_quant_i8(a[i], scale_a);
   xo_gemm_i8i8_i32(aq, mp, k, wq, m, acc);
-  xo_dequant_epi(acc, mp, m, scale_a, ws, bias, out);
+  for (int r = 0; r < mp; r++)
+    for (int c = 0; c < m; c++) {
+      float v = (float)acc[(size_t)r * m + c] * scale_a * ws[c];
+      if (epi == XO_EPI_BIAS) {
+        v = v + bias[c];
+      } else if (epi == XO_EPI_SILU_BIAS) {
+        float z = v + bias[c];
+        v = z * xo_fast_sigmoid(z);
+      }
+      out[(size_t)r * m + c] = v;
+    }
   if (scale_a_out) *scale_a_out = scale_a;
   free(aq);
   free(acc);

@@ -67,6 +67,13 @@ void xo_gemv_i8_rowblocked(const float *x, int b, int k, int m, const int8_t *q,
                            const float *s, const float *bias, float *y);
 void xo_lin_fwd_i8_kn(const float *x, int b, int k, int n, const int8_t *q_kn,
                       const float *s, const float *bias, float *y);
+/* ---- int4 weights (opt125m_decode.rs:63-105) ---- */
+void xo_quant_cols_i4(const float *w_kn, int k, int n, uint8_t *packed_kn, float *s);
+void xo_lin_fwd_i4_kn(const float *x, int b, int k, int n, const uint8_t *packed_kn,
+                      const float *s, const float *bias, float *y);
+void xo_quant_rows_i4(const float *w, int m, int k, uint8_t *packed, float *s);
+void xo_gemv_i4(const float *x, int b, int k, int m, const uint8_t *packed,
+                const float *s, const float *bias, float *y);
 void xo_gemv_f32(const float *x, int b, int k, int m, const float *w,
                  const float *bias, float *y);
 void xo_gemv_bf16w(const float *x, int b, int k, int m, const uint16_t *w,
@@ -86,6 +93,12 @@ void xo_gemm_i8i8_i32(const int8_t *a, int mp, int k, const int8_t *w, int m,
 void xo_w8a8_linear(const float *a, int mp, int k, const int8_t *wq,
                     const float *ws, int m, const float *bias, float *out,
                     float *scale_a_out);
+/* dequant epilogues of ctx2.rs Epi (None / Bias / SiluBias). */
+enum { XO_EPI_NONE = 0, XO_EPI_BIAS = 1, XO_EPI_SILU_BIAS = 2 };
+float xo_fast_sigmoid(float x);
+void xo_w8a8_linear_epi(const float *a, int mp, int k, const int8_t *wq,
+                        const float *ws, int m, const float *bias, int epi, float *out,
+                        float *scale_a_out);
 
 /* ---- fused norm + GEMV (ctx_decode.rs:566-643) ---- */
 enum { XO_NORM_NONE = 0, XO_NORM_LN = 1, XO_NORM_RMS = 2, XO_NORM_RMS1P = 3 };

@@ -62,6 +62,10 @@ def lib():
         "xo_gemv_i8": (None, [f32p, C.c_int, C.c_int, C.c_int, i8p, f32p, C.c_void_p, f32p]),
         "xo_gemv_i8_rowblocked": (None, [f32p, C.c_int, C.c_int, C.c_int, i8p, f32p, C.c_void_p, f32p]),
         "xo_lin_fwd_i8_kn": (None, [f32p, C.c_int, C.c_int, C.c_int, i8p, f32p, C.c_void_p, f32p]),
+        "xo_quant_cols_i4": (None, [f32p, C.c_int, C.c_int, u8p, f32p]),
+        "xo_lin_fwd_i4_kn": (None, [f32p, C.c_int, C.c_int, C.c_int, u8p, f32p, C.c_void_p, f32p]),
+        "xo_quant_rows_i4": (None, [f32p, C.c_int, C.c_int, u8p, f32p]),
+        "xo_gemv_i4": (None, [f32p, C.c_int, C.c_int, C.c_int, u8p, f32p, C.c_void_p, f32p]),
         "xo_gemv_f32": (None, [f32p, C.c_int, C.c_int, C.c_int, f32p, C.c_void_p, f32p]),
         "xo_gemv_bf16w": (None, [f32p, C.c_int, C.c_int, C.c_int, u16p, C.c_void_p, f32p]),
         "xo_bfp16_encode": (None, [f32p, C.c_int, C.c_int, i8p, u8p]),
@@ -70,6 +74,9 @@ def lib():
         "xo_gemm_i8i8_i32": (None, [i8p, C.c_int, C.c_int, i8p, C.c_int, i32p]),
         "xo_w8a8_linear": (None, [f32p, C.c_int, C.c_int, i8p, f32p, C.c_int, C.c_void_p, f32p,
                                   C.POINTER(C.c_float)]),
+        "xo_fast_sigmoid": (C.c_float, [C.c_float]),
+        "xo_w8a8_linear_epi": (None, [f32p, C.c_int, C.c_int, i8p, f32p, C.c_int, C.c_void_p, C.c_int,
+                                      f32p, C.POINTER(C.c_float)]),
         "xo_norm_row": (None, [f32p, C.c_int, C.c_int, C.c_void_p, C.c_void_p, C.c_float, f32p]),
         "xo_fold_weight": (None, [f32p, C.c_int, C.c_int, f32p, C.c_void_p, C.c_void_p, f32p, f32p]),
         "xo_attend_one": (None, [f32p, f32p, f32p, C.c_int, C.c_int, C.c_int, f32p]),
@@ -144,6 +151,79 @@ def gemv_i8(x, q, s, bias=None):
     lib().xo_gemv_i8(x, b, k, m, np.ascontiguousarray(q), np.ascontiguousarray(s, np.float32),
                      ptr(None if bias is None else np.ascontiguousarray(bias, np.float32)), y)
     return y
+
+
+EPI_NONE, EPI_BIAS, EPI_SILU_BIAS = 0, 1, 2
+
+
+def w8a8_linear(a, wq, ws, bias=None, epi=None):
+    """forward_view_int8 + dequant_epi (ctx2.rs:771-830, 1386-1435); returns
+    (out, scale_a)."""
+    a = np.ascontiguousarray(a, np.float32)
+    mp, k = a.shape
+    m = wq.shape[0]
+    if epi is None:
+        epi = EPI_BIAS if bias is not None else EPI_NONE
+    out = np.empty((mp, m), np.float32)
+    sa = C.c_float()
+    bb = None if bias is None else np.ascontiguousarray(bias, np.float32)
+    lib().xo_w8a8_linear_epi(a, mp, k, np.ascontiguousarray(wq, np.int8),
+                             np.ascontiguousarray(ws, np.float32), m, ptr(bb), epi, out, C.byref(sa))
+    return out, sa.value
+
+
+def quant_rows_i4(w):
+    """Lin::load int4 (opt125m_decode.rs:63-79) on an [M, K] matrix: packed
+    uint8 [M, K/2] (k = 2j low nibble, 2j+1 high) and scales [M]."""
+    w = np.ascontiguousarray(w, np.float32)
+    m, k = w.shape
+    q = np.empty((m, k // 2), np.uint8)
+    s = np.empty(m, np.float32)
+    lib().xo_quant_rows_i4(w, m, k, q, s)
+    return q, s
+
+
+def quant_cols_i4(w_kn):
+    """Lin::load int4 in the reference's [K, N] layout: packed [K, N/2]."""
+    w_kn = np.ascontiguousarray(w_kn, np.float32)
+    k, n = w_kn.shape
+    q = np.empty((k, n // 2), np.uint8)
+    s = np.empty(n, np.float32)
+    lib().xo_quant_cols_i4(w_kn, k, n, q, s)
+    return q, s
+
+
+def gemv_i4(x, packed, s, bias=None):
+    x = np.ascontiguousarray(x, np.float32)
+    b = x.shape[0]
+    m, k2 = packed.shape
+    y = np.empty((b, m), np.float32)
+    bb = None if bias is None else np.ascontiguousarray(bias, np.float32)
+    lib().xo_gemv_i4(x, b, 2 * k2, m, np.ascontiguousarray(packed), np.ascontiguousarray(s, np.float32),
+                     ptr(bb), y)
+    return y
+
+
+def lin_fwd_i4_kn(x, packed_kn, s, bias=None):
+    x = np.ascontiguousarray(x, np.float32)
+    b, k = x.shape
+    n = 2 * packed_kn.shape[1]
+    y = np.empty((b, n), np.float32)
+    bb = None if bias is None else np.ascontiguousarray(bias, np.float32)
+    lib().xo_lin_fwd_i4_kn(x, b, k, n, np.ascontiguousarray(packed_kn),
+                           np.ascontiguousarray(s, np.float32), ptr(bb), y)
+    return y
+
+
+def unpack_i4(packed):
+    """Sign-extended nibbles of a packed [R, C/2] array as int8 [R, C]."""
+    p = np.asarray(packed, np.uint8)
+    lo = (p & 0x0F).astype(np.int8)
+    hi = (p >> 4).astype(np.int8)
+    out = np.empty((p.shape[0], 2 * p.shape[1]), np.int8)
+    out[:, 0::2] = np.where(lo >= 8, lo - 16, lo)
+    out[:, 1::2] = np.where(hi >= 8, hi - 16, hi)
+    return out
 
 
 def gemv_bf16w(x, wbits, bias=None):

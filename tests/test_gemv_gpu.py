@@ -206,11 +206,14 @@ def test_constant_input_layernorm(gpu, xe):
     close(got, O.gemv_i8(beta[None], q, s))
 
 
-@pytest.mark.parametrize("b", [1, 3, 8])
+@pytest.mark.parametrize("b", [1, 3, 8, 9, 16, 40, 64, 200, 512])
 def test_i8act_bit_exact(gpu, xe, b):
+    """int8 x int8 -> i32, exact: the sdot4 GEMV up to 8 rows, the int8 MFMA
+    GEMM beyond (ragged row and batch counts, K not a multiple of 64)."""
     dev, ctx = gpu
     rng = np.random.default_rng(b)
-    for m, k in [(3072, 768), (768, 3072), (1000, 1152)]:
+    for m, k in [(3072, 768), (768, 3072), (1000, 1152), (130, 1040)]:
+        print("[case] i8act m=%d k=%d b=%d" % (m, k, b), flush=True)
         q = rng.integers(-127, 128, (m, k)).astype(np.int8)
         xq = rng.integers(-127, 128, (b, k)).astype(np.int8)
         w = ctx.register_weight_q8(q, np.ones(m, np.float32))
@@ -242,6 +245,55 @@ def test_w8a8_linear_bit_exact(gpu, xe):
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
+@pytest.mark.parametrize("b", [1, 8, 64, 512])
+@pytest.mark.parametrize("epi", ["none", "bias", "silu_bias"])
+def test_w8a8_device_epilogues_bit_exact(gpu, xe, b, epi):
+    """xe_w8a8_linear_dev: amax, quant, product and the dequant epilogue
+    (Epi::None / Bias / SiluBias, ctx2.rs:1386-1435) all on the device, equal
+    to the oracle bit for bit (scale_a included), at the reference's
+    Whisper-encoder shapes (K = 768, N in {768, 1536, 3072}, Mp <= 512)."""
+    dev, ctx = gpu
+    rng = np.random.default_rng(100 + b)
+    m, k = {1: 3072, 8: 1536, 64: 768, 512: 1536}[b], 768
+    print("[case] w8a8 dev m=%d k=%d b=%d epi=%s" % (m, k, b, epi), flush=True)
+    wf = (rng.standard_normal((m, k)) * 0.02).astype(np.float32)
+    bias = rng.standard_normal(m).astype(np.float32)
+    x = (rng.standard_normal((b, k)) * 3.0).astype(np.float32)
+    x[0, 5] = 0.0
+    code = {"none": xe.XE_EPI_NONE, "bias": xe.XE_EPI_BIAS, "silu_bias": xe.XE_EPI_SILU_BIAS}[epi]
+    w = ctx.register_weight(wf, xe.XE_I8, bias=bias)
+    xb = xe.Buf.from_array(dev, x)
+    yb = xe.Buf(dev, b * m * 4)
+    sab = xe.Buf(dev, 4)
+    ctx.w8a8_linear_dev(w, xb, b, code, yb, sab)
+    ctx.synchronize()
+    got = yb.read(np.float32, b * m).reshape(b, m)
+    sa = sab.read(np.float32, 1)[0]
+    for bb in (xb, yb, sab):
+        bb.free()
+    w.free()
+    q, s = O.quant_rows_i8(wf)
+    want, osa = O.w8a8_linear(x, q, s, bias, {"none": O.EPI_NONE, "bias": O.EPI_BIAS,
+                                               "silu_bias": O.EPI_SILU_BIAS}[epi])
+    assert sa == np.float32(osa)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_w8a8_all_zero_activations(gpu, xe):
+    """quant_scale's guard: an all-zero tensor gives scale_a = 1.0 and the
+    bias alone (ctx2.rs:1376)."""
+    dev, ctx = gpu
+    m, k, b = 256, 768, 16
+    rng = np.random.default_rng(5)
+    wf = (rng.standard_normal((m, k)) * 0.02).astype(np.float32)
+    bias = rng.standard_normal(m).astype(np.float32)
+    w = ctx.register_weight(wf, xe.XE_I8, bias=bias)
+    got, sa = ctx.w8a8_linear(w, np.zeros((b, k), np.float32))
+    w.free()
+    assert sa == 1.0
+    assert np.array_equal(got, np.broadcast_to(bias, (b, m)))
+
+
 def test_registration_rejects_bad_k(gpu, xe):
     dev, ctx = gpu
     with pytest.raises(xe.XdnaError, match="multiple of 16"):
@@ -266,4 +318,45 @@ def test_norm_gemm_int8_batched(gpu, xe, m, k, b):
     err = np.linalg.norm(got - want) / np.linalg.norm(want)
     print("[gemm] m=%d k=%d b=%d rel-L2 %.3g max abs %.3g" % (m, k, b, err,
                                                             np.max(np.abs(got - want))), flush=True)
+    close(got, want)
+
+
+# ---- int4 weights (Lin int4 branch, opt125m_decode.rs:63-105) ----
+
+@pytest.mark.parametrize("m,k", [(768, 768), (3072, 768), (768, 3072), (6912, 1152)])
+@pytest.mark.parametrize("b", [1, 4, 8, 16])
+def test_gemv_int4_against_reference_loop(gpu, xe, m, k, b):
+    """OPT's int4 linear: weights quantised by the reference's Lin::load int4
+    rule in its own [K, N/2] packing, registered as is, and the output
+    compared with the reference's k-outer Lin::fwd int4 loop (bias added);
+    b = 16 runs the MFMA GEMM path."""
+    dev, ctx = gpu
+    print("[case] int4 GEMV m=%d k=%d b=%d" % (m, k, b), flush=True)
+    rng = np.random.default_rng(m + 3 * k + b)
+    w_kn = (rng.standard_normal((k, m)) * 0.02).astype(np.float32)
+    bias = rng.normal(0.0, 0.1, m).astype(np.float32)
+    x = rng.standard_normal((b, k)).astype(np.float32)
+    qk, s = O.quant_cols_i4(w_kn)
+    w = ctx.register_weight_q4_kn(qk, s, bias)
+    got = ctx.gemv(w, x)
+    w.free()
+    want = O.lin_fwd_i4_kn(x, qk, s, bias)
+    close(got, want)
+
+
+def test_gemv_int4_fp32_registration_and_fused_ln(gpu, xe):
+    """xe_register_fused with XE_I4 quantises on the host like Lin::load int4
+    (codes equal the oracle's [M, K] packing) and applies the LN prologue."""
+    dev, ctx = gpu
+    m, k, b = 1152, 1152, 2
+    rng = np.random.default_rng(77)
+    wf = (rng.standard_normal((m, k)) * 0.02).astype(np.float32)
+    gamma = rng.normal(1.0, 0.1, k).astype(np.float32)
+    beta = rng.normal(0.0, 0.1, k).astype(np.float32)
+    x = rng.standard_normal((b, k)).astype(np.float32)
+    w = ctx.register_fused(wf, xe.Norm.Ln(gamma, beta, 1e-5), xe.XE_I4)
+    got = ctx.fused_norm_gemv(w, x)
+    w.free()
+    q, s = O.quant_rows_i4(wf)
+    want = O.gemv_i4(O.norm_rows(x, 1, gamma, beta, 1e-5), q, s)
     close(got, want)

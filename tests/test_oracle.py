@@ -242,6 +242,105 @@ def test_w8a8_int32_bruteforce_and_dequant_order():
     assert not np.array_equal(want.astype(np.float32), other.astype(np.float32))
 
 
+# -------------------------------------------------------------- int4 ----
+
+def test_i4_quant_nibbles_and_scales_closed_form():
+    """Lin::load int4 (opt125m_decode.rs:63-79): scale amax/7 (1.0 for an
+    all-zero column), round half away from zero, clamp +-7, two's-complement
+    nibbles with the even column low.  Checked against hand-computed codes."""
+    # column 0: amax 7 -> scale 1: values land on their own integers (and ties)
+    # column 1: all zero -> scale 1.0, code 0
+    # column 2: amax 14 -> scale 2: 3 -> 1.5 -> 2 (half away), -3 -> -2
+    # column 3: amax 0.7 -> scale 0.1
+    w_kn = np.array([[7.0, 0.0, 14.0, 0.7],
+                     [-0.5, 0.0, 3.0, -0.7],
+                     [2.5, 0.0, -3.0, 0.04],
+                     [-7.0, 0.0, -14.0, -0.049]], np.float32)
+    q, s = O.quant_cols_i4(w_kn)
+    assert s.tolist() == [1.0, 1.0, 2.0, np.float32(0.7) / np.float32(7.0)]
+    codes = O.unpack_i4(q)
+    assert codes.tolist() == [[7, 0, 7, 7], [-1, 0, 2, -7], [3, 0, -2, 0], [-7, 0, -7, 0]]
+    # raw nibbles: -1 -> 0xF, -7 -> 0x9, 7 -> 0x7 (even column in the low nibble)
+    assert int(q[1, 0]) == (0x0 << 4) | 0xF and int(q[3, 0]) == (0x0 << 4) | 0x9
+    assert int(q[0, 1]) == (0x7 << 4) | 0x7
+
+
+def test_i4_sign_extension_all_nibbles():
+    # ((v ^ 8) - 8) of every nibble, through the GEMV with one-hot x
+    packed = np.array([[(v << 4) | v for v in range(16)]], np.uint8).reshape(1, 16)
+    want = [0, 1, 2, 3, 4, 5, 6, 7, -8, -7, -6, -5, -4, -3, -2, -1]
+    assert O.unpack_i4(packed)[0, 0::2].tolist() == want
+    eye = np.eye(32, dtype=np.float32)
+    y = O.gemv_i4(eye, packed, np.ones(1, np.float32))[:, 0]
+    assert y[0::2].tolist() == want and y[1::2].tolist() == want
+
+
+def test_i4_rows_equal_reference_column_layout_and_loop_bitwise():
+    """[M, K] packing along K is the reference's [K, N/2] packing transposed:
+    same codes and scales; the [M, K] GEMV equals the reference's k-outer
+    [K, N] loop (opt125m_decode.rs:83-105) bit for bit."""
+    rng = np.random.default_rng(11)
+    k, n, b = 96, 80, 3
+    w_kn = (rng.standard_normal((k, n)) * 0.02).astype(np.float32)
+    w_kn[:, 5] = 0.0
+    qk, sk = O.quant_cols_i4(w_kn)
+    qr, sr = O.quant_rows_i4(w_kn.T.copy())
+    assert np.array_equal(sr, sk) and sk[5] == 1.0
+    assert np.array_equal(O.unpack_i4(qr), O.unpack_i4(qk).T)
+    x = rng.standard_normal((b, k)).astype(np.float32)
+    bias = rng.standard_normal(n).astype(np.float32)
+    y_kn = O.lin_fwd_i4_kn(x, qk, sk, bias)
+    y_mk = O.gemv_i4(x, qr, sr, bias)
+    assert np.array_equal(y_kn.view(np.uint32), y_mk.view(np.uint32))
+
+
+def test_i4_gemv_integer_inputs_exact():
+    rng = np.random.default_rng(12)
+    codes = rng.integers(-7, 8, (33, 64)).astype(np.int64)
+    nib = (codes & 0xF).astype(np.uint8)
+    packed = (nib[:, 0::2] | (nib[:, 1::2] << 4)).astype(np.uint8)
+    x = rng.integers(-8, 9, (2, 64)).astype(np.float32)
+    want = x.astype(np.int64) @ codes.T
+    assert np.array_equal(O.gemv_i4(x, packed, np.ones(33, np.float32)), want.astype(np.float32))
+    # the scale multiplies after the sum
+    s = rng.uniform(0.001, 0.02, 33).astype(np.float32)
+    got = O.gemv_i4(x, packed, s)
+    assert np.array_equal(got, (want.astype(np.float32) * s[None, :]).astype(np.float32))
+
+
+def test_fast_sigmoid_accuracy_and_symmetry():
+    """fast_sigmoid (ctx2.rs:1338-1348) on fast_exp_nonpos: within the
+    reference's own fast_exp bound (5e-4 relative, npu-asr-host/src/lib.rs:
+    847-859) of the exact logistic, and s(x) + s(-x) = 1."""
+    for v in np.linspace(-30, 30, 601):
+        v = float(np.float32(v))
+        got = O.lib().xo_fast_sigmoid(v)
+        exact = 1.0 / (1.0 + math.exp(-v))
+        assert abs(got - exact) <= 5e-4 * exact
+        assert abs(got + O.lib().xo_fast_sigmoid(-v) - 1.0) < 1e-6
+
+
+def test_w8a8_epilogues_none_bias_silu():
+    """dequant_epi's three epilogues over one product: Bias = None + bias
+    exactly (one fp32 add), SiluBias = z * sigmoid(z) of the Bias output."""
+    rng = np.random.default_rng(9)
+    a = rng.standard_normal((6, 64)).astype(np.float32)
+    wf = (rng.standard_normal((40, 64)) * 0.02).astype(np.float32)
+    q, s = O.quant_rows_i8(wf)
+    bias = rng.standard_normal(40).astype(np.float32)
+    y0, sa0 = O.w8a8_linear(a, q, s, bias, O.EPI_NONE)
+    y1, sa1 = O.w8a8_linear(a, q, s, bias, O.EPI_BIAS)
+    y2, _ = O.w8a8_linear(a, q, s, bias, O.EPI_SILU_BIAS)
+    assert sa0 == sa1 == np.float32(np.max(np.abs(a))) / np.float32(127.0)
+    assert np.array_equal(y1, (y0 + bias[None, :]).astype(np.float32))
+    z = y1.astype(np.float64)
+    assert np.allclose(y2, z / (1.0 + np.exp(-z)), rtol=5e-4, atol=1e-7)
+    # the product itself is the brute-force integer one
+    aq = O.round_half_away_i8(a / np.float32(sa0))
+    acc = aq.astype(np.int64) @ q.astype(np.int64).T
+    assert np.array_equal(y0, ((acc.astype(np.float32) * np.float32(sa0)) * s[None, :]).astype(np.float32))
+
+
 def test_quant_scale_zero_guard():
     assert L().xo_quant_scale(np.zeros(16, np.float32), 16) == 1.0
     assert L().xo_quant_scale(np.array([0.0, -2.54, 1.0], np.float32), 3) == np.float32(2.54) / np.float32(127.0)

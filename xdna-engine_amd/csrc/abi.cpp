@@ -90,6 +90,20 @@ void xe_ctx::ensure_attn(size_t work_floats) {
   }
 }
 
+// Layout: [0, 256) partial maxima (w8a8_partial_floats() <= 64 floats),
+// [256, 512) scale_a, then the int8 activations.
+char *xe_ctx::ensure_w8a8(size_t aq_bytes) {
+  const size_t n = 512 + aq_bytes;
+  if (n > w8a8_ws_size) {
+    if (w8a8_ws) XE_HIP(hipFree(w8a8_ws));
+    w8a8_ws = nullptr;
+    w8a8_ws_size = 0;
+    XE_HIP(hipMalloc(&w8a8_ws, n));
+    w8a8_ws_size = n;
+  }
+  return w8a8_ws;
+}
+
 void xe_ctx::ensure_gemm(size_t xn_floats) {
   if (!gemm_ws) {
     XE_HIP(hipMalloc(&gemm_ws, gemm_op_ws_floats() * sizeof(float)));
@@ -137,7 +151,8 @@ xe_weight *new_weight(xe_ctx *ctx, int wdtype, int m, int k) {
   XE_REQUIRE(ctx && ctx->dev, "null ctx");
   XE_REQUIRE(m > 0 && k > 0, "weight shape must be positive");
   XE_REQUIRE(k % 16 == 0, "weight K must be a multiple of 16");
-  XE_REQUIRE(wdtype == XE_I8 || wdtype == XE_BF16 || wdtype == XE_BFP16, "unknown weight dtype");
+  XE_REQUIRE(wdtype == XE_I8 || wdtype == XE_BF16 || wdtype == XE_BFP16 || wdtype == XE_I4,
+             "unknown weight dtype");
   auto *w = new xe_weight;
   w->ctx = ctx;
   w->wdtype = wdtype;
@@ -168,6 +183,12 @@ void fill_weight_from_f32(xe_weight *wt, const float *w_mk, const float *bias) {
     std::vector<float> sc(m);
     quant_rows_i8(w_mk, m, k, q.data(), sc.data());
     wt->w = dev_upload(q.data(), n, s);
+    wt->scale = dev_upload(sc.data(), m, s);
+  } else if (wt->wdtype == XE_I4) {
+    std::vector<uint8_t> q(n / 2);
+    std::vector<float> sc(m);
+    quant_rows_i4(w_mk, m, k, q.data(), sc.data());
+    wt->w = dev_upload(q.data(), n / 2, s);
     wt->scale = dev_upload(sc.data(), m, s);
   } else if (wt->wdtype == XE_BF16) {
     std::vector<uint16_t> b(n);
@@ -235,6 +256,40 @@ void launch_linear(xe_ctx *ctx, const xe_weight *w, const void *x, int x_dtype, 
     launch_gemm_op(gemv_args(w, x, x_dtype, batch, y), ctx->gemm_xn, ctx->gemm_ws, ctx->gemm_cnt, s);
   }
   ctx->dispatches++;
+}
+
+// int8 x int8 -> i32 with an output stage: the sdot4 GEMV up to 8 rows, the
+// int8 MFMA GEMM beyond.
+void launch_i8act(xe_ctx *ctx, const xe_weight *w, const int8_t *xq_dev, int batch, const W8a8Epi &e,
+                  hipStream_t s) {
+  if (batch <= 8)
+    launch_gemv_i8act(static_cast<const int8_t *>(w->w), xq_dev, w->m, w->k, batch, e, s);
+  else
+    launch_w8a8_mfma(static_cast<const int8_t *>(w->w), xq_dev, w->m, w->k, batch, e, s);
+  ctx->dispatches++;
+}
+
+// forward_view_int8 on the device: quant (two kernels), product + dequant.
+void run_w8a8(xe_ctx *ctx, const xe_weight *w, const float *x_dev, int batch, int epi, float *y_dev,
+              float *scale_a_dev, hipStream_t s) {
+  XE_REQUIRE(w->wdtype == XE_I8, "xe_w8a8_linear needs an XE_I8 weight");
+  XE_REQUIRE(batch >= 1 && batch <= kMaxOpBatch, "batch must be 1..512");
+  XE_REQUIRE(epi == XE_EPI_NONE || epi == XE_EPI_BIAS || epi == XE_EPI_SILU_BIAS, "unknown epilogue");
+  XE_REQUIRE(epi == XE_EPI_NONE || w->bias, "a bias epilogue needs a weight with a bias");
+  const size_t n = static_cast<size_t>(batch) * w->k;
+  char *ws = ctx->ensure_w8a8(n);
+  float *partial = reinterpret_cast<float *>(ws);
+  float *sa = scale_a_dev ? scale_a_dev : reinterpret_cast<float *>(ws + 256);
+  int8_t *aq = reinterpret_cast<int8_t *>(ws + 512);
+  launch_w8a8_quant(x_dev, n, partial, aq, sa, s);
+  ctx->dispatches += 2;
+  W8a8Epi e;
+  e.y = y_dev;
+  e.scale_a = sa;
+  e.ws = w->scale;
+  e.bias = w->bias;
+  e.epi = epi;
+  launch_i8act(ctx, w, aq, batch, e, s);
 }
 
 int run_gemv_host(xe_ctx *ctx, const xe_weight *w, const void *x, int x_dtype, int batch,
@@ -411,6 +466,7 @@ void xe_ctx_destroy(xe_ctx *ctx) {
     if (ctx->gemm_ws) (void)hipFree(ctx->gemm_ws);
     if (ctx->gemm_cnt) (void)hipFree(ctx->gemm_cnt);
     if (ctx->gemm_xn) (void)hipFree(ctx->gemm_xn);
+    if (ctx->w8a8_ws) (void)hipFree(ctx->w8a8_ws);
     delete ctx;
     return 0;
   }, -1);
@@ -461,6 +517,43 @@ xe_weight *xe_register_weight_q8(xe_ctx *ctx, int m, int k, const int8_t *q, con
   }, nullptr);
 }
 
+xe_weight *xe_register_weight_q4(xe_ctx *ctx, int m, int k, const uint8_t *packed, const float *scales,
+                                 const float *bias) {
+  return guard([&]() -> xe_weight * {
+    XE_REQUIRE(packed && scales, "null weight or scales");
+    DeviceGuard dg(ctx ? ctx->dev->ordinal : 0);
+    xe_weight *wt = new_weight(ctx, XE_I4, m, k);
+    hipStream_t s = ctx->dev->stream;
+    wt->w = dev_upload(packed, static_cast<size_t>(m) * k / 2, s);
+    wt->scale = dev_upload(scales, m, s);
+    if (bias) wt->bias = dev_upload(bias, m, s);
+    return wt;
+  }, nullptr);
+}
+
+xe_weight *xe_register_weight_q4_kn(xe_ctx *ctx, int m, int k, const uint8_t *packed_kn,
+                                    const float *scales, const float *bias) {
+  return guard([&]() -> xe_weight * {
+    XE_REQUIRE(packed_kn && scales, "null weight or scales");
+    XE_REQUIRE(m % 2 == 0, "int4 [K, N/2] layout needs an even N");
+    DeviceGuard dg(ctx ? ctx->dev->ordinal : 0);
+    xe_weight *wt = new_weight(ctx, XE_I4, m, k);
+    // [k][m/2] (two output columns a byte) -> [m][k/2] (two k a byte)
+    std::vector<uint8_t> mk(static_cast<size_t>(m) * k / 2, 0);
+    for (int r = 0; r < k; r++)
+      for (int c = 0; c < m; c++) {
+        const uint8_t byte = packed_kn[static_cast<size_t>(r) * (m / 2) + c / 2];
+        const uint8_t nib = (c & 1) ? static_cast<uint8_t>(byte >> 4) : static_cast<uint8_t>(byte & 0x0F);
+        mk[static_cast<size_t>(c) * (k / 2) + r / 2] |= static_cast<uint8_t>((r & 1) ? nib << 4 : nib);
+      }
+    hipStream_t s = ctx->dev->stream;
+    wt->w = dev_upload(mk.data(), mk.size(), s);
+    wt->scale = dev_upload(scales, m, s);
+    if (bias) wt->bias = dev_upload(bias, m, s);
+    return wt;
+  }, nullptr);
+}
+
 xe_weight *xe_register_weight_bfp16(xe_ctx *ctx, int m, int k, const int8_t *mant,
                                     const uint8_t *exps, const float *bias) {
   return guard([&]() -> xe_weight * {
@@ -493,8 +586,9 @@ xe_weight *xe_register_weight_view(xe_ctx *ctx, int wdtype, int m, int k, const 
                                    const float *bias_dev) {
   return guard([&]() -> xe_weight * {
     XE_REQUIRE(w_dev, "null weight pointer");
-    XE_REQUIRE(wdtype == XE_I8 || wdtype == XE_BF16 || wdtype == XE_BFP16, "unknown weight dtype");
-    XE_REQUIRE(wdtype != XE_I8 || scale_dev, "int8 weight view needs scales");
+    XE_REQUIRE(wdtype == XE_I8 || wdtype == XE_BF16 || wdtype == XE_BFP16 || wdtype == XE_I4,
+               "unknown weight dtype");
+    XE_REQUIRE((wdtype != XE_I8 && wdtype != XE_I4) || scale_dev, "int8/int4 weight view needs scales");
     XE_REQUIRE(wdtype != XE_BFP16 || exps_dev, "bfp16 weight view needs exponents");
     DeviceGuard dg(ctx ? ctx->dev->ordinal : 0);
     xe_weight *wt = new_weight(ctx, wdtype, m, k);
@@ -586,10 +680,11 @@ int xe_gemv_i8act_dev(xe_ctx *ctx, const xe_weight *w, const int8_t *xq_dev, int
   return guard([&]() -> int {
     XE_REQUIRE(ctx && w && xq_dev && acc_dev, "null argument");
     XE_REQUIRE(w->wdtype == XE_I8, "xe_gemv_i8act needs an XE_I8 weight");
+    XE_REQUIRE(batch >= 1 && batch <= kMaxOpBatch, "batch must be 1..512");
     DeviceGuard dg(ctx->dev->ordinal);
-    launch_gemv_i8act(static_cast<const int8_t *>(w->w), xq_dev, w->m, w->k, batch, acc_dev,
-                      ctx->dev->stream);
-    ctx->dispatches++;
+    W8a8Epi e;
+    e.acc = acc_dev;
+    launch_i8act(ctx, w, xq_dev, batch, e, ctx->dev->stream);
     return 0;
   }, -1);
 }
@@ -598,7 +693,7 @@ int xe_gemv_i8act(xe_ctx *ctx, const xe_weight *w, const int8_t *xq, int batch, 
   return guard([&]() -> int {
     XE_REQUIRE(ctx && w && xq && acc, "null argument");
     XE_REQUIRE(w->wdtype == XE_I8, "xe_gemv_i8act needs an XE_I8 weight");
-    XE_REQUIRE(batch >= 1 && batch <= 8, "batch must be 1..8");
+    XE_REQUIRE(batch >= 1 && batch <= kMaxOpBatch, "batch must be 1..512");
     DeviceGuard dg(ctx->dev->ordinal);
     hipStream_t s = ctx->dev->stream;
     const size_t xb = static_cast<size_t>(batch) * w->k;
@@ -606,11 +701,21 @@ int xe_gemv_i8act(xe_ctx *ctx, const xe_weight *w, const int8_t *xq, int batch, 
     char *d = static_cast<char *>(ctx->ensure_scratch(xb + ab + 256));
     int32_t *da = reinterpret_cast<int32_t *>(d + ((xb + 255) / 256) * 256);
     XE_HIP(hipMemcpyAsync(d, xq, xb, hipMemcpyHostToDevice, s));
-    launch_gemv_i8act(static_cast<const int8_t *>(w->w), reinterpret_cast<int8_t *>(d), w->m,
-                      w->k, batch, da, s);
-    ctx->dispatches++;
+    W8a8Epi e;
+    e.acc = da;
+    launch_i8act(ctx, w, reinterpret_cast<int8_t *>(d), batch, e, s);
     XE_HIP(hipMemcpyAsync(acc, da, ab, hipMemcpyDeviceToHost, s));
     XE_HIP(hipStreamSynchronize(s));
+    return 0;
+  }, -1);
+}
+
+int xe_w8a8_linear_dev(xe_ctx *ctx, const xe_weight *w, const float *x_dev, int batch, int epi,
+                       float *y_dev, float *scale_a_dev) {
+  return guard([&]() -> int {
+    XE_REQUIRE(ctx && w && x_dev && y_dev, "null argument");
+    DeviceGuard dg(ctx->dev->ordinal);
+    run_w8a8(ctx, w, x_dev, batch, epi, y_dev, scale_a_dev, ctx->dev->stream);
     return 0;
   }, -1);
 }
@@ -619,25 +724,25 @@ int xe_w8a8_linear(xe_ctx *ctx, const xe_weight *w, const float *x, int batch, f
                    float *scale_a_out) {
   return guard([&]() -> int {
     XE_REQUIRE(ctx && w && x && y, "null argument");
-    XE_REQUIRE(w->wdtype == XE_I8, "xe_w8a8_linear needs an XE_I8 weight");
-    XE_REQUIRE(batch >= 1 && batch <= 8, "batch must be 1..8");
-    // forward_view_int8 (ctx2.rs:771-830): host activation quant, device
-    // int8 x int8 -> i32, host dequant in the exact order of dequant_epi.
-    const size_t n = static_cast<size_t>(batch) * w->k;
-    const float scale_a = quant_scale(x, n);
-    std::vector<int8_t> xq(n);
-    for (size_t i = 0; i < n; i++) xq[i] = quant_i8(x[i], scale_a);
-    std::vector<int32_t> acc(static_cast<size_t>(batch) * w->m);
-    XE_REQUIRE(xe_gemv_i8act(ctx, w, xq.data(), batch, acc.data()) == 0, g_err);
-    std::vector<float> ws(w->m), bias;
+    XE_REQUIRE(batch >= 1 && batch <= kMaxOpBatch, "batch must be 1..512");
     DeviceGuard dg(ctx->dev->ordinal);
-    XE_HIP(hipMemcpy(ws.data(), w->scale, w->m * 4, hipMemcpyDeviceToHost));
-    if (w->bias) {
-      bias.resize(w->m);
-      XE_HIP(hipMemcpy(bias.data(), w->bias, w->m * 4, hipMemcpyDeviceToHost));
-    }
-    dequant_epi(acc.data(), batch, w->m, scale_a, ws.data(), w->bias ? bias.data() : nullptr, y);
-    if (scale_a_out) *scale_a_out = scale_a;
+    hipStream_t s = ctx->dev->stream;
+    // forward_view_int8 (ctx2.rs:771-830) with Epi::Bias when the op has a
+    // bias, Epi::None otherwise; x in and y (and scale_a) out are the only
+    // host transfers
+    const size_t xb = static_cast<size_t>(batch) * w->k * 4;
+    const size_t yb = static_cast<size_t>(batch) * w->m * 4;
+    char *d = static_cast<char *>(ctx->ensure_scratch(xb + yb + 512));
+    float *dx = reinterpret_cast<float *>(d);
+    float *dy = reinterpret_cast<float *>(d + ((xb + 255) / 256) * 256);
+    float *dsa = reinterpret_cast<float *>(d + ((xb + 255) / 256) * 256 + ((yb + 255) / 256) * 256);
+    XE_HIP(hipMemcpyAsync(dx, x, xb, hipMemcpyHostToDevice, s));
+    run_w8a8(ctx, w, dx, batch, w->bias ? XE_EPI_BIAS : XE_EPI_NONE, dy, dsa, s);
+    XE_HIP(hipMemcpyAsync(y, dy, yb, hipMemcpyDeviceToHost, s));
+    float sa = 0.f;
+    XE_HIP(hipMemcpyAsync(&sa, dsa, 4, hipMemcpyDeviceToHost, s));
+    XE_HIP(hipStreamSynchronize(s));
+    if (scale_a_out) *scale_a_out = sa;
     return 0;
   }, -1);
 }

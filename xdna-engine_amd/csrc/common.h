@@ -94,6 +94,10 @@ struct xe_ctx {
   unsigned *gemm_cnt = nullptr;
   float *gemm_xn = nullptr;
   size_t gemm_xn_floats = 0;
+  // W8A8: partial maxima, the device scale_a and the int8 activations
+  char *w8a8_ws = nullptr;
+  size_t w8a8_ws_size = 0;
+  char *ensure_w8a8(size_t aq_bytes);
   void *ensure_scratch(size_t n);
   void ensure_gemm(size_t xn_floats);
   void *ensure_pinned(size_t n);
@@ -145,9 +149,70 @@ void launch_gemv(const GemvLaunch &p, hipStream_t s);
 void launch_gemm_op(const GemvLaunch &L, float *xn, float *ws, unsigned *cnt, hipStream_t s);
 size_t gemm_op_ws_floats();
 size_t gemm_op_cnt_words();
-// int8 activations x int8 weights -> int32 (exact).
+// Output of an int8 x int8 -> i32 product: the raw accumulator (acc set), or
+// the W8A8 dequant of dequant_epi (rust/npu-asr/src/ctx2.rs:1386-1435):
+// v = (acc * scale_a) * ws[c]; EPI_BIAS adds bias[c]; EPI_SILU_BIAS gives
+// z * fast_sigmoid(z) of z = v + bias[c] (ctx2.rs:1338-1348).
+enum Epi { EPI_NONE = 0, EPI_BIAS = 1, EPI_SILU_BIAS = 2 };
+struct W8a8Epi {
+  int32_t *acc = nullptr;          // [batch, m] raw, or null
+  float *y = nullptr;              // [batch, m] dequantised
+  const float *scale_a = nullptr;  // device scalar
+  const float *ws = nullptr;       // [m] weight scales
+  const float *bias = nullptr;     // [m]
+  int epi = EPI_NONE;
+};
+
+// fast_exp_nonpos (rust/npu-asr-host/src/lib.rs:38-55): 2^floor + a degree-5
+// polynomial of 2^frac, evaluated in the reference's order (no contraction).
+__device__ __forceinline__ float fast_exp_nonpos(float x) {
+  x = x < -87.0f ? -87.0f : x;
+  const float y = x * 1.442695040888963f;
+  const float yf = floorf(y);
+  const float f = y - yf;
+  const float p = 1.0f + f * (0.6931471805599453f +
+                              f * (0.2402265069591007f +
+                                   f * (0.05550410866482158f +
+                                        f * (0.009618129107628477f + f * 0.0013333558146428443f))));
+  const uint32_t e = static_cast<uint32_t>(static_cast<int>(yf) + 127);
+  return p * __uint_as_float(e << 23);
+}
+
+__device__ __forceinline__ float fast_sigmoid(float x) {
+  if (x >= 0.0f) return 1.0f / (1.0f + fast_exp_nonpos(-x));
+  const float e = fast_exp_nonpos(x);
+  return e / (1.0f + e);
+}
+
+__device__ __forceinline__ void w8a8_store(const W8a8Epi &e, int b, int r, int m, int32_t a) {
+  const size_t o = static_cast<size_t>(b) * m + r;
+  if (e.acc) {
+    e.acc[o] = a;
+    return;
+  }
+  float v = static_cast<float>(a) * e.scale_a[0] * e.ws[r];
+  if (e.epi == EPI_BIAS) {
+    v = v + e.bias[r];
+  } else if (e.epi == EPI_SILU_BIAS) {
+    const float z = v + e.bias[r];
+    v = z * fast_sigmoid(z);
+  }
+  e.y[o] = v;
+}
+
+// int8 activations x int8 weights -> int32 (exact), with the output stage
+// above.  <= 8 rows: an sdot4 GEMV; more (up to the reference's Mp = 512):
+// launch_w8a8_mfma.
 void launch_gemv_i8act(const int8_t *q, const int8_t *xq, int m, int k, int batch,
-                       int32_t *acc, hipStream_t s);
+                       const W8a8Epi &e, hipStream_t s);
+void launch_w8a8_mfma(const int8_t *wq, const int8_t *aq, int m, int k, int batch, const W8a8Epi &e,
+                      hipStream_t s);
+// Dynamic per-tensor activation quant (quant_scale + quant_i8, ctx2.rs:
+// 1352-1377): partial maxima (w8a8_partial_floats() floats), then aq and the
+// device scalar scale_out.
+void launch_w8a8_quant(const float *a, size_t n, float *partial, int8_t *aq, float *scale_out,
+                       hipStream_t s);
+size_t w8a8_partial_floats();
 
 struct AttnLaunch {
   // q fp32 [batch, q_stride] with the hq heads at q_off (head h at h*hd)

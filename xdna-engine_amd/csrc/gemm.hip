@@ -58,7 +58,13 @@ struct WLoad {  // one lane's 16 weights of a step (raw)
 template <int WT>
 __device__ __forceinline__ void load_w(const __amdgpu_buffer_rsrc_t &rw, const __amdgpu_buffer_rsrc_t &re, int row,
                                        int k, bool ok, int K, WLoad<WT> &o) {
-  if constexpr (WT == XE_BF16) {
+  if constexpr (WT == XE_I4) {
+    // 16 nibbles (8 bytes) of row `row` from element k (k a multiple of 16)
+    typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+    const u32x2 v = __builtin_bit_cast(
+        u32x2, __builtin_amdgcn_raw_buffer_load_b64(rw, ok ? row * (K / 2) + k / 2 : kNoRec, 0, 2));
+    o.q = u32x4{v.x, v.y, 0u, 0u};
+  } else if constexpr (WT == XE_BF16) {
     const int off = ok ? (row * K + k) * 2 : kNoRec;
     o.q = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, off, 0, 2));
     o.q2 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, ok ? off + 16 : kNoRec, 0, 2));
@@ -75,6 +81,20 @@ __device__ __forceinline__ void to_bf16(const WLoad<WT> &w, bf16x8 &a0, bf16x8 &
   if constexpr (WT == XE_BF16) {
     a0 = __builtin_bit_cast(bf16x8, w.q);
     a1 = __builtin_bit_cast(bf16x8, w.q2);
+  } else if constexpr (WT == XE_I4) {
+    // signed nibbles (at most 4 significant bits: exact in bf16), k order
+    const uint32_t d[2] = {w.q.x, w.q.y};
+    uint32_t p[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const uint32_t word = d[i / 4];
+      const int j = 2 * (i & 3);
+      const float f0 = static_cast<float>(static_cast<int>(__builtin_amdgcn_sbfe(static_cast<int>(word), 4 * j, 4)));
+      const float f1 = static_cast<float>(static_cast<int>(__builtin_amdgcn_sbfe(static_cast<int>(word), 4 * j + 4, 4)));
+      p[i] = pack_hi16(f0, f1);
+    }
+    a0 = __builtin_bit_cast(bf16x8, u32x4{p[0], p[1], p[2], p[3]});
+    a1 = __builtin_bit_cast(bf16x8, u32x4{p[4], p[5], p[6], p[7]});
   } else {
     const uint32_t d[4] = {w.q.x, w.q.y, w.q.z, w.q.w};
     uint32_t p[8];
@@ -103,7 +123,7 @@ __device__ __forceinline__ void epilogue4(const gdev::GemvParams &p, int wdtype,
 #pragma unroll
   for (int i = 0; i < 4; i++) {
     const int r = min(r0 + i, p.m - 1);
-    t[i] = acc[i] * (wdtype == XE_I8 ? p.scale[r] : 1.0f) + (p.bias ? p.bias[r] : 0.0f);
+    t[i] = acc[i] * ((wdtype == XE_I8 || wdtype == XE_I4) ? p.scale[r] : 1.0f) + (p.bias ? p.bias[r] : 0.0f);
   }
   float *yrow = p.y + static_cast<size_t>(b) * p.ldy;
   if (p.act == ACT_GEGLU_TANH) {
@@ -346,6 +366,7 @@ GemmFn pick_gemm(int wdtype, int mb) {
     case XE_I8: return pick_mb<XE_I8>(mb);
     case XE_BF16: return pick_mb<XE_BF16>(mb);
     case XE_BFP16: return pick_mb<XE_BFP16>(mb);
+    case XE_I4: return pick_mb<XE_I4>(mb);
   }
   return nullptr;
 }
@@ -406,7 +427,7 @@ void launch_gemm(const gdev::GemvParams &p, int wdtype, float *ws, unsigned *cnt
   XE_REQUIRE(p.k % 16 == 0, "gemm: K must be a multiple of 16");
   XE_REQUIRE(!p.x_bf16, "gemm: fp32 activations only");
   XE_REQUIRE(p.act != ACT_GEGLU_TANH || p.m % 4 == 0, "gemm: GeGLU rows must pair within 4-row groups");
-  XE_REQUIRE(wdtype != XE_I8 || p.scale, "gemm: int8 weight without scales");
+  XE_REQUIRE((wdtype != XE_I8 && wdtype != XE_I4) || p.scale, "gemm: int8/int4 weight without scales");
   XE_REQUIRE(wdtype != XE_BFP16 || p.exps, "gemm: bfp16 weight without exponents");
   // buffer offsets are 32-bit: weights and activations below 2 GB
   const size_t wb = static_cast<size_t>(p.m) * p.k * (wdtype == XE_BF16 ? 2 : 1);

@@ -109,7 +109,7 @@ template <int NB>
 __global__ __launch_bounds__(kThreads) void gemv_i8act_kernel(const int8_t *__restrict__ q,
                                                              const int8_t *__restrict__ xq,
                                                              int m, int k, int batch,
-                                                             int32_t *__restrict__ acc_out) {
+                                                             W8a8Epi e) {
   extern __shared__ float4 xs4[];
   int8_t *xs = reinterpret_cast<int8_t *>(xs4);
   for (int i = threadIdx.x; i < batch * k; i += kThreads) xs[i] = xq[i];
@@ -147,7 +147,7 @@ __global__ __launch_bounds__(kThreads) void gemv_i8act_kernel(const int8_t *__re
     acc[b] = v;
   }
   if (kl == 0 && r < m)
-    for (int b = 0; b < batch && b < NB; b++) acc_out[static_cast<size_t>(b) * m + r] = acc[b];
+    for (int b = 0; b < batch && b < NB; b++) w8a8_store(e, b, r, m, acc[b]);
 }
 
 // ---------------------------------------------------------------------------
@@ -181,6 +181,7 @@ GemvFn pick(int wt, int nb, int lpr, int rpl) {
     case XE_I8: return pick_nb<XE_I8>(nb, lpr, rpl);
     case XE_BF16: return pick_nb<XE_BF16>(nb, lpr, rpl);
     case XE_BFP16: return pick_nb<XE_BFP16>(nb, lpr, rpl);
+    case XE_I4: return pick_nb<XE_I4>(nb, lpr, rpl);
   }
   return nullptr;
 }
@@ -194,7 +195,7 @@ void launch_gemv(const GemvLaunch &L, hipStream_t s) {
   XE_REQUIRE(L.act != ACT_GEGLU_TANH || L.m % 2 == 0, "gemv: GeGLU needs paired rows");
   XE_REQUIRE(L.norm == XE_NORM_NONE || L.gamma, "gemv: norm without gamma");
   XE_REQUIRE(L.norm != XE_NORM_LN || L.beta, "gemv: LayerNorm without beta");
-  XE_REQUIRE(L.wdtype != XE_I8 || L.scale, "gemv: int8 weight without scales");
+  XE_REQUIRE((L.wdtype != XE_I8 && L.wdtype != XE_I4) || L.scale, "gemv: int8/int4 weight without scales");
   XE_REQUIRE(L.wdtype != XE_BFP16 || L.exps, "gemv: bfp16 weight without exponents");
   XE_REQUIRE(!L.sub || L.x_dtype == XE_F32, "gemv: residual prologue needs fp32 x");
   const int nb = L.batch <= 1 ? 1 : L.batch <= 2 ? 2 : L.batch <= 4 ? 4 : 8;
@@ -234,7 +235,7 @@ void launch_gemv_phase(const sdev::Phase &ph, hipStream_t s) {
 }
 
 void launch_gemv_i8act(const int8_t *q, const int8_t *xq, int m, int k, int batch,
-                       int32_t *acc, hipStream_t s) {
+                       const W8a8Epi &e, hipStream_t s) {
   XE_REQUIRE(m > 0 && k > 0 && batch > 0 && batch <= 8, "gemv_i8act: bad shape");
   XE_REQUIRE(k % 16 == 0, "gemv_i8act: K must be a multiple of 16");
   const size_t lds = static_cast<size_t>(batch) * k;
@@ -245,7 +246,7 @@ void launch_gemv_i8act(const int8_t *q, const int8_t *xq, int m, int k, int batc
   if (lds > 64 * 1024)
     XE_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(fn),
                                hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
-  hipLaunchKernelGGL(fn, dim3(grid), dim3(kThreads), lds, s, q, xq, m, k, batch, acc);
+  hipLaunchKernelGGL(fn, dim3(grid), dim3(kThreads), lds, s, q, xq, m, k, batch, e);
   XE_HIP(hipGetLastError());
 }
 

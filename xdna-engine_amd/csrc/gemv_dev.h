@@ -248,6 +248,10 @@ struct Chunk<XE_I8> {
   uint4 q;
 };
 template <>
+struct Chunk<XE_I4> {
+  uint2 q;  // 16 nibbles, k order (nibble i of the 64 bits = element i)
+};
+template <>
 struct Chunk<XE_BFP16> {
   uint4 q;
   uint32_t e;  // two biased exponents (low 16 bits)
@@ -273,14 +277,28 @@ __device__ __forceinline__ void mask_chunk(Chunk<WT> &c, bool keep) {
   if constexpr (WT == XE_BF16) {
     mask_u4(c.lo, keep);
     mask_u4(c.hi, keep);
+  } else if constexpr (WT == XE_I4) {
+    c.q.x = keep ? c.q.x : 0u;
+    c.q.y = keep ? c.q.y : 0u;
   } else {
     mask_u4(c.q, keep);
   }
 }
 
+// 8-byte streaming load (int4 chunks).
+__device__ __forceinline__ uint2 ld_nt8(const void *ptr) {
+  typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+  const u32x2 v = __builtin_nontemporal_load(gptr(static_cast<const u32x2 *>(ptr)));
+  return make_uint2(v.x, v.y);
+}
+
 template <int WT>
 __device__ __forceinline__ void load_chunk(const GemvParams &p, int row, int c, Chunk<WT> &out) {
-  if constexpr (WT == XE_I8) {
+  if constexpr (WT == XE_I4) {
+    const uint2 *base = reinterpret_cast<const uint2 *>(static_cast<const uint8_t *>(p.w) +
+                                                        static_cast<size_t>(row) * (p.k / 2));
+    out.q = ld_nt8(base + c);
+  } else if constexpr (WT == XE_I8) {
     const uint4 *base = reinterpret_cast<const uint4 *>(static_cast<const int8_t *>(p.w) +
                                                         static_cast<size_t>(row) * p.k);
     out.q = ld_nt16(base + c);
@@ -301,11 +319,28 @@ __device__ __forceinline__ void load_chunk(const GemvParams &p, int row, int c, 
 __device__ __forceinline__ float sb(uint32_t w, int j) {
   return static_cast<float>(static_cast<int>(static_cast<int8_t>(w >> (8 * j))));
 }
+// Signed nibble j of w (bits 4j..4j+3), the reference's ((v ^ 8) - 8).
+__device__ __forceinline__ float sn(uint32_t w, int j) {
+  // the builtin is typed unsigned: convert its sign-extended bits as int
+  return static_cast<float>(static_cast<int>(__builtin_amdgcn_sbfe(static_cast<int>(w), 4 * j, 4)));
+}
 
 // acc += dot(chunk, x[16])
 template <int WT>
 __device__ __forceinline__ float chunk_dot(const Chunk<WT> &ch, const float4 (&xv)[4], float acc) {
-  if constexpr (WT == XE_I8) {
+  if constexpr (WT == XE_I4) {
+    const uint32_t w2[2] = {ch.q.x, ch.q.y};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const uint32_t w = w2[i / 2];
+      const int j0 = 4 * (i & 1);
+      acc = __builtin_fmaf(xv[i].x, sn(w, j0), acc);
+      acc = __builtin_fmaf(xv[i].y, sn(w, j0 + 1), acc);
+      acc = __builtin_fmaf(xv[i].z, sn(w, j0 + 2), acc);
+      acc = __builtin_fmaf(xv[i].w, sn(w, j0 + 3), acc);
+    }
+    return acc;
+  } else if constexpr (WT == XE_I8) {
     const uint32_t w4[4] = {ch.q.x, ch.q.y, ch.q.z, ch.q.w};
 #pragma unroll
     for (int i = 0; i < 4; i++) {
@@ -611,7 +646,7 @@ __device__ __forceinline__ void gemv_tiles(const GemvParams &p, float4 *xs4, flo
 #pragma unroll
         for (int i = 0; i < RPL; i++) {
           float t = acc[b][i];
-          if (WT == XE_I8) t = t * gptr(p.scale)[row[i]];
+          if (WT == XE_I8 || WT == XE_I4) t = t * gptr(p.scale)[row[i]];
           if (p.bias) t = t + gptr(p.bias)[row[i]];
           v[i] = t;
         }

@@ -9,6 +9,10 @@
 //                   first, blocks of 8 along k share e = floor(log2 max|x|),
 //                   mantissa = round-half-even(x / 2^(e-6)); +128 (the sim's
 //                   overflow case) saturates to 127; stored exponent e + 127.
+//   quant_rows_i4   Lin::load int4 branch (opt125m_decode.rs:63-79) on [m,k]:
+//                   scale = max|row|/7 (1.0 for an all-zero row), q =
+//                   round-half-away(w/scale) clamped +-7, two's-complement
+//                   nibbles packed along k (byte j: k = 2j low, 2j+1 high).
 //   quant_scale / quant_i8 / dequant_epi   W8A8 (ctx2.rs:1352-1435).
 #pragma once
 
@@ -35,6 +39,7 @@ inline float bf16_round(float x) {
 
 inline int8_t quant_i8(float x, float scale) {
   float v = std::round(x / scale);
+  if (v != v) return 0;  // Rust's saturating `as i8` maps NaN to 0
   v = v < -127.0f ? -127.0f : (v > 127.0f ? 127.0f : v);
   return static_cast<int8_t>(v);
 }
@@ -59,6 +64,29 @@ inline void quant_rows_i8(const float *w, int m, int k, int8_t *q, float *s) {
     const float sc = amax > 0.0f ? amax / 127.0f : 1.0f;
     s[r] = sc;
     for (int j = 0; j < k; j++) q[static_cast<size_t>(r) * k + j] = quant_i8(row[j], sc);
+  }
+}
+
+inline void quant_rows_i4(const float *w, int m, int k, uint8_t *packed, float *s) {
+  for (int r = 0; r < m; r++) {
+    const float *row = w + static_cast<size_t>(r) * k;
+    float amax = 0.f;
+    for (int j = 0; j < k; j++) {
+      const float v = std::fabs(row[j]);
+      amax = v > amax ? v : amax;
+    }
+    const float sc = amax > 0.0f ? amax / 7.0f : 1.0f;
+    s[r] = sc;
+    for (int j = 0; j < k; j += 2) {
+      unsigned nib[2];
+      for (int h = 0; h < 2; h++) {
+        float v = std::round(row[j + h] / sc);
+        if (v != v) v = 0.0f;
+        v = v < -7.0f ? -7.0f : (v > 7.0f ? 7.0f : v);
+        nib[h] = static_cast<unsigned>(static_cast<int>(v)) & 0x0Fu;
+      }
+      packed[static_cast<size_t>(r) * (k / 2) + j / 2] = static_cast<uint8_t>(nib[0] | (nib[1] << 4));
+    }
   }
 }
 

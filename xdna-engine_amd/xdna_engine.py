@@ -24,7 +24,8 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libxdna_engine.so")
 
-XE_F32, XE_BF16, XE_I8, XE_BFP16, XE_I32 = 0, 1, 2, 3, 4
+XE_F32, XE_BF16, XE_I8, XE_BFP16, XE_I32, XE_I4 = 0, 1, 2, 3, 4, 5
+XE_EPI_NONE, XE_EPI_BIAS, XE_EPI_SILU_BIAS = 0, 1, 2
 XE_NORM_NONE, XE_NORM_LN, XE_NORM_RMS, XE_NORM_RMS1P = 0, 1, 2, 3
 XE_LAYOUT_MK, XE_LAYOUT_KN = 0, 1
 XE_OPT, XE_WHISPER, XE_GEMMA3 = 0, 1, 2
@@ -37,9 +38,11 @@ EXPORTS = [
     "xe_probe_attn", "xe_ctx_create",
     "xe_ctx_destroy",
     "xe_ctx_dispatches", "xe_ctx_reset_dispatches", "xe_register_weight",
-    "xe_register_weight_q8", "xe_register_weight_bfp16", "xe_register_weight_bf16",
+    "xe_register_weight_q8", "xe_register_weight_q4", "xe_register_weight_q4_kn",
+    "xe_register_weight_bfp16", "xe_register_weight_bf16",
     "xe_register_fused", "xe_weight_set_norm", "xe_weight_free", "xe_weight_shape", "xe_gemv",
     "xe_fused_norm_gemv", "xe_gemv_dev", "xe_gemv_i8act", "xe_gemv_i8act_dev", "xe_w8a8_linear",
+    "xe_w8a8_linear_dev",
     "xe_attn_decode", "xe_attn_decode_dev", "xe_attn_decode_dev_static", "xe_ctx_synchronize", "xe_decoder_create",
     "xe_decoder_destroy", "xe_decoder_init_synthetic", "xe_decoder_set_tensor",
     "xe_decoder_get_tensor_q8", "xe_decoder_reset", "xe_decoder_set_cross", "xe_decoder_step",
@@ -129,6 +132,8 @@ def lib():
         "xe_register_weight": (vp, [vp, i, i, i, vp, i, vp]),
         "xe_register_weight_q8": (vp, [vp, i, i, vp, vp, vp]),
         "xe_register_weight_bfp16": (vp, [vp, i, i, vp, vp, vp]),
+        "xe_register_weight_q4": (vp, [vp, i, i, vp, vp, vp]),
+        "xe_register_weight_q4_kn": (vp, [vp, i, i, vp, vp, vp]),
         "xe_register_weight_bf16": (vp, [vp, i, i, vp, vp]),
         "xe_register_fused": (vp, [vp, i, i, i, vp, i, i, vp, vp, f, vp]),
         "xe_weight_set_norm": (i, [vp, i, vp, vp, f]),
@@ -140,6 +145,7 @@ def lib():
         "xe_gemv_i8act": (i, [vp, vp, vp, i, vp]),
         "xe_gemv_i8act_dev": (i, [vp, vp, vp, i, vp]),
         "xe_w8a8_linear": (i, [vp, vp, vp, i, vp, C.POINTER(f)]),
+        "xe_w8a8_linear_dev": (i, [vp, vp, vp, i, i, vp, vp]),
         "xe_attn_decode": (i, [vp, vp, vp, vp, vp, i, i, i, i, i, f, vp]),
         "xe_attn_decode_dev": (i, [vp, vp, vp, vp, vp, i, i, i, i, i, f, vp]),
         "xe_attn_decode_dev_static": (i, [vp, vp, vp, vp, vp, i, i, i, i, i, f, vp]),
@@ -330,6 +336,20 @@ class CtxDecode:
         m, k = q.shape
         return Weight(lib().xe_register_weight_q8(self.h, m, k, _p(q), _p(s), _p(b)))
 
+    def register_weight_q4(self, packed, scales, bias=None):
+        """int4 [m, k/2] packed along k (opt125m_decode.rs:63-105 codes)."""
+        packed = np.ascontiguousarray(packed, np.uint8)
+        s, b = _f32(scales), _f32(bias)
+        m, k2 = packed.shape
+        return Weight(lib().xe_register_weight_q4(self.h, m, 2 * k2, _p(packed), _p(s), _p(b)))
+
+    def register_weight_q4_kn(self, packed_kn, scales, bias=None):
+        """int4 in the reference's own [K, N/2] packing (Lin::load)."""
+        packed_kn = np.ascontiguousarray(packed_kn, np.uint8)
+        s, b = _f32(scales), _f32(bias)
+        k, m2 = packed_kn.shape
+        return Weight(lib().xe_register_weight_q4_kn(self.h, 2 * m2, k, _p(packed_kn), _p(s), _p(b)))
+
     def register_weight_bfp16(self, mant, exps, bias=None):
         mant = np.ascontiguousarray(mant, np.int8)
         exps = np.ascontiguousarray(exps, np.uint8)
@@ -414,6 +434,11 @@ class CtxDecode:
         sa = C.c_float()
         _check(lib().xe_w8a8_linear(self.h, weight.h, _p(x), b, _p(y), C.byref(sa)))
         return y, sa.value
+
+    def w8a8_linear_dev(self, weight, x_buf, batch, epi, y_buf, sa_buf=None):
+        """Device-pointer W8A8 (asynchronous); epi: XE_EPI_NONE/BIAS/SILU_BIAS."""
+        _check(lib().xe_w8a8_linear_dev(self.h, weight.h, x_buf.ptr, batch, epi, y_buf.ptr,
+                                        None if sa_buf is None else sa_buf.ptr))
 
     # -- attention (ctx_decode.rs:468-555) --
     def attn(self, q, kc, vc, lens, scale):
