@@ -486,6 +486,18 @@ void validate_config(const xe_model_config &c, int max_batch) {
   if (c.family != XE_GEMMA3) XE_REQUIRE(c.n_heads == c.n_kv_heads, "OPT/Whisper are MHA");
 }
 
+// Splits per (stream, kv head) of the split-K attention phases of a batch:
+// about four workgroups per CU over the batch's (stream, kv head) pairs, at
+// most one per 64 cache rows and at most 64.  (A stream's blocks past its
+// filled length return at once; split_range sizes chunks from the length.)
+int attn_splits_for(const xe_decoder *d, int batch, int hkv) {
+  const auto &c = d->c;
+  const int cus = d->dev->num_cus > 0 ? d->dev->num_cus : 256;
+  int ms = (4 * cus) / std::max(1, batch * hkv);
+  const int cap = (std::max(c.max_ctx, c.family == XE_WHISPER ? c.n_cross : 0) + 63) / 64;
+  return std::max(1, std::min(std::min(ms, cap), 64));
+}
+
 void alloc_decoder(xe_decoder *d) {
   const auto &c = d->c;
   hipStream_t s = d->s;
@@ -559,13 +571,15 @@ void alloc_decoder(xe_decoder *d) {
   d->step_flags = dalloc<unsigned int>(static_cast<size_t>(d->step_grid) * 32, s);
   d->step_status = dalloc<unsigned int>(64, s);
   d->ll_forced = dalloc<int32_t>(static_cast<size_t>(c.max_ctx + 1) * B, s);
-  // split-K attention: ~4 workgroups per CU at the largest batch, chunks >= 32 keys
+  // split-K attention: the phase plan of a batch takes attn_splits_for(); the
+  // workspace holds the partials of the largest batch x splits product
   const int hkv_max = std::max(c.n_kv_heads, wh ? c.n_heads : 0);
-  int ms = (4 * d->dev->num_cus) / std::max(1, hkv_max);
-  const int cap = (std::max(c.max_ctx, wh ? c.n_cross : 0) + 63) / 64;
-  ms = std::max(1, std::min(std::min(ms, cap), 64));
-  d->attn_splits = ms;
-  d->attn_work = dalloc<float>(attn_work_floats(B, std::max(c.n_heads, 1), c.head_dim, ms), s, false);
+  size_t part_rows = 0;
+  for (int b = 1; b <= B; b++)
+    part_rows = std::max(part_rows, static_cast<size_t>(b) * attn_splits_for(d, b, hkv_max));
+  d->attn_splits = attn_splits_for(d, B, hkv_max);
+  d->attn_work = dalloc<float>(attn_work_floats(static_cast<int>(part_rows), std::max(c.n_heads, 1), c.head_dim, 1),
+                               s, false);
   if (gem) {
     const int half = c.head_dim / 2;
     std::vector<float> cs(static_cast<size_t>(c.max_ctx) * half), sn(cs.size());
@@ -890,7 +904,7 @@ void build_plan(xe_decoder *d, int B, xe_decoder::Plan &plan) {
       a.out = d->att;
       a.out_stride = hq;
       a.work = d->attn_work;
-      a.max_splits = d->attn_splits;
+      a.max_splits = attn_splits_for(d, B, c.n_kv_heads);
       // KV bytes depend on the positions; profile_step fills them in
       pb.attn(a, "attn_self", 4.0 * B * (nq + hq) + 4.0 * B * hk);
     }
@@ -937,7 +951,7 @@ void build_plan(xe_decoder *d, int B, xe_decoder::Plan &plan) {
       a.out = d->att;
       a.out_stride = D;
       a.work = d->attn_work;
-      a.max_splits = d->attn_splits;
+      a.max_splits = attn_splits_for(d, B, c.n_heads);
       pb.attn(a, "attn_cross", static_cast<double>(c.n_cross) * D * 2 * 2 + 8.0 * B * D);
       GemvCall o;
       o.m = &l.xo;
