@@ -247,6 +247,22 @@ int xe_attn_decode_dev_static(xe_ctx *ctx, const float *q_dev,
 /* Wait for the ctx stream; returns 0 or -1. */
 int xe_ctx_synchronize(xe_ctx *ctx);
 
+/* ---- asynchronous submission (xrt_shim.h:47-54: shim_run_*_start returns
+ * a run handle without waiting, shim_run_wait blocks, shim_run_free) ----
+ * The *_dev entry points queue their work on the ctx stream and return at
+ * once; xe_ctx_record then takes a handle on everything queued so far, so
+ * shim_run_matmul8_start maps to xe_gemv_dev + xe_ctx_record.  Buffers the
+ * work reads or writes must stay alive until the handle completes. */
+typedef struct xe_run xe_run;
+xe_run *xe_ctx_record(xe_ctx *ctx);
+/* 1 = complete, 0 = still running, -1 = error (xe_last_error). */
+int xe_run_query(xe_run *run);
+/* Block until complete: 0, or -1 (for a resident dispatch, also when its
+ * step reported a failure). */
+int xe_run_wait(xe_run *run);
+/* Free a handle (waits for its work first). */
+void xe_run_free(xe_run *run);
+
 /* Kernel probes (the reference's decode_gemv_probe.rs / mha_decode_probe.rs
  * timing runs): the launches of one xe_gemv_dev per weight in ws (same
  * shape; rotating copies defeat the 256 MB last-level cache) or of one
@@ -345,6 +361,30 @@ int xe_decoder_init_synthetic(xe_decoder *dec, uint64_t seed);
  * xe_register_weight.  Returns 0 or -1 (unknown kind / wrong size). */
 int xe_decoder_set_tensor(xe_decoder *dec, int kind, int layer,
                           const float *data, size_t count);
+/* Shape [rows, cols] of tensor (kind, layer) of a model ([out, in] for
+ * matrices; vectors are 1 x n); -1 when the family has no such tensor.
+ * Host only (the tensor table of npu-weights/src/spec.rs, per family). */
+int xe_model_tensor_shape(const xe_model_config *cfg, int kind, int layer,
+                          int *rows, int *cols);
+/* The decoder's model configuration. */
+int xe_decoder_config(xe_decoder *dec, xe_model_config *out);
+/* Load a decoder's weights from a safetensors file (the reference's weight
+ * arena loader, npu-weights/src/arena.rs:14-99, and its Hugging Face
+ * sources): either a baked OPT arena (metadata arch "opt", format_version
+ * 1; names and [in, out] linears of arch/opt.rs:1-20) or a Hugging Face
+ * checkpoint of the model family (OPTForCausalLM, the Whisper decoder,
+ * Gemma3ForCausalLM names; [out, in] linears).  F32 / BF16 / F16 tensors;
+ * each is quantised like xe_decoder_set_tensor.  Tensors the model does not
+ * use (encoder weights, a tied lm_head) are skipped; a tied lm_head /
+ * proj_out stands in for a missing token embedding.  Every tensor the model
+ * needs must be present.  Returns the number of tensors loaded, or -1. */
+int xe_decoder_load_safetensors(xe_decoder *dec, const char *path);
+/* Host-only dry run of the loader for a config: the number of tensors that
+ * map, and (report, may be NULL) one line per tensor "name -> kind layer
+ * [T]" or "name -> skipped" after a first line "arena" / "hf".  -1 (with
+ * the loader's message) when the file would not load. */
+int xe_safetensors_plan(const char *path, const xe_model_config *cfg,
+                        char *report, int cap);
 /* Read back a quantised int8 tensor (q [rows*cols], scales [rows]). */
 int xe_decoder_get_tensor_q8(xe_decoder *dec, int kind, int layer, int8_t *q,
                              float *scales);
@@ -389,6 +429,26 @@ int xe_decoder_profile_step(xe_decoder *dec, int batch, int max_entries, char *l
  * backend); returns -1 on error. */
 enum { XE_EXEC_GRAPH = 0, XE_EXEC_PERSISTENT = 1, XE_EXEC_EAGER = 2, XE_EXEC_LL = 3 };
 int xe_decoder_executor(xe_decoder *dec, int batch);
+/* Resident decode step (ElfResident, npu-xrt/src/lib.rs:591-629 and
+ * xrt_shim.h:95-111: a constant program bound once, per-token parameters
+ * written to a host-mapped scratchpad, then dispatched).  open() builds the
+ * decoder's step for `batch` streams once (its HIP graph, or the low-latency
+ * kernel's plan); write() puts tokens [batch] and positions [batch] into
+ * pinned host memory (no device work); dispatch() copies them to the
+ * device, runs the step and waits; dispatch_start() returns a run handle
+ * instead (xe_run_wait / xe_run_query; write() and read() refuse while it
+ * is in flight); read() gives the last completed dispatch's greedy tokens
+ * [batch] and/or logits [batch, vocab] (either may be NULL).  The step is
+ * the one xe_decoder_step runs; the streams' cache positions advance alike.
+ * Close the resident step before the decoder. */
+typedef struct xe_resident xe_resident;
+xe_resident *xe_resident_open(xe_decoder *dec, int batch);
+void xe_resident_close(xe_resident *res);
+int xe_resident_write(xe_resident *res, const int32_t *tokens,
+                      const int32_t *pos);
+int xe_resident_dispatch(xe_resident *res);
+xe_run *xe_resident_dispatch_start(xe_resident *res);
+int xe_resident_read(xe_resident *res, int32_t *next, float *logits);
 /* Mean device time (microseconds) of the last generate's decode steps. */
 double xe_decoder_last_step_us(xe_decoder *dec);
 /* Bytes of weights one decode step streams (int8/bf16/bfp16 + scales). */

@@ -63,6 +63,77 @@ def vec(om, kind, layer=-1):
     return om.tensor_f32(kind, layer)
 
 
+def checkpoint(name, cfgd, om):
+    """The oracle's weights as a Hugging Face checkpoint of the family:
+    {parameter name: fp32 array}, linears [out, in] dequantised (q * scale).
+    The names are the ones HF's modules own (load() checks that none is
+    missing and every shape matches); Whisper's are those of
+    WhisperForConditionalGeneration (model.decoder.*)."""
+    L = cfgd["n_layers"]
+    d = cfgd["d_model"]
+    if name == "opt":
+        sd = {"model.decoder.embed_tokens.weight": weight(om, O.XE_T_TOK_EMB, -1),
+              "model.decoder.embed_positions.weight": vec(om, O.XE_T_POS_EMB).reshape(cfgd["max_pos"] + 2, -1),
+              "model.decoder.final_layer_norm.weight": vec(om, O.XE_T_LNF_W),
+              "model.decoder.final_layer_norm.bias": vec(om, O.XE_T_LNF_B)}
+        for l in range(cfgd["n_layers"]):
+            p = "model.decoder.layers.%d." % l
+            for hf, kind, bkind in (("self_attn.q_proj", O.XE_T_Q_W, O.XE_T_Q_B),
+                                    ("self_attn.k_proj", O.XE_T_K_W, O.XE_T_K_B),
+                                    ("self_attn.v_proj", O.XE_T_V_W, O.XE_T_V_B),
+                                    ("self_attn.out_proj", O.XE_T_O_W, O.XE_T_O_B),
+                                    ("fc1", O.XE_T_FC1_W, O.XE_T_FC1_B),
+                                    ("fc2", O.XE_T_FC2_W, O.XE_T_FC2_B)):
+                sd[p + hf + ".weight"] = weight(om, kind, l)
+                sd[p + hf + ".bias"] = vec(om, bkind, l)
+            sd[p + "self_attn_layer_norm.weight"] = vec(om, O.XE_T_LN1_W, l)
+            sd[p + "self_attn_layer_norm.bias"] = vec(om, O.XE_T_LN1_B, l)
+            sd[p + "final_layer_norm.weight"] = vec(om, O.XE_T_LN2_W, l)
+            sd[p + "final_layer_norm.bias"] = vec(om, O.XE_T_LN2_B, l)
+        return sd
+    if name == "whisper":
+        sd = {"model.decoder.embed_tokens.weight": weight(om, O.XE_T_TOK_EMB, -1),
+              "model.decoder.embed_positions.weight": vec(om, O.XE_T_POS_EMB).reshape(cfgd["max_pos"], d),
+              "model.decoder.layer_norm.weight": vec(om, O.XE_T_LNF_W), "model.decoder.layer_norm.bias": vec(om, O.XE_T_LNF_B)}
+        for l in range(cfgd["n_layers"]):
+            p = "model.decoder.layers.%d." % l
+            for hf, kind, bkind in (("self_attn.q_proj", O.XE_T_Q_W, O.XE_T_Q_B),
+                                    ("self_attn.k_proj", O.XE_T_K_W, None),
+                                    ("self_attn.v_proj", O.XE_T_V_W, O.XE_T_V_B),
+                                    ("self_attn.out_proj", O.XE_T_O_W, O.XE_T_O_B),
+                                    ("encoder_attn.q_proj", O.XE_T_XQ_W, O.XE_T_XQ_B),
+                                    ("encoder_attn.k_proj", O.XE_T_XK_W, None),
+                                    ("encoder_attn.v_proj", O.XE_T_XV_W, O.XE_T_XV_B),
+                                    ("encoder_attn.out_proj", O.XE_T_XO_W, O.XE_T_XO_B),
+                                    ("fc1", O.XE_T_FC1_W, O.XE_T_FC1_B),
+                                    ("fc2", O.XE_T_FC2_W, O.XE_T_FC2_B)):
+                sd[p + hf + ".weight"] = weight(om, kind, l)
+                if bkind is not None:
+                    sd[p + hf + ".bias"] = vec(om, bkind, l)
+            for hf, wk, bk in (("self_attn_layer_norm", O.XE_T_LN1_W, O.XE_T_LN1_B),
+                               ("encoder_attn_layer_norm", O.XE_T_LNX_W, O.XE_T_LNX_B),
+                               ("final_layer_norm", O.XE_T_LN2_W, O.XE_T_LN2_B)):
+                sd[p + hf + ".weight"] = vec(om, wk, l)
+                sd[p + hf + ".bias"] = vec(om, bk, l)
+        return sd
+    sd = {"model.embed_tokens.weight": weight(om, O.XE_T_TOK_EMB, -1),
+          "model.norm.weight": vec(om, O.XE_T_LNF_W)}
+    for l in range(L):
+        p = "model.layers.%d." % l
+        for hf, kind in (("self_attn.q_proj", O.XE_T_Q_W), ("self_attn.k_proj", O.XE_T_K_W),
+                         ("self_attn.v_proj", O.XE_T_V_W), ("self_attn.o_proj", O.XE_T_O_W),
+                         ("mlp.gate_proj", O.XE_T_FC1_W), ("mlp.up_proj", O.XE_T_UP_W),
+                         ("mlp.down_proj", O.XE_T_FC2_W)):
+            sd[p + hf + ".weight"] = weight(om, kind, l)
+        for hf, kind in (("self_attn.q_norm", O.XE_T_QNORM_W), ("self_attn.k_norm", O.XE_T_KNORM_W),
+                         ("input_layernorm", O.XE_T_LN1_W),
+                         ("post_attention_layernorm", O.XE_T_POST_ATTN_W),
+                         ("pre_feedforward_layernorm", O.XE_T_LN2_W),
+                         ("post_feedforward_layernorm", O.XE_T_POST_FFN_W)):
+            sd[p + hf + ".weight"] = vec(om, kind, l)
+    return sd
+
+
 def build_opt(cfgd, om):
     import torch
     from transformers import OPTConfig, OPTForCausalLM
@@ -73,24 +144,7 @@ def build_opt(cfgd, om):
                    activation_function="relu", enable_bias=True, tie_word_embeddings=True,
                    pad_token_id=1, bos_token_id=2, eos_token_id=2)
     m = OPTForCausalLM(hc)
-    sd = {"model.decoder.embed_tokens.weight": weight(om, O.XE_T_TOK_EMB, -1),
-          "model.decoder.embed_positions.weight": vec(om, O.XE_T_POS_EMB).reshape(cfgd["max_pos"] + 2, -1),
-          "model.decoder.final_layer_norm.weight": vec(om, O.XE_T_LNF_W),
-          "model.decoder.final_layer_norm.bias": vec(om, O.XE_T_LNF_B)}
-    for l in range(cfgd["n_layers"]):
-        p = "model.decoder.layers.%d." % l
-        for hf, kind, bkind in (("self_attn.q_proj", O.XE_T_Q_W, O.XE_T_Q_B),
-                                ("self_attn.k_proj", O.XE_T_K_W, O.XE_T_K_B),
-                                ("self_attn.v_proj", O.XE_T_V_W, O.XE_T_V_B),
-                                ("self_attn.out_proj", O.XE_T_O_W, O.XE_T_O_B),
-                                ("fc1", O.XE_T_FC1_W, O.XE_T_FC1_B),
-                                ("fc2", O.XE_T_FC2_W, O.XE_T_FC2_B)):
-            sd[p + hf + ".weight"] = weight(om, kind, l)
-            sd[p + hf + ".bias"] = vec(om, bkind, l)
-        sd[p + "self_attn_layer_norm.weight"] = vec(om, O.XE_T_LN1_W, l)
-        sd[p + "self_attn_layer_norm.bias"] = vec(om, O.XE_T_LN1_B, l)
-        sd[p + "final_layer_norm.weight"] = vec(om, O.XE_T_LN2_W, l)
-        sd[p + "final_layer_norm.bias"] = vec(om, O.XE_T_LN2_B, l)
+    sd = checkpoint("opt", cfgd, om)
     load(m, sd)
 
     def logits(prefix):
@@ -112,29 +166,8 @@ def build_whisper(cfgd, om):
                        activation_function="gelu", scale_embedding=False, pad_token_id=0,
                        bos_token_id=1, eos_token_id=2, decoder_start_token_id=1)
     m = WhisperDecoder(hc)
-    sd = {"embed_tokens.weight": weight(om, O.XE_T_TOK_EMB, -1),
-          "embed_positions.weight": vec(om, O.XE_T_POS_EMB).reshape(cfgd["max_pos"], d),
-          "layer_norm.weight": vec(om, O.XE_T_LNF_W), "layer_norm.bias": vec(om, O.XE_T_LNF_B)}
-    for l in range(cfgd["n_layers"]):
-        p = "layers.%d." % l
-        for hf, kind, bkind in (("self_attn.q_proj", O.XE_T_Q_W, O.XE_T_Q_B),
-                                ("self_attn.k_proj", O.XE_T_K_W, None),
-                                ("self_attn.v_proj", O.XE_T_V_W, O.XE_T_V_B),
-                                ("self_attn.out_proj", O.XE_T_O_W, O.XE_T_O_B),
-                                ("encoder_attn.q_proj", O.XE_T_XQ_W, O.XE_T_XQ_B),
-                                ("encoder_attn.k_proj", O.XE_T_XK_W, None),
-                                ("encoder_attn.v_proj", O.XE_T_XV_W, O.XE_T_XV_B),
-                                ("encoder_attn.out_proj", O.XE_T_XO_W, O.XE_T_XO_B),
-                                ("fc1", O.XE_T_FC1_W, O.XE_T_FC1_B),
-                                ("fc2", O.XE_T_FC2_W, O.XE_T_FC2_B)):
-            sd[p + hf + ".weight"] = weight(om, kind, l)
-            if bkind is not None:
-                sd[p + hf + ".bias"] = vec(om, bkind, l)
-        for hf, wk, bk in (("self_attn_layer_norm", O.XE_T_LN1_W, O.XE_T_LN1_B),
-                           ("encoder_attn_layer_norm", O.XE_T_LNX_W, O.XE_T_LNX_B),
-                           ("final_layer_norm", O.XE_T_LN2_W, O.XE_T_LN2_B)):
-            sd[p + hf + ".weight"] = vec(om, wk, l)
-            sd[p + hf + ".bias"] = vec(om, bk, l)
+    pre = "model.decoder."
+    sd = {k[len(pre):]: v for k, v in checkpoint("whisper", cfgd, om).items()}
     load(m, sd)
     # the encoder output as the decoder sees it: synthetic N(0,1) rounded to bf16
     enc = vec(om, O.XE_T_ENC_OUT).reshape(cfgd["n_cross"], d)
@@ -167,21 +200,7 @@ def build_gemma3(cfgd, om):
                           hidden_activation="gelu_pytorch_tanh", tie_word_embeddings=True,
                           attention_bias=False, pad_token_id=0, bos_token_id=2, eos_token_id=1)
     m = Gemma3ForCausalLM(hc)
-    sd = {"model.embed_tokens.weight": weight(om, O.XE_T_TOK_EMB, -1),
-          "model.norm.weight": vec(om, O.XE_T_LNF_W)}
-    for l in range(L):
-        p = "model.layers.%d." % l
-        for hf, kind in (("self_attn.q_proj", O.XE_T_Q_W), ("self_attn.k_proj", O.XE_T_K_W),
-                         ("self_attn.v_proj", O.XE_T_V_W), ("self_attn.o_proj", O.XE_T_O_W),
-                         ("mlp.gate_proj", O.XE_T_FC1_W), ("mlp.up_proj", O.XE_T_UP_W),
-                         ("mlp.down_proj", O.XE_T_FC2_W)):
-            sd[p + hf + ".weight"] = weight(om, kind, l)
-        for hf, kind in (("self_attn.q_norm", O.XE_T_QNORM_W), ("self_attn.k_norm", O.XE_T_KNORM_W),
-                         ("input_layernorm", O.XE_T_LN1_W),
-                         ("post_attention_layernorm", O.XE_T_POST_ATTN_W),
-                         ("pre_feedforward_layernorm", O.XE_T_LN2_W),
-                         ("post_feedforward_layernorm", O.XE_T_POST_FFN_W)):
-            sd[p + hf + ".weight"] = vec(om, kind, l)
+    sd = checkpoint("gemma3", cfgd, om)
     load(m, sd)
 
     def logits(prefix):

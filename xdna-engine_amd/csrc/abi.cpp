@@ -477,6 +477,66 @@ void xe_ctx_reset_dispatches(xe_ctx *ctx) {
   if (ctx) ctx->dispatches = 0;
 }
 
+xe_run *xe_ctx_record(xe_ctx *ctx) {
+  return guard([&]() -> xe_run * {
+    XE_REQUIRE(ctx, "null ctx");
+    DeviceGuard dg(ctx->dev->ordinal);
+    auto *r = new xe_run;
+    r->ordinal = ctx->dev->ordinal;
+    const hipError_t e = hipEventCreateWithFlags(&r->ev, hipEventDisableTiming);
+    if (e != hipSuccess) {
+      delete r;
+      XE_HIP(e);
+    }
+    const hipError_t e2 = hipEventRecord(r->ev, ctx->dev->stream);
+    if (e2 != hipSuccess) {
+      (void)hipEventDestroy(r->ev);
+      delete r;
+      XE_HIP(e2);
+    }
+    return r;
+  }, nullptr);
+}
+
+int xe_run_query(xe_run *run) {
+  return guard([&]() -> int {
+    XE_REQUIRE(run, "null run");
+    if (run->done) return 1;
+    DeviceGuard dg(run->ordinal);
+    const hipError_t e = hipEventQuery(run->ev);
+    if (e == hipErrorNotReady) return 0;
+    XE_HIP(e);
+    run->done = true;
+    if (run->res) resident_done(run->res);
+    return 1;
+  }, -1);
+}
+
+int xe_run_wait(xe_run *run) {
+  return guard([&]() -> int {
+    XE_REQUIRE(run, "null run");
+    if (run->done) return 0;
+    DeviceGuard dg(run->ordinal);
+    XE_HIP(hipEventSynchronize(run->ev));
+    run->done = true;
+    if (run->res) resident_done(run->res);
+    return 0;
+  }, -1);
+}
+
+void xe_run_free(xe_run *run) {
+  guard([&]() -> int {
+    if (!run) return 0;
+    DeviceGuard dg(run->ordinal);
+    (void)hipEventSynchronize(run->ev);  // a handle freed early still lets the work finish
+    (void)hipEventDestroy(run->ev);
+    xe_resident *res = run->done ? nullptr : run->res;
+    delete run;
+    if (res) resident_done(res);  // its status is still checked (an error is reported here)
+    return 0;
+  }, -1);
+}
+
 int xe_ctx_synchronize(xe_ctx *ctx) {
   return guard([&]() -> int {
     XE_REQUIRE(ctx, "null ctx");

@@ -104,7 +104,21 @@ struct xe_ctx {
   void ensure_attn(size_t work_floats);
 };
 
+// A pending asynchronous submission: an event recorded on a stream after the
+// work (shim_run_*_start / shim_run_wait, xrt_shim.h:47-54).  For a resident
+// decode dispatch, `res` is checked once the event has completed.
+struct xe_resident;
+struct xe_run {
+  int ordinal = 0;
+  hipEvent_t ev = nullptr;
+  xe_resident *res = nullptr;
+  bool done = false;
+};
+
 namespace xe {
+
+// Completion work of a resident dispatch (its status word; decoder.hip).
+void resident_done(xe_resident *r);
 
 // ---------------------------------------------------------------------------
 // Kernel launch surfaces (implemented in gemv.hip / attn.hip)

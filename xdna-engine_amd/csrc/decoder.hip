@@ -334,6 +334,7 @@ struct xe_decoder {
   float *attn_work = nullptr;
   int attn_splits = 1;
   int32_t *host_tok = nullptr;  // pinned staging [max_ctx + 1][max_batch] x 2
+  int last_exec = XE_EXEC_GRAPH;  // executor of the last step launched (status messages)
   // persistent step kernel: one flag slot (128 B) per workgroup + status word
   unsigned int *step_flags = nullptr;
   unsigned int *step_status = nullptr;
@@ -1524,6 +1525,7 @@ void run_ll(xe_decoder *d, int B, int n_steps, const int32_t *forced, int n_forc
             uint64_t *trace = nullptr) {
   xe_decoder::LLPlan &P = ll_plan_for(d, B);
   XE_REQUIRE(P.ok, "low-latency executor unsupported here: " + P.why);
+  d->last_exec = XE_EXEC_LL;
   const auto &c = d->c;
   const bool gem = c.family == XE_GEMMA3, opt = c.family == XE_OPT;
   ll::StepParams sp{};
@@ -1564,7 +1566,14 @@ void run_ll(xe_decoder *d, int B, int n_steps, const int32_t *forced, int n_forc
   sp.status = d->step_status;
   int khz = 0;
   XE_HIP(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, d->dev->ordinal));
-  sp.limit = static_cast<uint64_t>(khz > 0 ? khz : 100000) * 50;  // 50 ms per wait
+  // 50 ms per wait; XE_WAIT_LIMIT_US overrides it and XE_LL_STALL_TEST=1
+  // makes the end-of-step wait expect an epoch that never comes (both for
+  // tests of the bounded-wait failure path)
+  const char *lim = std::getenv("XE_WAIT_LIMIT_US");
+  const double lim_us = lim ? std::max(1.0, std::atof(lim)) : 50000.0;
+  sp.limit = static_cast<uint64_t>(static_cast<double>(khz > 0 ? khz : 100000) * lim_us / 1000.0);
+  const char *stall = std::getenv("XE_LL_STALL_TEST");
+  sp.stall = (stall && std::atoi(stall) > 0) ? 1u : 0u;
   sp.kin_a = P.kin_a;
   sp.kin_f = P.kin_f;
   sp.scratch = P.scratch;
@@ -1626,6 +1635,7 @@ void run_step(xe_decoder *d, int B, uint64_t *trace = nullptr) {
     run_ll(d, B, 1, nullptr, 0, true);
     return;
   }
+  d->last_exec = XE_EXEC_PERSISTENT;
   xe_decoder::Plan &plan = plan_for(d, B);
   switch (exec_for(plan)) {
     case Exec::Persistent: {
@@ -1669,8 +1679,11 @@ void check_step_status(xe_decoder *d) {
   if (st) {
     XE_HIP(hipMemset(d->step_flags, 0, static_cast<size_t>(d->step_grid) * 128));
     XE_HIP(hipMemset(d->step_status, 0, 4));
-    fail(st == 2u ? "low-latency step kernel: GEMV tile not compiled (host/device tile menus differ); results are invalid"
-                  : "persistent step kernel: a phase barrier timed out (flags re-armed); results are invalid");
+    if (st == 2u)
+      fail("low-latency step kernel: GEMV tile not compiled (host/device tile menus differ); results are invalid");
+    fail(d->last_exec == XE_EXEC_LL
+             ? "low-latency step kernel: an exchange wait timed out (every workgroup stopped); results are invalid"
+             : "persistent step kernel: a phase barrier timed out (flags re-armed); results are invalid");
   }
 }
 
@@ -1901,6 +1914,33 @@ int xe_decoder_set_tensor(xe_decoder *d, int kind, int layer, const float *data,
   }, -1);
 }
 
+int xe_model_tensor_shape(const xe_model_config *cfg, int kind, int layer, int *rows, int *cols) {
+  try {
+    XE_REQUIRE(cfg, "null config");
+    XE_REQUIRE(layer >= -1 && layer < cfg->n_layers, "layer out of range");
+    Spec sp;
+    if (kind < 0 || kind >= XE_T_COUNT || !tensor_spec(*cfg, kind, layer, sp)) {
+      set_error("tensor kind not used by this model family");
+      return -1;
+    }
+    if (rows) *rows = sp.rows;
+    if (cols) *cols = sp.cols;
+    return 0;
+  } catch (const std::exception &e) {
+    set_error(e.what());
+    return -1;
+  }
+}
+
+int xe_decoder_config(xe_decoder *d, xe_model_config *out) {
+  if (!d || !out) {
+    set_error("null argument");
+    return -1;
+  }
+  *out = d->c;
+  return 0;
+}
+
 int xe_decoder_get_tensor_q8(xe_decoder *d, int kind, int layer, int8_t *q, float *scales) {
   return guard_d([&]() -> int {
     XE_REQUIRE(d && q && scales, "null argument");
@@ -1981,6 +2021,152 @@ int xe_decoder_step(xe_decoder *d, const int32_t *tokens, const int32_t *pos, in
     check_step_status(d);
     for (int b = 0; b < batch; b++) d->hpos[b] = pos[b] + 1;
     d->live = std::max(d->live, batch);
+    return 0;
+  }, -1);
+}
+
+// ---------------------------------------------------------------------------
+// Resident decode step (the reference's ElfResident: a constant program bound
+// once, per-token parameters written into a host-mapped scratchpad, then
+// dispatch -- npu-xrt/src/lib.rs:591-629, xrt_shim.h:95-111).  Here the
+// program is the decoder's step for one batch size (its HIP graph or the
+// low-latency kernel, built on first use and kept), the scratchpad is pinned
+// host memory holding tokens and positions, and dispatch copies them to the
+// device, launches the step and (dispatch) waits or (dispatch_start) returns
+// a run handle.
+// ---------------------------------------------------------------------------
+}  // extern "C"
+
+struct xe_resident {
+  xe_decoder *d = nullptr;
+  int batch = 0;
+  int32_t *stage = nullptr;  // pinned: tokens [batch] | positions [batch] | next [batch]
+  bool written = false;
+  bool in_flight = false;
+  int n_done = 0;            // completed dispatches
+};
+
+namespace xe {
+void resident_done(xe_resident *r) {
+  if (!r || !r->in_flight) return;
+  r->in_flight = false;
+  r->n_done++;
+  DeviceGuard dg(r->d->dev->ordinal);
+  check_step_status(r->d);
+}
+}  // namespace xe
+
+extern "C" {
+
+xe_resident *xe_resident_open(xe_decoder *d, int batch) {
+  return guard_d([&]() -> xe_resident * {
+    XE_REQUIRE(d, "null decoder");
+    XE_REQUIRE(batch >= 1 && batch <= d->max_batch, "batch out of range");
+    DeviceGuard dg(d->dev->ordinal);
+    auto *r = new xe_resident;
+    r->d = d;
+    r->batch = batch;
+    const hipError_t e = hipHostMalloc(reinterpret_cast<void **>(&r->stage), 3 * batch * sizeof(int32_t),
+                                       hipHostMallocDefault);
+    if (e != hipSuccess) {
+      delete r;
+      XE_HIP(e);
+    }
+    if (!use_ll(d, batch)) {  // capture the step graph once, now
+      xe_decoder::Plan &plan = plan_for(d, batch);
+      if (exec_for(plan) == Exec::Graph) (void)graph_for(d, plan);
+    }
+    return r;
+  }, nullptr);
+}
+
+void xe_resident_close(xe_resident *r) {
+  guard_d([&]() -> int {
+    if (!r) return 0;
+    DeviceGuard dg(r->d->dev->ordinal);
+    (void)hipStreamSynchronize(r->d->s);
+    (void)hipHostFree(r->stage);
+    delete r;
+    return 0;
+  }, -1);
+}
+
+int xe_resident_write(xe_resident *r, const int32_t *tokens, const int32_t *pos) {
+  return guard_d([&]() -> int {
+    XE_REQUIRE(r && tokens && pos, "null argument");
+    XE_REQUIRE(!r->in_flight, "a dispatch is in flight: wait for it before writing new parameters");
+    const auto &c = r->d->c;
+    for (int b = 0; b < r->batch; b++) {
+      XE_REQUIRE(tokens[b] >= 0 && tokens[b] < c.vocab, "token id out of range");
+      XE_REQUIRE(pos[b] >= 0 && pos[b] < c.max_ctx, "position out of range");
+      if (c.family != XE_GEMMA3) XE_REQUIRE(pos[b] < c.max_pos, "position beyond the table");
+    }
+    std::memcpy(r->stage, tokens, r->batch * 4);
+    std::memcpy(r->stage + r->batch, pos, r->batch * 4);
+    r->written = true;
+    return 0;
+  }, -1);
+}
+
+namespace {
+void resident_submit(xe_resident *r) {
+  XE_REQUIRE(r, "null resident step");
+  XE_REQUIRE(r->written, "xe_resident_write first");
+  XE_REQUIRE(!r->in_flight, "a dispatch is already in flight");
+  xe_decoder *d = r->d;
+  XE_REQUIRE(d->c.family != XE_WHISPER || d->cross_ready, "Whisper: set_cross first");
+  const int B = r->batch;
+  XE_HIP(hipMemcpyAsync(d->tokens, r->stage, B * 4, hipMemcpyHostToDevice, d->s));
+  XE_HIP(hipMemcpyAsync(d->pos, r->stage + B, B * 4, hipMemcpyHostToDevice, d->s));
+  run_step(d, B);
+  XE_HIP(hipMemcpyAsync(r->stage + 2 * B, d->next, B * 4, hipMemcpyDeviceToHost, d->s));
+  for (int b = 0; b < B; b++) d->hpos[b] = r->stage[B + b] + 1;
+  d->live = std::max(d->live, B);
+  r->in_flight = true;
+}
+}  // namespace
+
+int xe_resident_dispatch(xe_resident *r) {
+  return guard_d([&]() -> int {
+    DeviceGuard dg(r ? r->d->dev->ordinal : 0);
+    resident_submit(r);
+    XE_HIP(hipStreamSynchronize(r->d->s));
+    resident_done(r);
+    return 0;
+  }, -1);
+}
+
+xe_run *xe_resident_dispatch_start(xe_resident *r) {
+  return guard_d([&]() -> xe_run * {
+    DeviceGuard dg(r ? r->d->dev->ordinal : 0);
+    resident_submit(r);
+    auto *run = new xe_run;
+    run->ordinal = r->d->dev->ordinal;
+    run->res = r;
+    hipError_t e = hipEventCreateWithFlags(&run->ev, hipEventDisableTiming);
+    if (e == hipSuccess) e = hipEventRecord(run->ev, r->d->s);
+    if (e != hipSuccess) {
+      if (run->ev) (void)hipEventDestroy(run->ev);
+      delete run;
+      (void)hipStreamSynchronize(r->d->s);
+      r->in_flight = false;
+      XE_HIP(e);
+    }
+    return run;
+  }, nullptr);
+}
+
+int xe_resident_read(xe_resident *r, int32_t *next, float *logits) {
+  return guard_d([&]() -> int {
+    XE_REQUIRE(r, "null resident step");
+    XE_REQUIRE(!r->in_flight, "a dispatch is in flight: wait for its run first");
+    XE_REQUIRE(r->n_done > 0, "no completed dispatch");
+    if (next) std::memcpy(next, r->stage + 2 * r->batch, r->batch * 4);
+    if (logits) {
+      DeviceGuard dg(r->d->dev->ordinal);
+      XE_HIP(hipMemcpy(logits, r->d->logits, static_cast<size_t>(r->batch) * r->d->c.vocab * 4,
+                       hipMemcpyDeviceToHost));
+    }
     return 0;
   }, -1);
 }

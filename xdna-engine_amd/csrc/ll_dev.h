@@ -205,6 +205,10 @@ struct StepParams {
   unsigned ep0;  // epoch of step 0 (>= 1; buffers start at epoch 0)
   unsigned *status;
   uint64_t limit;  // wall-clock ticks a single wait may take
+  // failure-path test hook: the end-of-step argmax wait expects an epoch this
+  // many steps ahead, which never arrives, so every workgroup's wait runs
+  // into its limit and the launch stops the bounded way (0: off)
+  unsigned stall;
   // LDS layout (floats) of a role (A: attention side, F: FFN side):
   // residual [nb][d] | input [nb][kin] | scratch | weight stage [stage] |
   // key/value stage [kv_floats] (A) | trace marks

@@ -330,7 +330,7 @@ __global__ __launch_bounds__(kT) void ll_step_kernel(StepParams sp) {
       put(argv, b, 2 * static_cast<int>(blockIdx.x) + 1, __int_as_float(idx), ep);
     }
     // ---- every workgroup: the same argmax over all partials ----
-    ok = get(argv, nb, 2 * grid, scr, 2 * grid, ep, c);
+    ok = get(argv, nb, 2 * grid, scr, 2 * grid, ep + sp.stall, c);
     if (!ok) break;
     mark(step, tslots + 1);
 #pragma unroll

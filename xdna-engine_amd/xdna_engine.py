@@ -48,6 +48,9 @@ EXPORTS = [
     "xe_decoder_get_tensor_q8", "xe_decoder_reset", "xe_decoder_set_cross", "xe_decoder_step",
     "xe_decoder_generate", "xe_decoder_last_step_us", "xe_decoder_weight_bytes",
     "xe_decoder_feed", "xe_decoder_decode", "xe_decoder_profile_step", "xe_decoder_executor",
+    "xe_model_tensor_shape", "xe_decoder_config", "xe_decoder_load_safetensors", "xe_safetensors_plan",
+    "xe_ctx_record", "xe_run_query", "xe_run_wait", "xe_run_free", "xe_resident_open", "xe_resident_close",
+    "xe_resident_write", "xe_resident_dispatch", "xe_resident_dispatch_start", "xe_resident_read",
 ]
 
 
@@ -164,6 +167,20 @@ def lib():
         "xe_decoder_profile_step": (i, [vp, i, i, vp, vp, vp]),
         "xe_decoder_weight_bytes": (u64, [vp]),
         "xe_decoder_executor": (i, [vp, i]),
+        "xe_ctx_record": (vp, [vp]),
+        "xe_run_query": (i, [vp]),
+        "xe_run_wait": (i, [vp]),
+        "xe_run_free": (None, [vp]),
+        "xe_resident_open": (vp, [vp, i]),
+        "xe_resident_close": (None, [vp]),
+        "xe_resident_write": (i, [vp, vp, vp]),
+        "xe_resident_dispatch": (i, [vp]),
+        "xe_resident_dispatch_start": (vp, [vp]),
+        "xe_resident_read": (i, [vp, vp, vp]),
+        "xe_model_tensor_shape": (i, [C.POINTER(ModelConfig), i, i, C.POINTER(i), C.POINTER(i)]),
+        "xe_decoder_config": (i, [vp, C.POINTER(ModelConfig)]),
+        "xe_decoder_load_safetensors": (i, [vp, C.c_char_p]),
+        "xe_safetensors_plan": (i, [C.c_char_p, C.POINTER(ModelConfig), C.c_char_p, i]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name, None)
@@ -323,6 +340,10 @@ class CtxDecode:
     def synchronize(self):
         _check(lib().xe_ctx_synchronize(self.h))
 
+    def record(self):
+        """A run handle on the work queued so far (xe_ctx_record)."""
+        return Run(lib().xe_ctx_record(self.h))
+
     # -- registration (ctx_decode.rs:269-317, 566-612) --
     def register_weight(self, w, wdtype=XE_I8, layout=XE_LAYOUT_MK, bias=None):
         w = _f32(w)
@@ -459,6 +480,84 @@ class CtxDecode:
                                         hq, hkv, hd, max_ctx, scale, out_buf.ptr))
 
 
+class Run:
+    """An asynchronous submission (shim_run_* handles)."""
+
+    def __init__(self, h):
+        if not h:
+            raise XdnaError(last_error())
+        self.h = h
+
+    def query(self):
+        return _check(lib().xe_run_query(self.h)) == 1
+
+    def wait(self):
+        _check(lib().xe_run_wait(self.h))
+
+    def free(self):
+        if self.h:
+            lib().xe_run_free(self.h)
+            self.h = None
+
+
+class Resident:
+    """ElfResident: the decode step of `batch` streams, bound once."""
+
+    def __init__(self, dec, batch):
+        self.dec, self.batch = dec, batch
+        self.h = lib().xe_resident_open(dec.h, batch)
+        if not self.h:
+            raise XdnaError(last_error())
+
+    def write(self, tokens, pos):
+        t = np.ascontiguousarray(tokens, np.int32)
+        p = np.ascontiguousarray(pos, np.int32)
+        assert t.size == self.batch and p.size == self.batch
+        _check(lib().xe_resident_write(self.h, _p(t), _p(p)))
+
+    def dispatch(self):
+        _check(lib().xe_resident_dispatch(self.h))
+
+    def dispatch_start(self):
+        return Run(lib().xe_resident_dispatch_start(self.h))
+
+    def read(self, want_logits=False):
+        nxt = np.empty(self.batch, np.int32)
+        lg = np.empty((self.batch, self.dec.cfg.vocab), np.float32) if want_logits else None
+        _check(lib().xe_resident_read(self.h, _p(nxt), _p(lg)))
+        return nxt, lg
+
+    def close(self):
+        if self.h:
+            lib().xe_resident_close(self.h)
+            self.h = None
+
+
+def tensor_shape(cfg, kind, layer):
+    """(rows, cols) of tensor (kind, layer) of cfg, or None if the family has none."""
+    r, c = C.c_int(), C.c_int()
+    if lib().xe_model_tensor_shape(C.byref(cfg), kind, layer, C.byref(r), C.byref(c)) != 0:
+        return None
+    return r.value, c.value
+
+
+def safetensors_plan(path, cfg):
+    """Host-only dry run of the loader: {name: (kind, layer, transposed) or None}
+    and the naming ("arena" / "hf")."""
+    buf = C.create_string_buffer(1 << 20)
+    _check(lib().xe_safetensors_plan(os.fsencode(path), C.byref(cfg), buf, len(buf)))
+    lines = buf.value.decode().split("\n")
+    out = {}
+    for ln in lines[1:]:
+        name, _, rhs = ln.rpartition(" -> ")
+        if rhs == "skipped":
+            out[name] = None
+        else:
+            f = rhs.split()
+            out[name] = (int(f[0]), int(f[1]), len(f) > 2)
+    return lines[0], out
+
+
 class Decoder:
     """Decode backend: reset / precompute_cross / step / generate."""
 
@@ -480,6 +579,11 @@ class Decoder:
     def set_tensor(self, kind, layer, data):
         d = _f32(data).reshape(-1)
         _check(lib().xe_decoder_set_tensor(self.h, kind, layer, _p(d), d.size))
+
+    def load_safetensors(self, path):
+        """npu-weights arena / Hugging Face checkpoint -> the decoder's
+        weights; returns the number of tensors loaded."""
+        return _check(lib().xe_decoder_load_safetensors(self.h, os.fsencode(path)))
 
     def get_tensor_q8(self, kind, layer, rows, cols):
         q = np.empty((rows, cols), np.int8)
