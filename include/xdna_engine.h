@@ -128,6 +128,17 @@ void xe_ctx_reset_dispatches(xe_ctx *ctx);
  * opt125m_decode.rs:63-79; XE_BFP16; XE_BF16 RNE).  bias may be NULL. */
 xe_weight *xe_register_weight(xe_ctx *ctx, int wdtype, int m, int k,
                               const float *w, int layout, const float *bias);
+/* int8 quantisation rules of the reference:
+ *   XE_Q8_LIN  Lin::load (opt125m_decode.rs:45-62): fp32 scale amax/127,
+ *              round half away from zero (xe_register_weight's rule);
+ *   XE_Q8_ELF  the fused decode ELF's static rows (route_b_kernels/
+ *              decode_fused/gen_decode.py:158-165, 291-298): numpy round
+ *              half to even of w / (amax/127), the scale stored as bf16. */
+enum xe_q8_rule { XE_Q8_LIN = 0, XE_Q8_ELF = 1 };
+/* xe_register_weight with XE_I8 under the given rule (enum xe_q8_rule). */
+xe_weight *xe_register_weight_q8_rule(xe_ctx *ctx, int m, int k,
+                                      const float *w, int layout,
+                                      const float *bias, int rule);
 /* Pre-quantised int8 weight: q [m,k] row-major, scales [m] (fp32). */
 xe_weight *xe_register_weight_q8(xe_ctx *ctx, int m, int k, const int8_t *q,
                                  const float *scales, const float *bias);

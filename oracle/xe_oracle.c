@@ -211,6 +211,33 @@ void xo_quant_rows_i8(const float *w, int m, int k, int8_t *q, float *s) {
   }
 }
 
+/* qrow of the fused-decode generator (route_b_kernels/decode_fused/
+ * gen_decode.py:158-165) and w_or_i8 (:291-298): s = max|row| / 127 in fp32
+ * (1.0 for an all-zero row), q = numpy round (half to even) of w / s,
+ * clamped to +-127; the scale the GEMV output is multiplied by is stored as
+ * bf16 (`weights_to_write[...] = bf16(s)`), so s_out = bf16(s) while q uses
+ * the fp32 s. */
+void xo_quant_rows_i8_elf(const float *w, int m, int k, int8_t *q, float *s_out) {
+  for (int r = 0; r < m; r++) {
+    const float *row = w + (size_t)r * k;
+    float amax = 0.f;
+    for (int j = 0; j < k; j++) {
+      float v = fabsf(row[j]);
+      amax = v > amax ? v : amax;
+    }
+    float sc = amax / 127.0f;
+    if (!(sc > 0.0f)) sc = 1.0f;
+    for (int j = 0; j < k; j++) {
+      float v = rintf(row[j] / sc); /* round half to even (default mode) */
+      if (v != v) v = 0.0f;
+      if (v < -127.0f) v = -127.0f;
+      if (v > 127.0f) v = 127.0f;
+      q[(size_t)r * k + j] = (int8_t)v;
+    }
+    s_out[r] = xo_bf16_round(sc);
+  }
+}
+
 /* The reference's own layout: W [K,N], per-column scale
  * (opt125m_decode.rs:45-62 verbatim shape). */
 void xo_quant_cols_i8(const float *w_kn, int k, int n, int8_t *q_kn, float *s) {

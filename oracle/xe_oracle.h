@@ -55,6 +55,8 @@ float xo_quant_scale(const float *a, size_t n);
 void xo_quant_rows_i8(const float *w, int m, int k, int8_t *q, float *s);
 void xo_quant_cols_i8(const float *w_kn, int k, int n, int8_t *q_kn,
                       float *s);
+/* gen_decode.py qrow (:158-165): half-even rounding, bf16-stored scale. */
+void xo_quant_rows_i8_elf(const float *w, int m, int k, int8_t *q, float *s_out);
 void xo_dequant_epi(const int32_t *acc, int mp, int n, float scale_a,
                     const float *ws, const float *bias, float *out);
 

@@ -58,6 +58,7 @@ def lib():
         "xo_quant_scale": (C.c_float, [f32p, C.c_size_t]),
         "xo_quant_rows_i8": (None, [f32p, C.c_int, C.c_int, i8p, f32p]),
         "xo_quant_cols_i8": (None, [f32p, C.c_int, C.c_int, i8p, f32p]),
+        "xo_quant_rows_i8_elf": (None, [f32p, C.c_int, C.c_int, i8p, f32p]),
         "xo_dequant_epi": (None, [i32p, C.c_int, C.c_int, C.c_float, f32p, C.c_void_p, f32p]),
         "xo_gemv_i8": (None, [f32p, C.c_int, C.c_int, C.c_int, i8p, f32p, C.c_void_p, f32p]),
         "xo_gemv_i8_rowblocked": (None, [f32p, C.c_int, C.c_int, C.c_int, i8p, f32p, C.c_void_p, f32p]),
@@ -140,6 +141,16 @@ def quant_rows_i8(w):
     q = np.empty((m, k), np.int8)
     s = np.empty(m, np.float32)
     lib().xo_quant_rows_i8(w, m, k, q, s)
+    return q, s
+
+
+def quant_rows_i8_elf(w):
+    """gen_decode.py qrow: half-even rounding, scale stored as bf16."""
+    w = np.ascontiguousarray(w, np.float32)
+    m, k = w.shape
+    q = np.empty((m, k), np.int8)
+    s = np.empty(m, np.float32)
+    lib().xo_quant_rows_i8_elf(w, m, k, q, s)
     return q, s
 
 

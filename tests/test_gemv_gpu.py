@@ -360,3 +360,24 @@ def test_gemv_int4_fp32_registration_and_fused_ln(gpu, xe):
     q, s = O.quant_rows_i4(wf)
     want = O.gemv_i4(O.norm_rows(x, 1, gamma, beta, 1e-5), q, s)
     close(got, want)
+
+
+@pytest.mark.parametrize("rule", ["lin", "elf"])
+def test_int8_quant_rules(gpu, xe, rule):
+    """xe_register_weight_q8_rule: Lin::load's rule (half away, fp32 scale)
+    or the fused ELF's qrow (half even, bf16 scale, gen_decode.py:158-165);
+    the stored codes and scales are the oracle's, and the GEMV with bias
+    matches the oracle's on them."""
+    dev, ctx = gpu
+    rng = np.random.default_rng(44)
+    m, k = 2304, 768
+    wf = (rng.standard_normal((m, k)) * 0.02).astype(np.float32)
+    wf[7, :4] = [0.5, 1.5, 2.5, 127.0]  # exact ties at scale 1.0
+    bias = rng.normal(0.0, 0.1, m).astype(np.float32)
+    x = rng.standard_normal((2, k)).astype(np.float32)
+    code = xe.XE_Q8_LIN if rule == "lin" else xe.XE_Q8_ELF
+    w = ctx.register_weight_q8_rule(wf, code, bias=bias)
+    got = ctx.gemv(w, x)
+    w.free()
+    q, s = O.quant_rows_i8(wf) if rule == "lin" else O.quant_rows_i8_elf(wf)
+    close(got, O.gemv_i8(x, q, s, bias))

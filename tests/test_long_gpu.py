@@ -241,3 +241,16 @@ def test_config3_ctx32768_device(gpu, xe, hq, hkv, hd, b):
     finally:
         kb.free()
         vb.free()
+
+
+# The low-latency plan's A/B switches, each against the oracle on the bench's
+# plan shapes (a fresh decoder per setting: the plan is built at first use).
+LL_KNOBS = [("XE_LL_FFN_SPLIT", "0"), ("XE_LL_TAIL", "0"), ("XE_LL_TAIL", "2"),
+            ("XE_LL_STAGE", "0"), ("XE_LL_KV", "0")]
+
+
+@pytest.mark.parametrize("knob,value", LL_KNOBS)
+def test_ll_plan_switches(gpu, xe, default_executor, monkeypatch, knob, value):
+    monkeypatch.setenv(knob, value)
+    run_pair(xe, gpu, gemma_long(xe), seed=6, batch=1, n_prompt=300, n_new=40,
+             label="gemma-ll-%s=%s" % (knob, value), want_exec="ll", logit_steps=1, prompt_seed=9)

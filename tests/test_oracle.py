@@ -242,6 +242,29 @@ def test_w8a8_int32_bruteforce_and_dequant_order():
     assert not np.array_equal(want.astype(np.float32), other.astype(np.float32))
 
 
+def test_quant_rows_elf_is_numpy_qrow():
+    """gen_decode.py:158-165 qrow is numpy code: its own operations (float32
+    max / 127, np.round half-to-even, clip), then the scale through the
+    reference's bf16 RNE (npu-xrt/src/lib.rs:809-817, pinned above) --
+    equal bit for bit; exact ties decide the rounding mode."""
+    rng = np.random.default_rng(31)
+    w = (rng.standard_normal((40, 96)) * 0.02).astype(np.float32)
+    w[3] = 0.0
+    # exact ties: amax 127 -> scale 1.0 (row 5), values k + 0.5
+    w[5, :8] = [127.0, 0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 3.5]
+    q, s = O.quant_rows_i8_elf(w)
+    m = w.astype(np.float32)
+    s32 = (np.abs(m).max(axis=1) / 127.0).astype(np.float32)
+    s32 = np.where(s32 > 0, s32, np.float32(1.0)).astype(np.float32)
+    want_q = np.clip(np.round(m / s32[:, None]), -127, 127).astype(np.int8)
+    assert np.array_equal(q, want_q)
+    assert np.array_equal(s, O.bf16_to_f32(O.bf16_bits(s32)))
+    assert q[5, :8].tolist() == [127, 0, 2, 2, 0, -2, -2, 4]      # half to even
+    lin_q, _ = O.quant_rows_i8(w)
+    assert lin_q[5, :8].tolist() == [127, 1, 2, 3, -1, -2, -3, 4]  # Lin: half away (differs)
+    assert s[3] == 1.0 and not q[3].any()
+
+
 # -------------------------------------------------------------- int4 ----
 
 def test_i4_quant_nibbles_and_scales_closed_form():

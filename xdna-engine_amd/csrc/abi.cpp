@@ -577,6 +577,34 @@ xe_weight *xe_register_weight_q8(xe_ctx *ctx, int m, int k, const int8_t *q, con
   }, nullptr);
 }
 
+xe_weight *xe_register_weight_q8_rule(xe_ctx *ctx, int m, int k, const float *w, int layout,
+                                      const float *bias, int rule) {
+  return guard([&]() -> xe_weight * {
+    XE_REQUIRE(w, "null weight");
+    XE_REQUIRE(rule == XE_Q8_LIN || rule == XE_Q8_ELF, "unknown int8 quantisation rule");
+    DeviceGuard dg(ctx ? ctx->dev->ordinal : 0);
+    xe_weight *wt = new_weight(ctx, XE_I8, m, k);
+    try {
+      std::vector<float> mk = to_mk(w, m, k, layout);
+      if (rule == XE_Q8_LIN) {
+        fill_weight_from_f32(wt, mk.data(), bias);
+      } else {
+        hipStream_t s = ctx->dev->stream;
+        std::vector<int8_t> q(mk.size());
+        std::vector<float> sc(m);
+        quant_rows_i8_elf(mk.data(), m, k, q.data(), sc.data());
+        wt->w = dev_upload(q.data(), q.size(), s);
+        wt->scale = dev_upload(sc.data(), m, s);
+        if (bias) wt->bias = dev_upload(bias, m, s);
+      }
+    } catch (...) {
+      free_weight(wt);
+      throw;
+    }
+    return wt;
+  }, nullptr);
+}
+
 xe_weight *xe_register_weight_q4(xe_ctx *ctx, int m, int k, const uint8_t *packed, const float *scales,
                                  const float *bias) {
   return guard([&]() -> xe_weight * {

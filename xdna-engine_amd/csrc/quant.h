@@ -67,6 +67,30 @@ inline void quant_rows_i8(const float *w, int m, int k, int8_t *q, float *s) {
   }
 }
 
+// qrow of route_b_kernels/decode_fused/gen_decode.py:158-165 (the fused
+// decode ELF's static int8 rows): fp32 s = max|row| / 127 (1.0 for an all-zero
+// row), q = round half to even of w / s, clamped to +-127; the scale applied
+// to the GEMV output is stored as bf16 (w_or_i8, :291-298).
+inline void quant_rows_i8_elf(const float *w, int m, int k, int8_t *q, float *s) {
+  for (int r = 0; r < m; r++) {
+    const float *row = w + static_cast<size_t>(r) * k;
+    float amax = 0.f;
+    for (int j = 0; j < k; j++) {
+      const float v = std::fabs(row[j]);
+      amax = v > amax ? v : amax;
+    }
+    float sc = amax / 127.0f;
+    if (!(sc > 0.0f)) sc = 1.0f;
+    for (int j = 0; j < k; j++) {
+      float v = std::nearbyint(row[j] / sc);
+      if (v != v) v = 0.0f;
+      v = v < -127.0f ? -127.0f : (v > 127.0f ? 127.0f : v);
+      q[static_cast<size_t>(r) * k + j] = static_cast<int8_t>(v);
+    }
+    s[r] = bf16_round(sc);
+  }
+}
+
 inline void quant_rows_i4(const float *w, int m, int k, uint8_t *packed, float *s) {
   for (int r = 0; r < m; r++) {
     const float *row = w + static_cast<size_t>(r) * k;

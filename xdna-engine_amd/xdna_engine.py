@@ -26,6 +26,7 @@ LIB_PATH = os.path.join(HERE, "libxdna_engine.so")
 
 XE_F32, XE_BF16, XE_I8, XE_BFP16, XE_I32, XE_I4 = 0, 1, 2, 3, 4, 5
 XE_EPI_NONE, XE_EPI_BIAS, XE_EPI_SILU_BIAS = 0, 1, 2
+XE_Q8_LIN, XE_Q8_ELF = 0, 1
 XE_NORM_NONE, XE_NORM_LN, XE_NORM_RMS, XE_NORM_RMS1P = 0, 1, 2, 3
 XE_LAYOUT_MK, XE_LAYOUT_KN = 0, 1
 XE_OPT, XE_WHISPER, XE_GEMMA3 = 0, 1, 2
@@ -38,7 +39,7 @@ EXPORTS = [
     "xe_probe_attn", "xe_ctx_create",
     "xe_ctx_destroy",
     "xe_ctx_dispatches", "xe_ctx_reset_dispatches", "xe_register_weight",
-    "xe_register_weight_q8", "xe_register_weight_q4", "xe_register_weight_q4_kn",
+    "xe_register_weight_q8", "xe_register_weight_q4", "xe_register_weight_q4_kn", "xe_register_weight_q8_rule",
     "xe_register_weight_bfp16", "xe_register_weight_bf16",
     "xe_register_fused", "xe_weight_set_norm", "xe_weight_free", "xe_weight_shape", "xe_gemv",
     "xe_fused_norm_gemv", "xe_gemv_dev", "xe_gemv_i8act", "xe_gemv_i8act_dev", "xe_w8a8_linear",
@@ -136,6 +137,7 @@ def lib():
         "xe_register_weight_q8": (vp, [vp, i, i, vp, vp, vp]),
         "xe_register_weight_bfp16": (vp, [vp, i, i, vp, vp, vp]),
         "xe_register_weight_q4": (vp, [vp, i, i, vp, vp, vp]),
+        "xe_register_weight_q8_rule": (vp, [vp, i, i, vp, i, vp, i]),
         "xe_register_weight_q4_kn": (vp, [vp, i, i, vp, vp, vp]),
         "xe_register_weight_bf16": (vp, [vp, i, i, vp, vp]),
         "xe_register_fused": (vp, [vp, i, i, i, vp, i, i, vp, vp, f, vp]),
@@ -356,6 +358,14 @@ class CtxDecode:
         s, b = _f32(scales), _f32(bias)
         m, k = q.shape
         return Weight(lib().xe_register_weight_q8(self.h, m, k, _p(q), _p(s), _p(b)))
+
+    def register_weight_q8_rule(self, w, rule, layout=XE_LAYOUT_MK, bias=None):
+        """int8 under a reference rule: XE_Q8_LIN (Lin::load) or XE_Q8_ELF
+        (gen_decode.py qrow: half-even, bf16 scale)."""
+        w = _f32(w)
+        m, k = (w.shape if layout == XE_LAYOUT_MK else w.shape[::-1])
+        b = _f32(bias)
+        return Weight(lib().xe_register_weight_q8_rule(self.h, m, k, _p(w), layout, _p(b), rule))
 
     def register_weight_q4(self, packed, scales, bias=None):
         """int4 [m, k/2] packed along k (opt125m_decode.rs:63-105 codes)."""
