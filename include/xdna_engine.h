@@ -404,6 +404,15 @@ int xe_decoder_reset(xe_decoder *dec);
 /* precompute_cross (whisper_decoder.rs:1143-1232): enc [n_cross, d] fp32, or
  * NULL to use the synthetic XE_T_ENC_OUT tensor of the last init. */
 int xe_decoder_set_cross(xe_decoder *dec, const float *enc);
+/* Per-utterance int8 cross K and/or V (the fused decode ELF's int8_cross_k /
+ * int8_cross_v, whisper_decoder.rs:951-960, quantised as :1186-1219 and
+ * applied as route_b_kernels/decode_fused/gen_decode.py:263-282): channel
+ * scale s = max_t|x| / 127, q = round(x / s); scores use q * s_k, the
+ * attention output is scaled by s_v.  Half the cross-attention bytes per
+ * token.  Takes effect at the next xe_decoder_set_cross (call it again
+ * after switching); such a decoder steps on the phase kernels (graph
+ * executor). */
+int xe_decoder_set_cross_int8(xe_decoder *dec, int k_int8, int v_int8);
 /* step(tok, pos) -> logits (whisper_decoder.rs:1293-1349) for `batch`
  * streams with per-stream positions.  logits [batch, vocab] may be NULL;
  * next [batch] receives the greedy token (argmax with the family's tie

@@ -939,6 +939,10 @@ struct xo_model {
    * (opt125m_decode.rs:263-268, whisper_decoder.rs:458, 472). */
   int kv_f32;
   float *kcf, *vcf, *xkf, *xvf;
+  /* int8 cross K/V [L][h][n_cross][hd] + channel scales [L][h * hd] */
+  int cross_i8k, cross_i8v;
+  int8_t *xk8, *xv8;
+  float *xks, *xvs;
   int mutation; /* XO_MUT_*: a planted composition mistake (tests only) */
   int kouter;   /* int8 linears through the reference's k-outer [K, N] loop */
 };
@@ -1072,6 +1076,7 @@ void xo_model_free(xo_model *m) {
     }
   free(m->kc); free(m->vc); free(m->xk); free(m->xv);
   free(m->kcf); free(m->vcf); free(m->xkf); free(m->xvf);
+  free(m->xk8); free(m->xv8); free(m->xks); free(m->xvs);
   free(m->rope_cos); free(m->rope_sin);
   free(m);
 }
@@ -1204,6 +1209,34 @@ int xo_model_prime_kv(xo_model *m, int b, int n_pos, uint64_t seed) {
   return 0;
 }
 
+void xo_quant_cross_i8(const float *x, int T, int H, int hd, int8_t *q, float *s) {
+  int D = H * hd;
+  for (int c = 0; c < D; c++) s[c] = 0.0f;
+  for (int t = 0; t < T; t++)
+    for (int c = 0; c < D; c++) {
+      float a = fabsf(x[(size_t)t * D + c]);
+      if (a > s[c]) s[c] = a;
+    }
+  /* headroom 1.0 (the default of INT8_CK_HEADROOM / INT8_CV_HEADROOM) */
+  for (int c = 0; c < D; c++) s[c] = s[c] > 0.0f ? s[c] * 1.0f / 127.0f : 1.0f;
+  for (int t = 0; t < T; t++)
+    for (int h = 0; h < H; h++)
+      for (int d = 0; d < hd; d++) {
+        int c = h * hd + d;
+        float inv = s[c] != 0.0f ? 1.0f / s[c] : 0.0f;
+        float r = roundf(x[(size_t)t * D + c] * inv); /* Rust round(): half away from zero */
+        r = r != r ? 0.0f : r < -127.0f ? -127.0f : r > 127.0f ? 127.0f : r; /* NaN -> 0 (`as i8`) */
+        q[((size_t)h * T + t) * hd + d] = (int8_t)r;
+      }
+}
+
+int xo_model_set_cross_i8(xo_model *m, int k_int8, int v_int8) {
+  if (m->c.family != XE_WHISPER) return -1;
+  m->cross_i8k = k_int8 ? 1 : 0;
+  m->cross_i8v = v_int8 ? 1 : 0;
+  return 0;
+}
+
 int xo_model_set_cross(xo_model *m, const float *enc) {
   if (m->c.family != XE_WHISPER) return -1;
   int Tn = m->c.n_cross, D = m->c.d_model, H = m->c.n_heads, hd = m->c.head_dim, L = m->c.n_layers;
@@ -1239,8 +1272,63 @@ int xo_model_set_cross(xo_model *m, const float *enc) {
         }
     }
   }
+  /* per-utterance int8 (whisper_decoder.rs:1186-1219): from the fp32
+   * projections, not from the bf16 copies */
+  free(m->xk8); free(m->xv8); free(m->xks); free(m->xvs);
+  m->xk8 = m->xv8 = NULL;
+  m->xks = m->xvs = NULL;
+  if (m->cross_i8k || m->cross_i8v) {
+    float *kf = (float *)malloc((size_t)Tn * D * 4), *vf = (float *)malloc((size_t)Tn * D * 4);
+    if (m->cross_i8k) {
+      m->xk8 = (int8_t *)malloc((size_t)L * Tn * D);
+      m->xks = (float *)malloc((size_t)L * D * 4);
+    }
+    if (m->cross_i8v) {
+      m->xv8 = (int8_t *)malloc((size_t)L * Tn * D);
+      m->xvs = (float *)malloc((size_t)L * D * 4);
+    }
+    for (int l = 0; l < L; l++) {
+#pragma omp parallel for schedule(static)
+      for (int t = 0; t < Tn; t++) {
+        xo_lin(m, XE_T_XK_W, l, -1, e + (size_t)t * D, kf + (size_t)t * D);
+        xo_lin(m, XE_T_XV_W, l, XE_T_XV_B, e + (size_t)t * D, vf + (size_t)t * D);
+      }
+      if (m->xk8) xo_quant_cross_i8(kf, Tn, H, hd, m->xk8 + (size_t)l * Tn * D, m->xks + (size_t)l * D);
+      if (m->xv8) xo_quant_cross_i8(vf, Tn, H, hd, m->xv8 + (size_t)l * Tn * D, m->xvs + (size_t)l * D);
+    }
+    free(kf);
+    free(vf);
+  }
   free(e);
   return 0;
+}
+
+void xo_head_attend_x8(const float *qh, const int8_t *k8, const float *sk, const uint16_t *kb,
+                       const int8_t *v8, const float *sv, const uint16_t *vb, int len, int hd,
+                       float scale, float *sc, float *oh) {
+  float qs[1024];
+  for (int d = 0; d < hd; d++) qs[d] = k8 ? qh[d] * sk[d] : qh[d];
+  for (int j = 0; j < len; j++) {
+    float dot = 0.f;
+    for (int d = 0; d < hd; d++)
+      dot += qs[d] * (k8 ? (float)k8[(size_t)j * hd + d] : xo_bf16_bits_to_f32(kb[(size_t)j * hd + d]));
+    sc[j] = dot * scale;
+  }
+  float mx = -INFINITY;
+  for (int j = 0; j < len; j++) mx = fmaxf(mx, sc[j]);
+  float sum = 0.f;
+  for (int j = 0; j < len; j++) {
+    sc[j] = expf(sc[j] - mx);
+    sum += sc[j];
+  }
+  float inv = 1.0f / sum;
+  for (int j = 0; j < len; j++) sc[j] = sc[j] * inv;
+  for (int d = 0; d < hd; d++) {
+    float acc = 0.f;
+    for (int j = 0; j < len; j++)
+      acc += sc[j] * (v8 ? (float)v8[(size_t)j * hd + d] : xo_bf16_bits_to_f32(vb[(size_t)j * hd + d]));
+    oh[d] = v8 ? acc * sv[d] : acc;
+  }
 }
 
 static void xo_rope_apply(const xo_model *m, float *v, int pos) {
@@ -1352,9 +1440,9 @@ static void xo_head_attend(const float *qh, const uint16_t *kb, const uint16_t *
  * Whisper: HostDecoder::step host path (whisper_decoder.rs:401-535).
  * Gemma-3: HF Gemma3DecoderLayer built from rmsnorm_ref / geglu_ref
  * (npu-gemma/src/lib.rs:55-77) and GEMMA3_1B (config.rs:156-170) with the
- * BASELINE simplification of one RoPE theta and global attention
- * (parity unpinned beyond those primitives: the reference has no Gemma
- * decode loop, npu-gemma/src/lib.rs:9-15).
+ * BASELINE simplification of one RoPE theta and global attention (the
+ * reference has no Gemma decode loop, npu-gemma/src/lib.rs:9-15; the
+ * composition is checked against Hugging Face's Gemma3ForCausalLM).
  * Numerics of the build, applied identically on the GPU: fp32 activations,
  * weights as stored (int8 per-row scale / bf16 / bfp16), K/V rounded to
  * bf16 when written to the cache, tied quantised embedding for the lm-head. */
@@ -1448,7 +1536,12 @@ static void xo_step_one(xo_model *m, int b, int tok, int pos, float *logits) {
       float xscale = m->mutation == XO_MUT_WHISPER_CROSS_SCALE ? 1.0f : scale;
       for (int hh = 0; hh < H; hh++) {
         size_t base = ((size_t)l * H + hh) * Tn * hd;
-        if (m->kv_f32)
+        if (m->xk8 || m->xv8)
+          xo_head_attend_x8(q + hh * hd, m->xk8 ? m->xk8 + base : NULL,
+                            m->xks ? m->xks + (size_t)l * D + hh * hd : NULL, m->xk + base,
+                            m->xv8 ? m->xv8 + base : NULL, m->xvs ? m->xvs + (size_t)l * D + hh * hd : NULL,
+                            m->xv + base, Tn, hd, xscale, sc, ctx + hh * hd);
+        else if (m->kv_f32)
           xo_head_attend(q + hh * hd, NULL, NULL, m->xkf + base, m->xvf + base, Tn, hd, xscale, 0,
                          sc, ctx + hh * hd);
         else

@@ -161,8 +161,23 @@ int xo_model_set_mutation(xo_model *m, int code);
 int xo_model_set_kouter(xo_model *m, int on);
 /* Synthetic bf16 K/V rows [0, n_pos) for stream b (timing at long contexts). */
 int xo_model_prime_kv(xo_model *m, int b, int n_pos, uint64_t seed);
+/* int8 per-utterance cross K and/or V (the fused decode ELF's int8_cross_k /
+ * int8_cross_v); takes effect at the next xo_model_set_cross. */
+int xo_model_set_cross_i8(xo_model *m, int k_int8, int v_int8);
 /* enc [n_cross, d]; NULL = the synthetic XE_T_ENC_OUT tensor. */
 int xo_model_set_cross(xo_model *m, const float *enc);
+/* Per-channel int8 of one layer's cross K or V (whisper_decoder.rs:1186-1219,
+ * write_buf_i8 :1110-1134): x fp32 [T, H*hd] (the projection's rows), channel
+ * (h, d) scale s = max_t |x| / 127 (1.0 for an all-zero channel), q = clamp(
+ * round_half_away(x * (1/s)), -127, 127) stored head-major [H, T, hd]. */
+void xo_quant_cross_i8(const float *x, int T, int H, int hd, int8_t *q, float *s);
+/* One head's attention over int8 and/or bf16 cross K/V: with k8, scores
+ * (sum_d (q[d] s_k[d]) k8[t][d]) * scale (gen_decode.py:263-272: the channel
+ * scale applied to q); with v8, out[d] = s_v[d] * sum_t p_t v8[t][d]
+ * (:273-279: applied after the sum); kb / vb (bf16) otherwise. */
+void xo_head_attend_x8(const float *qh, const int8_t *k8, const float *sk, const uint16_t *kb,
+                       const int8_t *v8, const float *sv, const uint16_t *vb, int len, int hd,
+                       float scale, float *sc, float *oh);
 /* One step for every stream b < batch: tokens[b] at pos[b]. */
 void xo_model_step(xo_model *m, const int *tokens, const int *pos, int batch,
                    float *logits);

@@ -100,6 +100,10 @@ def lib():
         "xo_model_set_kouter": (C.c_int, [C.c_void_p, C.c_int]),
         "xo_model_prime_kv": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_uint64]),
         "xo_model_set_cross": (C.c_int, [C.c_void_p, C.c_void_p]),
+        "xo_model_set_cross_i8": (C.c_int, [C.c_void_p, C.c_int, C.c_int]),
+        "xo_quant_cross_i8": (None, [f32p, C.c_int, C.c_int, C.c_int, i8p, f32p]),
+        "xo_head_attend_x8": (None, [f32p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
+                                     C.c_void_p, C.c_int, C.c_int, C.c_float, f32p, f32p]),
         "xo_model_step": (None, [C.c_void_p, i32p, i32p, C.c_int, f32p]),
         "xo_model_argmax": (C.c_int, [C.c_void_p, f32p]),
         "xo_model_tensor_numel": (C.c_size_t, [C.c_void_p, C.c_int, C.c_int]),
@@ -152,6 +156,29 @@ def quant_rows_i8_elf(w):
     s = np.empty(m, np.float32)
     lib().xo_quant_rows_i8_elf(w, m, k, q, s)
     return q, s
+
+
+def quant_cross_i8(x, heads, hd):
+    """Per-channel int8 of one layer's cross K or V (whisper_decoder.rs:1186-1219):
+    x fp32 [T, heads*hd] -> q int8 [heads, T, hd], scales [heads*hd]."""
+    x = np.ascontiguousarray(x, np.float32)
+    t = x.shape[0]
+    q = np.empty((heads, t, hd), np.int8)
+    s = np.empty(heads * hd, np.float32)
+    lib().xo_quant_cross_i8(x, t, heads, hd, q, s)
+    return q, s
+
+
+def head_attend_x8(q, scale, k8=None, sk=None, kb=None, v8=None, sv=None, vb=None):
+    """One head over int8 (with channel scales) and/or bf16 keys / values [T, hd]."""
+    q = np.ascontiguousarray(q, np.float32)
+    hd = q.shape[0]
+    arrs = [None if a is None else np.ascontiguousarray(a) for a in (k8, sk, kb, v8, sv, vb)]
+    t = next(a.shape[0] for a in (arrs[0], arrs[2]) if a is not None)
+    sc = np.empty(t, np.float32)
+    out = np.empty(hd, np.float32)
+    lib().xo_head_attend_x8(q, *[ptr(a) for a in arrs], t, hd, scale, sc, out)
+    return out
 
 
 def gemv_i8(x, q, s, bias=None):
@@ -354,6 +381,10 @@ class OracleModel:
     def set_kv_f32(self, on=True):
         """fp32 K/V caches (the reference CPU decoders' choice) instead of bf16."""
         assert lib().xo_model_set_kv_f32(self.h, 1 if on else 0) == 0
+
+    def set_cross_i8(self, k_int8=True, v_int8=True):
+        """int8 per-utterance cross K / V from the next set_cross on."""
+        assert lib().xo_model_set_cross_i8(self.h, int(bool(k_int8)), int(bool(v_int8))) == 0
 
     def set_cross(self, enc=None):
         e = None if enc is None else np.ascontiguousarray(enc, np.float32)

@@ -19,7 +19,7 @@ import numpy as np
 import pytest
 
 import oracle_lib as O
-from parity_util import greedy_identity
+from parity_util import compare_logits, greedy_identity
 
 pytestmark = pytest.mark.gpu
 
@@ -161,6 +161,72 @@ def test_whisper_small_short(gpu, xe, executor):
     pr = prompts(cfg, 1, 4, seed=1)
     got = dec.generate(pr, 12)
     greedy_identity(got, om, pr, "whisper-small", eps=5e-3)
+    dec.close()
+    om.close()
+
+
+# ---- per-utterance int8 cross K / V (gen_decode.py:263-282) ----
+
+@pytest.mark.parametrize("k8,v8", [(1, 0), (0, 1), (1, 1)])
+def test_whisper_int8_cross_kv(gpu, xe, k8, v8):
+    """int8 cross K and/or V with per-channel scales, quantised on the GPU
+    from the fp32 projections (whisper_decoder.rs:1186-1219) and read by the
+    phase kernels: step logits and a greedy stream against the oracle with
+    the same quantisation; the decoder runs the graph executor."""
+    dev, _ = gpu
+    cfg = tiny(xe, xe.XE_WHISPER, xe.XE_I8)
+    print("[case] tiny whisper int8 cross k=%d v=%d" % (k8, v8), flush=True)
+    dec = xe.Decoder(dev, cfg, max_batch=2)
+    dec.init_synthetic(9)
+    dec.set_cross_int8(k8, v8)
+    dec.precompute_cross(None)
+    assert dec.executor(1) == "graph" and dec.executor(2) == "graph"
+    om = O.OracleModel(oracle_cfg(cfg), 9, 2)
+    om.set_cross_i8(k8, v8)
+    om.set_cross(None)
+    rng = np.random.default_rng(5)
+    for p in range(8):
+        toks = rng.integers(0, cfg.vocab, 2).astype(np.int32)
+        pos = np.array([p, p + 3], np.int32)
+        got, nxt = dec.step(toks, pos)
+        want = om.step(toks, pos)
+        compare_logits(got, want, "whisper-int8-cross-k%d-v%d-step%d" % (k8, v8, p))
+    om.close()
+    dec.reset()
+    pr = prompts(cfg, 2, 4, seed=6)
+    got = dec.generate(pr, 30)
+    om = O.OracleModel(oracle_cfg(cfg), 9, 2)
+    om.set_cross_i8(k8, v8)
+    om.set_cross(None)
+    greedy_identity(got, om, pr, "whisper-int8-cross-k%d-v%d" % (k8, v8))
+    om.close()
+    # back to bf16 cross K / V: the low-latency executor again, oracle's stream
+    dec.set_cross_int8(0, 0)
+    dec.precompute_cross(None)
+    dec.reset()
+    got = dec.generate(pr[:1], 12)
+    om = O.OracleModel(oracle_cfg(cfg), 9, 1)
+    om.set_cross(None)
+    greedy_identity(got, om, pr[:1], "whisper-bf16-cross-after-int8")
+    om.close()
+    dec.close()
+
+
+def test_whisper_small_int8_cross(gpu, xe):
+    """Config 4 shape (Whisper-small, 1500 frames) with int8 cross K and V:
+    a short greedy stream against the oracle."""
+    dev, _ = gpu
+    cfg = xe.WHISPER_SMALL
+    dec = xe.Decoder(dev, cfg, max_batch=1)
+    dec.init_synthetic(1)
+    dec.set_cross_int8(1, 1)
+    dec.precompute_cross(None)
+    om = O.OracleModel(oracle_cfg(cfg), 1, 1)
+    om.set_cross_i8(1, 1)
+    om.set_cross(None)
+    pr = prompts(cfg, 1, 4, seed=1)
+    got = dec.generate(pr, 12)
+    greedy_identity(got, om, pr, "whisper-small-int8-cross", eps=5e-3)
     dec.close()
     om.close()
 

@@ -530,3 +530,89 @@ def test_synth_statistics_and_determinism():
     # element i depends only on (seed, tensor, i)
     base = L().xo_synth_base(7, 1234)
     assert all(L().xo_synth_value(base, i, 0.0, 0.02) == a[i] for i in (0, 1, 99_999, 399_999))
+
+
+# ---- int8 per-utterance cross K/V (whisper_decoder.rs:1186-1219,
+# write_buf_i8 :1110-1134; kernel side gen_decode.py:263-282) ----
+
+def test_cross_i8_quant_scale_rounding_and_layout():
+    """Channel (h, d) scale = max_t |x| / 127; Rust round() is half away from
+    zero (a half-even rint would give 2, -2, 0, -126 below); a zero channel
+    gets scale 1 and zeros; NaN stores 0; output is head-major [H, T, hd]."""
+    T, H, hd = 6, 2, 4
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((T, H * hd)).astype(np.float32)
+    x[:, 0] = [2.5, -2.5, 0.5, -126.5, 127.0, 1.0]   # max 127: scale 1, inverse 1
+    x[:, 1] = 0.0
+    x[2, 5] = np.nan
+    q, s = O.quant_cross_i8(x, H, hd)
+    assert q.shape == (H, T, hd)
+    assert s[0] == np.float32(1.0)
+    assert list(q[0, :, 0]) == [3, -3, 1, -127, 127, 1]
+    assert s[1] == 1.0 and not q[0, :, 1].any()
+    assert q[1, 2, 1] == 0  # NaN
+    for c in range(2, H * hd):
+        h, d = divmod(c, hd)
+        col = x[:, c].astype(np.float64)
+        if c == 5:
+            col = np.where(np.isnan(col), 0.0, col)
+        amax = np.max(np.abs(col))
+        assert s[c] == np.float32(np.float32(amax) / np.float32(127.0))
+        qc = q[h, :, d].astype(np.float64)
+        assert np.max(np.abs(qc)) == 127                      # the channel max maps to +-127
+        ok = ~np.isnan(x[:, c])
+        assert np.all(np.abs(qc[ok] * s[c] - col[ok]) <= s[c] * (0.5 + 1e-6))  # half a step
+
+
+def test_cross_i8_attention_identities():
+    """int8 K scores use q * s_k, int8 V outputs are scaled by s_v: against a
+    float64 attention over the dequantised K / V, and the one-key closed form
+    (the output is the key's value row)."""
+    T, hd = 37, 64
+    rng = np.random.default_rng(4)
+    kf = rng.standard_normal((T, hd)).astype(np.float32)
+    vf = rng.standard_normal((T, hd)).astype(np.float32) * 3
+    k8, sk = O.quant_cross_i8(kf, 1, hd)
+    v8, sv = O.quant_cross_i8(vf, 1, hd)
+    k8, v8 = k8[0], v8[0]
+    q = rng.standard_normal(hd).astype(np.float32)
+    scale = 1.0 / 8.0
+    kd = k8.astype(np.float64) * sk.astype(np.float64)
+    vd = v8.astype(np.float64) * sv.astype(np.float64)
+    sc = kd @ q.astype(np.float64) * scale
+    p = np.exp(sc - sc.max())
+    p /= p.sum()
+    want = p @ vd
+    got = O.head_attend_x8(q, scale, k8=k8, sk=sk, v8=v8, sv=sv)
+    assert np.max(np.abs(got - want)) <= 1e-5 * np.max(np.abs(want))
+    one = O.head_attend_x8(q, scale, k8=k8[:1], sk=sk, v8=v8[:1], sv=sv)
+    assert np.array_equal(one, (v8[0].astype(np.float32) * sv).astype(np.float32))
+    # int8 K with bf16 V, and bf16 K with int8 V, equal the same algebra
+    vb = O.bf16_bits(vf)
+    got_k = O.head_attend_x8(q, scale, k8=k8, sk=sk, vb=vb)
+    want_k = p @ O.bf16_to_f32(vb).astype(np.float64).reshape(T, hd)
+    assert np.max(np.abs(got_k - want_k)) <= 1e-5 * np.max(np.abs(want_k))
+
+
+def test_cross_i8_decoder_close_to_bf16_cross():
+    """The oracle decoder with int8 cross K / V: logits within the
+    quantisation's reach of the bf16-cross decoder (2 layers), and the flag
+    acts at set_cross."""
+    cfg = O.ModelConfig()
+    vals = dict(family=1, n_layers=2, d_model=256, n_heads=4, n_kv_heads=4, head_dim=64, ffn=1024,
+                vocab=1000, max_pos=448, max_ctx=64, wdtype=2, eps=1e-5, rope_theta=0.0, n_cross=100)
+    for k, v in vals.items():
+        setattr(cfg, k, v)
+    a = O.OracleModel(cfg, 5, 1)
+    b = O.OracleModel(cfg, 5, 1)
+    a.set_cross(None)
+    b.set_cross_i8(True, True)
+    toks, pos = np.array([7], np.int32), np.array([0], np.int32)
+    la0 = a.step(toks, pos)
+    b.reset()
+    b.set_cross(None)
+    lb = b.step(toks, pos)
+    rel = np.linalg.norm(lb - la0) / np.linalg.norm(la0)
+    assert 0 < rel < 3e-2, rel
+    a.close()
+    b.close()

@@ -36,6 +36,8 @@ AttnParams to_params(const AttnLaunch &L) {
   p.out_stride = L.out_stride ? L.out_stride : L.hq * L.hd;
   p.work = L.work;
   p.max_splits = L.max_splits;
+  p.k_scale = L.k_scale;
+  p.v_scale = L.v_scale;
   return p;
 }
 
@@ -46,10 +48,10 @@ namespace {
 using adev::AttnParams;
 using adev::kThreads;
 
-template <int HD, int G>
+template <int HD, int G, int KV8 = 0>
 __global__ __launch_bounds__(kThreads) void attn_kernel(AttnParams p) {
   __shared__ float lds[adev::attn_lds_floats(HD, G)];
-  adev::attn_split_block<HD, G, false>(p, blockIdx.x, blockIdx.y, blockIdx.z, lds);
+  adev::attn_split_block<HD, G, false, KV8>(p, blockIdx.x, blockIdx.y, blockIdx.z, lds);
 }
 
 template <int HD, int G>
@@ -71,7 +73,28 @@ AttnFn pick_g(int g, bool merge) {
   return nullptr;
 }
 
-AttnFn pick(int hd, int g, bool merge) {
+// int8 K and/or V (kv8 bit 0 / bit 1): one query head a KV head (Whisper's
+// cross attention).
+template <int HD>
+AttnFn pick_kv8(int kv8) {
+  switch (kv8) {
+    case 1: return attn_kernel<HD, 1, 1>;
+    case 2: return attn_kernel<HD, 1, 2>;
+    case 3: return attn_kernel<HD, 1, 3>;
+  }
+  return nullptr;
+}
+
+AttnFn pick(int hd, int g, bool merge, int kv8 = 0) {
+  if (kv8 && !merge) {
+    if (g != 1) return nullptr;
+    switch (hd) {
+      case 64: return pick_kv8<64>(kv8);
+      case 128: return pick_kv8<128>(kv8);
+      case 256: return pick_kv8<256>(kv8);
+    }
+    return nullptr;
+  }
   switch (hd) {
     case 64: return pick_g<64>(g, merge);
     case 128: return pick_g<128>(g, merge);
@@ -80,14 +103,16 @@ AttnFn pick(int hd, int g, bool merge) {
   return nullptr;
 }
 
+int kv8_of(const AttnParams &p) { return (p.k_scale ? 1 : 0) | (p.v_scale ? 2 : 0); }
+
 }  // namespace
 
 // One attention phase of a step: split partials or the merge.
 void launch_attn_phase(const sdev::Phase &ph, hipStream_t s) {
   const AttnParams &p = ph.u.attn;
   const bool merge = ph.kind == sdev::PH_MERGE;
-  AttnFn fn = pick(ph.hd, ph.g, merge);
-  XE_REQUIRE(fn, "attn phase: unsupported head_dim / group");
+  AttnFn fn = pick(ph.hd, ph.g, merge, kv8_of(p));
+  XE_REQUIRE(fn, "attn phase: unsupported head_dim / group (int8 K/V: one query head a KV head)");
   if (merge) {
     const int blocks = (ph.g * ph.hd + kThreads - 1) / kThreads;
     hipLaunchKernelGGL(fn, dim3(blocks, p.hkv, p.batch), dim3(kThreads), 0, s, p);
@@ -138,12 +163,14 @@ void launch_attn(const AttnLaunch &L, hipStream_t s) {
   XE_REQUIRE(L.max_splits >= 1 && L.max_splits <= adev::kMaxSplits, "attn: max_splits must be 1..256");
   XE_REQUIRE(L.work, "attn: workspace missing");
   const int g = L.hq / L.hkv;
-  AttnFn fn = pick(L.hd, g, false);
+  const AttnParams p = adev::to_params(L);
+  AttnFn fn = pick(L.hd, g, false, kv8_of(p));
   AttnFn merge = pick(L.hd, g, true);
-  XE_REQUIRE(fn && merge, "attn: unsupported head_dim / GQA group (hd 64/128/256, group 1/2/4/8)");
+  XE_REQUIRE(fn && merge, "attn: unsupported head_dim / GQA group (hd 64/128/256, group 1/2/4/8; "
+                          "int8 K/V: group 1)");
   XE_REQUIRE(!L.rope_cos || (L.rope_sin && L.pos), "attn: RoPE needs sin table and positions");
   XE_REQUIRE(!L.k_new || (L.v_new && (L.pos || L.lens || L.fixed_len)), "attn: append needs v_new");
-  const AttnParams p = adev::to_params(L);
+  XE_REQUIRE(!kv8_of(p) || !L.k_new, "attn: int8 K/V caches take no append");
   hipLaunchKernelGGL(fn, dim3(L.max_splits, L.hkv, L.batch), dim3(kThreads), 0, s, p);
   XE_HIP(hipGetLastError());
   if (L.max_splits > 1) {

@@ -27,6 +27,11 @@
 // Fused in front (decode step): the Gemma per-head RMSNorm (1 + w) and RoPE of
 // q and the new k, and the bf16 append of the new k/v at position pos, done
 // by the block whose range holds pos (the only one that reads it).
+// int8 K and/or V (KV8 bit 0 / bit 1; Whisper's per-utterance cross K/V,
+// route_b_kernels/decode_fused/gen_decode.py:263-282): 8 int8 of a key a
+// lane (8-byte loads); the per-channel K scale multiplies q once
+// (scores = sum_d (q[d] s_k[d]) k8[d]), the V scale multiplies the p-weighted
+// sums when they are written (out[d] = s_v[d] sum_t p_t v8[t][d]).
 #pragma once
 
 #include "gemv_dev.h"
@@ -65,6 +70,7 @@ struct AttnParams {
   int out_stride;
   float *work;
   int max_splits;
+  const float *k_scale, *v_scale;  // int8 K / V channel scales [hkv * hd], or null (bf16)
 };
 
 __device__ __forceinline__ uint16_t f32_to_bf16_rne(float x) {
@@ -150,10 +156,38 @@ __device__ __forceinline__ void head_transform(const AttnParams &p, const float 
   }
 }
 
+// A lane's eight elements of one key row, loaded raw (16 bytes of bf16 or 8
+// of int8) and converted at use, so the loads of a block stay in flight
+// while earlier keys compute.
+template <bool I8>
+struct Raw8 {
+  uint32_t w[I8 ? 2 : 4];
+  __device__ __forceinline__ void load(const uint16_t *base, size_t elem) {
+    if constexpr (I8) {
+      const uint2 v = *reinterpret_cast<const uint2 *>(reinterpret_cast<const int8_t *>(base) + elem);
+      w[0] = v.x;
+      w[1] = v.y;
+    } else {
+      const uint4 v = *reinterpret_cast<const uint4 *>(base + elem);
+      w[0] = v.x;
+      w[1] = v.y;
+      w[2] = v.z;
+      w[3] = v.w;
+    }
+  }
+  __device__ __forceinline__ float get(int e) const {
+    if constexpr (I8)
+      return static_cast<float>(static_cast<int>(__builtin_amdgcn_sbfe(static_cast<int>(w[e >> 2]), 8 * (e & 3), 8)));
+    else
+      return __uint_as_float((e & 1) ? (w[e >> 1] & 0xffff0000u) : (w[e >> 1] << 16));
+  }
+};
+
 // One split block: keys [split*chunk, ...) of (stream b, kv head kvh).
-template <int HD, int G, bool COH>
+template <int HD, int G, bool COH, int KV8 = 0>
 __device__ __forceinline__ void attn_split_block(const AttnParams &p, int split, int kvh, int b, float *lds) {
-  constexpr int EPL = 8;       // bf16 elements per lane per key (16 B)
+  constexpr bool K8 = (KV8 & 1) != 0, V8 = (KV8 & 2) != 0;
+  constexpr int EPL = 8;       // elements per lane per key (16 B of bf16, 8 B of int8)
   constexpr int L = HD / EPL;  // lanes per key
   constexpr int KPW = 64 / L;  // keys per wave per load
   constexpr int UK = 4;        // keys per lane group per block update
@@ -171,15 +205,18 @@ __device__ __forceinline__ void attn_split_block(const AttnParams &p, int split,
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int posi = len - 1;
 
-  uint16_t *kbase = p.kc + p.kv_bstride * b + static_cast<size_t>(kvh) * p.max_ctx * HD;
-  uint16_t *vbase = p.vc + p.kv_bstride * b + static_cast<size_t>(kvh) * p.max_ctx * HD;
+  // element offsets (bytes for int8, uint16 units for bf16 through load8)
+  const size_t kvoff = p.kv_bstride * b + static_cast<size_t>(kvh) * p.max_ctx * HD;
+  uint16_t *kbase = p.kc + (K8 ? 0 : kvoff);
+  uint16_t *vbase = p.vc + (V8 ? 0 : kvoff);
+  const size_t kel = K8 ? kvoff : 0, vel = V8 ? kvoff : 0;
 
   // ---- q heads of this group (norm + rope), new k/v append ----
   for (int g = wave; g < G; g += kWaves) {
     const float *src = p.q + static_cast<size_t>(b) * p.q_stride + (kvh * G + g) * HD;
     head_transform<HD, COH>(p, src, qs[g], p.q_norm_w, posi);
   }
-  const bool appender = p.k_new && split == nsplits - 1;
+  const bool appender = !K8 && !V8 && p.k_new && split == nsplits - 1;
   if (appender && wave == 0) {
     const float *ksrc = p.k_new + static_cast<size_t>(b) * p.kv_new_stride + kvh * HD;
     const float *vsrc = p.v_new + static_cast<size_t>(b) * p.kv_new_stride + kvh * HD;
@@ -199,7 +236,8 @@ __device__ __forceinline__ void attn_split_block(const AttnParams &p, int split,
 #pragma unroll
   for (int g = 0; g < G; g++)
 #pragma unroll
-    for (int e = 0; e < EPL; e++) qr[g][e] = qs[g][kl * EPL + e];
+    for (int e = 0; e < EPL; e++)
+      qr[g][e] = K8 ? qs[g][kl * EPL + e] * p.k_scale[kvh * HD + kl * EPL + e] : qs[g][kl * EPL + e];
   float m[G], l[G], acc[G][EPL];
 #pragma unroll
   for (int g = 0; g < G; g++) {
@@ -211,26 +249,23 @@ __device__ __forceinline__ void attn_split_block(const AttnParams &p, int split,
   const float sc2 = p.scale * kLog2e;
 
   for (int base = s0 + wave * KPW + kg; base < s1; base += STEP * UK) {
-    uint4 kv[UK], vv[UK];
+    Raw8<K8> kv[UK];
+    Raw8<V8> vv[UK];
     bool ok[UK];
 #pragma unroll
     for (int u = 0; u < UK; u++) {
       const int key = base + u * STEP;
       ok[u] = key < s1;
       const int kk = ok[u] ? key : s0;
-      kv[u] = *reinterpret_cast<const uint4 *>(kbase + static_cast<size_t>(kk) * HD + kl * EPL);
-      vv[u] = *reinterpret_cast<const uint4 *>(vbase + static_cast<size_t>(kk) * HD + kl * EPL);
+      kv[u].load(kbase, kel + static_cast<size_t>(kk) * HD + kl * EPL);
+      vv[u].load(vbase, vel + static_cast<size_t>(kk) * HD + kl * EPL);
     }
     float s[UK][G];
 #pragma unroll
     for (int u = 0; u < UK; u++) {
-      const uint32_t w[4] = {kv[u].x, kv[u].y, kv[u].z, kv[u].w};
       float kf[EPL];
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        kf[2 * i] = __uint_as_float(w[i] << 16);
-        kf[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
-      }
+      for (int e = 0; e < EPL; e++) kf[e] = kv[u].get(e);
 #pragma unroll
       for (int g = 0; g < G; g++) {
         float d = 0.f;
@@ -261,14 +296,9 @@ __device__ __forceinline__ void attn_split_block(const AttnParams &p, int split,
 #pragma unroll
       for (int e = 0; e < EPL; e++) acc[g][e] *= corr;
 #pragma unroll
-      for (int u = 0; u < UK; u++) {
-        const uint32_t w[4] = {vv[u].x, vv[u].y, vv[u].z, vv[u].w};
+      for (int u = 0; u < UK; u++)
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-          acc[g][2 * i] = __builtin_fmaf(pu[u], __uint_as_float(w[i] << 16), acc[g][2 * i]);
-          acc[g][2 * i + 1] = __builtin_fmaf(pu[u], __uint_as_float(w[i] & 0xffff0000u), acc[g][2 * i + 1]);
-        }
-      }
+        for (int e = 0; e < EPL; e++) acc[g][e] = __builtin_fmaf(pu[u], vv[u].get(e), acc[g][e]);
     }
   }
 
@@ -320,6 +350,7 @@ __device__ __forceinline__ void attn_split_block(const AttnParams &p, int split,
       lt += red[w][g][1] * f;
       at += red[w][g][2 + e] * f;
     }
+    if (V8) at = at * p.v_scale[kvh * HD + e];
     if (single) {
       const float o = p.div_norm ? at / lt : at * (1.0f / lt);
       act_st<COH>(p.out + static_cast<size_t>(b) * p.out_stride + (kvh * G + g) * HD + e, o);

@@ -260,6 +260,10 @@ struct AttnLaunch {
   // workspace for the split partials
   float *work = nullptr;
   int max_splits = 0;
+  // int8 K / V instead of bf16 (kc / vc then hold int8 [batch, hkv, max_ctx,
+  // hd]; no append): per-channel scales [hkv * hd], or null
+  const float *k_scale = nullptr;
+  const float *v_scale = nullptr;
 };
 
 size_t attn_work_floats(int batch, int hq, int hd, int max_splits);

@@ -170,6 +170,40 @@ __global__ void cross_pack_kernel(const float *src, int t_rows, int heads, int h
   }
 }
 
+// f32 [T, H*hd] rows -> int8 head-major [H, T, hd] with per-channel scales:
+// the host quantisation of the reference's int8 cross K / V
+// (rust/npu-engine/src/asr/whisper_decoder.rs:1186-1219, write_buf_i8
+// :1110-1134): s[c] = max_t |x[t][c]| / 127 (1.0 for a zero channel),
+// q = clamp(round(x * (1/s)), -127, 127), round half away from zero.
+// One workgroup a head; thread (wave w, lane j) takes channel j + 64 i of
+// rows w, w + 4, ...  (one 256-byte row segment a wave per load).
+__global__ __launch_bounds__(256) void cross_quant_kernel(const float *src, int t_rows, int heads, int hd,
+                                                          int8_t *dst, float *scale) {
+  __shared__ float red[4][256];
+  const int h = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int D = heads * hd;
+  for (int j0 = 0; j0 < hd; j0 += 64) {
+    const int j = j0 + lane;
+    float mx = 0.f;
+    if (j < hd)
+      for (int t = wave; t < t_rows; t += 4) mx = fmaxf(mx, fabsf(src[static_cast<size_t>(t) * D + h * hd + j]));
+    red[wave][lane] = mx;
+    __syncthreads();
+    const float m = fmaxf(fmaxf(red[0][lane], red[1][lane]), fmaxf(red[2][lane], red[3][lane]));
+    const float s = m > 0.f ? m * 1.0f / 127.0f : 1.0f;
+    const float inv = s != 0.f ? 1.0f / s : 0.f;
+    if (j < hd) {
+      if (wave == 0) scale[h * hd + j] = s;
+      for (int t = wave; t < t_rows; t += 4) {
+        float r = roundf(src[static_cast<size_t>(t) * D + h * hd + j] * inv);
+        r = r != r ? 0.f : fminf(fmaxf(r, -127.f), 127.f);  // NaN -> 0 (Rust `as i8`)
+        dst[(static_cast<size_t>(h) * t_rows + t) * hd + j] = static_cast<int8_t>(r);
+      }
+    }
+    __syncthreads();  // red is reused by the next channel block
+  }
+}
+
 // --------------------------------------------------------------------------
 // tensor table (mirrors the oracle's xo_tensor_spec: same shapes and laws)
 // --------------------------------------------------------------------------
@@ -293,7 +327,8 @@ struct Layer {
   float *ln1_w = nullptr, *ln1_b = nullptr, *ln2_w = nullptr, *ln2_b = nullptr;
   float *qn = nullptr, *kn = nullptr, *post_attn = nullptr, *post_ffn = nullptr;
   float *lnx_w = nullptr, *lnx_b = nullptr, *xq_b = nullptr, *xv_b = nullptr, *xo_b = nullptr;
-  uint16_t *ck = nullptr, *cv = nullptr;  // Whisper cross K/V bf16 [H, T, hd]
+  uint16_t *ck = nullptr, *cv = nullptr;  // Whisper cross K/V bf16 [H, T, hd] (int8 [H, T, hd] when quantised)
+  float *cks = nullptr, *cvs = nullptr;    // int8 cross K / V channel scales [H * hd]
 };
 
 template <typename T>
@@ -377,6 +412,7 @@ struct xe_decoder {
   int32_t *ll_forced = nullptr;    // device [max_ctx + 1][max_batch] prompt tokens
   double last_step_us = 0.0;
   bool cross_ready = false;
+  int cross_i8k = 0, cross_i8v = 0;  // per-utterance int8 cross K / V (xe_decoder_set_cross_int8)
   // Host copy of every stream's next position (the one the kernels append
   // the K/V row at and read the RoPE / position row of): feed() sets it to
   // the prompt length, step() to pos + 1, decode() and profile_step()
@@ -544,6 +580,8 @@ void alloc_decoder(xe_decoder *d) {
       l.xo_b = dalloc<float>(D, s);
       l.ck = dalloc<uint16_t>(static_cast<size_t>(c.n_cross) * D, s);
       l.cv = dalloc<uint16_t>(static_cast<size_t>(c.n_cross) * D, s);
+      l.cks = dalloc<float>(D, s);
+      l.cvs = dalloc<float>(D, s);
     }
   }
   d->xa = dalloc<float>(static_cast<size_t>(B) * D, s);
@@ -605,18 +643,25 @@ void alloc_decoder(xe_decoder *d) {
   XE_HIP(hipStreamSynchronize(s));
 }
 
-void free_decoder(xe_decoder *d) {
+// Every cached execution plan (graphs, device phase lists, exchange arenas).
+void drop_plans(xe_decoder *d) {
   if (d->s) (void)hipStreamSynchronize(d->s);
   for (auto &kv : d->plans) {
     if (kv.second.graph) (void)hipGraphExecDestroy(kv.second.graph);
     if (kv.second.dev_phases) (void)hipFree(kv.second.dev_phases);
   }
-  if (d->step_flags) (void)hipFree(d->step_flags);
+  d->plans.clear();
   for (auto &kv : d->ll_plans) {
     if (kv.second.dev_a) (void)hipFree(kv.second.dev_a);
     if (kv.second.dev_f) (void)hipFree(kv.second.dev_f);
     if (kv.second.arena) (void)hipFree(kv.second.arena);
   }
+  d->ll_plans.clear();
+}
+
+void free_decoder(xe_decoder *d) {
+  drop_plans(d);
+  if (d->step_flags) (void)hipFree(d->step_flags);
   for (void *p : d->ll_fc2t)
     if (p) (void)hipFree(p);
   if (d->ll_forced) (void)hipFree(d->ll_forced);
@@ -633,7 +678,8 @@ void free_decoder(xe_decoder *d) {
                     static_cast<void *>(l.lnx_w), static_cast<void *>(l.lnx_b),
                     static_cast<void *>(l.xq_b), static_cast<void *>(l.xv_b),
                     static_cast<void *>(l.xo_b), static_cast<void *>(l.ck),
-                    static_cast<void *>(l.cv)})
+                    static_cast<void *>(l.cv), static_cast<void *>(l.cks),
+                    static_cast<void *>(l.cvs)})
       if (p) (void)hipFree(p);
   }
   for (void *p : {static_cast<void *>(d->pos_emb), static_cast<void *>(d->lnf_w),
@@ -954,7 +1000,10 @@ void build_plan(xe_decoder *d, int B, xe_decoder::Plan &plan) {
       a.out_stride = D;
       a.work = d->attn_work;
       a.max_splits = attn_splits_for(d, B, c.n_heads);
-      pb.attn(a, "attn_cross", static_cast<double>(c.n_cross) * D * 2 * 2 + 8.0 * B * D);
+      a.k_scale = d->cross_i8k ? l.cks : nullptr;
+      a.v_scale = d->cross_i8v ? l.cvs : nullptr;
+      pb.attn(a, "attn_cross",
+              static_cast<double>(c.n_cross) * D * ((d->cross_i8k ? 1 : 2) + (d->cross_i8v ? 1 : 2)) + 8.0 * B * D);
       GemvCall o;
       o.m = &l.xo;
       o.bias = l.xo_b;
@@ -1031,7 +1080,7 @@ void build_plan(xe_decoder *d, int B, xe_decoder::Plan &plan) {
   }
   bool gemm_phases = false;
   for (const auto &ph : plan.phases) gemm_phases |= ph.kind == sdev::PH_GEMM || ph.kind == sdev::PH_GEMM_PRO;
-  plan.persistent = !getenv("XE_NO_PERSIST") && B <= 4 && !gemm_phases &&
+  plan.persistent = !getenv("XE_NO_PERSIST") && B <= 4 && !gemm_phases && !d->cross_i8k && !d->cross_i8v &&
                     step_kernel_supported(c.wdtype, plan.step_nb, hd, c.n_heads / c.n_kv_heads) &&
                     plan.step_lds <= 150 * 1024;
 }
@@ -1180,6 +1229,7 @@ void build_ll_plan(xe_decoder *d, int B, xe_decoder::LLPlan &P) {
   const int g = c.n_heads / c.n_kv_heads;
   P.ok = false;
   if (B > ll::kMaxNB) { P.why = "batch > 4"; return; }
+  if (d->cross_i8k || d->cross_i8v) { P.why = "int8 cross K/V runs on the phase kernels"; return; }
   P.nb_t = B <= 1 ? 1 : B <= 2 ? 2 : 4;
   P.hd = hd;
   P.g = g;
@@ -1778,8 +1828,12 @@ void precompute_cross(xe_decoder *d) {
       g.y = tmp;
       g.ldy = D;
       run_gemv_now(g, T, d->s);
-      hipLaunchKernelGGL(cross_pack_kernel, dim3(1024), dim3(256), 0, d->s, tmp, T, c.n_heads,
-                         c.head_dim, which == 0 ? l.ck : l.cv);
+      if (which == 0 ? d->cross_i8k : d->cross_i8v)
+        hipLaunchKernelGGL(cross_quant_kernel, dim3(c.n_heads), dim3(256), 0, d->s, tmp, T, c.n_heads, c.head_dim,
+                           reinterpret_cast<int8_t *>(which == 0 ? l.ck : l.cv), which == 0 ? l.cks : l.cvs);
+      else
+        hipLaunchKernelGGL(cross_pack_kernel, dim3(1024), dim3(256), 0, d->s, tmp, T, c.n_heads,
+                           c.head_dim, which == 0 ? l.ck : l.cv);
       XE_HIP(hipGetLastError());
     }
   }
@@ -2005,6 +2059,22 @@ int xe_decoder_set_cross(xe_decoder *d, const float *enc) {
       XE_HIP(hipMemcpyAsync(d->enc, tmp.data(), n * 4, hipMemcpyHostToDevice, d->s));
     }
     precompute_cross(d);
+    return 0;
+  }, -1);
+}
+
+int xe_decoder_set_cross_int8(xe_decoder *d, int k_int8, int v_int8) {
+  return guard_d([&]() -> int {
+    XE_REQUIRE(d, "null decoder");
+    XE_REQUIRE(d->c.family == XE_WHISPER, "cross attention is Whisper-only");
+    DeviceGuard dg(d->dev->ordinal);
+    const int k = k_int8 ? 1 : 0, v = v_int8 ? 1 : 0;
+    if (k != d->cross_i8k || v != d->cross_i8v) {
+      drop_plans(d);  // the cross-attention phase and the executor choice change
+      d->cross_i8k = k;
+      d->cross_i8v = v;
+      d->cross_ready = false;
+    }
     return 0;
   }, -1);
 }

@@ -46,7 +46,8 @@ EXPORTS = [
     "xe_w8a8_linear_dev",
     "xe_attn_decode", "xe_attn_decode_dev", "xe_attn_decode_dev_static", "xe_ctx_synchronize", "xe_decoder_create",
     "xe_decoder_destroy", "xe_decoder_init_synthetic", "xe_decoder_set_tensor",
-    "xe_decoder_get_tensor_q8", "xe_decoder_reset", "xe_decoder_set_cross", "xe_decoder_step",
+    "xe_decoder_get_tensor_q8", "xe_decoder_reset", "xe_decoder_set_cross", "xe_decoder_set_cross_int8",
+    "xe_decoder_step",
     "xe_decoder_generate", "xe_decoder_last_step_us", "xe_decoder_weight_bytes",
     "xe_decoder_feed", "xe_decoder_decode", "xe_decoder_profile_step", "xe_decoder_executor",
     "xe_model_tensor_shape", "xe_decoder_config", "xe_decoder_load_safetensors", "xe_safetensors_plan",
@@ -161,6 +162,7 @@ def lib():
         "xe_decoder_get_tensor_q8": (i, [vp, i, i, vp, vp]),
         "xe_decoder_reset": (i, [vp]),
         "xe_decoder_set_cross": (i, [vp, vp]),
+        "xe_decoder_set_cross_int8": (i, [vp, i, i]),
         "xe_decoder_step": (i, [vp, vp, vp, i, vp, vp]),
         "xe_decoder_generate": (i, [vp, vp, i, i, i, vp]),
         "xe_decoder_last_step_us": (C.c_double, [vp]),
@@ -607,6 +609,10 @@ class Decoder:
     def precompute_cross(self, enc=None):
         e = _f32(enc)
         _check(lib().xe_decoder_set_cross(self.h, _p(e)))
+
+    def set_cross_int8(self, k_int8=True, v_int8=True):
+        """Per-utterance int8 cross K / V from the next precompute_cross on."""
+        _check(lib().xe_decoder_set_cross_int8(self.h, int(bool(k_int8)), int(bool(v_int8))))
 
     def step(self, tokens, pos, want_logits=True):
         tokens = np.ascontiguousarray(np.atleast_1d(tokens), np.int32)
