@@ -189,6 +189,8 @@ __device__ __forceinline__ void attn_split_block(const AttnParams &p, int split,
   constexpr bool K8 = (KV8 & 1) != 0, V8 = (KV8 & 2) != 0;
   constexpr int EPL = 8;       // elements per lane per key (16 B of bf16, 8 B of int8)
   constexpr int L = HD / EPL;  // lanes per key
+  constexpr int kLog2L = L == 8 ? 3 : L == 16 ? 4 : L == 32 ? 5 : 6;
+  static_assert((1 << kLog2L) == L, "lanes per key: 8, 16, 32 or 64");
   constexpr int KPW = 64 / L;  // keys per wave per load
   constexpr int UK = 4;        // keys per lane group per block update
   constexpr int STEP = kWaves * KPW;
@@ -260,7 +262,10 @@ __device__ __forceinline__ void attn_split_block(const AttnParams &p, int split,
       kv[u].load(kbase, kel + static_cast<size_t>(kk) * HD + kl * EPL);
       vv[u].load(vbase, vel + static_cast<size_t>(kk) * HD + kl * EPL);
     }
-    float s[UK][G];
+    // the block's UK x G partial dot products, then their sums over the L
+    // lanes of each key, level by level through DPP and permlane swaps (no
+    // LDS crossbar round trips)
+    float sd[UK * G];
 #pragma unroll
     for (int u = 0; u < UK; u++) {
       float kf[EPL];
@@ -271,11 +276,15 @@ __device__ __forceinline__ void attn_split_block(const AttnParams &p, int split,
         float d = 0.f;
 #pragma unroll
         for (int e = 0; e < EPL; e++) d = __builtin_fmaf(qr[g][e], kf[e], d);
-#pragma unroll
-        for (int off = L / 2; off >= 1; off >>= 1) d += __shfl_xor(d, off, 64);
-        s[u][g] = d * sc2;
+        sd[u * G + g] = d;
       }
     }
+    gdev::group_sums<UK * G>(sd, kLog2L);
+    float s[UK][G];
+#pragma unroll
+    for (int u = 0; u < UK; u++)
+#pragma unroll
+      for (int g = 0; g < G; g++) s[u][g] = sd[u * G + g] * sc2;
 #pragma unroll
     for (int g = 0; g < G; g++) {
       float mb = m[g];
