@@ -213,12 +213,33 @@ __device__ __forceinline__ void attn_split_block(const AttnParams &p, int split,
   uint16_t *vbase = p.vc + (V8 ? 0 : kvoff);
   const size_t kel = K8 ? kvoff : 0, vel = V8 ? kvoff : 0;
 
+  const int kg = lane / L, kl = lane % L;
+  const int base0 = s0 + wave * KPW + kg;
+  const bool appender = !K8 && !V8 && p.k_new && split == nsplits - 1;
+  // UK keys' K and V rows from `base` (keys past the range read key s0)
+  auto load_block = [&](int base, Raw8<K8> (&kv)[UK], Raw8<V8> (&vv)[UK], bool (&ok)[UK]) {
+#pragma unroll
+    for (int u = 0; u < UK; u++) {
+      const int key = base + u * STEP;
+      ok[u] = key < s1;
+      const int kk = ok[u] ? key : s0;
+      kv[u].load(kbase, kel + static_cast<size_t>(kk) * HD + kl * EPL);
+      vv[u].load(vbase, vel + static_cast<size_t>(kk) * HD + kl * EPL);
+    }
+  };
+  // the first block's loads go out before the head transforms, so their HBM
+  // latency overlaps the prologue (not in the appender's block: it reads
+  // back the row it appends)
+  Raw8<K8> kv0[UK];
+  Raw8<V8> vv0[UK];
+  bool ok0[UK];
+  if (!appender) load_block(base0, kv0, vv0, ok0);
+
   // ---- q heads of this group (norm + rope), new k/v append ----
   for (int g = wave; g < G; g += kWaves) {
     const float *src = p.q + static_cast<size_t>(b) * p.q_stride + (kvh * G + g) * HD;
     head_transform<HD, COH>(p, src, qs[g], p.q_norm_w, posi);
   }
-  const bool appender = !K8 && !V8 && p.k_new && split == nsplits - 1;
   if (appender && wave == 0) {
     const float *ksrc = p.k_new + static_cast<size_t>(b) * p.kv_new_stride + kvh * HD;
     const float *vsrc = p.v_new + static_cast<size_t>(b) * p.kv_new_stride + kvh * HD;
@@ -233,7 +254,6 @@ __device__ __forceinline__ void attn_split_block(const AttnParams &p, int split,
   __syncthreads();  // the appended row is read back by this block only
 
   // ---- main loop: online softmax per lane group ----
-  const int kg = lane / L, kl = lane % L;
   float qr[G][EPL];
 #pragma unroll
   for (int g = 0; g < G; g++)
@@ -250,17 +270,19 @@ __device__ __forceinline__ void attn_split_block(const AttnParams &p, int split,
   }
   const float sc2 = p.scale * kLog2e;
 
-  for (int base = s0 + wave * KPW + kg; base < s1; base += STEP * UK) {
+  for (int base = base0; base < s1; base += STEP * UK) {
     Raw8<K8> kv[UK];
     Raw8<V8> vv[UK];
     bool ok[UK];
+    if (base == base0 && !appender) {
 #pragma unroll
-    for (int u = 0; u < UK; u++) {
-      const int key = base + u * STEP;
-      ok[u] = key < s1;
-      const int kk = ok[u] ? key : s0;
-      kv[u].load(kbase, kel + static_cast<size_t>(kk) * HD + kl * EPL);
-      vv[u].load(vbase, vel + static_cast<size_t>(kk) * HD + kl * EPL);
+      for (int u = 0; u < UK; u++) {
+        kv[u] = kv0[u];
+        vv[u] = vv0[u];
+        ok[u] = ok0[u];
+      }
+    } else {
+      load_block(base, kv, vv, ok);
     }
     // the block's UK x G partial dot products, then their sums over the L
     // lanes of each key, level by level through DPP and permlane swaps (no
