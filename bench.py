@@ -322,11 +322,55 @@ def attn_case(xe, dev, ctx, hq, hkv, hd, mc, b, seed, eager):
     return rec
 
 
+# The decoder's projections at b = 64 (Gemma-3-1B): the batched MFMA GEMM.
+GEMM_SHAPES = [("qkv", 1536, 1152), ("o", 1152, 1024), ("gateup", 13824, 1152), ("down", 1152, 6912),
+               ("lmhead", 262144, 1152)]
+
+
+def gemm_case(xe, dev, ctx, name, m, k, b, seed, eager, reps=0, copies=0):
+    """One b = 64 projection shape on the batched GEMM (int8 weights, fp32
+    activations, no prologue) over rotating weight copies (>= 512 MB, or
+    `copies`); `reps` 0 sizes the repetitions from the bytes."""
+    per = m * k + 4 * m
+    n = copies or max(2, min(64, -(-ROTATE_BYTES // per)))
+    wb = xe.Buf(dev, n * m * k)
+    wb.fill_synthetic(xe.XE_I8, seed, 1, n * m * k, std=60.0)
+    sb = xe.Buf(dev, n * m * 4)
+    sb.fill_synthetic(xe.XE_F32, seed, 2, n * m, mean=0.0105, std=0.003)
+    views = [ctx.register_weight_view(xe.XE_I8, m, k, wb.ptr + i * m * k, sb.ptr + i * m * 4, None)
+             for i in range(n)]
+    xb = xe.Buf(dev, b * k * 4)
+    xb.fill_synthetic(xe.XE_F32, seed, 3, b * k)
+    yb = xe.Buf(dev, b * m * 4)
+    r = reps or int(max(3, min(200, 2e5 / (n * per / 4e6))))
+    print("[kernels] gemm %s %dx%d b=%d: %d copies x %d" % (name, m, k, b, n, r), file=sys.stderr, flush=True)
+    us = ctx.probe_gemv(views, xb.ptr, xe.XE_F32, b, yb.ptr, r, eager)
+    flop = 2.0 * m * k * b
+    by = per + 4 * b * (k + m)
+    rec = {"kernel": "GEMM int8 %s %dx%d b=%d" % (name, m, k, b), "us": round(us, 2), "bytes": by,
+           "gbps": round(by / us / 1e3, 1), "frac": round(by / us / 1e3 / HBM_PEAK_GBPS, 4),
+           "tflops": round(flop / us / 1e6, 1), "copies": n}
+    print("[kernels] %s" % rec, file=sys.stderr, flush=True)
+    for w in views:
+        w.free()
+    for buf in (wb, sb, xb, yb):
+        buf.free()
+    return rec
+
+
 def run_kernels(args):
     xe = load_xe()
     dev = xe.Device(0)
     ctx = xe.CtxDecode(dev)
     recs = []
+    if args.gemm_only:
+        for name, m, k in GEMM_SHAPES:
+            recs.append(gemm_case(xe, dev, ctx, name, m, k, 64, args.seed + m + k, args.eager,
+                                  args.reps, args.copies))
+        ctx.close()
+        dev.close()
+        return {"metric": "batched GEMM (b = 64 projections)", "unit": "GB/s", "peak": HBM_PEAK_GBPS,
+                "kernels": recs}
     for wd in (xe.XE_I8, xe.XE_BFP16, xe.XE_BF16):
         for (m, k) in GEMV_SHAPES:
             recs += gemv_case(xe, dev, ctx, wd, m, k, (1, 4, 8), args.seed + m + k, args.eager)
@@ -335,6 +379,8 @@ def run_kernels(args):
             for b in (1, 16, 64):
                 recs.append(attn_case(xe, dev, ctx, hq, hkv, hd, mc, b, args.seed + mc + b,
                                       args.eager))
+    for name, m, k in GEMM_SHAPES:
+        recs.append(gemm_case(xe, dev, ctx, name, m, k, 64, args.seed + m + k, args.eager))
     ctx.close()
     dev.close()
     return {"metric": "isolated kernel HBM GB/s (BASELINE configs 2 and 3)", "unit": "GB/s",
@@ -364,6 +410,10 @@ def main():
                          "FETCH_SIZE / WRITE_SIZE counters")
     ap.add_argument("--kernels", action="store_true",
                     help="only the isolated kernels: config-2 GEMVs and config-3 mha_decode")
+    ap.add_argument("--gemm-only", action="store_true",
+                    help="with --kernels: only the b = 64 projection GEMMs")
+    ap.add_argument("--reps", type=int, default=0, help="--kernels GEMMs: repetitions (0: by size)")
+    ap.add_argument("--copies", type=int, default=0, help="--kernels GEMMs: weight copies (0: >= 512 MB)")
     ap.add_argument("--eager", action="store_true",
                     help="--kernels with plain launches instead of graph replays (for runs under "
                          "rocprofv3's kernel trace, which has crashed on graph launches here)")
