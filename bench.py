@@ -202,9 +202,21 @@ def run_batch(xe, dev, cfg, args, B, steps, warmup, profile):
                     "steps in the timed region)" % ((K + 255) // 256) if executor == "ll" else
                     "whole decode step (%s executor: every kernel of the step)" % executor)
     else:
-        r_bytes = sum(b for l, u, b in prof if l.startswith("gemv"))
-        r_us = sum(u for l, u, b in prof if l.startswith("gemv"))
-        r_kernel = "gemv (decode GEMV family, one profiled step)"
+        # the phase-kernel family with the most device time in one profiled
+        # step at the end context: the projections (MFMA GEMM beyond 8
+        # streams, GEMV up to 8) or the attention partials + merge
+        proj = "gemm_kernel" if B > 8 else "gemv_kernel"
+        fams = {
+            "%s (projections: phases gemv_qkv / o / gateup / down / lmhead)" % proj:
+                [(u, b) for l, u, b in prof if l.startswith("gemv") and not l.endswith("_pro")],
+            "attn_kernel + attn_merge_kernel (self-attention over the cache)":
+                [(u, b) for l, u, b in prof if l.startswith("attn")],
+        }
+        fam_us = {k: sum(u for u, _ in v) for k, v in fams.items()}
+        r_kernel = max(fam_us, key=fam_us.get)
+        r_bytes = sum(b for _, b in fams[r_kernel])
+        r_us = fam_us[r_kernel]
+        r_kernel += ", one profiled step at position %d" % (last + 1)
     r_gbps = r_bytes / r_us / 1e3
     res = {
         "value": round(tok_s, 2), "unit": "tok/s", "steps": K, "warmup": W,

@@ -94,13 +94,10 @@ def test_ll_plan_prompt3900(gpu, xe, default_executor):
              label="gemma-ll-p3900", want_exec="ll", prompt_seed=1)
 
 
-@pytest.mark.parametrize("mfma", ["0", "1"])
-def test_ll_plan_three_streams(gpu, xe, default_executor, monkeypatch, mfma):
-    """Three streams on the low-latency executor at max_ctx 4096, with the
-    int8 GEMVs on the VALU (default) and on the matrix cores."""
-    monkeypatch.setenv("XE_LL_MFMA", mfma)
+def test_ll_plan_three_streams(gpu, xe, default_executor):
+    """Three streams on the low-latency executor at max_ctx 4096."""
     run_pair(xe, gpu, gemma_long(xe), seed=4, batch=3, n_prompt=700, n_new=120,
-             label="gemma-ll-b3-mfma%s" % mfma, want_exec="ll", prompt_seed=2)
+             label="gemma-ll-b3", want_exec="ll", prompt_seed=2)
 
 
 def test_gemma3_1b_full_model_ll_plan(gpu, xe, default_executor):
@@ -249,7 +246,7 @@ def test_config3_ctx32768_device(gpu, xe, hq, hkv, hd, b):
 # The low-latency plan's A/B switches, each against the oracle on the bench's
 # plan shapes (a fresh decoder per setting: the plan is built at first use).
 LL_KNOBS = [("XE_LL_FFN_SPLIT", "0"), ("XE_LL_TAIL", "0"), ("XE_LL_TAIL", "2"),
-            ("XE_LL_STAGE", "0"), ("XE_LL_KV", "0"), ("XE_LL_MFMA", "1")]
+            ("XE_LL_STAGE", "0"), ("XE_LL_KV", "0")]
 
 
 @pytest.mark.parametrize("knob,value", LL_KNOBS)

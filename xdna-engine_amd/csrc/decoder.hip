@@ -397,7 +397,6 @@ struct xe_decoder {
     uint64_t *arena = nullptr;  // every exchange vector of the step
     ll::Vec arg{};
     int kin_a = 0, kin_f = 0, scratch = 0, nb_t = 1, grid = 0, hd = 64, g = 1;
-    int head_mfma = 0;
     int stage_a = 0, stage_f = 0;  // LDS weight stage bytes per role (ll::StageLayout), 0: none staged
     int kv_floats = 0;             // LDS key/value stage (attention side), 0: none
     size_t lds_bytes = 0;
@@ -1241,13 +1240,6 @@ void build_ll_plan(xe_decoder *d, int B, xe_decoder::LLPlan &P) {
   const int n_a = (P.grid + ll::kRoleStride - 1) / ll::kRoleStride, n_f = P.grid - n_a;
   const char *tail_env = std::getenv("XE_LL_TAIL");
   const int tail_mode = tail_env ? std::atoi(tail_env) : 1;
-  // int8 GEMVs on the matrix cores (XE_LL_MFMA=1; off by default: at one to
-  // four streams the digitisation and the fp64 combination cost more than
-  // the VALU dequantisation they replace, b=1 1033 vs 1163 tok/s)
-  const char *mf_env = std::getenv("XE_LL_MFMA");
-  const int mf_mode = mf_env ? std::atoi(mf_env) : 0;  // 0 off, 1 on, 2 lm-head only, 3 layers only
-  const bool mfma_on = mf_mode == 1 || mf_mode == 3;
-  const bool mfma_head = mf_mode == 1 || mf_mode == 2;
 
   // exchange arena: offsets first, one allocation after
   size_t pairs = 0;
@@ -1319,11 +1311,6 @@ void build_ll_plan(xe_decoder *d, int B, xe_decoder::LLPlan &P) {
     gd.k = m.cols;
     ll_tile(m.rows, ranks, m.cols, act == ACT_GEGLU_TANH, m.wdtype, gd.lpr, gd.rpl);
     gd.tail_split = tail_mode == 2 || (tail_mode == 1 && out_lds > 0) ? 1 : 0;
-    {
-      const int unit = (act == ACT_GEGLU_TANH ? 2 : 1) * (out_lds > 0 ? 4 : 1);
-      const int per_rank = (m.rows / unit + ranks - 1) / ranks * unit;
-      gd.mfma = mfma_on && m.wdtype == XE_I8 && ll::mfma_gemv_ok(m.cols, per_rank, out_lds > 0) ? 1 : 0;
-    }
     gd.in_vec = in_vec >= 0 ? 1 : 0;
     gd.norm = norm_kind;
     gd.gamma = gamma;
@@ -1525,7 +1512,6 @@ void build_ll_plan(xe_decoder *d, int B, xe_decoder::LLPlan &P) {
   P.arg.ld = arg_ld;
 
   ll_tile(c.vocab, P.grid, D, false, c.wdtype, P.head_lpr, P.head_rpl);
-  P.head_mfma = mfma_head && c.wdtype == XE_I8 && ll::mfma_gemv_ok(D, (c.vocab + P.grid - 1) / P.grid, false) ? 1 : 0;
   // inputs per role (GEMV inputs padded, ll::xstride; attention q rows and
   // fold sources plain): A holds QKV / O / cross-attention inputs and q rows,
   // F the FFN inputs
@@ -1537,7 +1523,6 @@ void build_ll_plan(xe_decoder *d, int B, xe_decoder::LLPlan &P) {
   P.scratch = std::max(std::max(ll::attn_scratch_floats(hd, g), ll::attn_scratch_floats(hd, 1)),
                        std::max(ll::kMaxSplits * (ll::kDM + 2) + ll::kMaxSplits + ll::kW * (ll::kDM + 1), P.nb_t * 2 * P.grid));
   P.scratch = std::max(P.scratch, 5 * ll::nw_floats(D));
-  if ((mfma_on || mfma_head) && c.wdtype == XE_I8) P.scratch = std::max(P.scratch, ll::kMfmaKsumFloats);
   if (ffn_split)  // the partials' staging and the reduce tables
     P.scratch = std::max(P.scratch, std::max(ll::dpart_obuf_floats(P.nb_t, D), ll::kW * P.nb_t * ll::kRedRows + 512));
   P.scratch += 16;
@@ -1617,7 +1602,6 @@ void run_ll(xe_decoder *d, int B, int n_steps, const int32_t *forced, int n_forc
   sp.head_eps = c.eps;
   sp.head_lpr = P.head_lpr;
   sp.head_rpl = P.head_rpl;
-  sp.head_mfma = P.head_mfma;
   sp.logits = want_logits ? d->logits : nullptr;
   sp.arg = P.arg;
   sp.last_max = opt ? 1 : 0;

@@ -99,8 +99,6 @@ struct GemvD {
   // FFN's hidden vector, read by the next phase, LK_DPART) instead of `out`,
   // at this float offset into each input row
   int out_lds;
-  // 1: int8 weights on the matrix cores (gemv_rows_mfma)
-  int mfma;
 };
 
 struct AttnD {
@@ -195,7 +193,6 @@ struct StepParams {
   const float *head_gamma, *head_beta;
   float head_eps;
   int head_lpr, head_rpl;
-  int head_mfma;  // 1: the lm-head GEMV on the matrix cores (int8)
   float *logits;  // [nb][vocab] plain fp32 (read by the host after the launch); may be null
   Vec arg;        // [2][nb][grid * 2]: (max, index) pairs per workgroup, by step parity
   int last_max;
@@ -941,345 +938,13 @@ __device__ __forceinline__ bool gemv_rows(const GD &g, int nb, int r0, int r1, c
   return ok;
 }
 
-// ---------------------------------------------------------------------------
-// int8 GEMV on the matrix cores.  At <= 4 streams the VALU form above is
-// bound by the int8 dequantisation (bit-field extract, convert, FMA: three
-// operations a weight on the few CUs a phase runs on), so int8 phases run on
-// v_mfma_i32_16x16x64_i8 instead: A = 16 weight rows x 64 k as stored (no
-// conversion), B = the inputs as integer digits.  Stream b's fp32 input is
-// written as X = rint(x 2^(27 - E_b)) (E_b: max |x| < 2^E_b, so |X| < 2^27
-// and the error is at most 2^(E_b - 28): 2^-28 of the largest element) in
-// four signed base-128 digits X = d0 2^21 + d1 2^14 + d2 2^7 + d3
-// (|d| <= 127, one sign); B column 4 b + j holds digit j.  The i32 sums are
-// exact (127 * 127 * K < 2^31 for K <= 8192), and a row's value (C0 2^21 +
-// C1 2^14 + C2 2^7 + C3) 2^(E_b - 27) is combined exactly in fp64, then
-// rounded once to fp32: the dot product of the digit-exact input to fp32
-// rounding, at least as accurate as an fp32 sum.  A lane holds A and B for
-// the same 16 k (its 16-byte chunk), so the sums do not depend on the
-// instruction's internal k order.
-// ---------------------------------------------------------------------------
-constexpr int kMfmaMaxK = 2048;  // digitize() holds kMfmaMaxK / kT elements a thread
-constexpr int kDigitPad = 16;  // bytes between a stream's digit rows
-constexpr int kMfmaKsumFloats = kW * 64 * 4;  // scratch for the K-segment sums (one i32x4 a lane)
-
-__host__ __device__ inline bool mfma_gemv_ok(int k, int rows_per_rank, bool out_lds) {
-  // inputs up to kMfmaMaxK (larger K, e.g. the FFN output GEMV without the
-  // split, stay on the VALU form); a GEMV that keeps its outputs in LDS takes one
-  // row block a wave (the outputs share bytes with the digits)
-  return k % 16 == 0 && k <= kMfmaMaxK && (!out_lds || rows_per_rank <= 16 * kW);
-}
-
-typedef int i32x4v __attribute__((ext_vector_type(4)));
-
-// The digits of nb input rows, written over the rows themselves (row b at
-// b * xst floats holds digit j of element i at byte j * (K + kDigitPad) + i).
-// ebits[b] = E_b - 27.  All kT threads; begins and ends with a barrier.
-template <int NB>
-__device__ __forceinline__ void digitize(float *xs, int xst, int nb, int K, float *red, int (&ebits)[NB]) {
-  constexpr int MAXE = kMfmaMaxK / kT;
-  XE_LDS float *X = lptr(xs);
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  lds_barrier();  // the rows are complete (LDS only: the weight loads in flight stay in flight)
-  float mx[NB];
-#pragma unroll
-  for (int b = 0; b < NB; b++) mx[b] = 0.f;
-  for (int i = threadIdx.x; i < K; i += kT)
-#pragma unroll
-    for (int b = 0; b < NB; b++)
-      if (b < nb) mx[b] = fmaxf(mx[b], fabsf(X[b * xst + xpad(i)]));
-  XE_LDS float *r = lptr(red);
-#pragma unroll
-  for (int b = 0; b < NB; b++) {
-    mx[b] = gdev::wave_max(mx[b]);
-    if (lane == 0) r[wave * NB + b] = mx[b];
-  }
-  lds_barrier();
-  float scl[NB];
-#pragma unroll
-  for (int b = 0; b < NB; b++) {
-    float m = 0.f;
-#pragma unroll
-    for (int w = 0; w < kW; w++) m = fmaxf(m, r[w * NB + b]);
-    int e = 0;
-    (void)frexpf(m, &e);  // m = f 2^e, f in [0.5, 1): m < 2^e (e = 0 for m = 0)
-    ebits[b] = e - 27;
-    scl[b] = ldexpf(1.0f, 27 - e);
-  }
-  int xi[NB][MAXE];
-#pragma unroll
-  for (int u = 0; u < MAXE; u++) {
-    const int i = static_cast<int>(threadIdx.x) + u * kT;
-#pragma unroll
-    for (int b = 0; b < NB; b++)
-      xi[b][u] = (i < K && b < nb) ? static_cast<int>(rintf(X[b * xst + xpad(i)] * scl[b])) : 0;
-  }
-  lds_barrier();  // every input element is in registers
-  XE_LDS int8_t *D = reinterpret_cast<XE_LDS int8_t *>(X);
-  const int rs = K + kDigitPad;
-#pragma unroll
-  for (int u = 0; u < MAXE; u++) {
-    const int i = static_cast<int>(threadIdx.x) + u * kT;
-    if (i >= K) break;
-#pragma unroll
-    for (int b = 0; b < NB; b++) {
-      if (b >= nb) break;
-      const int v = xi[b][u];
-      const int a = v < 0 ? -v : v;
-      const int sg = v < 0 ? -1 : 1;
-      XE_LDS int8_t *p = D + b * xst * 4 + i;
-      p[0] = static_cast<int8_t>(sg * (a >> 21));
-      p[rs] = static_cast<int8_t>(sg * ((a >> 14) & 127));
-      p[2 * rs] = static_cast<int8_t>(sg * ((a >> 7) & 127));
-      p[3 * rs] = static_cast<int8_t>(sg * (a & 127));
-    }
-  }
-  lds_barrier();
-}
-
-// fp64 quad sum over lanes 4q .. 4q + 3 (DPP on both halves).
-__device__ __forceinline__ double quad_sum(double v) {
-  auto get = [](double x, auto ctrl) {
-    const uint64_t u = __builtin_bit_cast(uint64_t, x);
-    const uint32_t lo = static_cast<uint32_t>(
-        __builtin_amdgcn_update_dpp(0, static_cast<int>(static_cast<uint32_t>(u)), decltype(ctrl)::value, 0xF, 0xF,
-                                    true));
-    const uint32_t hi = static_cast<uint32_t>(
-        __builtin_amdgcn_update_dpp(0, static_cast<int>(static_cast<uint32_t>(u >> 32)), decltype(ctrl)::value, 0xF,
-                                    0xF, true));
-    return __builtin_bit_cast(double, static_cast<uint64_t>(hi) << 32 | lo);
-  };
-  v += get(v, std::integral_constant<int, gdev::kDppXor1>{});
-  v += get(v, std::integral_constant<int, gdev::kDppXor2>{});
-  return v;
-}
-
-template <int NB, bool HEAD, typename GD, typename Prep, typename Sub>
-__device__ __forceinline__ bool gemv_rows_mfma(const GD &g, int nb, int r0, int r1, float *xs, unsigned ep,
-                                               Prep prep, float *logits, int vocab, int last_max, ArgBest &best,
-                                               Sub tsub, const float *stage, bool staged, float *kred, float *lout,
-                                               int lout_ld, float *red) {
-  // a round = U K blocks of one row block (U x 16 B of weights a lane); two
-  // rounds are in flight (ping-pong), both issued before the input wait
-  constexpr int U = 6;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int K = g.k, nch = K / 16, nkb = (K + 63) / 64;
-  const int nrb = (r1 - r0 + 15) / 16;
-  int S = nrb >= kW ? 1 : kW / max(nrb, 1);
-  S = min(S, nkb);
-  const int items = nrb * S;  // (row block, K segment) pairs; wave w takes w, w + kW, ...
-  // one item a wave when segments meet in LDS or outputs stay in LDS (both
-  // need a barrier before the epilogue)
-  const bool single = S > 1 || g.out_lds;
-  const int xst = xstride(K);
-  const XE_LDS uint8_t *st = reinterpret_cast<const XE_LDS uint8_t *>(lptr(stage));
-  const StageLayout L = stage_layout(XE_I8, r1 - r0, K, g.bias != nullptr);
-  const __amdgpu_buffer_rsrc_t rw = gdev::coherent_rsrc(g.w);
-  const int kg = lane >> 4;  // the lane's 16-byte chunk within a K block
-
-  struct Pos {
-    int it, kb, rb, k0, k1;
-    bool ok;
-  };
-  auto at_item = [&](int it) {
-    Pos p;
-    p.it = it;
-    p.ok = it < items;
-    p.rb = it / S;
-    const int seg = it % S;
-    p.k0 = seg * nkb / S;
-    p.k1 = (seg + 1) * nkb / S;
-    p.kb = p.k0;
-    return p;
-  };
-  auto next_pos = [&](Pos p) {
-    if (!p.ok) return p;
-    p.kb += U;
-    if (p.kb < p.k1) return p;
-    if (single) {
-      p.ok = false;
-      return p;
-    }
-    return at_item(p.it + kW);
-  };
-  // weights of one round (loads past the slice, the row block or the round's
-  // K blocks read zeros: no branch around a load)
-  auto load_round = [&](const Pos &p, i32x4v (&w)[U]) {
-    const int row = r0 + p.rb * 16 + (lane & 15);
-    const bool row_ok = p.ok && row < r1;
-#pragma unroll
-    for (int u = 0; u < U; u++) {
-      const int c = (p.kb + u) * 4 + kg;
-      const bool valid = row_ok && p.kb + u < p.k1 && c < nch;
-      if (staged) {
-        w[u] = *reinterpret_cast<const XE_LDS i32x4v *>(st + (valid ? L.w + (row - r0) * K + c * 16 : 0));
-      } else {
-        w[u] = __builtin_bit_cast(i32x4v, __builtin_amdgcn_raw_buffer_load_b128(rw, valid ? row * K + c * 16
-                                                                                           : kNoRecord, 0,
-                                                                                 kNontemporal));
-      }
-    }
-  };
-
-  Pos p0 = at_item(wave);
-  Pos p1 = next_pos(p0);
-  i32x4v b0[U], b1[U];
-  // the epilogue gives lane (kg, stream, j) row 4 kg + j of its row block;
-  // with one item a wave, that row's constants travel with the first loads
-  const int dj0 = lane & 3;
-  float pre_s = 1.f, pre_b = 0.f;
-  if (!staged) {  // both rounds in flight during the wait
-    load_round(p0, b0);
-    load_round(p1, b1);
-    if (single && p0.ok) {
-      const int row = r0 + p0.rb * 16 + 4 * kg + dj0;
-      const int rr = row < r1 ? row : r0;
-      pre_s = gptr(g.scale)[rr];
-      if (g.bias) pre_b = gptr(g.bias)[rr];
-    }
-  }
-  if (!prep()) return false;
-  if (staged) {  // every wave's stage copies have landed (its own loads, then the barrier)
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    load_round(p0, b0);
-    load_round(p1, b1);
-  }
-  int ebits[NB];
-  digitize<NB>(xs, xst, nb, K, red, ebits);
-  const XE_LDS int8_t *dg = reinterpret_cast<const XE_LDS int8_t *>(lptr(xs));
-  const int dcol = lane & 15, db = dcol >> 2, dj = dcol & 3;
-  const bool bcol = db < nb;
-  const int doff = db * xst * 4 + dj * (K + kDigitPad);
-
-  auto consume = [&](const Pos &p, const i32x4v (&w)[U], i32x4v &acc) {
-#pragma unroll
-    for (int u = 0; u < U; u++) {
-      const int k = (p.kb + u) * 64 + kg * 16;
-      const bool valid = bcol && p.kb + u < p.k1 && k < K;
-      i32x4v x = *reinterpret_cast<const XE_LDS i32x4v *>(dg + (valid ? doff + k : 0));
-      x = valid ? x : i32x4v{0, 0, 0, 0};
-      acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(w[u], x, acc, 0, 0, 0);
-    }
-  };
-  // row value = (C0 2^21 + C1 2^14 + C2 2^7 + C3) 2^(E - 27), exact in fp64.
-  // The quad sum leaves all four row sums in each lane of a stream's quad;
-  // lane j of the quad finishes row 4 kg + j (one output a lane)
-  auto epilogue = [&](int rb, const i32x4v &acc) {
-    double v[4];
-#pragma unroll
-    for (int i = 0; i < 4; i++) v[i] = quad_sum(ldexp(static_cast<double>(acc[i]), 21 - 7 * dj));
-    const double vj = dj == 0 ? v[0] : dj == 1 ? v[1] : dj == 2 ? v[2] : v[3];
-    int eb = ebits[0];
-#pragma unroll
-    for (int b = 1; b < NB; b++) eb = db == b ? ebits[b] : eb;
-    const int row = r0 + rb * 16 + 4 * kg + dj;
-    const bool ok = bcol && row < r1;
-    const int rr = row < r1 ? row : r0;
-    float sc, bi = 0.f;
-    if (staged) {
-      sc = reinterpret_cast<const XE_LDS float *>(st + L.s)[rr - r0];
-      if (g.bias) bi = reinterpret_cast<const XE_LDS float *>(st + L.b)[rr - r0];
-    } else if (single) {
-      sc = pre_s;
-      bi = pre_b;
-    } else {
-      sc = gptr(g.scale)[rr];
-      if (g.bias) bi = gptr(g.bias)[rr];
-    }
-    float t = static_cast<float>(ldexp(vj, eb)) * sc;
-    if (g.bias) t = t + bi;
-    const int b = db;
-    if constexpr (HEAD) {
-      if (!ok) return;
-      if (logits) gptr_w(logits)[static_cast<size_t>(b) * vocab + row] = t;
-#pragma unroll
-      for (int bb = 0; bb < NB; bb++)
-        if (bb == b && sdev::better(t, row, best.v[bb], best.i[bb], last_max)) {
-          best.v[bb] = t;
-          best.i[bb] = row;
-        }
-    } else if (g.act == ACT_GEGLU_TANH) {
-      // (gate, up) pairs start on even rows: the even lane takes its odd
-      // neighbour's value
-      const float up = __int_as_float(
-          __builtin_amdgcn_update_dpp(0, __float_as_int(t), gdev::kDppXor1, 0xF, 0xF, true));
-      if (!ok || (dj & 1)) return;
-      const float o = gdev::gelu_tanh(t) * up;
-      if (g.out_lds) lptr(lout)[b * lout_ld + (row - r0) / 2] = o;
-      else put(g.out, b, row / 2, o, ep);
-    } else {
-      if (!ok) return;
-      float o = t;
-      if (g.act == ACT_RELU) o = o > 0.f ? o : 0.f;
-      else if (g.act == ACT_GELU_ERF) o = gdev::gelu_erf(o);
-      if (g.out_lds) lptr(lout)[b * lout_ld + row - r0] = o;
-      else put(g.out, b, row, o, ep);
-    }
-  };
-
-  // the wave's rounds, flattened over its items; the epilogue of an item
-  // runs after its last round (single: after the loop and the barrier)
-  i32x4v acc = {0, 0, 0, 0};
-  bool first = true;
-  auto step = [&](Pos &p, const Pos &q, i32x4v (&w)[U]) {
-    consume(p, w, acc);
-    if (first) {
-      tsub(1);
-      first = false;
-    }
-    if (!single && (!q.ok || q.it != p.it)) {
-      epilogue(p.rb, acc);
-      acc = i32x4v{0, 0, 0, 0};
-    }
-  };
-  Pos p = p0, q = p1;
-  while (p.ok) {
-    step(p, q, b0);
-    const Pos p2 = next_pos(q);
-    if (p2.ok) load_round(p2, b0);
-    if (!q.ok) break;
-    step(q, p2, b1);
-    const Pos p3 = next_pos(p2);
-    if (p3.ok) load_round(p3, b1);
-    p = p2;
-    q = p3;
-  }
-  if (single) {
-    if (S > 1) {  // the segments of a row block meet in LDS (exact integer sums, segment order)
-      XE_LDS int *kr = reinterpret_cast<XE_LDS int *>(lptr(kred));
-      if (p0.ok)
-#pragma unroll
-        for (int i = 0; i < 4; i++) kr[(wave * 64 + lane) * 4 + i] = acc[i];
-      lds_barrier();
-      if (p0.ok && p0.it % S == 0)
-        for (int s2 = 1; s2 < S; s2++)
-#pragma unroll
-          for (int i = 0; i < 4; i++) acc[i] += kr[((wave + s2) * 64 + lane) * 4 + i];
-    } else {
-      lds_barrier();  // the outputs kept in LDS share bytes with the digits
-    }
-    if (p0.ok && p0.it % S == 0) epilogue(p0.rb, acc);
-  }
-  tsub(2);
-  // no wave leaves while another still reads the digits or the segment sums:
-  // the next phase's LDS writes (its input polls, its gains' LDS-direct
-  // copies into the scratch area) reuse those bytes
-  lds_barrier();
-  return true;
-}
-
 template <int WT, int NB, bool HEAD, typename GD, typename Prep, typename Sub>
 __device__ __forceinline__ bool gemv_any(const GD &g, int nb, int r0, int r1, const float *xs, unsigned ep,
                                          Prep prep, float *logits, int vocab, int last_max, ArgBest &best,
                                          const Ctl &c, Sub tsub, const float *stage = nullptr,
                                          bool staged = false, float *kred = nullptr, float *lout = nullptr,
-                                         int lout_ld = 0, float *red = nullptr) {
+                                         int lout_ld = 0) {
   (void)c;
-  if constexpr (WT == XE_I8) {
-    if (g.mfma)
-      return gemv_rows_mfma<NB, HEAD>(g, nb, r0, r1, const_cast<float *>(xs), ep, prep, logits, vocab, last_max,
-                                      best, tsub, stage, staged, kred, lout, lout_ld, red);
-  }
   return gemv_rows<WT, NB, HEAD>(g, nb, r0, r1, xs, ep, prep, logits, vocab, last_max, best, tsub, stage, staged,
                                  kred, lout, lout_ld);
 }

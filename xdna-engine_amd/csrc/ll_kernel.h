@@ -44,7 +44,7 @@ struct HeadArgs {
   const uint8_t *exps;
   const float *gamma, *beta;
   float *logits;
-  int vocab, d, lpr, rpl, norm, last_max, mfma;
+  int vocab, d, lpr, rpl, norm, last_max;
   float eps;
 };
 struct HeadOut {
@@ -63,7 +63,6 @@ __device__ __noinline__ HeadOut head_gemv(const HeadArgs h, int nb, int r0, int 
   hg.k = h.d;
   hg.lpr = h.lpr;
   hg.rpl = h.rpl;
-  hg.mfma = h.mfma;
   HeadOut o;
 #pragma unroll
   for (int b = 0; b < kMaxNB; b++) {
@@ -77,10 +76,7 @@ __device__ __noinline__ HeadOut head_gemv(const HeadArgs h, int nb, int r0, int 
     norm_rows(xr, nb, h.d, h.norm, h.eps, xin, red, nw);
     return true;
   };
-  // the K-segment sums of the matrix-core form go to the scratch area nw
-  // (its norm gains are read by then)
-  o.ok = gemv_any<WT, NB, true>(hg, nb, r0, r1, xin, ep, prep, h.logits, h.vocab, h.last_max, o.best, c, NoSub{},
-                                nullptr, false, nw, nullptr, 0, red) ? 1 : 0;
+  o.ok = gemv_any<WT, NB, true>(hg, nb, r0, r1, xin, ep, prep, h.logits, h.vocab, h.last_max, o.best, c, NoSub{}) ? 1 : 0;
   return o;
 }
 
@@ -214,7 +210,7 @@ __global__ __launch_bounds__(kT) void ll_step_kernel(StepParams sp) {
           auto tsub = [&](int sub) { mark(step, tslots + 4 + sp.n_a + sp.n_f + kSubSlots * ((is_a ? 0 : sp.n_a) + i) + sub); };
           // K-segment sums go to the scratch area (its norm gains are read by then)
           ok = gemv_any<WT, NB, false>(g, nb, r0, r1, xin, ep, prep, nullptr, 0, 0, none, c, tsub, stage,
-                                       g.staged != 0, scr, xin + g.out_lds, kin, red);
+                                       g.staged != 0, scr, xin + g.out_lds, kin);
           break;
         }
         case LK_ATTN: {
@@ -295,8 +291,7 @@ __global__ __launch_bounds__(kT) void ll_step_kernel(StepParams sp) {
       int r0, r1;
       rank_rows(sp.vocab, static_cast<int>(blockIdx.x), grid, r0, r1);
       const HeadArgs ha{sp.emb, sp.emb_scale, sp.emb_exps, sp.head_gamma, sp.head_beta, sp.logits,
-                        sp.vocab, sp.d, sp.head_lpr, sp.head_rpl, sp.head_norm, sp.last_max, sp.head_mfma,
-                        sp.head_eps};
+                        sp.vocab, sp.d, sp.head_lpr, sp.head_rpl, sp.head_norm, sp.last_max, sp.head_eps};
       const HeadOut ho = head_gemv<WT, NB>(ha, nb, r0, r1, xr, xin, red, scr, ep, c);
       ok = ho.ok != 0;
       best = ho.best;
