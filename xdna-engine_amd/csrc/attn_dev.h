@@ -270,20 +270,8 @@ __device__ __forceinline__ void attn_split_block(const AttnParams &p, int split,
   }
   const float sc2 = p.scale * kLog2e;
 
-  for (int base = base0; base < s1; base += STEP * UK) {
-    Raw8<K8> kv[UK];
-    Raw8<V8> vv[UK];
-    bool ok[UK];
-    if (base == base0 && !appender) {
-#pragma unroll
-      for (int u = 0; u < UK; u++) {
-        kv[u] = kv0[u];
-        vv[u] = vv0[u];
-        ok[u] = ok0[u];
-      }
-    } else {
-      load_block(base, kv, vv, ok);
-    }
+  // one block of UK keys per lane group: scores, online softmax, P.V
+  auto block = [&](const Raw8<K8>(&kv)[UK], const Raw8<V8>(&vv)[UK], const bool(&ok)[UK]) {
     // the block's UK x G partial dot products, then their sums over the L
     // lanes of each key, level by level through DPP and permlane swaps (no
     // LDS crossbar round trips)
@@ -331,6 +319,20 @@ __device__ __forceinline__ void attn_split_block(const AttnParams &p, int split,
 #pragma unroll
         for (int e = 0; e < EPL; e++) acc[g][e] = __builtin_fmaf(pu[u], vv[u].get(e), acc[g][e]);
     }
+  };
+  // two blocks in flight: the next block's loads go out before this block's
+  // arithmetic (keys past the range read key s0 and are masked)
+  constexpr int BS = STEP * UK;
+  Raw8<K8> kb[UK];
+  Raw8<V8> vb[UK];
+  bool ob[UK];
+  if (appender) load_block(base0, kv0, vv0, ok0);
+  for (int base = base0; base < s1; base += 2 * BS) {
+    load_block(base + BS, kb, vb, ob);
+    block(kv0, vv0, ok0);
+    if (base + BS >= s1) break;
+    load_block(base + 2 * BS, kv0, vv0, ok0);
+    block(kb, vb, ob);
   }
 
   // ---- merge lane groups inside the wave ----

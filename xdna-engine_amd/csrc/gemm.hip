@@ -32,7 +32,7 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kBM = 64, kBN = 64, kBK = 64;
+constexpr int kBN = 64, kBK = 64;
 constexpr int kGT = 256;             // threads
 constexpr int kXS = kBK + 8;         // LDS row stride (bf16) of a staged part
 constexpr int kNoRec = 0x7ffffff0;  // past every buffer: loads return zeros
@@ -142,6 +142,91 @@ __device__ __forceinline__ void epilogue4(const gdev::GemvParams &p, int wdtype,
   }
 }
 
+// This thread's 16 activations (row srow, k sk .. sk + 15 of the step) split
+// into three bf16 parts by truncation, x = hi + mid + lo exactly, stored in
+// the LDS tile of each part.
+__device__ __forceinline__ void stage_parts(const f32x4 (&x)[4], uint16_t (*xs)[kBN * kXS], int srow, int sk) {
+  uint32_t hp[8], mp[8], lp[8];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const float v[4] = {x[i].x, x[i].y, x[i].z, x[i].w};
+    float h[4], m[4], l[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      h[q] = trunc_bf16(v[q]);
+      const float r = v[q] - h[q];
+      m[q] = trunc_bf16(r);
+      l[q] = trunc_bf16(r - m[q]);
+    }
+    hp[2 * i] = pack_hi16(h[0], h[1]);
+    hp[2 * i + 1] = pack_hi16(h[2], h[3]);
+    mp[2 * i] = pack_hi16(m[0], m[1]);
+    mp[2 * i + 1] = pack_hi16(m[2], m[3]);
+    lp[2 * i] = pack_hi16(l[0], l[1]);
+    lp[2 * i + 1] = pack_hi16(l[2], l[3]);
+  }
+  uint32_t *dh = reinterpret_cast<uint32_t *>(xs[0] + srow * kXS + sk);
+  uint32_t *dm = reinterpret_cast<uint32_t *>(xs[1] + srow * kXS + sk);
+  uint32_t *dl = reinterpret_cast<uint32_t *>(xs[2] + srow * kXS + sk);
+  *reinterpret_cast<u32x4 *>(dh) = u32x4{hp[0], hp[1], hp[2], hp[3]};
+  *reinterpret_cast<u32x4 *>(dh + 4) = u32x4{hp[4], hp[5], hp[6], hp[7]};
+  *reinterpret_cast<u32x4 *>(dm) = u32x4{mp[0], mp[1], mp[2], mp[3]};
+  *reinterpret_cast<u32x4 *>(dm + 4) = u32x4{mp[4], mp[5], mp[6], mp[7]};
+  *reinterpret_cast<u32x4 *>(dl) = u32x4{lp[0], lp[1], lp[2], lp[3]};
+  *reinterpret_cast<u32x4 *>(dl + 4) = u32x4{lp[4], lp[5], lp[6], lp[7]};
+}
+
+// Split-K tail, after every wave of the workgroup has stored its partial
+// tile ws[tile][z][b][r] with agent-scope stores: the workgroup counts itself
+// in cnt[tile]; the last one to arrive adds the partials in split order (the
+// same order on every run), runs the epilogue and re-arms the counter.
+template <int WT, int BM>
+__device__ __forceinline__ void splitk_finish(const gdev::GemvParams &p, float *ws, unsigned *cnt, int tile, int ks,
+                                              int nb, int m0, int b0, int &last) {
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's partial stores have completed
+  __syncthreads();
+  if (threadIdx.x == 0)
+    last = __hip_atomic_fetch_add(cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == static_cast<unsigned>(ks - 1);
+  __syncthreads();
+  if (!last) return;
+  // the reduction: item = (stream bb, row quad q), two items a thread per
+  // round; every split's partial of both items in flight at once (ks <=
+  // kMaxSplitsK), then summed in split order
+  const __amdgpu_buffer_rsrc_t rws = gdev::coherent_rsrc(ws + static_cast<size_t>(tile) * ks * (BM * kBN));
+  const int items = nb * (BM / 4);
+  for (int it0 = threadIdx.x; it0 < items; it0 += 2 * kGT) {
+    f32x4 v[2][kMaxSplitsK];
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+      const int it = it0 + r * kGT;
+      const int bb = it / (BM / 4), q = it % (BM / 4);
+#pragma unroll
+      for (int zz = 0; zz < kMaxSplitsK; zz++)
+        v[r][zz] = __builtin_bit_cast(
+            f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                       rws, zz < ks && it < items ? ((zz * kBN + bb) * BM + 4 * q) * 4 : kNoRec, 0, gdev::kCoherentSc1));
+    }
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+      const int it = it0 + r * kGT;
+      if (it >= items) continue;
+      const int bb = it / (BM / 4), q = it % (BM / 4);
+      float sum[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int zz = 0; zz < kMaxSplitsK; zz++) {
+        if (zz < ks) {
+          sum[0] += v[r][zz].x;
+          sum[1] += v[r][zz].y;
+          sum[2] += v[r][zz].z;
+          sum[3] += v[r][zz].w;
+        }
+      }
+      epilogue4(p, WT, m0 + 4 * q, b0 + bb, sum);
+    }
+  }
+  if (threadIdx.x == 0) __hip_atomic_store(cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Split-K: blockIdx.z takes K steps [z * spk, (z + 1) * spk).  With more than
 // one split, each workgroup stores its partial tile (agent-scope stores) in
 // ws[tile][z][b][r] and counts itself in cnt[tile]; the last one to arrive
@@ -150,10 +235,10 @@ __device__ __forceinline__ void epilogue4(const gdev::GemvParams &p, int wdtype,
 // MB: MFMA row blocks per wave (the wave's 16 * MB weight rows share each
 // activation fragment read from LDS); a workgroup covers 64 * MB rows.
 template <int WT, int MB>
-__global__ __launch_bounds__(kGT) void gemm_kernel(gdev::GemvParams p, float *ws, unsigned *cnt, int spk) {
+__global__ __launch_bounds__(kGT) __attribute__((amdgpu_waves_per_eu(2))) void gemm_kernel(gdev::GemvParams p, float *ws, unsigned *cnt, int spk) {
   constexpr int BM = 64 * MB;
-  // three parts x [kBN][kXS] bf16
-  __shared__ __attribute__((aligned(16))) uint16_t xs[3][kBN * kXS];
+  // two buffers (step parity) x three parts x [kBN][kXS] bf16
+  __shared__ __attribute__((aligned(16))) uint16_t xs[2][3][kBN * kXS];
   __shared__ int last;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int m0 = blockIdx.x * BM, b0 = blockIdx.y * kBN;
@@ -171,24 +256,29 @@ __global__ __launch_bounds__(kGT) void gemm_kernel(gdev::GemvParams p, float *ws
   const int wk = 16 * (lane >> 4);
   // activation staging: thread t stages row t / 4, k (t % 4) * 16 .. + 16
   const int srow = threadIdx.x >> 2, sk = (threadIdx.x & 3) * 16;
-  const bool srow_ok = srow < nb;
 
-  // three-stage pipeline: the weights and activations of steps s + 1 and
-  // s + 2 are in flight while step s computes
+  // pipeline of NS stages: the weights and activations of the next NS - 1
+  // steps are in flight while a step computes (b = 64 probe, QKV / O /
+  // gate-up / down: 12.9 / 12.5 / 20.5 / 18.9 us at two stages, 13.3 / 13.0
+  // / 21.2 / 19.5 at three, 13.5 / 13.2 / 21.6 / 20.1 at four: with two
+  // waves per SIMD the other wave covers the latency the deeper stages would)
+  constexpr int NS = 2;
   struct Stage {
     WLoad<WT> w[MB];
     f32x4 x[4];
   };
-  // k past this split's end reads zeros.  (One per-lane bound, no uniform
-  // "step is live" flag: the compiler would unswitch on it, issue each load
-  // twice and wait for the first before the second.)
+  // k at or past xlim reads zeros: one per-lane bound folds "row exists" and
+  // "k inside this split" into one compare (a separate loop-invariant flag
+  // gets the loads unswitched into branches that wait for every load in
+  // flight)
   const int kend = min(K, (step0 + nsteps) * kBK);
+  const int xlim = srow < nb ? kend : 0;
+  const int xrow = (b0 + srow) * p.ldx;
   auto issue = [&](int step, Stage &st) {
     const int k = (step0 + step) * kBK + sk;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-      const bool ok = srow_ok && k + 4 * i < kend;
-      const int off = ok ? ((b0 + srow) * p.ldx + k + 4 * i) * 4 : kNoRec;
+      const int off = k + 4 * i < xlim ? (xrow + k + 4 * i) * 4 : kNoRec;
       st.x[i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, 0));
     }
     const int kw = (step0 + step) * kBK + wk;
@@ -205,72 +295,70 @@ __global__ __launch_bounds__(kGT) void gemm_kernel(gdev::GemvParams p, float *ws
 #pragma unroll
     for (int j = 0; j < 4; j++) acc[mb][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+  // Step s stages into LDS buffer s & 1 and reads it after one barrier: a
+  // wave writes buffer s & 1 only after the barrier of step s - 1, which
+  // every wave reaches after its reads of step s - 2.  Column blocks past the
+  // batch hold zeros (their rows load as zeros) and are computed anyway: a
+  // uniform branch per block keeps the scheduler from hoisting the reads.
   auto compute = [&](int step, const Stage &st) {
-    if (step >= nsteps) return;  // uniform
-    // stage this step's activations as three bf16 parts
-    uint32_t hp[8], mp[8], lp[8];
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const float v[4] = {st.x[i].x, st.x[i].y, st.x[i].z, st.x[i].w};
-      float h[4], m[4], l[4];
-#pragma unroll
-      for (int q = 0; q < 4; q++) {
-        h[q] = trunc_bf16(v[q]);
-        const float r = v[q] - h[q];
-        m[q] = trunc_bf16(r);
-        l[q] = trunc_bf16(r - m[q]);
-      }
-      hp[2 * i] = pack_hi16(h[0], h[1]);
-      hp[2 * i + 1] = pack_hi16(h[2], h[3]);
-      mp[2 * i] = pack_hi16(m[0], m[1]);
-      mp[2 * i + 1] = pack_hi16(m[2], m[3]);
-      lp[2 * i] = pack_hi16(l[0], l[1]);
-      lp[2 * i + 1] = pack_hi16(l[2], l[3]);
-    }
-    if (step > 0) __syncthreads();  // the previous step's reads are done
-    uint32_t *dh = reinterpret_cast<uint32_t *>(xs[0] + srow * kXS + sk);
-    uint32_t *dm = reinterpret_cast<uint32_t *>(xs[1] + srow * kXS + sk);
-    uint32_t *dl = reinterpret_cast<uint32_t *>(xs[2] + srow * kXS + sk);
-    *reinterpret_cast<u32x4 *>(dh) = u32x4{hp[0], hp[1], hp[2], hp[3]};
-    *reinterpret_cast<u32x4 *>(dh + 4) = u32x4{hp[4], hp[5], hp[6], hp[7]};
-    *reinterpret_cast<u32x4 *>(dm) = u32x4{mp[0], mp[1], mp[2], mp[3]};
-    *reinterpret_cast<u32x4 *>(dm + 4) = u32x4{mp[4], mp[5], mp[6], mp[7]};
-    *reinterpret_cast<u32x4 *>(dl) = u32x4{lp[0], lp[1], lp[2], lp[3]};
-    *reinterpret_cast<u32x4 *>(dl + 4) = u32x4{lp[4], lp[5], lp[6], lp[7]};
+    uint16_t(*xb)[kBN * kXS] = xs[step & 1];
+    stage_parts(st.x, xb, srow, sk);
     __syncthreads();
     bf16x8 a0[MB], a1[MB];
 #pragma unroll
     for (int mb = 0; mb < MB; mb++) to_bf16<WT>(st.w[mb], a0[mb], a1[mb]);
+    // a part's eight fragments are read before its MFMAs (all reads in
+    // flight at once); with one row block the next part's reads also go out
+    // before the current part's MFMAs (more row blocks: the registers are
+    // worth more than the overlap)
+    constexpr int RA = MB == 1 ? 2 : 1;
+    bf16x8 bx[RA][4][2];
+    auto rd = [&](int part, bf16x8(&d)[4][2]) {
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-      if (16 * j < nb) {  // column blocks past the batch are skipped (uniform)
-        const int brow = 16 * j + (lane & 15);
-#pragma unroll
-        for (int part = 0; part < 3; part++) {
-          const uint16_t *src = xs[part] + brow * kXS + wk;
-          const bf16x8 x0 = *reinterpret_cast<const bf16x8 *>(src);
-          const bf16x8 x1 = *reinterpret_cast<const bf16x8 *>(src + 8);
-#pragma unroll
-          for (int mb = 0; mb < MB; mb++) {
-            acc[mb][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0[mb], x0, acc[mb][j], 0, 0, 0);
-            acc[mb][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1[mb], x1, acc[mb][j], 0, 0, 0);
-          }
-        }
+      for (int j = 0; j < 4; j++) {
+        const uint16_t *src = xb[part] + (16 * j + (lane & 15)) * kXS + wk;
+        d[j][0] = *reinterpret_cast<const bf16x8 *>(src);
+        d[j][1] = *reinterpret_cast<const bf16x8 *>(src + 8);
       }
+    };
+    if constexpr (RA == 2) rd(0, bx[0]);
+#pragma unroll
+    for (int part = 0; part < 3; part++) {
+      if constexpr (RA == 2) {
+        if (part < 2) rd(part + 1, bx[(part + 1) & 1]);
+      } else {
+        rd(part, bx[0]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int h = 0; h < 2; h++)
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+#pragma unroll
+          for (int mb = 0; mb < MB; mb++)
+            acc[mb][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(h ? a1[mb] : a0[mb], bx[part % RA][j][h],
+                                                                  acc[mb][j], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
     }
   };
 
-  Stage sa, sb, sc;
-  issue(0, sa);
-  issue(1, sb);
-  for (int st = 0; st < nsteps; st += 3) {
-    issue(st + 2, sc);
-    compute(st, sa);
-    issue(st + 3, sa);
-    compute(st + 1, sb);
-    issue(st + 4, sb);
-    compute(st + 2, sc);
+  // Whole groups of NS steps, then the remainder (its stages are already in
+  // flight).  No step inside the loop is conditional: a conditional step
+  // makes the compiler wait for every load in flight at the loop's head.
+  Stage sg[NS];
+#pragma unroll
+  for (int j = 0; j < NS - 1; j++) issue(j, sg[j]);
+  int s0 = 0;
+  for (; s0 + NS <= nsteps; s0 += NS) {
+#pragma unroll
+    for (int j = 0; j < NS; j++) {
+      issue(s0 + j + NS - 1, sg[(j + NS - 1) % NS]);
+      compute(s0 + j, sg[j]);
+    }
   }
+#pragma unroll
+  for (int j = 0; j < NS - 1; j++)
+    if (s0 + j < nsteps) compute(s0 + j, sg[j]);
 
   // lane holds rows rl(mb) + i (i = 0..3) of column block j's stream
   if (ks == 1) {
@@ -300,36 +388,7 @@ __global__ __launch_bounds__(kGT) void gemm_kernel(gdev::GemvParams p, float *ws
         __hip_atomic_store(part + b * BM + rl + i, acc[mb][j][i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
-  __builtin_amdgcn_s_waitcnt(0);  // this wave's partial stores have completed
-  __syncthreads();
-  if (threadIdx.x == 0)
-    last = __hip_atomic_fetch_add(cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == static_cast<unsigned>(ks - 1);
-  __syncthreads();
-  if (!last) return;
-  // the reduction: item = (stream bb, row quad q); every split's partial in
-  // flight at once (ks <= kMaxSplitsK), then summed in split order
-  const __amdgpu_buffer_rsrc_t rws = gdev::coherent_rsrc(ws + static_cast<size_t>(tile) * ks * (BM * kBN));
-  for (int it = threadIdx.x; it < nb * (BM / 4); it += kGT) {
-    const int bb = it / (BM / 4), q = it % (BM / 4);
-    f32x4 v[kMaxSplitsK];
-#pragma unroll
-    for (int zz = 0; zz < kMaxSplitsK; zz++)
-      v[zz] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                            rws, zz < ks ? ((zz * kBN + bb) * BM + 4 * q) * 4 : kNoRec, 0,
-                                            gdev::kCoherentSc1));
-    float sum[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int zz = 0; zz < kMaxSplitsK; zz++) {
-      if (zz < ks) {
-        sum[0] += v[zz].x;
-        sum[1] += v[zz].y;
-        sum[2] += v[zz].z;
-        sum[3] += v[zz].w;
-      }
-    }
-    epilogue4(p, WT, m0 + 4 * q, b0 + bb, sum);
-  }
-  if (threadIdx.x == 0) __hip_atomic_store(cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  splitk_finish<WT, BM>(p, ws, cnt, tile, ks, nb, m0, b0, last);
 }
 
 // Norm / residual prologue of one stream row (blockIdx.x): p.x, p.sub and
