@@ -13,12 +13,19 @@
 //   Accumulation is fp32.  Numerically this is the fp32 GEMV of the b <= 8
 //   path up to summation order, so greedy streams stay the oracle's.
 //
-// Workgroup: 4 waves, 64 weight rows (16 per wave) x 64 streams (4 MFMA
-// column blocks), K in steps of 64.  The activation tile of a step is staged
-// in LDS as its three parts, the next step's weights and activations are
-// loaded before the current step's MFMAs.  Within a lane's 16 contiguous k
-// the two MFMAs of a step take k 0..7 and 8..15: the A and B operands use
-// the same k permutation, so the dot products are unchanged.
+// Two kernels share these operand rules:
+//   gemm_ks_kernel (the decoder's projections): a workgroup tile of 16, 32 or
+//   64 weight rows x 64 streams whose four waves split every 128-k step; each
+//   lane loads its own operands straight into registers, and the waves'
+//   partial tiles meet in LDS once, after the K loop.
+//   gemm_kernel (outputs too wide for one workgroup a CU: the lm-head): 4
+//   waves, 64 * MB weight rows x 64 streams, K in steps of 64; the
+//   activation tile of a step is staged in LDS as its three parts, the next
+//   step's weights and activations are loaded before the current step's
+//   MFMAs.  Within a lane's 16 contiguous k the two MFMAs of a step take k
+//   0..7 and 8..15: the A and B operands use the same k permutation, so the
+//   dot products are unchanged.
+// Both split K across workgroups when the tiles leave most CUs idle.
 //
 // The norm / residual prologue of a GEMV phase (gemv_dev.h gemv_prologue)
 // runs as its own kernel, one workgroup per stream row, writing the
@@ -391,6 +398,245 @@ __global__ __launch_bounds__(kGT) __attribute__((amdgpu_waves_per_eu(2))) void g
   splitk_finish<WT, BM>(p, ws, cnt, tile, ks, nb, m0, b0, last);
 }
 
+// ---- K-sliced GEMM: no LDS staging inside the K loop ----
+//
+// Workgroup tile: 64 weight rows x 64 streams, K in steps of 128.  Wave w
+// takes k 32 w .. 32 w + 31 of every step for the whole tile (4 row blocks x
+// 4 stream blocks = 16 MFMA blocks, 48 MFMAs a step with the three activation
+// planes), so no operand is shared between waves: a lane loads the 8
+// activations and the 8 weights of each block it feeds straight into
+// registers (k 8 * (lane / 16) .. + 7 of the wave's slice, the same k for the
+// A and B operands), splits the activations into their bf16 planes and
+// converts the weights in registers.  The four waves' partial tiles are added
+// in LDS in wave order once, after the K loop.
+constexpr int kKsBK = 128;  // k per step (32 per wave)
+
+template <int WT>
+struct WLoad8 {  // one lane's 8 weights of one row block (raw)
+  uint32_t q[WT == XE_BF16 ? 4 : (WT == XE_I4 ? 1 : 2)];
+  uint32_t e;  // bfp16: the block's exponent byte
+};
+
+template <int WT>
+__device__ __forceinline__ void load_w8(const __amdgpu_buffer_rsrc_t &rw, const __amdgpu_buffer_rsrc_t &re, int row,
+                                        int k, bool ok, int K, WLoad8<WT> &o) {
+  typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+  if constexpr (WT == XE_I4) {
+    o.q[0] = __builtin_amdgcn_raw_buffer_load_b32(rw, ok ? row * (K / 2) + k / 2 : kNoRec, 0, 2);
+  } else if constexpr (WT == XE_BF16) {
+    const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, ok ? (row * K + k) * 2 : kNoRec, 0, 2));
+    o.q[0] = v.x;
+    o.q[1] = v.y;
+    o.q[2] = v.z;
+    o.q[3] = v.w;
+  } else {
+    const u32x2 v = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rw, ok ? row * K + k : kNoRec, 0, 2));
+    o.q[0] = v.x;
+    o.q[1] = v.y;
+    if constexpr (WT == XE_BFP16)
+      o.e = __builtin_amdgcn_raw_buffer_load_b8(re, ok ? row * (K / 8) + k / 8 : kNoRec, 0, 2);
+  }
+}
+
+// bf16 A operand (8 k) of one row block.
+template <int WT>
+__device__ __forceinline__ bf16x8 to_bf16x8(const WLoad8<WT> &w) {
+  if constexpr (WT == XE_BF16) {
+    return __builtin_bit_cast(bf16x8, u32x4{w.q[0], w.q[1], w.q[2], w.q[3]});
+  } else if constexpr (WT == XE_I4) {
+    uint32_t p[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int word = static_cast<int>(w.q[0]);
+      // (the builtin's result type is unsigned: convert through int)
+      const float f0 = static_cast<float>(static_cast<int>(__builtin_amdgcn_sbfe(word, 8 * i, 4)));
+      const float f1 = static_cast<float>(static_cast<int>(__builtin_amdgcn_sbfe(word, 8 * i + 4, 4)));
+      p[i] = pack_hi16(f0, f1);
+    }
+    return __builtin_bit_cast(bf16x8, u32x4{p[0], p[1], p[2], p[3]});
+  } else {
+    uint32_t p[4];
+    const int e = WT == XE_BFP16 ? static_cast<int>(w.e & 0xffu) - 133 : 0;
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+      float f[4];
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        f[j] = static_cast<float>(static_cast<int>(static_cast<int8_t>(w.q[i] >> (8 * j))));
+        if constexpr (WT == XE_BFP16) f[j] = __builtin_ldexpf(f[j], e);
+      }
+      p[2 * i] = pack_hi16(f[0], f[1]);
+      p[2 * i + 1] = pack_hi16(f[2], f[3]);
+    }
+    return __builtin_bit_cast(bf16x8, u32x4{p[0], p[1], p[2], p[3]});
+  }
+}
+
+// Three bf16 planes of 8 fp32 activations, x = hi + mid + lo exactly (each
+// plane takes the next 8 significant bits by truncation).
+__device__ __forceinline__ void split3(const f32x4 &x0, const f32x4 &x1, bf16x8 (&o)[3]) {
+  const float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+  float r[8], l[8];
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    r[i] = v[i] - trunc_bf16(v[i]);
+    l[i] = r[i] - trunc_bf16(r[i]);
+  }
+  uint32_t h[4], m[4], w[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    h[i] = pack_hi16(v[2 * i], v[2 * i + 1]);
+    m[i] = pack_hi16(r[2 * i], r[2 * i + 1]);
+    w[i] = pack_hi16(l[2 * i], l[2 * i + 1]);
+  }
+  o[0] = __builtin_bit_cast(bf16x8, u32x4{h[0], h[1], h[2], h[3]});
+  o[1] = __builtin_bit_cast(bf16x8, u32x4{m[0], m[1], m[2], m[3]});
+  o[2] = __builtin_bit_cast(bf16x8, u32x4{w[0], w[1], w[2], w[3]});
+}
+
+template <int WT, int MB>
+__global__ __launch_bounds__(kGT) void gemm_ks_kernel(gdev::GemvParams p, float *ws, unsigned *cnt, int spk) {
+  constexpr int BM = 16 * MB;
+  // the four waves' partial tiles [wave][stream][row] (row stride padded)
+  constexpr int kRS = BM + 4;
+  __shared__ __attribute__((aligned(16))) float red[4][kBN * kRS];
+  __shared__ int last;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int m0 = blockIdx.x * BM, b0 = blockIdx.y * kBN;
+  const int K = p.k;
+  const int ks = gridDim.z, z = blockIdx.z;
+  const int step0 = z * spk;
+  const int nsteps = min((K + kKsBK - 1) / kKsBK, step0 + spk) - step0;
+  const int nb = min(kBN, p.batch - b0);
+  const __amdgpu_buffer_rsrc_t rw = gdev::coherent_rsrc(p.w);
+  const __amdgpu_buffer_rsrc_t re = gdev::coherent_rsrc(WT == XE_BFP16 ? static_cast<const void *>(p.exps) : p.w);
+  const __amdgpu_buffer_rsrc_t rx = gdev::coherent_rsrc(p.x);
+
+  // this lane's k within a step, its weight row in block 0 and its stream in
+  // stream block 0
+  const int lk = 32 * wave + 8 * (lane >> 4);
+  const int lr = lane & 15;
+  const int kend = min(K, (step0 + nsteps) * kKsBK);
+  // activation rows past the batch read zeros (xlim 0); k past the split too
+  int xoff[4], xlim[4];
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const int b = 16 * j + lr;
+    xoff[j] = (b0 + b) * p.ldx;
+    xlim[j] = b < nb ? kend : 0;
+  }
+
+  struct Stage {
+    WLoad8<WT> w[MB];
+    f32x4 x[4][2];
+  };
+  auto issue = [&](int step, Stage &st) {
+    const int k = (step0 + step) * kKsBK + lk;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const bool ok = k < xlim[j];
+      st.x[j][0] = __builtin_bit_cast(
+          f32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, ok ? (xoff[j] + k) * 4 : kNoRec, 0, 0));
+      st.x[j][1] = __builtin_bit_cast(
+          f32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, ok ? (xoff[j] + k + 4) * 4 : kNoRec, 0, 0));
+    }
+#pragma unroll
+    for (int mb = 0; mb < MB; mb++) {
+      const int row = m0 + 16 * mb + lr;
+      load_w8<WT>(rw, re, row, k, row < p.m && k < kend, K, st.w[mb]);
+    }
+  };
+
+  f32x4 acc[MB][4];
+#pragma unroll
+  for (int mb = 0; mb < MB; mb++)
+#pragma unroll
+    for (int j = 0; j < 4; j++) acc[mb][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // the MFMAs of one stream block interleave the row blocks, and with fewer
+  // than four row blocks the stream blocks too (at least four independent
+  // accumulators between two MFMAs on the same one)
+  auto compute = [&](const Stage &st) {
+    bf16x8 a[MB];
+#pragma unroll
+    for (int mb = 0; mb < MB; mb++) a[mb] = to_bf16x8<WT>(st.w[mb]);
+    constexpr int JG = MB >= 4 ? 1 : 4 / MB;  // stream blocks a group
+#pragma unroll
+    for (int j0 = 0; j0 < 4; j0 += JG) {
+      bf16x8 bx[JG][3];
+#pragma unroll
+      for (int jj = 0; jj < JG; jj++) split3(st.x[j0 + jj][0], st.x[j0 + jj][1], bx[jj]);
+#pragma unroll
+      for (int pl = 0; pl < 3; pl++)
+#pragma unroll
+        for (int jj = 0; jj < JG; jj++)
+#pragma unroll
+          for (int mb = 0; mb < MB; mb++)
+            acc[mb][j0 + jj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[mb], bx[jj][pl], acc[mb][j0 + jj], 0, 0, 0);
+    }
+  };
+
+  // two stages: the next step's loads are in flight while a step computes
+  // (three or four stages measured no faster at b = 64)
+  Stage s0, s1;
+  issue(0, s0);
+  int s = 0;
+  for (; s + 2 <= nsteps; s += 2) {
+    issue(s + 1, s1);
+    // the loads go out before this step's arithmetic waits for its own
+    __builtin_amdgcn_sched_barrier(0);
+    compute(s0);
+    issue(s + 2, s0);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(s1);
+  }
+  if (s < nsteps) compute(s0);
+
+  // the waves' partial tiles into LDS: lane holds rows 16 mb + 4 (lane / 16)
+  // + i of stream 16 j + lane % 16
+#pragma unroll
+  for (int mb = 0; mb < MB; mb++)
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+      *reinterpret_cast<f32x4 *>(&red[wave][(16 * j + lr) * kRS + 16 * mb + 4 * (lane >> 4)]) = acc[mb][j];
+  __syncthreads();
+  // item = (stream bb, row quad q): 64 x BM / 4 items, MB a thread
+  constexpr int QN = BM / 4;
+  float sum[MB][4];
+#pragma unroll
+  for (int r = 0; r < MB; r++) {
+    const int it = threadIdx.x + r * kGT;
+    const int bb = it / QN, q = it % QN;
+    f32x4 t = *reinterpret_cast<const f32x4 *>(&red[0][bb * kRS + 4 * q]);
+#pragma unroll
+    for (int w = 1; w < 4; w++) t += *reinterpret_cast<const f32x4 *>(&red[w][bb * kRS + 4 * q]);
+    sum[r][0] = t.x;
+    sum[r][1] = t.y;
+    sum[r][2] = t.z;
+    sum[r][3] = t.w;
+  }
+  if (ks == 1) {
+#pragma unroll
+    for (int r = 0; r < MB; r++) {
+      const int it = threadIdx.x + r * kGT;
+      const int bb = it / QN, q = it % QN;
+      if (bb < nb) epilogue4(p, WT, m0 + 4 * q, b0 + bb, sum[r]);
+    }
+    return;
+  }
+  const int tile = blockIdx.y * gridDim.x + blockIdx.x;
+  float *part = ws + (static_cast<size_t>(tile) * ks + z) * (BM * kBN);
+#pragma unroll
+  for (int r = 0; r < MB; r++) {
+    const int it = threadIdx.x + r * kGT;
+    const int bb = it / QN, q = it % QN;
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+      __hip_atomic_store(part + bb * BM + 4 * q + i, sum[r][i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  splitk_finish<WT, BM>(p, ws, cnt, tile, ks, nb, m0, b0, last);
+}
+
 // Norm / residual prologue of one stream row (blockIdx.x): p.x, p.sub and
 // p.res_out point at row 0 and advance by ldx / k per row; the normalised
 // row goes to xn [batch][k].
@@ -416,6 +662,26 @@ GemmFn pick_mb(int mb) {
     case 1: return gemm_kernel<WT, 1>;
     case 2: return gemm_kernel<WT, 2>;
     case 4: return gemm_kernel<WT, 4>;
+  }
+  return nullptr;
+}
+
+template <int WT>
+GemmFn pick_ks_mb(int mb) {
+  switch (mb) {
+    case 1: return gemm_ks_kernel<WT, 1>;
+    case 2: return gemm_ks_kernel<WT, 2>;
+    case 4: return gemm_ks_kernel<WT, 4>;
+  }
+  return nullptr;
+}
+
+GemmFn pick_ks(int wdtype, int mb) {
+  switch (wdtype) {
+    case XE_I8: return pick_ks_mb<XE_I8>(mb);
+    case XE_BF16: return pick_ks_mb<XE_BF16>(mb);
+    case XE_BFP16: return pick_ks_mb<XE_BFP16>(mb);
+    case XE_I4: return pick_ks_mb<XE_I4>(mb);
   }
   return nullptr;
 }
@@ -463,6 +729,36 @@ GemmShape gemm_shape(int m, int k, int batch) {
   return g;
 }
 
+// Shape of a K-sliced launch, or mb = 0 where none fits the chip in one
+// round (outputs wider than 64 rows a CU: the lm-head).  Candidates: 1, 2 or
+// 4 row blocks a wave, each with the most splits of K that keep the grid
+// within one workgroup per CU and at least two steps a split; the one with
+// the least work a workgroup (row blocks x steps) wins, ties to more row
+// blocks.  (b = 64 probe, us: QKV 1536 x 1152 9.5-10.2 against 12.8 for
+// gemm_kernel, O 1152 x 1024 9.4-10.3 against 12.6, gate/up 13824 x 1152
+// 18.7 against 20.5, down 1152 x 6912 18.6 against 18.9.)
+GemmShape gemm_ks_shape(int m, int k, int batch) {
+  const int steps = (k + kKsBK - 1) / kKsBK;
+  const int cus = gdev::cu_count();
+  const int tb = (batch + kBN - 1) / kBN;
+  GemmShape best{0, 1, steps, 0, tb};
+  int best_work = 0;
+  for (int mb = 4; mb >= 1; mb /= 2) {
+    const int tm = (m + 16 * mb - 1) / (16 * mb);
+    const int tiles = tm * tb;
+    if (tiles > cus) continue;
+    int ks = std::max(1, std::min(std::min(cus / tiles, steps / 2), kMaxSplitsK));
+    while (ks > 1 && static_cast<size_t>(tiles) * ks * 16 * mb * kBN > kGemmWsFloats) ks--;
+    const int spk = (steps + ks - 1) / ks;
+    const int work = mb * spk;
+    if (best.mb == 0 || work < best_work) {
+      best = GemmShape{mb, (steps + spk - 1) / spk, spk, tm, tb};
+      best_work = work;
+    }
+  }
+  return best;
+}
+
 }  // namespace
 
 bool gemm_needs_prologue(const gdev::GemvParams &p) { return p.sub != nullptr || p.norm != XE_NORM_NONE; }
@@ -493,8 +789,15 @@ void launch_gemm(const gdev::GemvParams &p, int wdtype, float *ws, unsigned *cnt
   const size_t wb = static_cast<size_t>(p.m) * p.k * (wdtype == XE_BF16 ? 2 : 1);
   XE_REQUIRE(wb < (size_t(1) << 31) && static_cast<size_t>(p.batch) * p.ldx * 4 < (size_t(1) << 31),
              "gemm: operand above 2 GB");
-  const GemmShape g = gemm_shape(p.m, p.k, p.batch);
-  GemmFn fn = pick_gemm(wdtype, g.mb);
+  GemmShape g = gemm_shape(p.m, p.k, p.batch);
+  GemmFn fn = nullptr;
+  const GemmShape gk = gemm_ks_shape(p.m, p.k, p.batch);
+  if (gk.mb > 0) {
+    g = gk;
+    fn = pick_ks(wdtype, g.mb);
+  } else {
+    fn = pick_gemm(wdtype, g.mb);
+  }
   XE_REQUIRE(fn, "gemm: unsupported weight dtype");
   XE_REQUIRE(g.ks == 1 || (ws && cnt && static_cast<size_t>(g.tm) * g.tb <= kGemmMaxTiles),
              "gemm: split-K workspace missing or too many tiles");
