@@ -494,14 +494,43 @@ __device__ __forceinline__ void split3(const f32x4 &x0, const f32x4 &x1, bf16x8 
   o[2] = __builtin_bit_cast(bf16x8, u32x4{w[0], w[1], w[2], w[3]});
 }
 
+// Coalesced operand loads through a wave-private LDS slice.  An MFMA operand
+// puts 16 different rows on consecutive lanes, so loading it straight from
+// memory makes every quad of lanes touch four cache lines (four times the
+// address-unit cycles of a contiguous quad: measured, this bound the kernel).
+// Each wave therefore loads its k-slice of the step row by row (4 or 8
+// consecutive lanes on one row), stores it to its own LDS area as is, and
+// reads the operands back in MFMA layout.  LDS traffic of one wave is
+// ordered, so no barrier is needed.
+template <int WT>
+constexpr int w_slice_dw() {  // dwords of one row's 32-k weight slice
+  return WT == XE_BF16 ? 16 : (WT == XE_I4 ? 4 : 8);
+}
+constexpr int kXD = 36;  // LDS row stride (dwords) of a wave's 32-k activation slice
+
+template <int WT, int MB>
+__host__ __device__ constexpr int ks_stage_dw() {  // LDS dwords of one wave's slices
+  return 64 * kXD + 16 * MB * (w_slice_dw<WT>() + 4);
+}
+
+template <int WT, int MB>
+__host__ __device__ constexpr int ks_lds_dw() {
+  return 4 * ks_stage_dw<WT, MB>() > 4 * kBN * (16 * MB + 4) ? 4 * ks_stage_dw<WT, MB>() : 4 * kBN * (16 * MB + 4);
+}
+
 template <int WT, int MB>
 __global__ __launch_bounds__(kGT) void gemm_ks_kernel(gdev::GemvParams p, float *ws, unsigned *cnt, int spk) {
   constexpr int BM = 16 * MB;
-  // the four waves' partial tiles [wave][stream][row] (row stride padded)
+  constexpr int WD = w_slice_dw<WT>(), WDP = WD + 4;
+  // the waves' operand slices during the K loop; afterwards the four waves'
+  // partial tiles [wave][stream][row] (row stride padded)
   constexpr int kRS = BM + 4;
-  __shared__ __attribute__((aligned(16))) float red[4][kBN * kRS];
+  __shared__ __attribute__((aligned(16))) uint32_t lds[ks_lds_dw<WT, MB>()];
+  float(*red)[kBN * kRS] = reinterpret_cast<float(*)[kBN * kRS]>(lds);
   __shared__ int last;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  uint32_t *xst = lds + wave * ks_stage_dw<WT, MB>();  // [64][kXD]
+  uint32_t *wst = xst + 64 * kXD;                       // [BM][WDP]
   const int m0 = blockIdx.x * BM, b0 = blockIdx.y * kBN;
   const int K = p.k;
   const int ks = gridDim.z, z = blockIdx.z;
@@ -512,38 +541,60 @@ __global__ __launch_bounds__(kGT) void gemm_ks_kernel(gdev::GemvParams p, float 
   const __amdgpu_buffer_rsrc_t re = gdev::coherent_rsrc(WT == XE_BFP16 ? static_cast<const void *>(p.exps) : p.w);
   const __amdgpu_buffer_rsrc_t rx = gdev::coherent_rsrc(p.x);
 
-  // this lane's k within a step, its weight row in block 0 and its stream in
-  // stream block 0
-  const int lk = 32 * wave + 8 * (lane >> 4);
-  const int lr = lane & 15;
+  // MFMA layout: lane feeds row / stream lane % 16 of a block with k
+  // 8 * (lane / 16) .. + 7 of the wave's 32-k slice
+  const int lr = lane & 15, lq = lane >> 4;
   const int kend = min(K, (step0 + nsteps) * kKsBK);
-  // activation rows past the batch read zeros (xlim 0); k past the split too
-  int xoff[4], xlim[4];
+  // coalesced activation loads: instruction i, lane -> stream row 8 i +
+  // lane / 8, 16 bytes at k 4 (lane % 8); rows past the batch read zeros
+  const int xr = lane >> 3, xc = 4 * (lane & 7);
+  int xoff[8], xlim[8];
 #pragma unroll
-  for (int j = 0; j < 4; j++) {
-    const int b = 16 * j + lr;
-    xoff[j] = (b0 + b) * p.ldx;
-    xlim[j] = b < nb ? kend : 0;
+  for (int i = 0; i < 8; i++) {
+    const int b = 8 * i + xr;
+    xoff[i] = (b0 + b) * p.ldx + xc;
+    xlim[i] = b < nb ? kend : 0;
   }
+  // coalesced weight loads: instruction mb, lane -> row 16 mb + lane / 4,
+  // a quarter of its 32-k slice
+  const int wr = lane >> 2, wq = lane & 3;
 
   struct Stage {
-    WLoad8<WT> w[MB];
-    f32x4 x[4][2];
+    uint32_t w[MB][WD / 4];
+    uint32_t e[MB];  // bfp16: exponent byte (MFMA layout)
+    f32x4 x[8];
   };
   auto issue = [&](int step, Stage &st) {
-    const int k = (step0 + step) * kKsBK + lk;
+    const int k0 = (step0 + step) * kKsBK + 32 * wave;
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-      const bool ok = k < xlim[j];
-      st.x[j][0] = __builtin_bit_cast(
-          f32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, ok ? (xoff[j] + k) * 4 : kNoRec, 0, 0));
-      st.x[j][1] = __builtin_bit_cast(
-          f32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, ok ? (xoff[j] + k + 4) * 4 : kNoRec, 0, 0));
-    }
+    for (int i = 0; i < 8; i++)
+      st.x[i] = __builtin_bit_cast(
+          f32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, k0 < xlim[i] ? (xoff[i] + k0) * 4 : kNoRec, 0, 0));
 #pragma unroll
     for (int mb = 0; mb < MB; mb++) {
-      const int row = m0 + 16 * mb + lr;
-      load_w8<WT>(rw, re, row, k, row < p.m && k < kend, K, st.w[mb]);
+      const int row = m0 + 16 * mb + wr;
+      const bool ok = row < p.m && k0 < kend;
+      if constexpr (WT == XE_BF16) {
+        const u32x4 v = __builtin_bit_cast(
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, ok ? (row * K + k0 + 8 * wq) * 2 : kNoRec, 0, 2));
+        st.w[mb][0] = v.x;
+        st.w[mb][1] = v.y;
+        st.w[mb][2] = v.z;
+        st.w[mb][3] = v.w;
+      } else if constexpr (WT == XE_I4) {
+        st.w[mb][0] = __builtin_amdgcn_raw_buffer_load_b32(rw, ok ? row * (K / 2) + k0 / 2 + 4 * wq : kNoRec, 0, 2);
+      } else {
+        typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+        const u32x2 v =
+            __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rw, ok ? row * K + k0 + 8 * wq : kNoRec, 0, 2));
+        st.w[mb][0] = v.x;
+        st.w[mb][1] = v.y;
+      }
+      if constexpr (WT == XE_BFP16) {
+        const int erow = m0 + 16 * mb + lr, ek = k0 + 8 * lq;
+        st.e[mb] = __builtin_amdgcn_raw_buffer_load_b8(re, erow < p.m && ek < kend ? erow * (K / 8) + ek / 8 : kNoRec,
+                                                      0, 2);
+      }
     }
   };
 
@@ -557,15 +608,41 @@ __global__ __launch_bounds__(kGT) void gemm_ks_kernel(gdev::GemvParams p, float 
   // than four row blocks the stream blocks too (at least four independent
   // accumulators between two MFMAs on the same one)
   auto compute = [&](const Stage &st) {
+    // the step's slices into LDS as loaded
+#pragma unroll
+    for (int i = 0; i < 8; i++) *reinterpret_cast<f32x4 *>(xst + (8 * i + xr) * kXD + xc) = st.x[i];
+#pragma unroll
+    for (int mb = 0; mb < MB; mb++) {
+      uint32_t *d = wst + (16 * mb + wr) * WDP + wq * (WD / 4);
+      if constexpr (WD / 4 == 4) {
+        *reinterpret_cast<u32x4 *>(d) = u32x4{st.w[mb][0], st.w[mb][1], st.w[mb][2], st.w[mb][3]};
+      } else if constexpr (WD / 4 == 2) {
+        typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+        *reinterpret_cast<u32x2 *>(d) = u32x2{st.w[mb][0], st.w[mb][1]};
+      } else {
+        d[0] = st.w[mb][0];
+      }
+    }
+    // and back in MFMA layout
     bf16x8 a[MB];
 #pragma unroll
-    for (int mb = 0; mb < MB; mb++) a[mb] = to_bf16x8<WT>(st.w[mb]);
+    for (int mb = 0; mb < MB; mb++) {
+      const uint32_t *src = wst + (16 * mb + lr) * WDP + lq * (WD / 4);
+      WLoad8<WT> wl;
+#pragma unroll
+      for (int i = 0; i < WD / 4; i++) wl.q[i] = src[i];
+      if constexpr (WT == XE_BFP16) wl.e = st.e[mb];
+      a[mb] = to_bf16x8<WT>(wl);
+    }
     constexpr int JG = MB >= 4 ? 1 : 4 / MB;  // stream blocks a group
 #pragma unroll
     for (int j0 = 0; j0 < 4; j0 += JG) {
       bf16x8 bx[JG][3];
 #pragma unroll
-      for (int jj = 0; jj < JG; jj++) split3(st.x[j0 + jj][0], st.x[j0 + jj][1], bx[jj]);
+      for (int jj = 0; jj < JG; jj++) {
+        const uint32_t *src = xst + (16 * (j0 + jj) + lr) * kXD + 8 * lq;
+        split3(*reinterpret_cast<const f32x4 *>(src), *reinterpret_cast<const f32x4 *>(src + 4), bx[jj]);
+      }
 #pragma unroll
       for (int pl = 0; pl < 3; pl++)
 #pragma unroll
@@ -591,6 +668,7 @@ __global__ __launch_bounds__(kGT) void gemm_ks_kernel(gdev::GemvParams p, float 
     compute(s1);
   }
   if (s < nsteps) compute(s0);
+  __syncthreads();  // every wave is done with its slices: the LDS becomes red
 
   // the waves' partial tiles into LDS: lane holds rows 16 mb + 4 (lane / 16)
   // + i of stream 16 j + lane % 16
