@@ -159,6 +159,9 @@ def greedy_identity(got, om, prompt, label, eps=1e-3):
     if parted:
         om.reset()
         exact, total = replay_stream(om, prompt, got, eps, label + "-replay")
-        assert exact >= 0.99 * total, (label, exact, total)
+        # every token is already within 2 * eps of the oracle's max; at most
+        # 1 % of them (at least one, for runs shorter than 100 tokens) may be
+        # such near-ties rather than the oracle's own argmax
+        assert total - exact <= max(1, total // 100), (label, exact, total)
     print("[%s] %d streams x %d tokens; %d parted at ties %s; min top-2 margin %.3g"
           % (label, got.shape[0], got.shape[1], len(parted), parted, rec["min_margin"]), flush=True)

@@ -703,14 +703,15 @@ __global__ __launch_bounds__(kGT) void gemm_ks_kernel(gdev::GemvParams p, float 
     return;
   }
   const int tile = blockIdx.y * gridDim.x + blockIdx.x;
-  float *part = ws + (static_cast<size_t>(tile) * ks + z) * (BM * kBN);
+  // the partial tile with 16-byte sc1 stores (what an agent-scope atomic
+  // store compiles to, four dwords at a time)
+  const __amdgpu_buffer_rsrc_t rp = gdev::coherent_rsrc(ws + (static_cast<size_t>(tile) * ks + z) * (BM * kBN));
 #pragma unroll
   for (int r = 0; r < MB; r++) {
     const int it = threadIdx.x + r * kGT;
     const int bb = it / QN, q = it % QN;
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-      __hip_atomic_store(part + bb * BM + 4 * q + i, sum[r][i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, f32x4{sum[r][0], sum[r][1], sum[r][2], sum[r][3]}),
+                                           rp, (bb * BM + 4 * q) * 4, 0, gdev::kCoherentSc1);
   }
   splitk_finish<WT, BM>(p, ws, cnt, tile, ks, nb, m0, b0, last);
 }
@@ -810,11 +811,13 @@ GemmShape gemm_shape(int m, int k, int batch) {
 // Shape of a K-sliced launch, or mb = 0 where none fits the chip in one
 // round (outputs wider than 64 rows a CU: the lm-head).  Candidates: 1, 2 or
 // 4 row blocks a wave, each with the most splits of K that keep the grid
-// within one workgroup per CU and at least two steps a split; the one with
-// the least work a workgroup (row blocks x steps) wins, ties to more row
-// blocks.  (b = 64 probe, us: QKV 1536 x 1152 9.5-10.2 against 12.8 for
-// gemm_kernel, O 1152 x 1024 9.4-10.3 against 12.6, gate/up 13824 x 1152
-// 18.7 against 20.5, down 1152 x 6912 18.6 against 18.9.)
+// within one workgroup per CU and at least two steps a split; the cheapest
+// by a cost fitted to b = 64 probes wins (ties to more row blocks): a step
+// costs 2 units for the activation slice plus one a row block, and a split
+// tile's reduction half a unit a row block a split.  (b = 64, us: QKV 1536 x
+// 1152 8.7 / 9.0 / 12.2 at 1 / 2 / 4 row blocks, O 1152 x 1024 7.5 / 8.5 /
+// 11.7, gate/up 13824 x 1152 - / - / 16.6, down 1152 x 6912 18.6 / 14.3 /
+// 16.2; gemm_kernel: 12.8, 12.6, 20.5, 18.9.)
 GemmShape gemm_ks_shape(int m, int k, int batch) {
   const int steps = (k + kKsBK - 1) / kKsBK;
   const int cus = gdev::cu_count();
@@ -828,9 +831,10 @@ GemmShape gemm_ks_shape(int m, int k, int batch) {
     int ks = std::max(1, std::min(std::min(cus / tiles, steps / 2), kMaxSplitsK));
     while (ks > 1 && static_cast<size_t>(tiles) * ks * 16 * mb * kBN > kGemmWsFloats) ks--;
     const int spk = (steps + ks - 1) / ks;
-    const int work = mb * spk;
+    const int kss = (steps + spk - 1) / spk;
+    const int work = 2 * spk * (2 + mb) + (kss > 1 ? mb * kss : 0);
     if (best.mb == 0 || work < best_work) {
-      best = GemmShape{mb, (steps + spk - 1) / spk, spk, tm, tb};
+      best = GemmShape{mb, kss, spk, tm, tb};
       best_work = work;
     }
   }
