@@ -205,9 +205,10 @@ def run_batch(xe, dev, cfg, args, B, steps, warmup, profile):
         # the phase-kernel family with the most device time in one profiled
         # step at the end context: the projections (MFMA GEMM beyond 8
         # streams, GEMV up to 8) or the attention partials + merge
-        proj = "gemm_kernel" if B > 8 else "gemv_kernel"
+        proj = ("gemm_ks_kernel (layer projections) + gemm_kernel (lm-head)" if B > 8 else
+                "gemv_kernel")
         fams = {
-            "%s (projections: phases gemv_qkv / o / gateup / down / lmhead)" % proj:
+            "%s (phases gemv_qkv / o / gateup / down / lmhead)" % proj:
                 [(u, b) for l, u, b in prof if l.startswith("gemv") and not l.endswith("_pro")],
             "attn_kernel + attn_merge_kernel (self-attention over the cache)":
                 [(u, b) for l, u, b in prof if l.startswith("attn")],
