@@ -124,14 +124,29 @@ __device__ __forceinline__ void to_bf16(const WLoad<WT> &w, bf16x8 &a0, bf16x8 &
   }
 }
 
-// Epilogue of rows r0 .. r0 + 3 (a GeGLU pair each half) of stream b.
-__device__ __forceinline__ void epilogue4(const gdev::GemvParams &p, int wdtype, int r0, int b, const float (&acc)[4]) {
-  float t[4];
+// Row scales and biases of rows r0 .. r0 + 3 (1 and 0 where absent).
+struct RowQuad {
+  float s[4], b[4];
+};
+
+__device__ __forceinline__ RowQuad load_quad(const gdev::GemvParams &p, int wdtype, int r0) {
+  RowQuad q;
 #pragma unroll
   for (int i = 0; i < 4; i++) {
     const int r = min(r0 + i, p.m - 1);
-    t[i] = acc[i] * ((wdtype == XE_I8 || wdtype == XE_I4) ? p.scale[r] : 1.0f) + (p.bias ? p.bias[r] : 0.0f);
+    q.s[i] = (wdtype == XE_I8 || wdtype == XE_I4) ? p.scale[r] : 1.0f;
+    q.b[i] = p.bias ? p.bias[r] : 0.0f;
   }
+  return q;
+}
+
+// Epilogue of rows r0 .. r0 + 3 (a GeGLU pair each half) of stream b, with
+// their scales and biases already loaded.
+__device__ __forceinline__ void epilogue4(const gdev::GemvParams &p, const RowQuad &rq, int r0, int b,
+                                          const float (&acc)[4]) {
+  float t[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) t[i] = acc[i] * rq.s[i] + rq.b[i];
   float *yrow = p.y + static_cast<size_t>(b) * p.ldy;
   if (p.act == ACT_GEGLU_TANH) {
 #pragma unroll
@@ -147,6 +162,10 @@ __device__ __forceinline__ void epilogue4(const gdev::GemvParams &p, int wdtype,
       yrow[r0 + i] = v * p.out_scale;
     }
   }
+}
+
+__device__ __forceinline__ void epilogue4(const gdev::GemvParams &p, int wdtype, int r0, int b, const float (&acc)[4]) {
+  epilogue4(p, load_quad(p, wdtype, r0), r0, b, acc);
 }
 
 // This thread's 16 activations (row srow, k sk .. sk + 15 of the step) split
@@ -188,8 +207,10 @@ __device__ __forceinline__ void stage_parts(const f32x4 (&x)[4], uint16_t (*xs)[
 // in cnt[tile]; the last one to arrive adds the partials in split order (the
 // same order on every run), runs the epilogue and re-arms the counter.
 template <int WT, int BM>
+// rq: this thread's row quad, prefetched (its q is the same in every item
+// the thread takes), or null.
 __device__ __forceinline__ void splitk_finish(const gdev::GemvParams &p, float *ws, unsigned *cnt, int tile, int ks,
-                                              int nb, int m0, int b0, int &last) {
+                                              int nb, int m0, int b0, int &last, const RowQuad *rq = nullptr) {
   __builtin_amdgcn_s_waitcnt(0);  // this wave's partial stores have completed
   __syncthreads();
   if (threadIdx.x == 0)
@@ -228,7 +249,8 @@ __device__ __forceinline__ void splitk_finish(const gdev::GemvParams &p, float *
           sum[3] += v[r][zz].w;
         }
       }
-      epilogue4(p, WT, m0 + 4 * q, b0 + bb, sum);
+      if (rq) epilogue4(p, *rq, m0 + 4 * q, b0 + bb, sum);
+      else epilogue4(p, WT, m0 + 4 * q, b0 + bb, sum);
     }
   }
   if (threadIdx.x == 0) __hip_atomic_store(cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -598,6 +620,10 @@ __global__ __launch_bounds__(kGT) void gemm_ks_kernel(gdev::GemvParams p, float 
     }
   };
 
+  // the epilogue's row scales and biases, in flight during the K loop: a
+  // thread's items all have row quad threadIdx.x % (BM / 4)
+  const RowQuad rq = load_quad(p, WT, m0 + 4 * (static_cast<int>(threadIdx.x) % (BM / 4)));
+
   f32x4 acc[MB][4];
 #pragma unroll
   for (int mb = 0; mb < MB; mb++)
@@ -698,7 +724,7 @@ __global__ __launch_bounds__(kGT) void gemm_ks_kernel(gdev::GemvParams p, float 
     for (int r = 0; r < MB; r++) {
       const int it = threadIdx.x + r * kGT;
       const int bb = it / QN, q = it % QN;
-      if (bb < nb) epilogue4(p, WT, m0 + 4 * q, b0 + bb, sum[r]);
+      if (bb < nb) epilogue4(p, rq, m0 + 4 * q, b0 + bb, sum[r]);
     }
     return;
   }
@@ -713,7 +739,7 @@ __global__ __launch_bounds__(kGT) void gemm_ks_kernel(gdev::GemvParams p, float 
     __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, f32x4{sum[r][0], sum[r][1], sum[r][2], sum[r][3]}),
                                            rp, (bb * BM + 4 * q) * 4, 0, gdev::kCoherentSc1);
   }
-  splitk_finish<WT, BM>(p, ws, cnt, tile, ks, nb, m0, b0, last);
+  splitk_finish<WT, BM>(p, ws, cnt, tile, ks, nb, m0, b0, last, &rq);
 }
 
 // Norm / residual prologue of one stream row (blockIdx.x): p.x, p.sub and
