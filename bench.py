@@ -19,6 +19,9 @@ Extra fields of the JSON line:
                 per-launch events in one profiled step at the end context.
   hbm           whole-step algorithmic bytes (weights + scales + KV read at
                 the mean context of the timed steps) / measured step time
+  configs       BASELINE configs 1 and 4: OPT-125m b=1, Whisper-small b=1 and
+                b=32 greedy decode tok/s, beside the reference's own published
+                per-token times for those workloads (other hardware)
   batch64       the metric's second batch size (config 5 at b = 64): the same
                 workload for 64 streams, the whole decode to ctx 4096 timed
                 (projections on the MFMA GEMM path); its roofline is the whole
@@ -404,6 +407,50 @@ def run_kernels(args):
             "kernels": recs}
 
 
+def run_configs(xe, dev):
+    """BASELINE configs 1 and 4, the workloads the reference publishes its own
+    per-token times for (OPT-125m host CPU path 47
+    ms/token, README.md:38; Whisper-small fused decoder ~75 ms/token on the
+    XDNA2 NPU, docs/data-movement-thesis.md:41; batched B=16 lockstep 16.13
+    ms/step, scripts/measure_phase2_sweep.sh:81).  Greedy decode of seeded
+    synthetic int8 weights, timed with the device synchronised on both sides;
+    the prompt is fed untimed.  Whisper decodes against a synthetic encoder
+    output (1500 frames, N(0, 1) rounded to bf16)."""
+    res = {}
+    runs = [("opt125m_b1", xe.OPT_125M, 0, 1, 32, 128),
+            ("whisper_small_b1", xe.WHISPER_SMALL, 1, 1, 4, 224),
+            ("whisper_small_b32", xe.WHISPER_SMALL, 1, 32, 4, 224)]
+    ref_ms = {"opt125m_b1": (47.0, "reference host CPU path, README.md:38"),
+              "whisper_small_b1": (75.0, "reference fused decoder on the XDNA2 NPU, "
+                                         "docs/data-movement-thesis.md:41"),
+              "whisper_small_b32": (16.13 / 16.0, "reference B=16 lockstep on the XDNA2 NPU, per "
+                                                  "stream-token, scripts/measure_phase2_sweep.sh:81")}
+    for name, cfg, seed, B, n_prompt, n_new in runs:
+        dec = xe.Decoder(dev, cfg, max_batch=B)
+        dec.init_synthetic(seed)
+        if cfg.family == xe.XE_WHISPER:
+            dec.precompute_cross(None)
+        rng = np.random.default_rng(seed)
+        dec.feed(rng.integers(0, cfg.vocab, (B, n_prompt)).astype(np.int32))
+        dec.decode(8, want_tokens=False)  # warm-up (also builds the step's plan)
+        dev.synchronize()
+        t0 = time.perf_counter()
+        dec.decode(n_new - 8, want_tokens=False)
+        dev.synchronize()
+        el = time.perf_counter() - t0
+        k = n_new - 8
+        ms_tok = el / k * 1e3
+        rms, rsrc = ref_ms[name]
+        res[name] = {"tok_s": round(B * k / el, 1), "ms_per_step": round(ms_tok, 4), "batch": B,
+                     "executor": dec.executor(B), "timed_steps": k,
+                     "workload": "%s int8, prompt %d, greedy steps %d..%d" % (
+                         name.split("_b")[0], n_prompt, n_prompt + 8, n_prompt + n_new - 1),
+                     "reference_ms_per_token": rms, "reference": rsrc,
+                     "speedup_vs_reference": round(rms / (ms_tok / B), 1)}
+        dec.close()
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -417,6 +464,8 @@ def main():
     ap.add_argument("--seed", type=int, default=2)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip BASELINE configs 1 and 4 (OPT-125m, Whisper-small decode)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only copy MIB MiB device to device (the library's streaming copy "
                          "kernel), three times: the plain copy that scales rocprofv3's "
@@ -481,6 +530,8 @@ def main():
         # the metric's second batch size: the whole decode to ctx, timed the same way
         out["batch%d" % args.batch2] = run_batch(xe, dev, cfg, args, args.batch2, 0, args.warmup,
                                                  profile=False)
+    if not args.no_configs:
+        out["configs"] = run_configs(xe, dev)
     dev.close()
     if not args.no_cpu:
         first, last = head["config"]["timed_positions"]
