@@ -321,6 +321,47 @@ def test_norm_gemm_int8_batched(gpu, xe, m, k, b):
     close(got, want)
 
 
+# The decoder's b = 64 projection shapes, every weight type: together they
+# take each tile height of the K-sliced kernel (16, 32 and 64 rows), its
+# split-K tail (QKV, O, down) and the unsplit path (gate/up), plus the
+# wide-output kernel: a 65536-row output, more 64-row tiles than CUs (the
+# lm-head's path), takes gemm_kernel.
+GEMM_SHAPES = [(1536, 1152), (1152, 1024), (13824, 1152), (1152, 6912), (65536, 1152)]
+
+
+@pytest.mark.parametrize("m,k", GEMM_SHAPES)
+@pytest.mark.parametrize("wd", ["i8", "i4", "bf16", "bfp16"])
+def test_gemm_b64_decoder_shapes(gpu, xe, m, k, wd):
+    """64 streams through the MFMA GEMM against the oracle's GEMV of the same
+    stored weights (fp32 activations, fp32 accumulation)."""
+    dev, ctx = gpu
+    b = 64
+    print("[case] GEMM %s m=%d k=%d b=%d" % (wd, m, k, b), flush=True)
+    rng = np.random.default_rng(m + 7 * k + len(wd))
+    x = rng.standard_normal((b, k)).astype(np.float32)
+    if wd == "i8":
+        q = rng.integers(-127, 128, (m, k)).astype(np.int8)
+        s = rng.uniform(0.001, 0.02, m).astype(np.float32)
+        w = ctx.register_weight_q8(q, s)
+        want = O.gemv_i8(x, q, s)
+    elif wd == "i4":
+        w_kn = (rng.standard_normal((k, m)) * 0.02).astype(np.float32)
+        qk, s = O.quant_cols_i4(w_kn)
+        w = ctx.register_weight_q4_kn(qk, s, None)
+        want = O.lin_fwd_i4_kn(x, qk, s, None)
+    elif wd == "bf16":
+        wbits = O.bf16_bits((rng.standard_normal((m, k)) * 0.02).astype(np.float32))
+        w = ctx.register_weight_bf16(wbits)
+        want = O.gemv_bf16w(x, wbits)
+    else:
+        mant, exps = O.bfp16_encode((rng.standard_normal((m, k)) * 0.02).astype(np.float32))
+        w = ctx.register_weight_bfp16(mant, exps)
+        want = O.gemv_bfp16(x, mant, exps)
+    got = ctx.gemv(w, x)
+    w.free()
+    close(got, want)
+
+
 # ---- int4 weights (Lin int4 branch, opt125m_decode.rs:63-105) ----
 
 @pytest.mark.parametrize("m,k", [(768, 768), (3072, 768), (768, 3072), (6912, 1152)])
