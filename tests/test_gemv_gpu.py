@@ -326,7 +326,8 @@ def test_norm_gemm_int8_batched(gpu, xe, m, k, b):
 # split-K tail (QKV, O, down) and the unsplit path (gate/up), plus the
 # wide-output kernel: a 65536-row output, more 64-row tiles than CUs (the
 # lm-head's path), takes gemm_kernel.
-GEMM_SHAPES = [(1536, 1152), (1152, 1024), (13824, 1152), (1152, 6912), (65536, 1152)]
+GEMM_SHAPES = [(1536, 1152), (1152, 1024), (13824, 1152), (1152, 6912), (65536, 1152),
+               (1000, 1040), (72, 48)]  # ragged: K % 32 == 16, rows not a tile multiple
 
 
 @pytest.mark.parametrize("m,k", GEMM_SHAPES)

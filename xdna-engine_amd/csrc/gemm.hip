@@ -591,11 +591,12 @@ __global__ __launch_bounds__(kGT) void gemm_ks_kernel(gdev::GemvParams p, float 
 #pragma unroll
     for (int i = 0; i < 8; i++)
       st.x[i] = __builtin_bit_cast(
-          f32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, k0 < xlim[i] ? (xoff[i] + k0) * 4 : kNoRec, 0, 0));
+          f32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, k0 + xc < xlim[i] ? (xoff[i] + k0) * 4 : kNoRec, 0, 0));
 #pragma unroll
     for (int mb = 0; mb < MB; mb++) {
+      // per lane: with K % 32 == 16 the last step's slice ends inside a row
       const int row = m0 + 16 * mb + wr;
-      const bool ok = row < p.m && k0 < kend;
+      const bool ok = row < p.m && k0 + 8 * wq < kend;
       if constexpr (WT == XE_BF16) {
         const u32x4 v = __builtin_bit_cast(
             u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, ok ? (row * K + k0 + 8 * wq) * 2 : kNoRec, 0, 2));
