@@ -38,6 +38,7 @@ AttnParams to_params(const AttnLaunch &L) {
   p.max_splits = L.max_splits;
   p.k_scale = L.k_scale;
   p.v_scale = L.v_scale;
+  p.cnt = L.cnt;
   return p;
 }
 
@@ -107,10 +108,12 @@ int kv8_of(const AttnParams &p) { return (p.k_scale ? 1 : 0) | (p.v_scale ? 2 : 
 
 }  // namespace
 
-// One attention phase of a step: split partials or the merge.
+// One attention phase of a step: split partials or the merge (none with
+// arrival counters: the split kernel merges in place).
 void launch_attn_phase(const sdev::Phase &ph, hipStream_t s) {
   const AttnParams &p = ph.u.attn;
   const bool merge = ph.kind == sdev::PH_MERGE;
+  if (merge && p.cnt) return;
   AttnFn fn = pick(ph.hd, ph.g, merge, kv8_of(p));
   XE_REQUIRE(fn, "attn phase: unsupported head_dim / group (int8 K/V: one query head a KV head)");
   if (merge) {
@@ -173,7 +176,7 @@ void launch_attn(const AttnLaunch &L, hipStream_t s) {
   XE_REQUIRE(!kv8_of(p) || !L.k_new, "attn: int8 K/V caches take no append");
   hipLaunchKernelGGL(fn, dim3(L.max_splits, L.hkv, L.batch), dim3(kThreads), 0, s, p);
   XE_HIP(hipGetLastError());
-  if (L.max_splits > 1) {
+  if (L.max_splits > 1 && !L.cnt) {
     const int blocks = (g * L.hd + kThreads - 1) / kThreads;
     hipLaunchKernelGGL(merge, dim3(blocks, L.hkv, L.batch), dim3(kThreads), 0, s, p);
     XE_HIP(hipGetLastError());

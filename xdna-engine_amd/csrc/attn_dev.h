@@ -20,10 +20,14 @@
 //     (m, l, acc) to the workspace (or the output when one split covers the
 //     whole length).
 // A "merge block" finishes 256 of the G*hd outputs of one (stream, kv head)
-// from the split partials.  Partials and merge are separate phases (separate
-// launches, or separate phases of the persistent step kernel): a
-// last-arriving-block merge needs device-scope release/acquire fences, which
-// write back and invalidate L2 on this part and measured ~80 us per launch.
+// from the split partials, as a phase of its own (a launch, or a phase of the
+// persistent step kernel).  With arrival counters (AttnParams::cnt) the
+// standalone split kernel merges in place instead: each split block stores
+// its partial with sc1 stores (past the XCD's own L2), waits for them, counts
+// itself in the (stream, kv head)'s counter with an agent-scope atomic, and
+// the last to arrive reads every partial with sc1 loads and writes the output
+// (no device-scope release/acquire fences: those write back and invalidate L2
+// on this part and measured ~80 us per launch).
 // Fused in front (decode step): the Gemma per-head RMSNorm (1 + w) and RoPE of
 // q and the new k, and the bf16 append of the new k/v at position pos, done
 // by the block whose range holds pos (the only one that reads it).
@@ -71,6 +75,8 @@ struct AttnParams {
   float *work;
   int max_splits;
   const float *k_scale, *v_scale;  // int8 K / V channel scales [hkv * hd], or null (bf16)
+  unsigned *cnt;  // [batch * hkv] arrival counters (zero between launches): merge in the
+                  // split kernel; null: a merge phase follows
 };
 
 __device__ __forceinline__ uint16_t f32_to_bf16_rne(float x) {
@@ -182,6 +188,109 @@ struct Raw8 {
       return __uint_as_float((e & 1) ? (w[e >> 1] & 0xffff0000u) : (w[e >> 1] << 16));
   }
 };
+
+// Phase 1 of a merge, heads [g0, g0 + ng) of one (stream, kv head) (waves
+// over heads, lanes over splits): wts[hh][s] = exp2(m_s - M) with M the
+// largest m_s, lsum[hh] = sum_s l_s wts[hh][s].  wbase: the partials of the
+// (stream, kv head), head g's split s at (g * max_splits + s) * (HD + 2).
+template <int HD, bool LDCOH>
+__device__ __forceinline__ void merge_weights(const AttnParams &p, const float *wbase, int nsplits, int g0, int ng,
+                                              float *wts, float *lsum) {
+  constexpr int RS = HD + 2;  // floats of one partial: m, l, acc[HD]
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  for (int hh = wave; hh < ng; hh += kWaves) {
+    const int row = (g0 + hh) * p.max_splits;
+    float ls = 0.f;
+    if (nsplits <= 64) {  // one split a lane: m and l in one round trip
+      const bool on = lane < nsplits;
+      const int src = (row + (on ? lane : 0)) * RS;
+      const float ms = act_ld<LDCOH>(wbase, src), lv = act_ld<LDCOH>(wbase, src + 1);
+      float mx = on ? ms : -INFINITY;
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+      const float f = !on || ms == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ms - mx);
+      if (on) {
+        wts[hh * kMaxSplits + lane] = f;
+        ls = lv * f;
+      }
+    } else {
+      float mx = -INFINITY;
+      for (int sidx = lane; sidx < nsplits; sidx += 64) mx = fmaxf(mx, act_ld<LDCOH>(wbase, (row + sidx) * RS));
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+      for (int sidx = lane; sidx < nsplits; sidx += 64) {
+        const int src = (row + sidx) * RS;
+        const float ms = act_ld<LDCOH>(wbase, src);
+        const float f = ms == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ms - mx);
+        wts[hh * kMaxSplits + sidx] = f;
+        ls += act_ld<LDCOH>(wbase, src + 1) * f;
+      }
+    }
+    ls = wave_sum(ls);
+    if (lane == 0) lsum[hh] = ls;
+  }
+}
+
+// Merges heads [g0, g0 + ng) of (stream b, kv head kvh) from the nsplits
+// partials: out = sum_s acc_s w_s / sum_s l_s w_s (even and odd splits summed
+// apart, in split order, then added).  A thread takes outputs threadIdx.x +
+// j * kThreads, j < NE (ng * HD <= NE * kThreads).  The acc values of splits
+// [0, 8) are loaded before phase 1, so with at most 8 splits the merge takes
+// one memory round trip.  LDCOH: sc1 loads of the partials; STCOH:
+// agent-scope output stores.  lds: ng * (kMaxSplits + 1) floats.
+template <int HD, int G, int NE, bool LDCOH, bool STCOH>
+__device__ __forceinline__ void merge_heads(const AttnParams &p, int kvh, int b, int nsplits, int g0, int ng,
+                                            float *lds) {
+  constexpr int RS = HD + 2;
+  constexpr int SC = 8;  // splits a thread holds in registers at once
+  float *wts = lds;                     // [ng][kMaxSplits]
+  float *lsum = lds + ng * kMaxSplits;  // [ng]
+  const float *wbase = p.work + (static_cast<size_t>(b) * p.hq + kvh * G) * p.max_splits * RS;
+  int src[NE], hw[NE];
+  bool ok[NE];
+  float at0[NE], at1[NE], v[SC][NE];
+#pragma unroll
+  for (int j = 0; j < NE; j++) {
+    const int t = threadIdx.x + j * kThreads;
+    ok[j] = t < ng * HD;
+    const int hh = ok[j] ? t / HD : 0, e = t % HD;
+    src[j] = (g0 + hh) * p.max_splits * RS + 2 + e;
+    hw[j] = hh * kMaxSplits;
+    at0[j] = 0.f;
+    at1[j] = 0.f;
+  }
+  auto load = [&](int s0) {
+#pragma unroll
+    for (int u = 0; u < SC; u++)
+#pragma unroll
+      for (int j = 0; j < NE; j++)
+        v[u][j] = ok[j] && s0 + u < nsplits ? act_ld<LDCOH>(wbase, src[j] + (s0 + u) * RS) : 0.f;
+  };
+  load(0);
+  merge_weights<HD, LDCOH>(p, wbase, nsplits, g0, ng, wts, lsum);
+  __syncthreads();
+  for (int s0 = 0; s0 < nsplits; s0 += SC) {
+    if (s0) load(s0);
+#pragma unroll
+    for (int u = 0; u < SC; u++) {
+      if (s0 + u >= nsplits) break;
+#pragma unroll
+      for (int j = 0; j < NE; j++) {
+        if (!ok[j]) continue;
+        if (u & 1) at1[j] += v[u][j] * wts[hw[j] + s0 + u];
+        else at0[j] += v[u][j] * wts[hw[j] + s0 + u];
+      }
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < NE; j++) {
+    if (!ok[j]) continue;
+    const int t = threadIdx.x + j * kThreads, hh = t / HD, e = t % HD;
+    const float at = at0[j] + at1[j];
+    const float o = p.div_norm ? at / lsum[hh] : at * (1.0f / lsum[hh]);
+    act_st<STCOH>(p.out + static_cast<size_t>(b) * p.out_stride + (kvh * G + g0 + hh) * HD + e, o);
+  }
+}
 
 // One split block: keys [split*chunk, ...) of (stream b, kv head kvh).
 template <int HD, int G, bool COH, int KV8 = 0>
@@ -369,6 +478,9 @@ __device__ __forceinline__ void attn_split_block(const AttnParams &p, int split,
 
   // ---- merge waves: thread t -> (head g, element e) ----
   const bool single = nsplits == 1;
+  // merge in place (standalone kernel with arrival counters): the partials
+  // go out with sc1 stores
+  const bool fuse = !COH && p.cnt && !single;
   float *wbase = p.work + (static_cast<size_t>(b) * p.hq + kvh * G) * p.max_splits * (HD + 2);
   for (int t = threadIdx.x; t < G * HD; t += kThreads) {
     const int g = t / HD, e = t % HD;
@@ -389,68 +501,56 @@ __device__ __forceinline__ void attn_split_block(const AttnParams &p, int split,
       act_st<COH>(p.out + static_cast<size_t>(b) * p.out_stride + (kvh * G + g) * HD + e, o);
     } else {
       float *dst = wbase + (static_cast<size_t>(g) * p.max_splits + split) * (HD + 2);
-      act_st<COH>(dst + 2 + e, at);
-      if (e == 0) {
-        act_st<COH>(dst, mx);
-        act_st<COH>(dst + 1, lt);
+      if (COH || fuse) {
+        act_st<true>(dst + 2 + e, at);
+        if (e == 0) {
+          act_st<true>(dst, mx);
+          act_st<true>(dst + 1, lt);
+        }
+      } else {
+        act_st<false>(dst + 2 + e, at);
+        if (e == 0) {
+          act_st<false>(dst, mx);
+          act_st<false>(dst + 1, lt);
+        }
+      }
+    }
+  }
+  if constexpr (!COH) {
+    if (fuse) {
+      // arrival: this wave's partial stores have completed before the count
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+      unsigned *cnt = p.cnt + static_cast<size_t>(b) * p.hkv + kvh;
+      int *flag = reinterpret_cast<int *>(lds);
+      if (threadIdx.x == 0)
+        flag[0] = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                  static_cast<unsigned>(nsplits - 1);
+      __syncthreads();
+      const bool last = flag[0] != 0;
+      __syncthreads();  // the flag is read before merge_heads reuses the LDS
+      if (last) {
+        merge_heads<HD, G, (G * HD + kThreads - 1) / kThreads, true, false>(p, kvh, b, nsplits, 0, G, lds);
+        if (threadIdx.x == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
     }
   }
   __syncthreads();  // LDS is reused by the caller's next block
 }
 
-// Merge block `blk` (outputs blk*256 .. +256 of the G*HD) of (stream b, kv head
-// kvh): weights exp2(m_s - M), out = sum_s acc_s w_s / sum_s l_s w_s.
+// Merge block `blk` of (stream b, kv head kvh): outputs blk*256 .. +256 of the
+// G*HD, i.e. heads [blk * HPB, +HPB) with HPB = 256 / HD.
 template <int HD, int G, bool COH>
 __device__ __forceinline__ void attn_merge_block(const AttnParams &p, int blk, int kvh, int b, float *lds) {
   constexpr int HPB = kThreads >= HD ? kThreads / HD : 1;  // heads per block
-  float(*wts)[kMaxSplits] = reinterpret_cast<float(*)[kMaxSplits]>(lds);
-  float *lsum = lds + 4 * kMaxSplits;
   const int len = stream_len(p, b);
   if (len <= 0) return;
   int chunk, nsplits;
   split_range(len, p.max_splits, chunk, nsplits);
   if (nsplits == 1) return;  // the split block wrote the output
-  const int t0 = blk * kThreads;  // first output element of this block
-  if (t0 >= G * HD) return;
-  const int g0 = t0 / HD;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const float *wbase = p.work + (static_cast<size_t>(b) * p.hq + kvh * G) * p.max_splits * (HD + 2);
-  for (int hh = wave; hh < HPB; hh += kWaves) {
-    const int g = g0 + hh;
-    if (g >= G) break;
-    float mx = -INFINITY;
-    for (int sidx = lane; sidx < nsplits; sidx += 64)
-      mx = fmaxf(mx, act_ld<COH>(wbase, (g * p.max_splits + sidx) * (HD + 2)));
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
-    float ls = 0.f;
-    for (int sidx = lane; sidx < nsplits; sidx += 64) {
-      const int src = (g * p.max_splits + sidx) * (HD + 2);
-      const float ms = act_ld<COH>(wbase, src);
-      const float f = ms == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ms - mx);
-      wts[hh][sidx] = f;
-      ls += act_ld<COH>(wbase, src + 1) * f;
-    }
-    ls = wave_sum(ls);
-    if (lane == 0) lsum[hh] = ls;
-  }
-  __syncthreads();
-  const int t = t0 + threadIdx.x;
-  if (t < G * HD) {
-    const int g = t / HD, e = t % HD, hh = g - g0;
-    const int src = g * p.max_splits * (HD + 2) + 2 + e;
-    float at0 = 0.f, at1 = 0.f;
-    int sidx = 0;
-    for (; sidx + 1 < nsplits; sidx += 2) {
-      at0 += act_ld<COH>(wbase, src + sidx * (HD + 2)) * wts[hh][sidx];
-      at1 += act_ld<COH>(wbase, src + (sidx + 1) * (HD + 2)) * wts[hh][sidx + 1];
-    }
-    if (sidx < nsplits) at0 += act_ld<COH>(wbase, src + sidx * (HD + 2)) * wts[hh][sidx];
-    const float at = at0 + at1;
-    const float o = p.div_norm ? at / lsum[hh] : at * (1.0f / lsum[hh]);
-    act_st<COH>(p.out + static_cast<size_t>(b) * p.out_stride + (kvh * G + g) * HD + e, o);
-  }
+  const int g0 = blk * HPB;
+  if (g0 >= G) return;
+  merge_heads<HD, G, 1, COH, COH>(p, kvh, b, nsplits, g0, min(HPB, G - g0), lds);
   __syncthreads();  // LDS is reused by the caller's next block
 }
 

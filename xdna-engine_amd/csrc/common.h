@@ -259,6 +259,9 @@ struct AttnLaunch {
   int out_stride = 0;
   // workspace for the split partials
   float *work = nullptr;
+  // arrival counters [batch * hkv], zero between launches: the split kernel
+  // merges its partials in place (no merge launch); null: a merge follows
+  unsigned *cnt = nullptr;
   int max_splits = 0;
   // int8 K / V instead of bf16 (kc / vc then hold int8 [batch, hkv, max_ctx,
   // hd]; no append): per-channel scales [hkv * hd], or null

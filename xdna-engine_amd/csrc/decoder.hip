@@ -367,6 +367,7 @@ struct xe_decoder {
   float *arg_v = nullptr;
   int *arg_i = nullptr;
   float *attn_work = nullptr;
+  unsigned *attn_cnt = nullptr;  // split-attention arrival counters [max_batch * hkv] (self-resetting)
   int attn_splits = 1;
   int32_t *host_tok = nullptr;  // pinned staging [max_ctx + 1][max_batch] x 2
   int last_exec = XE_EXEC_GRAPH;  // executor of the last step launched (status messages)
@@ -620,6 +621,7 @@ void alloc_decoder(xe_decoder *d) {
   d->attn_splits = attn_splits_for(d, B, hkv_max);
   d->attn_work = dalloc<float>(attn_work_floats(static_cast<int>(part_rows), std::max(c.n_heads, 1), c.head_dim, 1),
                                s, false);
+  d->attn_cnt = dalloc<unsigned>(static_cast<size_t>(B) * hkv_max, s);  // zeroed
   if (gem) {
     const int half = c.head_dim / 2;
     std::vector<float> cs(static_cast<size_t>(c.max_ctx) * half), sn(cs.size());
@@ -694,7 +696,8 @@ void free_decoder(xe_decoder *d) {
                   static_cast<void *>(d->next), static_cast<void *>(d->hist),
                   static_cast<void *>(d->arg_v), static_cast<void *>(d->arg_i),
                   static_cast<void *>(d->attn_work), static_cast<void *>(d->xn),
-                  static_cast<void *>(d->gemm_ws), static_cast<void *>(d->gemm_cnt)})
+                  static_cast<void *>(d->gemm_ws), static_cast<void *>(d->gemm_cnt),
+                  static_cast<void *>(d->attn_cnt)})
     if (p) (void)hipFree(p);
   if (d->host_tok) (void)hipHostFree(d->host_tok);
   if (d->s) (void)hipStreamDestroy(d->s);
@@ -845,7 +848,7 @@ struct PlanBuilder {
     ph.nblocks = a.max_splits * a.hkv * a.batch;
     ph.u.attn = adev::to_params(a);
     push(ph, label, bytes, adev::attn_lds_floats(ph.hd, ph.g) * sizeof(float));
-    if (a.max_splits > 1) {
+    if (a.max_splits > 1 && !a.cnt) {
       ph.kind = sdev::PH_MERGE;
       ph.nblocks = ((ph.g * ph.hd + 255) / 256) * a.hkv * a.batch;
       push(ph, label + "_merge",
@@ -864,6 +867,9 @@ void build_plan(xe_decoder *d, int B, xe_decoder::Plan &plan) {
   const int norm = gem ? XE_NORM_RMS1P : XE_NORM_LN;
   plan.step_nb = B <= 1 ? 1 : B <= 2 ? 2 : 4;
   PlanBuilder pb{plan, plan.step_nb, d->gemm_ws ? d->xn : nullptr, d->gemm_ws, d->gemm_cnt};
+  // beyond 4 streams (no persistent step kernel) the split attention kernel
+  // merges in place; the step kernel keeps a merge phase
+  unsigned *attn_cnt = B > 4 ? d->attn_cnt : nullptr;
 
   // embedding
   {
@@ -952,6 +958,7 @@ void build_plan(xe_decoder *d, int B, xe_decoder::Plan &plan) {
       a.out = d->att;
       a.out_stride = hq;
       a.work = d->attn_work;
+      a.cnt = attn_cnt;
       a.max_splits = attn_splits_for(d, B, c.n_kv_heads);
       // KV bytes depend on the positions; profile_step fills them in
       pb.attn(a, "attn_self", 4.0 * B * (nq + hq) + 4.0 * B * hk);
@@ -999,6 +1006,7 @@ void build_plan(xe_decoder *d, int B, xe_decoder::Plan &plan) {
       a.out = d->att;
       a.out_stride = D;
       a.work = d->attn_work;
+      a.cnt = attn_cnt;
       a.max_splits = attn_splits_for(d, B, c.n_heads);
       a.k_scale = d->cross_i8k ? l.cks : nullptr;
       a.v_scale = d->cross_i8v ? l.cvs : nullptr;
