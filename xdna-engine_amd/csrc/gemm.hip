@@ -760,6 +760,75 @@ __global__ __launch_bounds__(256) void gemm_prologue_kernel(gdev::GemvParams p, 
   for (int i = threadIdx.x; i < p.k; i += 256) xn[static_cast<size_t>(b) * p.k + i] = xs[i];
 }
 
+// The Gemma sandwich-norm prologue (x + post-norm(sub) -> res_out, then the
+// pre-norm) with every operand in registers: x, sub, post_w and gamma arrive
+// in one memory round trip, one block reduction gives both statistics, and
+// res_out and xn are stored from registers.  The same arithmetic in the same
+// order as gemv_prologue's fold path (bit-identical).  A thread takes float4
+// chunks threadIdx.x + j * 256, j < NV (K <= 1024 * NV).
+template <int NV>
+__global__ __launch_bounds__(256) void gemm_prologue_fold_kernel(gdev::GemvParams p, float *xn) {
+  __shared__ float red[2 * 4 * gdev::kMaxWaves];
+  const int b = blockIdx.x;
+  const int K = p.k, K4 = K / 4;
+  const float fk = static_cast<float>(K);
+  const float4 *x4 = reinterpret_cast<const float4 *>(static_cast<const float *>(p.x) + static_cast<size_t>(b) * p.ldx);
+  const float4 *s4 = reinterpret_cast<const float4 *>(p.sub + static_cast<size_t>(b) * K);
+  const float4 *w4 = reinterpret_cast<const float4 *>(p.post_w);
+  const float4 *g4 = reinterpret_cast<const float4 *>(p.gamma);
+  float4 v[NV], sv[NV], w[NV], g[NV];
+#pragma unroll
+  for (int j = 0; j < NV; j++) {
+    const int i = threadIdx.x + j * 256;
+    if (i < K4) {
+      v[j] = x4[i];
+      sv[j] = s4[i];
+      w[j] = w4[i];
+      g[j] = g4[i];
+    }
+  }
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};  // sum sub^2, x^2, x*s', s'^2
+#pragma unroll
+  for (int j = 0; j < NV; j++) {
+    if (threadIdx.x + j * 256 >= K4) continue;
+    const float xv[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+    const float su[4] = {sv[j].x, sv[j].y, sv[j].z, sv[j].w};
+    const float wv[4] = {w[j].x, w[j].y, w[j].z, w[j].w};
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      const float sp = su[c] * (1.0f + wv[c]);
+      acc[0] = __builtin_fmaf(su[c], su[c], acc[0]);
+      acc[1] = __builtin_fmaf(xv[c], xv[c], acc[1]);
+      acc[2] = __builtin_fmaf(xv[c], sp, acc[2]);
+      acc[3] = __builtin_fmaf(sp, sp, acc[3]);
+    }
+  }
+  int slot = 0;
+  gdev::block_sums<4, 4>(acc, red, slot);
+  const float inv_s = 1.0f / sqrtf(acc[0] / fk + p.eps);
+  const float st2 = acc[1] + 2.0f * inv_s * acc[2] + inv_s * inv_s * acc[3];
+  const float inv_t = 1.0f / sqrtf(fmaxf(st2, 0.f) / fk + p.eps);
+  const bool one_p = p.norm == XE_NORM_RMS1P;
+#pragma unroll
+  for (int j = 0; j < NV; j++) {
+    const int i = threadIdx.x + j * 256;
+    if (i >= K4) continue;
+    const float xv[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+    const float su[4] = {sv[j].x, sv[j].y, sv[j].z, sv[j].w};
+    const float wv[4] = {w[j].x, w[j].y, w[j].z, w[j].w};
+    const float gv[4] = {g[j].x, g[j].y, g[j].z, g[j].w};
+    float t[4], h[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      t[c] = xv[c] + su[c] * inv_s * (1.0f + wv[c]);
+      h[c] = one_p ? t[c] * inv_t * (1.0f + gv[c]) : t[c] * inv_t * gv[c];
+    }
+    if (p.res_out)
+      reinterpret_cast<float4 *>(p.res_out + static_cast<size_t>(b) * K)[i] = make_float4(t[0], t[1], t[2], t[3]);
+    reinterpret_cast<float4 *>(xn + static_cast<size_t>(b) * K)[i] = make_float4(h[0], h[1], h[2], h[3]);
+  }
+}
+
 using GemmFn = void (*)(gdev::GemvParams, float *, unsigned *, int);
 
 template <int WT>
@@ -875,6 +944,17 @@ bool gemm_needs_prologue(const gdev::GemvParams &p) { return p.sub != nullptr ||
 // Prologue (when the phase has one) into xn, then the GEMM reading xn.
 void launch_gemm_prologue(const gdev::GemvParams &p, float *xn, hipStream_t s) {
   XE_REQUIRE(!p.x_bf16, "gemm: fp32 activations only");
+  auto al16 = [](const void *q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
+  if (p.sub && p.post_w && p.gamma && (p.norm == XE_NORM_RMS1P || p.norm == XE_NORM_RMS) && p.k % 4 == 0 &&
+      p.ldx % 4 == 0 && p.k <= 4096 && al16(p.x) && al16(p.sub) && al16(p.post_w) && al16(p.gamma) &&
+      al16(p.res_out) && al16(xn)) {
+    const int nv = (p.k / 4 + 255) / 256;
+    auto fn = nv <= 1 ? gemm_prologue_fold_kernel<1> : nv <= 2 ? gemm_prologue_fold_kernel<2>
+                                                                : gemm_prologue_fold_kernel<4>;
+    hipLaunchKernelGGL(fn, dim3(p.batch), dim3(256), 0, s, p, xn);
+    XE_HIP(hipGetLastError());
+    return;
+  }
   const size_t lds = gdev::gemv_lds_floats(1, p.k, p.sub != nullptr) * sizeof(float);
   XE_REQUIRE(lds <= 160 * 1024 - 1024, "gemm prologue: K too large for LDS staging");
   if (lds > 64 * 1024)
