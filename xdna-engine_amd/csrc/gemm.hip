@@ -829,6 +829,77 @@ __global__ __launch_bounds__(256) void gemm_prologue_fold_kernel(gdev::GemvParam
   }
 }
 
+// The GEMM prologue without the Gemma fold (optional residual add -> res_out,
+// then LayerNorm / RMSNorm / none) with every operand in registers: thread t
+// takes elements t + j * 256, j < NS, the per-thread order of
+// gemv_prologue's plain path, so the sums and outputs are bit-identical.
+// K <= 256 * NS.
+template <int NS>
+__global__ __launch_bounds__(256) void gemm_prologue_reg_kernel(gdev::GemvParams p, float *xn) {
+  __shared__ float red[2 * 4 * gdev::kMaxWaves];
+  const int b = blockIdx.x, K = p.k;
+  const float fk = static_cast<float>(K);
+  const float *xr = static_cast<const float *>(p.x) + static_cast<size_t>(b) * p.ldx;
+  const float *sr = p.sub ? p.sub + static_cast<size_t>(b) * K : nullptr;
+  const bool ln = p.norm == XE_NORM_LN;
+  float t[NS], sv[NS], g[NS], be[NS];
+#pragma unroll
+  for (int j = 0; j < NS; j++) {
+    const int i = threadIdx.x + j * 256;
+    t[j] = sv[j] = g[j] = be[j] = 0.f;
+    if (i < K) {
+      t[j] = xr[i];
+      if (sr) sv[j] = sr[i];
+      if (p.norm != XE_NORM_NONE) g[j] = p.gamma[i];
+      if (ln) be[j] = p.beta[i];
+    }
+  }
+  if (sr) {
+#pragma unroll
+    for (int j = 0; j < NS; j++) {
+      const int i = threadIdx.x + j * 256;
+      if (i >= K) continue;
+      t[j] = t[j] + sv[j];
+      if (p.res_out) p.res_out[static_cast<size_t>(b) * K + i] = t[j];
+    }
+  }
+  int slot = 0;
+  if (ln) {
+    float v1[1] = {0.f};
+#pragma unroll
+    for (int j = 0; j < NS; j++)
+      if (threadIdx.x + j * 256 < K) v1[0] += t[j];
+    gdev::block_sums<4, 1>(v1, red, slot);
+    const float mean = v1[0] / fk;
+    float v2[1] = {0.f};
+#pragma unroll
+    for (int j = 0; j < NS; j++) {
+      if (threadIdx.x + j * 256 >= K) continue;
+      const float c = t[j] - mean;
+      v2[0] = __builtin_fmaf(c, c, v2[0]);
+    }
+    gdev::block_sums<4, 1>(v2, red, slot);
+    const float inv = 1.0f / sqrtf(v2[0] / fk + p.eps);
+#pragma unroll
+    for (int j = 0; j < NS; j++) t[j] = (t[j] - mean) * inv * g[j] + be[j];
+  } else if (p.norm != XE_NORM_NONE) {
+    float v1[1] = {0.f};
+#pragma unroll
+    for (int j = 0; j < NS; j++)
+      if (threadIdx.x + j * 256 < K) v1[0] = __builtin_fmaf(t[j], t[j], v1[0]);
+    gdev::block_sums<4, 1>(v1, red, slot);
+    const float inv = 1.0f / sqrtf(v1[0] / fk + p.eps);
+#pragma unroll
+    for (int j = 0; j < NS; j++)
+      t[j] = p.norm == XE_NORM_RMS1P ? t[j] * inv * (1.0f + g[j]) : t[j] * inv * g[j];
+  }
+#pragma unroll
+  for (int j = 0; j < NS; j++) {
+    const int i = threadIdx.x + j * 256;
+    if (i < K) xn[static_cast<size_t>(b) * K + i] = t[j];
+  }
+}
+
 using GemmFn = void (*)(gdev::GemvParams, float *, unsigned *, int);
 
 template <int WT>
@@ -951,6 +1022,14 @@ void launch_gemm_prologue(const gdev::GemvParams &p, float *xn, hipStream_t s) {
     const int nv = (p.k / 4 + 255) / 256;
     auto fn = nv <= 1 ? gemm_prologue_fold_kernel<1> : nv <= 2 ? gemm_prologue_fold_kernel<2>
                                                                 : gemm_prologue_fold_kernel<4>;
+    hipLaunchKernelGGL(fn, dim3(p.batch), dim3(256), 0, s, p, xn);
+    XE_HIP(hipGetLastError());
+    return;
+  }
+  if (!(p.sub && p.post_w) && p.k <= 4096 && (p.norm == XE_NORM_NONE || p.gamma) &&
+      (p.norm != XE_NORM_LN || p.beta)) {
+    auto fn = p.k <= 1024 ? gemm_prologue_reg_kernel<4> : p.k <= 2048 ? gemm_prologue_reg_kernel<8>
+                                                                       : gemm_prologue_reg_kernel<16>;
     hipLaunchKernelGGL(fn, dim3(p.batch), dim3(256), 0, s, p, xn);
     XE_HIP(hipGetLastError());
     return;
