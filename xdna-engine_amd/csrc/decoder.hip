@@ -525,14 +525,18 @@ void validate_config(const xe_model_config &c, int max_batch) {
 }
 
 // Splits per (stream, kv head) of the split-K attention phases of a batch:
-// about two workgroups per CU over the batch's (stream, kv head) pairs, at
-// most one per 64 cache rows and at most 64 (Gemma b = 64 over ctx 512..4096:
-// 8 splits 17.3k tok/s, 16: 16.5k, 4: 16.6k, 2: 13.6k).  (A stream's blocks past its
-// filled length return at once; split_range sizes chunks from the length.)
+// about one workgroup per CU over the batch's (stream, kv head) pairs, at
+// most one per 64 cache rows and at most 64.  Gemma over ctx 512..4096, with
+// the merge inside the split kernel: b = 64 at 4 splits 24.0k tok/s, 8: 22.9k,
+// 16: 19.9k, 2: 20.0k; b = 16 at 16 splits 7.70k, 32: 7.40k, 8: 7.47k.  Each
+// split block pays its q transform, its cross-wave merge and its partial
+// stores, so fewer, longer splits win once the chip is covered.  (A stream's
+// blocks past its filled length return at once; split_range sizes chunks
+// from the length.)
 int attn_splits_for(const xe_decoder *d, int batch, int hkv) {
   const auto &c = d->c;
   const int cus = d->dev->num_cus > 0 ? d->dev->num_cus : 256;
-  int ms = (2 * cus) / std::max(1, batch * hkv);
+  int ms = cus / std::max(1, batch * hkv);
   const int cap = (std::max(c.max_ctx, c.family == XE_WHISPER ? c.n_cross : 0) + 63) / 64;
   return std::max(1, std::min(std::min(ms, cap), 64));
 }
