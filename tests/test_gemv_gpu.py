@@ -324,10 +324,13 @@ def test_norm_gemm_int8_batched(gpu, xe, m, k, b):
 # The decoder's b = 64 projection shapes, every weight type: together they
 # take each tile height of the K-sliced kernel (16, 32 and 64 rows), its
 # split-K tail (QKV, O, down) and the unsplit path (gate/up), plus the
-# wide-output kernel: a 65536-row output, more 64-row tiles than CUs (the
-# lm-head's path), takes gemm_kernel.
+# wide-output kernel gemm_kernel: a 65536-row output (one row block a wave)
+# and 262144 rows or more (the Gemma lm-head's width, here with a short K:
+# four row blocks a wave), also ragged (rows past a 256-row tile, a last K
+# step of 16).
 GEMM_SHAPES = [(1536, 1152), (1152, 1024), (13824, 1152), (1152, 6912), (65536, 1152),
-               (1000, 1040), (72, 48)]  # ragged: K % 32 == 16, rows not a tile multiple
+               (1000, 1040), (72, 48),  # ragged: K % 32 == 16, rows not a tile multiple
+               (262144, 64), (262208, 80)]
 
 
 @pytest.mark.parametrize("m,k", GEMM_SHAPES)
