@@ -401,6 +401,17 @@ int xe_decoder_get_tensor_q8(xe_decoder *dec, int kind, int layer, int8_t *q,
                              float *scales);
 /* reset() (whisper_decoder.rs:1235-1243): clear every stream's KV cache. */
 int xe_decoder_reset(xe_decoder *dec);
+/* Fill positions [0, n_pos) of one stream's self-attention K / V cache
+ * (every layer and KV head) with the counter-based synthetic stream, bf16
+ * N(0, 1): element (pos, e) of (layer l, head h) is value pos * head_dim + e
+ * of stream id 2 (l n_kv_heads + h) (K) or that + 1 (V) under `seed`, and
+ * the stream's next position becomes n_pos.  A decode can then start at a
+ * long context without feeding a prompt of that length (parity tests and
+ * benchmarks at the contexts of BASELINE config 5).  No counterpart in the
+ * reference, whose decoders always start from an empty cache (reset(),
+ * whisper_decoder.rs:1235-1243); the oracle's xo_model_prime_kv fills the
+ * same values. */
+int xe_decoder_prime_kv(xe_decoder *dec, int stream, int n_pos, uint64_t seed);
 /* precompute_cross (whisper_decoder.rs:1143-1232): enc [n_cross, d] fp32, or
  * NULL to use the synthetic XE_T_ENC_OUT tensor of the last init. */
 int xe_decoder_set_cross(xe_decoder *dec, const float *enc);
@@ -431,8 +442,30 @@ int xe_decoder_generate(xe_decoder *dec, const int32_t *prompt, int n_prompt,
  * (out [batch, n_steps], may be NULL) and the device time of the whole run
  * measured with HIP events on the decoder stream (device_us, may be NULL). */
 int xe_decoder_feed(xe_decoder *dec, const int32_t *prompt, int n_prompt, int batch);
+/* decode() returns the number of steps that ran (n_steps unless a stop
+ * token ended the run early, below), or -1. */
 int xe_decoder_decode(xe_decoder *dec, int batch, int n_steps, int32_t *out,
                       double *device_us);
+/* Stop rule of the reference's greedy loops (EOT, whisper.rs:371-380 and,
+ * batched, :618-668): from the next feed() on, a stream whose generated
+ * token is stop_id has stopped; it is fed stop_id at its following positions
+ * (its KV cache advances, its output is ignored) and, in out rows of
+ * decode() / generate(), every token after its stop is stop_id.  A
+ * low-latency launch ends at the step where every stream has stopped; the
+ * phase-kernel executors launch no further steps after the next check
+ * (every 8 steps).  Prompt tokens never stop a stream; the argmax after the
+ * last prompt token can.  stop_id -1 (the default) removes the rule
+ * (Opt::generate, opt125m_decode.rs:296-315, has none). */
+int xe_decoder_set_stop(xe_decoder *dec, int32_t stop_id);
+/* greedy_decode_fused[_batch] (whisper.rs:344-389, 618-668): feed prompt
+ * [batch, n_prompt], then generate until every stream has emitted stop_id or
+ * max_new tokens (MAX_DECODE, whisper.rs:36).  out [batch, max_new] holds
+ * each stream's tokens, the stop token excluded, then stop_id; n_out [batch]
+ * (may be NULL) the number of tokens before the stop.  The decoder's own
+ * stop setting is restored afterwards. */
+int xe_decoder_generate_until(xe_decoder *dec, const int32_t *prompt, int n_prompt,
+                              int batch, int max_new, int32_t stop_id,
+                              int32_t *out, int32_t *n_out);
 /* One eager decode step with a HIP event after every launch (the step
  * advances the streams like decode).  Per launch: a label (32-byte slots in
  * labels), device microseconds and algorithmic bytes.  Returns the number of

@@ -1609,37 +1609,57 @@ static float xo_margin(const float *v, int n, int best) {
   return v[best] - second;
 }
 
-/* Opt::generate (opt125m_decode.rs:296-315) for every stream. */
-/* One stream of xo_model_generate. */
+/* One stream of Opt::generate (opt125m_decode.rs:296-315): the prompt fed
+ * from position 0, then greedy steps; the argmax after the last prompt token
+ * is the first emitted token.  With stop >= 0 the stream ends at the first
+ * emitted token equal to stop (the EOT rule of whisper.rs:371-380): that
+ * token and every later slot of out hold stop, *n_out is the number of
+ * tokens before it.  (The reference's batched loop keeps feeding EOT to a
+ * finished stream, whisper.rs:651; streams are independent, so nothing
+ * emitted depends on those steps and this stream simply ends.) */
 static void xo_generate_one(xo_model *m, int b, const int *prompt, int n_prompt, int n_new,
-                            int *out, float *margins) {
+                            int stop, int *out, float *margins, int *n_out) {
   int V = m->c.vocab;
   float *logits = (float *)malloc((size_t)V * 4);
   for (int p = 0; p < n_prompt; p++) xo_step_one(m, b, prompt[p], p, logits);
-  int pos = n_prompt;
+  int pos = n_prompt, n = n_new;
   for (int i = 0; i < n_new; i++) {
     int next = xo_model_argmax(m, logits);
     out[i] = next;
     if (margins) margins[i] = xo_margin(logits, V, next);
+    if (stop >= 0 && next == stop) {
+      n = i;
+      for (int j = i + 1; j < n_new; j++) {
+        out[j] = stop;
+        if (margins) margins[j] = INFINITY;
+      }
+      break;
+    }
     if (i + 1 == n_new) break;
     xo_step_one(m, b, next, pos, logits);
     pos++;
   }
+  if (n_out) *n_out = n;
   free(logits);
 }
 
-int xo_model_generate(xo_model *m, const int *prompt, int n_prompt, int batch,
-                      int n_new, int *out, float *margins) {
-  if (batch > m->batch || n_prompt < 1 || n_prompt + n_new > m->c.max_ctx + 1) return -1;
+int xo_model_generate_until(xo_model *m, const int *prompt, int n_prompt, int batch, int n_new,
+                            int stop, int *out, int *n_out, float *margins) {
+  if (batch > m->batch || n_prompt < 1 || n_new < 1 || n_prompt + n_new > m->c.max_ctx + 1) return -1;
   if (batch == 1) {
-    xo_generate_one(m, 0, prompt, n_prompt, n_new, out, margins);
+    xo_generate_one(m, 0, prompt, n_prompt, n_new, stop, out, margins, n_out);
     return 0;
   }
 #pragma omp parallel for schedule(dynamic, 1)
   for (int b = 0; b < batch; b++)
-    xo_generate_one(m, b, prompt + (size_t)b * n_prompt, n_prompt, n_new, out + (size_t)b * n_new,
-                    margins ? margins + (size_t)b * n_new : NULL);
+    xo_generate_one(m, b, prompt + (size_t)b * n_prompt, n_prompt, n_new, stop, out + (size_t)b * n_new,
+                    margins ? margins + (size_t)b * n_new : NULL, n_out ? n_out + b : NULL);
   return 0;
+}
+
+int xo_model_generate(xo_model *m, const int *prompt, int n_prompt, int batch,
+                      int n_new, int *out, float *margins) {
+  return xo_model_generate_until(m, prompt, n_prompt, batch, n_new, -1, out, NULL, margins);
 }
 
 size_t xo_model_tensor_numel(const xo_model *m, int kind, int layer) {

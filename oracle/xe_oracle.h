@@ -190,6 +190,11 @@ int xo_model_tensor_q8(const xo_model *m, int kind, int layer, int8_t *q,
  * receives top1 - top2 logit per emitted token (may be NULL). */
 int xo_model_generate(xo_model *m, const int *prompt, int n_prompt, int batch,
                       int n_new, int *out, float *margins);
+/* xo_model_generate with the EOT rule: stream b ends at its first emitted
+ * token equal to stop (stop < 0: never); out holds stop from there on and
+ * n_out[b] (may be NULL) the number of tokens before it. */
+int xo_model_generate_until(xo_model *m, const int *prompt, int n_prompt, int batch, int n_new,
+                            int stop, int *out, int *n_out, float *margins);
 void xo_set_threads(int n);
 
 #ifdef __cplusplus

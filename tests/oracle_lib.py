@@ -111,6 +111,8 @@ def lib():
         "xo_model_tensor_q8": (C.c_int, [C.c_void_p, C.c_int, C.c_int, i8p, f32p]),
         "xo_model_generate": (C.c_int, [C.c_void_p, i32p, C.c_int, C.c_int, C.c_int, i32p,
                                         C.c_void_p]),
+        "xo_model_generate_until": (C.c_int, [C.c_void_p, i32p, C.c_int, C.c_int, C.c_int, C.c_int,
+                                              i32p, i32p, C.c_void_p]),
         "xo_set_threads": (None, [C.c_int]),
     }
     for name, (res, args) in sig.items():
@@ -428,6 +430,17 @@ class OracleModel:
         assert lib().xo_model_generate(self.h, prompt, n_prompt, b, n_new, out,
                                        margins.ctypes.data_as(C.c_void_p)) == 0
         return out, margins
+
+    def generate_until(self, prompt, max_new, stop):
+        """EOT rule: (out [b, max_new] padded with stop, n_out [b], margins)."""
+        prompt = np.ascontiguousarray(prompt, np.int32)
+        b, n_prompt = prompt.shape
+        out = np.empty((b, max_new), np.int32)
+        n_out = np.empty(b, np.int32)
+        margins = np.empty((b, max_new), np.float32)
+        assert lib().xo_model_generate_until(self.h, prompt, n_prompt, b, max_new, int(stop), out, n_out,
+                                             margins.ctypes.data_as(C.c_void_p)) == 0
+        return out, n_out, margins
 
 
 # tensor kinds (include/xdna_engine.h enum xe_tensor)

@@ -99,8 +99,10 @@ def test_edge_lengths(gpu):
 
 
 def test_repeat_calls_rearm_counters(gpu):
-    """The split merge re-arms its arrival counters: repeated calls with
-    changing lengths keep matching."""
+    """The op layer merges the splits in place (the last split block of a
+    (stream, kv head) to arrive, counted with an arrival counter that it
+    re-arms): repeated calls with changing lengths, hence changing split
+    counts per stream (1 to 64), keep matching."""
     dev, ctx = gpu
     rng = np.random.default_rng(4)
     b, hq, hkv, hd, mc = 2, 12, 12, 64, 4096
@@ -110,3 +112,29 @@ def test_repeat_calls_rearm_counters(gpu):
     for lens in ([4096, 100], [64, 4000], [3000, 3001], [4096, 4096]):
         lens = np.array(lens, np.int32)
         close(ctx.attn(q, kc, vc, lens, 0.125), O.attn_decode(q, kc, vc, lens, 0.125))
+
+
+@pytest.mark.parametrize("hq,hkv,hd,ctxlen,b", [(4, 1, 256, 4096, 64), (4, 1, 256, 4096, 8),
+                                                (12, 12, 64, 1024, 16), (4, 1, 256, 32768, 2)])
+def test_in_place_merge_equals_merge_launch(gpu, monkeypatch, hq, hkv, hd, ctxlen, b):
+    """The in-place merge (the default) and the separate merge launch
+    (XE_ATTN_MERGE=launch) run the same per-output arithmetic in the same
+    order: bit-identical outputs, both within the oracle's bar.  Splits per
+    stream here: up to 16, 64, 5 and 64 (more than 8 take a second load round
+    of the merge)."""
+    dev, ctx = gpu
+    print("[case] attn merge in place vs launch hq=%d hd=%d ctx=%d b=%d" % (hq, hd, ctxlen, b), flush=True)
+    rng = np.random.default_rng(hq + hd + ctxlen + b)
+    lens = rng.integers(ctxlen // 2, ctxlen + 1, b).astype(np.int32)
+    lens[0] = ctxlen
+    q = O.bf16_to_f32(O.bf16_bits(rng.standard_normal((b, hq, hd)).astype(np.float32)))
+    kc = O.bf16_bits(rng.standard_normal((b, hkv, ctxlen, hd)).astype(np.float32))
+    vc = O.bf16_bits(rng.standard_normal((b, hkv, ctxlen, hd)).astype(np.float32))
+    scale = 1.0 / math.sqrt(hd)
+    fused = ctx.attn(q, kc, vc, lens, scale)
+    monkeypatch.setenv("XE_ATTN_MERGE", "launch")
+    launched = ctx.attn(q, kc, vc, lens, scale)
+    monkeypatch.delenv("XE_ATTN_MERGE")
+    assert np.array_equal(np.asarray(fused, np.float32).view(np.uint32),
+                          np.asarray(launched, np.float32).view(np.uint32))
+    close(fused, O.attn_decode(q, kc, vc, lens, scale))

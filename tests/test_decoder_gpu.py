@@ -324,3 +324,55 @@ def test_decode_bounds_follow_step_positions(gpu, xe):
     with pytest.raises(xe.XdnaError, match="past max_ctx"):
         dec.decode(1, batch=1)
     dec.close()
+
+
+# ---- the stop rule (EOT; whisper.rs:371-380 single stream, :618-668 batched) ----
+# (family, executor, streams, step of stream 0 whose token is the stop id)
+STOP_CASES = [("gemma", "ll", 2, 20), ("gemma", "graph", 2, 20), ("gemma", "graph", 12, 20),
+              ("whisper", "ll", 1, 14), ("opt", "graph", 3, 0), ("gemma", "ll", 1, 0)]
+
+
+@pytest.mark.parametrize("family,step,batch,at", STOP_CASES)
+def test_stop_token(gpu, xe, monkeypatch, family, step, batch, at):
+    """generate_until against the oracle's: each stream ends at its first
+    emitted stop token (tokens before it identical, n_out equal, the stop id
+    after), streams that never emit it run to max_new; stopped streams are
+    fed the stop id while the others continue.  Then a single stream stopped
+    mid-run: the device loop ends at once (low-latency: the launch stops at
+    that step) or at the next check (phase kernels: every 8 steps)."""
+    monkeypatch.setenv("XE_STEP", step)
+    fam = {"opt": xe.XE_OPT, "whisper": xe.XE_WHISPER, "gemma": xe.XE_GEMMA3}[family]
+    cfg = tiny(xe, fam, xe.XE_I8)
+    max_new = 48
+    print("[case] stop %s %s batch %d at %d" % (family, step, batch, at), flush=True)
+    dec, om = build(xe, gpu, cfg, seed=13, batch=batch)
+    if fam == xe.XE_WHISPER:
+        dec.precompute_cross(None)
+    pr = prompts(cfg, batch, 5, seed=3)
+    free, _ = om.generate(pr, max_new)
+    stop = int(free[0, at])
+    om.reset()
+    want, want_n, _ = om.generate_until(pr, max_new, stop)
+    assert want_n[0] <= at
+    got, got_n = dec.generate_until(pr, max_new, stop)
+    assert dec.executor(batch) == step
+    assert np.array_equal(got_n, want_n), (got_n, want_n)
+    assert np.array_equal(got, want)
+    # the decoder's own stop setting is back to none: a plain generate runs on
+    g2 = dec.generate(pr, max_new)
+    assert np.array_equal(g2, free)
+    # one stream through set_stop / feed / decode: the run ends early
+    dec.set_stop(stop)
+    dec.feed(pr[:1])
+    toks, _ = dec.decode(max_new - 1, batch=1)
+    k = int(want_n[0])  # decode step k - 1 emits the stop (step j emits token j + 1)
+    ran = dec.steps_run
+    if step == "ll":
+        assert ran == k, (ran, k)
+    else:
+        assert ran == min(max_new - 1, -(-k // 8) * 8), (ran, k)
+    assert np.array_equal(toks[0, :max(k - 1, 0)], want[0, 1:k])
+    assert np.all(toks[0, max(k - 1, 0):] == stop)
+    dec.set_stop(-1)
+    dec.close()
+    om.close()

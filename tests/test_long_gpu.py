@@ -11,6 +11,11 @@
   oracle's, and step logits are compared at the end.
 * Gemma-3-1B at 64 streams on the real shape (MFMA GEMM projections),
   teacher-forced step by step with every step's logits compared.
+* The graph executor's multi-split attention with the in-place merge (the
+  b = 64 bench plan): 64, 20 and 8 streams with prompts long enough for 3 to
+  11 splits per stream, greedy streams and step logits against the oracle;
+  and Gemma-3-1B at 64 streams (26 layers) and 8 streams on caches primed to
+  per-stream lengths 512..4000 (config 5's contexts), teacher-forced.
 * Whisper-small at 32 streams for the full 224 greedy steps of config 4,
   the GPU's own stream replayed by the oracle.
 * Config 3 mha_decode at context 32768 for 16 and 64 streams on device
@@ -149,6 +154,70 @@ def test_gemma3_1b_b64_real_shape(gpu, xe, default_executor, n_layers, rel_l2, a
             np.array([om.argmax(w[b]) for b in range(batch)], np.int32)
     print("[gemma3-1b-b64] %d layers: %d forced steps x %d streams; %d near-ties" %
           (n_layers, n_prompt + n_steps, batch, ties), flush=True)
+    dec.close()
+    om.close()
+
+
+# The graph executor's split attention beyond 4 streams: each (stream, kv
+# head) takes up to 256 / (streams x kv heads) splits (4 at 64 streams, 12 at
+# 20, 32 at 8) of at least 64 keys, and the split kernel merges in place (the
+# last block to arrive, counted per (stream, kv head), reads every partial).
+# Gemma's 4 query heads x 256 per kv head, with the new K/V row appended by
+# the last split.  Prompts long enough for several splits:
+#   64 streams, lengths 256..320: 4 then 3 splits (the bench's plan);
+#   20 streams, lengths 300..348: 5..6 splits;
+#    8 streams, lengths 600..664: 10..11 splits (more than the 8 a merging
+#      thread holds at once: a second load round).
+SPLIT_PLANS = [(64, 256, 64), (20, 300, 48), (8, 600, 64)]
+
+
+@pytest.mark.parametrize("batch,n_prompt,n_new", SPLIT_PLANS)
+def test_graph_plan_split_attention(gpu, xe, default_executor, batch, n_prompt, n_new):
+    run_pair(xe, gpu, gemma_long(xe), seed=7, batch=batch, n_prompt=n_prompt, n_new=n_new,
+             label="gemma-graph-b%d-p%d" % (batch, n_prompt), want_exec="graph", logit_steps=2,
+             prompt_seed=11)
+
+
+# Config 5's b = 64 plan at its own contexts (512 .. 4096): every stream's
+# cache primed with synthetic bf16 rows to its own length (the same values on
+# both sides), then teacher-forced steps with every stream's logits compared.
+# (layers, streams, rel-L2, atol): BASELINE's abs 1e-3.  The primed rows are
+# bit-identical on both sides, so only the few new rows can round apart
+# (measured at 26 layers: rel-L2 1.05e-5, max |d| 8.5e-5; 2 layers: 2.7e-6).
+# 8 streams at 2 layers take up to 32 splits (four load rounds of the merge).
+PRIMED = [(26, 64, 1e-4, 1e-3), (2, 8, 2e-5, 1e-3)]
+
+
+@pytest.mark.parametrize("n_layers,batch,rel_l2,atol", PRIMED)
+def test_gemma3_1b_primed_long_context(gpu, xe, default_executor, n_layers, batch, rel_l2, atol):
+    dev, _ = gpu
+    cfg = xe.GEMMA3_1B.replace(n_layers=n_layers, max_ctx=4096)
+    if n_layers < 26:
+        cfg = cfg.replace(vocab=4096)
+    rng = np.random.default_rng(20 + batch)
+    lens = rng.integers(512, 4000, batch).astype(np.int32)
+    lens[0], lens[-1] = 512, 4000
+    n_steps = 3
+    print("[case] gemma3 primed %d layers, %d streams, lengths %d..%d, %d forced steps" %
+          (n_layers, batch, lens.min(), lens.max(), n_steps), flush=True)
+    dec = xe.Decoder(dev, cfg, max_batch=batch)
+    dec.init_synthetic(2)
+    assert dec.executor(batch) == "graph"
+    om = O.OracleModel(oracle_cfg(cfg), 2, batch)
+    for b in range(batch):
+        dec.prime_kv(b, int(lens[b]), 900 + b)
+        om.prime_kv(b, int(lens[b]), 900 + b)
+    tok = rng.integers(0, cfg.vocab, batch).astype(np.int32)
+    pos = lens.copy()
+    ties = 0
+    for s in range(n_steps):
+        g, _ = dec.step(tok, pos)
+        w = om.step(tok, pos)
+        ties += compare_forced_step(g, w, "gemma3-primed-L%d-b%d-step%d" % (n_layers, batch, s),
+                                    om.argmax, rel_l2=rel_l2, atol=atol)
+        tok = np.array([om.argmax(w[b]) for b in range(batch)], np.int32)
+        pos = pos + 1
+    print("[gemma3-primed] %d layers, %d streams: %d near-ties" % (n_layers, batch, ties), flush=True)
     dec.close()
     om.close()
 

@@ -121,3 +121,32 @@ def test_kouter_mode_is_bit_identical():
     assert np.array_equal(la.view(np.uint32), lb.view(np.uint32))
     a.close()
     b.close()
+
+
+def test_oracle_stop_rule_truncates_the_free_stream():
+    """xo_model_generate_until (the EOT rule of whisper.rs:371-380, 618-668):
+    each stream is the plain greedy stream up to its first emitted stop
+    token, n_out counts the tokens before it and the stop token fills the
+    rest; a stream that never emits it is the plain stream.  Three streams of
+    a tiny OPT model; the stop token is one the first stream emits at step 9
+    (and a second case: the first token it emits, so n_out = 0)."""
+    c = O.ModelConfig()
+    for k, v in dict(family=0, n_layers=2, d_model=64, n_heads=2, n_kv_heads=2, head_dim=32, ffn=128,
+                     vocab=50, max_pos=64, max_ctx=64, wdtype=2, eps=1e-5, rope_theta=0.0,
+                     n_cross=0).items():
+        setattr(c, k, v)
+    om = O.OracleModel(c, 3, 3)
+    prompt = np.random.default_rng(0).integers(0, 50, (3, 4)).astype(np.int32)
+    free, _ = om.generate(prompt, 24)
+    for at in (9, 0):
+        om.reset()
+        stop = int(free[0, at])
+        out, n_out, _ = om.generate_until(prompt, 24, stop)
+        for b in range(3):
+            hits = np.nonzero(free[b] == stop)[0]
+            k = int(hits[0]) if hits.size else 24
+            assert n_out[b] == k, (b, n_out[b], k)
+            assert np.array_equal(out[b, :k], free[b, :k])
+            assert np.all(out[b, k:] == stop)
+        assert n_out[0] <= at
+    om.close()

@@ -80,13 +80,21 @@ void *xe_ctx::ensure_pinned(size_t n) {
   return host_pinned;
 }
 
-void xe_ctx::ensure_attn(size_t work_floats) {
+void xe_ctx::ensure_attn(size_t work_floats, size_t cnt_words) {
   if (work_floats > attn_work_floats) {
     if (attn_work) XE_HIP(hipFree(attn_work));
     attn_work = nullptr;
     attn_work_floats = 0;
     XE_HIP(hipMalloc(&attn_work, work_floats * sizeof(float)));
     attn_work_floats = work_floats;
+  }
+  if (cnt_words > attn_cnt_words) {
+    if (attn_cnt) XE_HIP(hipFree(attn_cnt));
+    attn_cnt = nullptr;
+    attn_cnt_words = 0;
+    XE_HIP(hipMalloc(&attn_cnt, cnt_words * sizeof(unsigned)));
+    XE_HIP(hipMemsetAsync(attn_cnt, 0, cnt_words * sizeof(unsigned), dev->stream));
+    attn_cnt_words = cnt_words;
   }
 }
 
@@ -463,6 +471,7 @@ void xe_ctx_destroy(xe_ctx *ctx) {
     if (ctx->scratch) (void)hipFree(ctx->scratch);
     if (ctx->host_pinned) (void)hipHostFree(ctx->host_pinned);
     if (ctx->attn_work) (void)hipFree(ctx->attn_work);
+    if (ctx->attn_cnt) (void)hipFree(ctx->attn_cnt);
     if (ctx->gemm_ws) (void)hipFree(ctx->gemm_ws);
     if (ctx->gemm_cnt) (void)hipFree(ctx->gemm_cnt);
     if (ctx->gemm_xn) (void)hipFree(ctx->gemm_xn);
@@ -847,7 +856,16 @@ static int attn_splits(const xe_ctx *ctx, int batch, int hkv, int max_ctx) {
 }
 
 // work: the split partials (attn_work_floats(batch, hq, hd, splits) floats);
-// null = the ctx's own workspace, grown on demand.
+// null = the ctx's own workspace, grown on demand, with the ctx's arrival
+// counters: the split kernel merges in place (the last split block of a
+// (stream, kv head) to arrive merges its partials, one launch).  A caller's
+// workspace (the allocation-free entry point) takes the separate merge launch.
+// XE_ATTN_MERGE=launch selects the merge launch for the ctx workspace too.
+static bool attn_merge_in_place() {
+  const char *e = std::getenv("XE_ATTN_MERGE");
+  return !(e && std::string(e) == "launch");
+}
+
 static int attn_impl(xe_ctx *ctx, const float *q, const uint16_t *kc, const uint16_t *vc,
                      const int32_t *lens, int batch, int hq, int hkv, int hd, int max_ctx,
                      float scale, float *out, float *work = nullptr) {
@@ -868,8 +886,11 @@ static int attn_impl(xe_ctx *ctx, const float *q, const uint16_t *kc, const uint
   if (work) {
     a.work = work;
   } else {
-    ctx->ensure_attn(attn_work_floats(batch, hq, hd, a.max_splits));
+    const bool in_place = attn_merge_in_place();
+    ctx->ensure_attn(attn_work_floats(batch, hq, hd, a.max_splits),
+                     in_place ? static_cast<size_t>(batch) * hkv : 0);
     a.work = ctx->attn_work;
+    a.cnt = in_place ? ctx->attn_cnt : nullptr;
   }
   launch_attn(a, ctx->dev->stream);
   ctx->dispatches++;
@@ -1061,7 +1082,8 @@ int xe_probe_attn(xe_ctx *ctx, const float *q_dev, const uint16_t *kc_dev, const
     XE_REQUIRE(ctx && q_dev && kc_dev && vc_dev && lens_dev && out_dev && us_per_call, "null argument");
     XE_REQUIRE(batch > 0 && hq > 0 && hkv > 0 && hd > 0 && reps > 0, "bad shape");
     DeviceGuard dg(ctx->dev->ordinal);
-    ctx->ensure_attn(attn_work_floats(batch, hq, hd, attn_splits(ctx, batch, hkv, max_ctx)));
+    ctx->ensure_attn(attn_work_floats(batch, hq, hd, attn_splits(ctx, batch, hkv, max_ctx)),
+                     attn_merge_in_place() ? static_cast<size_t>(batch) * hkv : 0);  // no allocation under capture
     *us_per_call = time_captured(ctx, reps, flags, [&]() {
       attn_impl(ctx, q_dev, kc_dev, vc_dev, lens_dev, batch, hq, hkv, hd, max_ctx, scale, out_dev);
     });

@@ -85,9 +85,12 @@ struct xe_ctx {
   size_t scratch_size = 0;
   void *host_pinned = nullptr;
   size_t host_pinned_size = 0;
-  // split-K attention workspace (partials)
+  // split-K attention workspace (partials) and the per-(stream, kv head)
+  // arrival counters of the in-place merge (zeroed once, self-resetting)
   float *attn_work = nullptr;
   size_t attn_work_floats = 0;
+  unsigned *attn_cnt = nullptr;
+  size_t attn_cnt_words = 0;
   // batched GEMM (more than 8 rows): split-K partials, arrival counters
   // (zeroed once, self-resetting) and the prologue's normalised rows
   float *gemm_ws = nullptr;
@@ -101,7 +104,7 @@ struct xe_ctx {
   void *ensure_scratch(size_t n);
   void ensure_gemm(size_t xn_floats);
   void *ensure_pinned(size_t n);
-  void ensure_attn(size_t work_floats);
+  void ensure_attn(size_t work_floats, size_t cnt_words = 0);
 };
 
 // A pending asynchronous submission: an event recorded on a stream after the

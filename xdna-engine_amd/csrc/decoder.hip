@@ -364,6 +364,10 @@ struct xe_decoder {
   uint16_t *kc = nullptr, *vc = nullptr;  // [L][B][hkv][max_ctx][hd]
   float *rope_cos = nullptr, *rope_sin = nullptr;
   int32_t *tokens = nullptr, *pos = nullptr, *next = nullptr, *hist = nullptr;
+  // stop rule: stop_dev[0] = the stop token (-1: none), stop_dev[1 + b] =
+  // stream b has emitted it (xe_decoder_set_stop)
+  int32_t *stop_dev = nullptr;
+  int stop_id = -1;
   float *arg_v = nullptr;
   int *arg_i = nullptr;
   float *attn_work = nullptr;
@@ -610,6 +614,8 @@ void alloc_decoder(xe_decoder *d) {
   d->pos = dalloc<int32_t>(B, s);
   d->next = dalloc<int32_t>(B, s);
   d->hist = dalloc<int32_t>(static_cast<size_t>(B) * (c.max_ctx + 1), s);
+  d->stop_dev = dalloc<int32_t>(static_cast<size_t>(B) + 1, s);
+  XE_HIP(hipMemsetAsync(d->stop_dev, 0xff, 4, s));  // no stop token
   d->arg_v = dalloc<float>(static_cast<size_t>(B) * sdev::kArgBlocks, s);
   d->arg_i = dalloc<int>(static_cast<size_t>(B) * sdev::kArgBlocks, s);
   d->step_grid = d->dev->num_cus > 0 ? d->dev->num_cus : 256;
@@ -698,7 +704,7 @@ void free_decoder(xe_decoder *d) {
                   static_cast<void *>(d->rope_cos), static_cast<void *>(d->rope_sin),
                   static_cast<void *>(d->tokens), static_cast<void *>(d->pos),
                   static_cast<void *>(d->next), static_cast<void *>(d->hist),
-                  static_cast<void *>(d->arg_v), static_cast<void *>(d->arg_i),
+                  static_cast<void *>(d->stop_dev), static_cast<void *>(d->arg_v), static_cast<void *>(d->arg_i),
                   static_cast<void *>(d->attn_work), static_cast<void *>(d->xn),
                   static_cast<void *>(d->gemm_ws), static_cast<void *>(d->gemm_cnt),
                   static_cast<void *>(d->attn_cnt)})
@@ -1083,6 +1089,8 @@ void build_plan(xe_decoder *d, int B, xe_decoder::Plan &plan) {
     ap.pos = d->pos;
     ap.hist = d->hist;
     ap.hist_stride = c.max_ctx + 1;
+    ap.stop = d->stop_dev;
+    ap.done = d->stop_dev + 1;
     ph.kind = sdev::PH_ARGMAX_PART;
     ph.nblocks = B * sdev::kArgBlocks;
     pb.push(ph, "argmax", 4.0 * B * c.vocab, 512 * sizeof(float));
@@ -1579,6 +1587,7 @@ xe_decoder::LLPlan &ll_plan_for(xe_decoder *d, int B) {
 }
 
 constexpr int kLLChunk = 256;  // decode steps per low-latency launch
+constexpr int kStopCheck = 8;  // phase-kernel steps between looks at the stop flags
 
 // n_steps tokens in one launch.  forced: device [n_forced][B] input tokens of
 // the first steps (prompt feeding); logits: written for every step (the last
@@ -1624,6 +1633,8 @@ void run_ll(xe_decoder *d, int B, int n_steps, const int32_t *forced, int n_forc
   sp.hist_stride = c.max_ctx + 1;
   sp.forced = forced;
   sp.n_forced = forced ? n_forced : 0;
+  sp.stop = d->stop_id;
+  sp.done = d->stop_dev + 1;
   sp.n_steps = n_steps;
   sp.ep0 = d->ll_epoch;
   sp.status = d->step_status;
@@ -2044,6 +2055,43 @@ int xe_decoder_reset(xe_decoder *d) {
   }, -1);
 }
 
+int xe_decoder_prime_kv(xe_decoder *d, int stream, int n_pos, uint64_t seed) {
+  return guard_d([&]() -> int {
+    XE_REQUIRE(d, "null decoder");
+    XE_REQUIRE(stream >= 0 && stream < d->max_batch, "stream out of range");
+    XE_REQUIRE(n_pos >= 0 && n_pos < d->c.max_ctx, "n_pos must be in [0, max_ctx)");
+    if (d->c.family != XE_GEMMA3) XE_REQUIRE(n_pos < d->c.max_pos, "n_pos beyond the position table");
+    DeviceGuard dg(d->dev->ordinal);
+    const auto &c = d->c;
+    const int hk = c.n_kv_heads, hd = c.head_dim;
+    const size_t count = static_cast<size_t>(n_pos) * hd;
+    if (count > 0) {
+      const unsigned blocks = static_cast<unsigned>(std::min<size_t>((count + 255) / 256, 4096));
+      for (int l = 0; l < c.n_layers; l++)
+        for (int h = 0; h < hk; h++) {
+          // element (pos, e) of (layer, stream, head) sits at the same offset
+          // as in the oracle's cache: [layer][stream][head][max_ctx][hd]
+          const size_t off = d->kv_layer_elems() * l + ((static_cast<size_t>(stream) * hk + h) * c.max_ctx) * hd;
+          const uint32_t id = static_cast<uint32_t>(2 * (l * hk + h));
+          synth_fill_kernel<<<blocks, 256, 0, d->s>>>(synth_base(seed, id), 0.0f, kIh4InvStd, 0, count,
+                                                      d->kc + off, XE_BF16);
+          XE_HIP(hipGetLastError());
+          synth_fill_kernel<<<blocks, 256, 0, d->s>>>(synth_base(seed, id + 1), 0.0f, kIh4InvStd, 0, count,
+                                                      d->vc + off, XE_BF16);
+          XE_HIP(hipGetLastError());
+        }
+    }
+    XE_HIP(hipStreamSynchronize(d->s));
+    int32_t *h = d->host_tok;
+    h[0] = n_pos;
+    XE_HIP(hipMemcpyAsync(d->pos + stream, h, 4, hipMemcpyHostToDevice, d->s));
+    XE_HIP(hipStreamSynchronize(d->s));
+    d->hpos[stream] = n_pos;
+    d->live = std::max(d->live, stream + 1);
+    return 0;
+  }, -1);
+}
+
 int xe_decoder_set_cross(xe_decoder *d, const float *enc) {
   return guard_d([&]() -> int {
     XE_REQUIRE(d, "null decoder");
@@ -2281,6 +2329,7 @@ void feed(xe_decoder *d, const int32_t *prompt, int n_prompt, int batch) {
   int32_t *zpos = h + static_cast<size_t>(n_prompt) * batch;
   for (int b = 0; b < batch; b++) zpos[b] = 0;
   XE_HIP(hipMemcpyAsync(d->pos, zpos, batch * 4, hipMemcpyHostToDevice, d->s));
+  XE_HIP(hipMemsetAsync(d->stop_dev + 1, 0, batch * 4, d->s));  // no stream has stopped
   if (use_ll(d, batch)) {  // the whole prompt in one launch, tokens forced
     XE_HIP(hipMemcpyAsync(d->ll_forced, h, static_cast<size_t>(n_prompt) * batch * 4, hipMemcpyHostToDevice, d->s));
     XE_HIP(hipMemcpyAsync(d->tokens, h, batch * 4, hipMemcpyHostToDevice, d->s));
@@ -2298,6 +2347,10 @@ void feed(xe_decoder *d, const int32_t *prompt, int n_prompt, int batch) {
   for (int p = 0; p < n_prompt; p++) {
     XE_HIP(hipMemcpyAsync(d->tokens, h + static_cast<size_t>(p) * batch, batch * 4,
                           hipMemcpyHostToDevice, d->s));
+    // only the last prompt step's argmax is a generated token: earlier
+    // steps' stop marks are cleared
+    if (p == n_prompt - 1 && p > 0 && d->stop_id >= 0)
+      XE_HIP(hipMemsetAsync(d->stop_dev + 1, 0, batch * 4, d->s));
     run_step(d, batch);
   }
   XE_HIP(hipStreamSynchronize(d->s));
@@ -2307,8 +2360,10 @@ void feed(xe_decoder *d, const int32_t *prompt, int n_prompt, int batch) {
 }
 
 // n_steps further greedy steps from the device state; out [batch, n_steps]
-// receives the tokens those steps emit (may be NULL).
-void decode(xe_decoder *d, int batch, int n_steps, int32_t *out, double *device_us) {
+// receives the tokens those steps emit (may be NULL).  With a stop token set
+// the run ends once every stream has emitted it (the stop token fills the
+// rest of a stopped stream's row); returns the steps that ran.
+int decode(xe_decoder *d, int batch, int n_steps, int32_t *out, double *device_us) {
   check_ready(d, batch);
   XE_REQUIRE(d->live > 0, "feed a prompt first");
   XE_REQUIRE(n_steps >= 0, "negative step count");
@@ -2318,11 +2373,35 @@ void decode(xe_decoder *d, int batch, int n_steps, int32_t *out, double *device_
   XE_HIP(hipEventCreate(&e0));
   XE_HIP(hipEventCreate(&e1));
   const bool ll_exec = use_ll(d, batch);
+  const bool stop = d->stop_id >= 0;
+  // with a stop token the host looks at the done flags after every chunk of
+  // steps (a low-latency launch also ends by itself once every stream is
+  // done) and launches no more once all streams have stopped
+  int32_t *hdone = d->host_tok;
+  auto all_done = [&]() -> bool {
+    XE_HIP(hipMemcpyAsync(hdone, d->stop_dev + 1, batch * 4, hipMemcpyDeviceToHost, d->s));
+    XE_HIP(hipStreamSynchronize(d->s));
+    for (int b = 0; b < batch; b++)
+      if (!hdone[b]) return false;
+    return true;
+  };
+  XE_HIP(hipStreamSynchronize(d->s));  // host_tok staging is free
+  std::vector<int32_t> pre_done(batch, 0);  // streams stopped before this run
+  if (stop) {
+    (void)all_done();
+    pre_done.assign(hdone, hdone + batch);
+  }
   XE_HIP(hipEventRecord(e0, d->s));
   if (ll_exec) {
-    for (int i = 0; i < n_steps; i += kLLChunk) run_ll(d, batch, std::min(kLLChunk, n_steps - i), nullptr, 0, false);
+    for (int i = 0; i < n_steps; i += kLLChunk) {
+      if (stop && all_done()) break;
+      run_ll(d, batch, std::min(kLLChunk, n_steps - i), nullptr, 0, false);
+    }
   } else {
-    for (int i = 0; i < n_steps; i++) run_step(d, batch);
+    for (int i = 0; i < n_steps; i++) {
+      if (stop && i % kStopCheck == 0 && all_done()) break;
+      run_step(d, batch);
+    }
   }
   XE_HIP(hipEventRecord(e1, d->s));
   XE_HIP(hipEventSynchronize(e1));
@@ -2331,17 +2410,29 @@ void decode(xe_decoder *d, int batch, int n_steps, int32_t *out, double *device_
   (void)hipEventDestroy(e0);
   (void)hipEventDestroy(e1);
   check_step_status(d);
-  if (n_steps > 0) d->last_step_us = 1000.0 * ms / n_steps;
+  // steps that ran (streams advance in lockstep)
+  int ran = n_steps;
+  if (stop && n_steps > 0) {
+    XE_HIP(hipMemcpy(hdone, d->pos, 4, hipMemcpyDeviceToHost));
+    ran = std::max(0, std::min(n_steps, hdone[0] - first_pos[0]));
+  }
+  if (ran > 0) d->last_step_us = 1000.0 * ms / ran;
   if (device_us) *device_us = 1000.0 * ms;
-  for (int b = 0; b < batch; b++) d->hpos[b] += n_steps;
+  for (int b = 0; b < batch; b++) d->hpos[b] += ran;
   if (out && n_steps > 0) {
     std::vector<int32_t> hist(static_cast<size_t>(batch) * (d->c.max_ctx + 1));
     XE_HIP(hipMemcpy(hist.data(), d->hist, hist.size() * 4, hipMemcpyDeviceToHost));
-    for (int b = 0; b < batch; b++)
-      for (int i = 0; i < n_steps; i++)
-        out[static_cast<size_t>(b) * n_steps + i] =
-            hist[static_cast<size_t>(b) * (d->c.max_ctx + 1) + first_pos[b] + i];
+    for (int b = 0; b < batch; b++) {
+      bool done = pre_done[b] != 0;  // a stream that had stopped emits nothing more
+      for (int i = 0; i < n_steps; i++) {
+        int32_t t = i < ran ? hist[static_cast<size_t>(b) * (d->c.max_ctx + 1) + first_pos[b] + i] : d->stop_id;
+        if (done) t = d->stop_id;
+        if (stop && t == d->stop_id) done = true;
+        out[static_cast<size_t>(b) * n_steps + i] = t;
+      }
+    }
   }
+  return ran;
 }
 
 }  // namespace
@@ -2361,7 +2452,20 @@ int xe_decoder_decode(xe_decoder *d, int batch, int n_steps, int32_t *out, doubl
   return guard_d([&]() -> int {
     XE_REQUIRE(d, "null decoder");
     DeviceGuard dg(d->dev->ordinal);
-    decode(d, batch, n_steps, out, device_us);
+    return decode(d, batch, n_steps, out, device_us);
+  }, -1);
+}
+
+int xe_decoder_set_stop(xe_decoder *d, int32_t stop_id) {
+  return guard_d([&]() -> int {
+    XE_REQUIRE(d, "null decoder");
+    XE_REQUIRE(stop_id >= -1 && stop_id < d->c.vocab, "stop token must be -1 (none) or a token id");
+    DeviceGuard dg(d->dev->ordinal);
+    XE_HIP(hipStreamSynchronize(d->s));  // host_tok staging is free
+    d->host_tok[0] = stop_id;
+    XE_HIP(hipMemcpyAsync(d->stop_dev, d->host_tok, 4, hipMemcpyHostToDevice, d->s));
+    XE_HIP(hipStreamSynchronize(d->s));
+    d->stop_id = stop_id;
     return 0;
   }, -1);
 }
@@ -2385,11 +2489,29 @@ int xe_decoder_generate(xe_decoder *d, const int32_t *prompt, int n_prompt, int 
     decode(d, batch, n_new - 1, rest.data(), nullptr);
     for (int b = 0; b < batch; b++) {
       out[static_cast<size_t>(b) * n_new] = first[b];
+      const bool done = d->stop_id >= 0 && first[b] == d->stop_id;
       for (int i = 0; i + 1 < n_new; i++)
-        out[static_cast<size_t>(b) * n_new + 1 + i] = rest[static_cast<size_t>(b) * (n_new - 1) + i];
+        out[static_cast<size_t>(b) * n_new + 1 + i] =
+            done ? d->stop_id : rest[static_cast<size_t>(b) * (n_new - 1) + i];
     }
     return 0;
   }, -1);
+}
+
+int xe_decoder_generate_until(xe_decoder *d, const int32_t *prompt, int n_prompt, int batch, int max_new,
+                              int32_t stop_id, int32_t *out, int32_t *n_out) {
+  const int prev = d ? d->stop_id : -1;
+  if (xe_decoder_set_stop(d, stop_id) != 0) return -1;
+  const int rc = xe_decoder_generate(d, prompt, n_prompt, batch, max_new, out);
+  if (xe_decoder_set_stop(d, prev) != 0) return -1;
+  if (rc != 0) return rc;
+  if (n_out)
+    for (int b = 0; b < batch; b++) {
+      int n = 0;
+      while (n < max_new && (stop_id < 0 || out[static_cast<size_t>(b) * max_new + n] != stop_id)) n++;
+      n_out[b] = n;
+    }
+  return 0;
 }
 
 int xe_decoder_profile_step(xe_decoder *d, int batch, int max_entries, char *labels, double *us,

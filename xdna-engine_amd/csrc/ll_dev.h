@@ -201,6 +201,11 @@ struct StepParams {
   int hist_stride;
   const int32_t *forced;  // [n_forced][nb] input tokens of the first steps, or null
   int n_forced;
+  // stop rule (whisper.rs:618-668): a stream whose generated token is `stop`
+  // is done (done[b], kept across launches) and is fed `stop` from then on;
+  // the launch ends once every stream is done.  stop < 0: no rule.
+  int stop;
+  int32_t *done;
   int n_steps;
   unsigned ep0;  // epoch of step 0 (>= 1; buffers start at epoch 0)
   unsigned *status;

@@ -85,7 +85,7 @@ __global__ __launch_bounds__(kT) void ll_step_kernel(StepParams sp) {
   extern __shared__ float4 lds4[];
   __shared__ float red[2 * 4 * gdev::kMaxWaves];
   __shared__ int bad;
-  __shared__ int s_tok[kMaxNB], s_pos[kMaxNB];
+  __shared__ int s_tok[kMaxNB], s_pos[kMaxNB], s_done[kMaxNB];
   __shared__ float s_bv[kW][kMaxNB];
   __shared__ int s_bi[kW][kMaxNB];
   float *lds = reinterpret_cast<float *>(lds4);
@@ -114,6 +114,7 @@ __global__ __launch_bounds__(kT) void ll_step_kernel(StepParams sp) {
     const int b = threadIdx.x;
     s_tok[b] = (sp.forced && sp.n_forced > 0) ? gptr(sp.forced)[b] : gptr(sp.tokens)[b];
     s_pos[b] = gptr(sp.pos)[b];
+    s_done[b] = sp.stop >= 0 ? gptr(sp.done)[b] : 0;
   }
   __syncthreads();
   const Ctl c{sp.status, sp.limit, &bad};
@@ -364,17 +365,29 @@ __global__ __launch_bounds__(kT) void ll_step_kernel(StepParams sp) {
         }
       if (idx < 0) idx = 0;
       const int ps = s_pos[b];
-      const int nxt = (sp.forced && step + 1 < sp.n_forced) ? gptr(sp.forced)[(step + 1) * nb + b] : idx;
+      // a forced (prompt) step's argmax is not a generated token
+      const bool gen = !(sp.forced && step + 1 < sp.n_forced);
+      int nxt = gen ? idx : gptr(sp.forced)[(step + 1) * nb + b];
+      if (gen && sp.stop >= 0 && (s_done[b] != 0 || idx == sp.stop)) {
+        s_done[b] = 1;
+        nxt = sp.stop;
+      }
       if (blockIdx.x == 0) {
         if (ps >= 0 && ps < sp.hist_stride) gptr_w(sp.hist)[static_cast<size_t>(b) * sp.hist_stride + ps] = idx;
         gptr_w(sp.next)[b] = idx;
         gptr_w(sp.tokens)[b] = nxt;
         gptr_w(sp.pos)[b] = ps + 1;
+        if (sp.stop >= 0) gptr_w(sp.done)[b] = s_done[b];
       }
       s_tok[b] = nxt;
       s_pos[b] = ps + 1;
     }
     __syncthreads();
+    if (sp.stop >= 0) {  // every workgroup holds the same flags: all leave at the same step
+      bool all = true;
+      for (int b = 0; b < nb; b++) all = all && s_done[b] != 0;
+      if (all) break;
+    }
     embed(sp, s_tok, s_pos, xr);
     __syncthreads();
     mark(step, tslots + 2);

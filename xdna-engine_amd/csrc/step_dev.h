@@ -53,6 +53,11 @@ struct ArgmaxParams {
   int *part_i;
   int32_t *next, *tokens, *pos, *hist;
   int hist_stride;
+  // stop rule (whisper.rs:618-668): stop[0] is the stop token (< 0: none);
+  // done[b] marks a stream that has emitted it, which is then fed the stop
+  // token.  done may be null (no rule).
+  const int32_t *stop;
+  int32_t *done;
 };
 
 struct Phase {
@@ -173,8 +178,16 @@ __device__ __forceinline__ void argmax_final_block(const ArgmaxParams &p, int b)
   }
   if (threadIdx.x != 0) return;
   if (idx < 0) idx = 0;
+  int tok = idx;
+  if (p.done) {
+    const int st = p.stop[0];
+    if (st >= 0 && (p.done[b] != 0 || idx == st)) {
+      p.done[b] = 1;
+      tok = st;
+    }
+  }
   p.next[b] = idx;
-  p.tokens[b] = idx;
+  p.tokens[b] = tok;
   const int ps = p.pos[b];
   if (ps >= 0 && ps < p.hist_stride) p.hist[static_cast<size_t>(b) * p.hist_stride + ps] = idx;
   p.pos[b] = ps + 1;

@@ -46,9 +46,11 @@ EXPORTS = [
     "xe_w8a8_linear_dev",
     "xe_attn_decode", "xe_attn_decode_dev", "xe_attn_decode_dev_static", "xe_ctx_synchronize", "xe_decoder_create",
     "xe_decoder_destroy", "xe_decoder_init_synthetic", "xe_decoder_set_tensor",
-    "xe_decoder_get_tensor_q8", "xe_decoder_reset", "xe_decoder_set_cross", "xe_decoder_set_cross_int8",
+    "xe_decoder_get_tensor_q8", "xe_decoder_reset", "xe_decoder_prime_kv", "xe_decoder_set_cross",
+    "xe_decoder_set_cross_int8",
     "xe_decoder_step",
-    "xe_decoder_generate", "xe_decoder_last_step_us", "xe_decoder_weight_bytes",
+    "xe_decoder_generate", "xe_decoder_last_step_us", "xe_decoder_weight_bytes", "xe_decoder_set_stop",
+    "xe_decoder_generate_until",
     "xe_decoder_feed", "xe_decoder_decode", "xe_decoder_profile_step", "xe_decoder_executor",
     "xe_model_tensor_shape", "xe_decoder_config", "xe_decoder_load_safetensors", "xe_safetensors_plan",
     "xe_ctx_record", "xe_run_query", "xe_run_wait", "xe_run_free", "xe_resident_open", "xe_resident_close",
@@ -161,10 +163,13 @@ def lib():
         "xe_decoder_set_tensor": (i, [vp, i, i, vp, sz]),
         "xe_decoder_get_tensor_q8": (i, [vp, i, i, vp, vp]),
         "xe_decoder_reset": (i, [vp]),
+        "xe_decoder_prime_kv": (i, [vp, i, i, u64]),
         "xe_decoder_set_cross": (i, [vp, vp]),
         "xe_decoder_set_cross_int8": (i, [vp, i, i]),
         "xe_decoder_step": (i, [vp, vp, vp, i, vp, vp]),
         "xe_decoder_generate": (i, [vp, vp, i, i, i, vp]),
+        "xe_decoder_set_stop": (i, [vp, C.c_int32]),
+        "xe_decoder_generate_until": (i, [vp, vp, i, i, i, C.c_int32, vp, vp]),
         "xe_decoder_last_step_us": (C.c_double, [vp]),
         "xe_decoder_feed": (i, [vp, vp, i, i]),
         "xe_decoder_decode": (i, [vp, i, i, vp, C.POINTER(C.c_double)]),
@@ -606,6 +611,11 @@ class Decoder:
     def reset(self):
         _check(lib().xe_decoder_reset(self.h))
 
+    def prime_kv(self, stream, n_pos, seed=0):
+        """Synthetic bf16 K/V rows [0, n_pos) of one stream (the oracle's
+        prime_kv values); the stream's next position becomes n_pos."""
+        _check(lib().xe_decoder_prime_kv(self.h, stream, n_pos, seed))
+
     def precompute_cross(self, enc=None):
         e = _f32(enc)
         _check(lib().xe_decoder_set_cross(self.h, _p(e)))
@@ -630,6 +640,20 @@ class Decoder:
         _check(lib().xe_decoder_generate(self.h, _p(prompt), n_prompt, b, n_new, _p(out)))
         return out
 
+    def set_stop(self, stop_id):
+        """Stop token of the device greedy loop (-1: none)."""
+        _check(lib().xe_decoder_set_stop(self.h, int(stop_id)))
+
+    def generate_until(self, prompt, max_new, stop_id):
+        """(out [batch, max_new] padded with stop_id, n_out [batch])."""
+        prompt = np.ascontiguousarray(np.atleast_2d(prompt), np.int32)
+        b, n_prompt = prompt.shape
+        out = np.empty((b, max_new), np.int32)
+        n_out = np.empty(b, np.int32)
+        _check(lib().xe_decoder_generate_until(self.h, _p(prompt), n_prompt, b, max_new, int(stop_id),
+                                               _p(out), _p(n_out)))
+        return out, n_out
+
     def feed(self, prompt):
         prompt = np.ascontiguousarray(np.atleast_2d(prompt), np.int32)
         b, n = prompt.shape
@@ -641,7 +665,7 @@ class Decoder:
         b = batch or self.batch
         out = np.empty((b, n_steps), np.int32) if want_tokens else None
         us = C.c_double()
-        _check(lib().xe_decoder_decode(self.h, b, n_steps, _p(out), C.byref(us)))
+        self.steps_run = _check(lib().xe_decoder_decode(self.h, b, n_steps, _p(out), C.byref(us)))
         return out, us.value
 
     def profile_step(self, batch=None, max_entries=4096):
