@@ -293,3 +293,33 @@ def test_gpu_reference_arena_equals_set_tensor(tmp_path, gpu, xe):
     a.close()
     b.close()
     om.close()
+
+
+def _raw_safetensors(path, header, data=b""):
+    h = header.encode()
+    with open(path, "wb") as f:
+        f.write(len(h).to_bytes(8, "little") + h + data)
+    return str(path)
+
+
+@pytest.mark.parametrize("header,msg", [
+    ('{"a":{"dtype":"F32","shape":[2],"data_offsets":[-8,0]}}', "non-negative integer"),
+    ('{"a":{"dtype":"F32","shape":[2],"data_offsets":[0,7.5]}}', "non-negative integer"),
+    ('{"a":{"dtype":"F32","shape":[2],"data_offsets":[0,"8"]}}', "non-negative integer"),
+    ('{"a":{"dtype":"F32","shape":[-2],"data_offsets":[0,8]}}', "non-negative integer"),
+    ('{"a":{"dtype":"F32","shape":[1e300],"data_offsets":[0,8]}}', "non-negative integer"),
+    ('{"a":{"dtype":"F32","shape":[4294967296,4294967296,16],"data_offsets":[0,8]}}', "overflows"),
+    ('{"a":{"dtype":"F32","shape":[3],"data_offsets":[0,8]}}', "does not match its shape"),
+    ('1234567', "object expected"),
+])
+def test_plan_refuses_malformed_headers(tmp_path, xe, header, msg):
+    """Header fields are checked before use: offsets and shape entries must
+    be non-negative integers below 2^53, a shape's element count must not
+    overflow, and a header that is a bare number at the end of the file is
+    parsed from a terminated copy (nothing is read past it)."""
+    p = _raw_safetensors(tmp_path / "bad.safetensors", header, b"\0" * 8)
+    if header == "1234567":  # the header ends the file
+        p = _raw_safetensors(tmp_path / "bare.safetensors", header)
+    cfg = xe.OPT_125M.replace(n_layers=1)
+    with pytest.raises(xe.XdnaError, match=msg):
+        xe.safetensors_plan(p, cfg)

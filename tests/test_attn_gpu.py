@@ -64,7 +64,7 @@ for (hq, hkv, hd) in [(12, 12, 64), (4, 1, 256)]:
     for ctxlen in [128, 1024, 4096]:
         for b in [1, 16, 64]:
             CASES.append((hq, hkv, hd, ctxlen, b))
-CASES += [(12, 12, 64, 32768, 2), (4, 1, 256, 32768, 8)]
+CASES += [(12, 12, 64, 32768, 1), (12, 12, 64, 32768, 2), (4, 1, 256, 32768, 1), (4, 1, 256, 32768, 8)]
 
 
 @pytest.mark.parametrize("hq,hkv,hd,ctxlen,b", CASES)

@@ -56,8 +56,8 @@ def test_norm_gemv_int8_config2(gpu, xe, m, k, b):
     close(got, want)
 
 
-@pytest.mark.parametrize("m,k", SHAPES[:4])
-@pytest.mark.parametrize("b", [1, 8])
+@pytest.mark.parametrize("m,k", SHAPES)
+@pytest.mark.parametrize("b", [1, 4, 8])
 def test_norm_gemv_bfp16_config2(gpu, xe, m, k, b):
     dev, ctx = gpu
     print("[case] bfp16 LN+GEMV m=%d k=%d b=%d" % (m, k, b), flush=True)
@@ -75,8 +75,8 @@ def test_norm_gemv_bfp16_config2(gpu, xe, m, k, b):
     close(got, want)
 
 
-@pytest.mark.parametrize("m,k", SHAPES[:3])
-@pytest.mark.parametrize("b", [1, 4])
+@pytest.mark.parametrize("m,k", SHAPES)
+@pytest.mark.parametrize("b", [1, 4, 8])
 def test_norm_gemv_bf16_config2(gpu, xe, m, k, b):
     dev, ctx = gpu
     print("[case] bf16 LN+GEMV m=%d k=%d b=%d" % (m, k, b), flush=True)
@@ -222,6 +222,45 @@ def test_i8act_bit_exact(gpu, xe, b):
         want = np.empty((b, m), np.int32)
         O.lib().xo_gemm_i8i8_i32(xq, b, k, q, m, want)
         assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("m,k", SHAPES)
+@pytest.mark.parametrize("b", [1, 4, 8])
+def test_i8act_config2_bit_exact(gpu, xe, m, k, b):
+    """Config 2's int8-activation variant at every shape and batch: x and W
+    int8 U[-127, 127], i32 outputs equal to the exact integer products."""
+    dev, ctx = gpu
+    print("[case] i8act config2 m=%d k=%d b=%d" % (m, k, b), flush=True)
+    rng = np.random.default_rng(m + 3 * k + b)
+    q = rng.integers(-127, 128, (m, k)).astype(np.int8)
+    xq = rng.integers(-127, 128, (b, k)).astype(np.int8)
+    w = ctx.register_weight_q8(q, rng.uniform(0.001, 0.02, m).astype(np.float32))
+    got = ctx.gemv_i8act(w, xq)
+    w.free()
+    want = np.empty((b, m), np.int32)
+    O.lib().xo_gemm_i8i8_i32(xq, b, k, q, m, want)
+    assert np.array_equal(got, want)
+
+
+def test_bfp16_encoder_half_even_ties(gpu, xe):
+    """The product's bfp16 encoder rounds exact half-quantum ties to even
+    (golden_ffn_gemm.py:47, numpy round): the block [64, 2.5, -2.5, 3.5,
+    0 ...] has e = floor(log2 64) = 6, quantum 2^(e - 6) = 1, so it stores
+    [64, 2, -2, 4, 0 ...] with exponent byte 6 + 127 = 133.  Read back through
+    the GEMV with one-hot inputs (y = W[:, i])."""
+    dev, ctx = gpu
+    k = 16
+    wf = np.zeros((2, k), np.float32)
+    wf[0, :4] = [64.0, 2.5, -2.5, 3.5]
+    wf[1, 8:12] = [-64.0, 0.5, 1.5, -0.5]  # quantum 1: 0, 2, -0
+    w = ctx.register_weight(wf, xe.XE_BFP16)
+    eye = np.eye(k, dtype=np.float32)
+    got = np.vstack([ctx.gemv(w, eye[:8]), ctx.gemv(w, eye[8:])])  # row i: W[:, i]
+    w.free()
+    want = np.zeros((2, k), np.float32)
+    want[0, :4] = [64, 2, -2, 4]
+    want[1, 8:12] = [-64, 0, 2, 0]
+    assert np.array_equal(np.asarray(got).T, want)
 
 
 def test_w8a8_linear_bit_exact(gpu, xe):

@@ -222,6 +222,32 @@ def test_gemma3_1b_primed_long_context(gpu, xe, default_executor, n_layers, batc
     om.close()
 
 
+def test_whisper_small_b1_228_positions(gpu, xe, default_executor):
+    """Config 4 at b = 1 over the positions bench.py times: a 4-token prompt
+    and 224 greedy steps (positions up to 227) on the low-latency executor,
+    against the oracle (a stream parting at a near-tie is replayed by the
+    oracle to its end)."""
+    run_pair(xe, gpu, xe.WHISPER_SMALL, seed=1, batch=1, n_prompt=4, n_new=224,
+             label="whisper-small-b1-228", want_exec="ll", logit_steps=1, prompt_seed=6, atol=2e-3)
+
+
+def test_whisper_small_bfp16(gpu, xe, default_executor):
+    """Config 4's bfp16 variant at the Whisper-small shape (12 layers, vocab
+    51865, 1500 cross frames): a short greedy stream and step logits."""
+    run_pair(xe, gpu, xe.WHISPER_SMALL.replace(wdtype=xe.XE_BFP16), seed=1, batch=1, n_prompt=4,
+             n_new=24, label="whisper-small-bfp16", want_exec="ll", logit_steps=1, prompt_seed=7,
+             atol=2e-3)
+
+
+def test_gemma3_1b_bf16_baseline(gpu, xe, default_executor):
+    """Config 5's bf16 baseline: Gemma-3-1B with bf16 weights (2.0 GB a
+    token), 26 layers, the tied 262144-row head, max_ctx 4096, a 32-token
+    prompt and a short greedy stream."""
+    run_pair(xe, gpu, xe.GEMMA3_1B.replace(wdtype=xe.XE_BF16, max_ctx=4096), seed=2, batch=1,
+             n_prompt=32, n_new=8, label="gemma3-1b-bf16", want_exec="ll", logit_steps=1,
+             prompt_seed=8, atol=5e-3)
+
+
 def test_whisper_small_b32_224_steps(gpu, xe, default_executor):
     """Config 4: Whisper-small, 32 streams, 4-token prompt, 224 greedy steps
     on the device loop.  The oracle replays the GPU's tokens: each must be

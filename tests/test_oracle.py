@@ -385,6 +385,21 @@ def test_bfp16_exact_on_representable_blocks():
     assert np.array_equal(exps.astype(np.int64) - 127, e)
 
 
+def test_bfp16_half_even_ties():
+    """Exact half-quantum ties round to even (golden_ffn_gemm.py:47 uses
+    numpy's round): [64, 2.5, -2.5, 3.5, 0 ...] has e = 6 and quantum 1, so it
+    encodes to [64, 2, -2, 4, 0 ...] with exponent byte 133; a half-away
+    encoder would give [64, 3, -3, 4].  A second block checks +-0.5 -> 0 and
+    1.5 -> 2 under a negative block maximum."""
+    w = np.zeros((2, 16), np.float32)
+    w[0, :4] = [64.0, 2.5, -2.5, 3.5]
+    w[1, 8:12] = [-64.0, 0.5, 1.5, -0.5]
+    mant, exps = O.bfp16_encode(w)
+    assert list(mant[0, :8]) == [64, 2, -2, 4, 0, 0, 0, 0]
+    assert list(mant[1, 8:16]) == [-64, 0, 2, 0, 0, 0, 0, 0]
+    assert exps[0, 0] == 133 and exps[1, 1] == 133
+
+
 def test_bfp16_error_bound_and_saturation():
     rng = np.random.default_rng(5)
     w = rng.standard_normal((16, 128)).astype(np.float32)

@@ -17,6 +17,8 @@
 #include <unistd.h>
 
 #include <cctype>
+#include <cmath>
+#include <cstdint>
 #include <cstdio>
 #include <cstdlib>
 #include <map>
@@ -167,6 +169,14 @@ struct TensorRef {
   size_t bytes = 0;
 };
 
+// A JSON number that must be a non-negative integer below 2^53 (exact in a
+// double): shape entries and data offsets.
+size_t json_index(const JVal &v, const std::string &what) {
+  XE_REQUIRE(v.t == JVal::NUM && v.num >= 0.0 && v.num < 9007199254740992.0 && std::floor(v.num) == v.num,
+             "safetensors header: " + what + " must be a non-negative integer");
+  return static_cast<size_t>(v.num);
+}
+
 struct StFile {
   int fd = -1;
   void *map = nullptr;
@@ -188,7 +198,10 @@ struct StFile {
     for (int i = 7; i >= 0; i--) hlen = hlen << 8 | b[i];  // little-endian u64
     XE_REQUIRE(hlen > 0 && hlen <= size - 8 && hlen < (uint64_t(100) << 20),
                std::string(path) + ": bad safetensors header length");
-    JParser jp{reinterpret_cast<const char *>(b + 8), reinterpret_cast<const char *>(b + 8 + hlen)};
+    // the header is parsed from a NUL-terminated copy: a number at its end
+    // cannot read on into tensor data or past the mapping
+    const std::string hdr(reinterpret_cast<const char *>(b + 8), static_cast<size_t>(hlen));
+    JParser jp{hdr.c_str(), hdr.c_str() + hdr.size()};
     JVal root = jp.value();
     XE_REQUIRE(root.t == JVal::OBJ, "safetensors header: object expected");
     const uint8_t *data0 = b + 8 + hlen;
@@ -208,14 +221,18 @@ struct StFile {
       r.dtype = dt->str;
       size_t n = 1;
       for (const auto &d : sh->arr) {
-        XE_REQUIRE(d.t == JVal::NUM && d.num >= 0, "safetensors header: bad shape of " + kv.first);
-        r.shape.push_back(static_cast<int64_t>(d.num));
-        n *= static_cast<size_t>(d.num);
+        const size_t dim = json_index(d, "shape of " + kv.first);
+        XE_REQUIRE(dim == 0 || n <= SIZE_MAX / dim, "safetensors header: shape of " + kv.first + " overflows");
+        r.shape.push_back(static_cast<int64_t>(dim));
+        n *= dim;
       }
-      const size_t o0 = static_cast<size_t>(off->arr[0].num), o1 = static_cast<size_t>(off->arr[1].num);
+      const size_t o0 = json_index(off->arr[0], "data_offsets of " + kv.first);
+      const size_t o1 = json_index(off->arr[1], "data_offsets of " + kv.first);
       XE_REQUIRE(o0 <= o1 && o1 <= data_size, "safetensors header: data_offsets of " + kv.first + " out of range");
       const size_t esz = r.dtype == "F32" ? 4 : (r.dtype == "BF16" || r.dtype == "F16") ? 2 : 0;
-      if (esz) XE_REQUIRE(o1 - o0 == n * esz, "safetensors: byte size of " + kv.first + " does not match its shape");
+      if (esz)
+        XE_REQUIRE(n <= SIZE_MAX / esz && o1 - o0 == n * esz,
+                   "safetensors: byte size of " + kv.first + " does not match its shape");
       r.data = data0 + o0;
       r.bytes = o1 - o0;
       tensors[kv.first] = r;
