@@ -476,11 +476,12 @@ int xe_decoder_profile_step(xe_decoder *dec, int batch, int max_entries, char *l
 /* Executor a decode step of `batch` streams runs on.  XE_EXEC_LL is the
  * default wherever its plan supports the model and batch: one cooperative
  * launch per token run, workgroups exchanging activations through HBM.  The
- * others launch one kernel per phase (HIP graph, a persistent kernel with
- * grid barriers, or eager launches), selected with XE_STEP=graph|persistent|
- * eager.  No counterpart in the reference (its executors are fixed per
- * backend); returns -1 on error. */
-enum { XE_EXEC_GRAPH = 0, XE_EXEC_PERSISTENT = 1, XE_EXEC_EAGER = 2, XE_EXEC_LL = 3 };
+ * others launch one kernel per phase: replayed from a HIP graph (the
+ * default beyond the low-latency plan, or XE_STEP=graph) or launched eagerly
+ * (XE_STEP=eager).  Value 1 is retired (a persistent phase kernel with grid
+ * barriers, removed: it was slower than both).  No counterpart in the
+ * reference (its executors are fixed per backend); returns -1 on error. */
+enum { XE_EXEC_GRAPH = 0, XE_EXEC_EAGER = 2, XE_EXEC_LL = 3 };
 int xe_decoder_executor(xe_decoder *dec, int batch);
 /* Resident decode step (ElfResident, npu-xrt/src/lib.rs:591-629 and
  * xrt_shim.h:95-111: a constant program bound once, per-token parameters

@@ -24,7 +24,7 @@ from parity_util import compare_logits, greedy_identity
 pytestmark = pytest.mark.gpu
 
 
-@pytest.fixture(params=["graph", "persistent", "ll"])
+@pytest.fixture(params=["graph", "ll"])
 def executor(request):
     """Run the test under each step executor (XE_STEP is read at every step)."""
     old = os.environ.get("XE_STEP")

@@ -256,11 +256,11 @@ constexpr int kMaxOpBatch = 512;  // the reference's largest batched tile (Mp <=
 
 void launch_linear(xe_ctx *ctx, const xe_weight *w, const void *x, int x_dtype, int batch,
                    float *y, hipStream_t s) {
-  if (batch <= 8) {
+  if (!gemm_preferred(w->m, w->k, batch)) {
     launch_gemv(gemv_args(w, x, x_dtype, batch, y), s);
   } else {
-    XE_REQUIRE(x_dtype == XE_F32, "more than 8 rows need fp32 x");
-    ctx->ensure_gemm(w->norm != XE_NORM_NONE ? static_cast<size_t>(batch) * w->k : 0);
+    // the prologue (norm, or bf16 x to fp32) writes batch x k floats
+    ctx->ensure_gemm(w->norm != XE_NORM_NONE || x_dtype == XE_BF16 ? static_cast<size_t>(batch) * w->k : 0);
     launch_gemm_op(gemv_args(w, x, x_dtype, batch, y), ctx->gemm_xn, ctx->gemm_ws, ctx->gemm_cnt, s);
   }
   ctx->dispatches++;
@@ -1065,7 +1065,8 @@ int xe_probe_gemv(xe_ctx *ctx, const xe_weight *const *ws, int n_weights, const 
       XE_REQUIRE(ws[i]->m == ws[0]->m && ws[i]->k == ws[0]->k, "probe weights differ in shape");
     }
     DeviceGuard dg(ctx->dev->ordinal);
-    if (batch > 8) ctx->ensure_gemm(static_cast<size_t>(batch) * ws[0]->k);  // no allocation under capture
+    if (gemm_preferred(ws[0]->m, ws[0]->k, batch))
+      ctx->ensure_gemm(static_cast<size_t>(batch) * ws[0]->k);  // no allocation under capture
     const double us = time_captured(ctx, reps, flags, [&]() {
       for (int i = 0; i < n_weights; i++)
         launch_linear(ctx, ws[i], x_dev, x_dtype, batch, y_dev, ctx->dev->stream);

@@ -20,9 +20,9 @@
 //     (m, l, acc) to the workspace (or the output when one split covers the
 //     whole length).
 // A "merge block" finishes 256 of the G*hd outputs of one (stream, kv head)
-// from the split partials, as a phase of its own (a launch, or a phase of the
-// persistent step kernel).  With arrival counters (AttnParams::cnt) the
-// standalone split kernel merges in place instead: each split block stores
+// from the split partials, as a launch of its own (a caller's workspace
+// without counters).  With arrival counters (AttnParams::cnt) the split
+// kernel merges in place instead: each split block stores
 // its partial with sc1 stores (past the XCD's own L2), waits for them, counts
 // itself in the (stream, kv head)'s counter with an agent-scope atomic, and
 // the last to arrive reads every partial with sc1 loads and writes the output

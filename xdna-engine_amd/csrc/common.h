@@ -164,6 +164,9 @@ void launch_gemv(const GemvLaunch &p, hipStream_t s);
 // ws / cnt: split-K workspace (gemm_op_ws_floats() floats) and per-tile
 // arrival counters (gemm_op_cnt_words(), zeroed once; they re-arm).
 void launch_gemm_op(const GemvLaunch &L, float *xn, float *ws, unsigned *cnt, hipStream_t s);
+// Whether a projection of `batch` rows over an m x k weight runs on the MFMA
+// GEMM (gemm.hip) instead of the GEMV.
+bool gemm_preferred(int m, int k, int batch);
 size_t gemm_op_ws_floats();
 size_t gemm_op_cnt_words();
 // Output of an int8 x int8 -> i32 product: the raw accumulator (acc set), or

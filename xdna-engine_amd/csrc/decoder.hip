@@ -375,23 +375,17 @@ struct xe_decoder {
   int attn_splits = 1;
   int32_t *host_tok = nullptr;  // pinned staging [max_ctx + 1][max_batch] x 2
   int last_exec = XE_EXEC_GRAPH;  // executor of the last step launched (status messages)
-  // persistent step kernel: one flag slot (128 B) per workgroup + status word
-  unsigned int *step_flags = nullptr;
+  // status word of the low-latency step kernel's bounded waits
   unsigned int *step_status = nullptr;
-  int step_grid = 0;
   // one execution plan per batch size: the phase list of a step
   struct Plan {
     std::vector<sdev::Phase> phases;
     std::vector<std::string> labels;
     std::vector<double> bytes;  // algorithmic bytes per phase
-    sdev::Phase *dev_phases = nullptr;
-    size_t step_lds = 0;
-    int step_nb = 1;
-    bool persistent = false;
     hipGraphExec_t graph = nullptr;
   };
   std::map<int, Plan> plans;
-  // low-latency persistent executor (ll_dev.h): one plan per batch size
+  // low-latency executor (ll_dev.h): one plan per batch size
   struct LLPlan {
     bool ok = false;
     std::string why;  // reason it is unsupported
@@ -602,7 +596,7 @@ void alloc_decoder(xe_decoder *d) {
   d->qx = dalloc<float>(static_cast<size_t>(B) * D, s);
   d->logits = dalloc<float>(static_cast<size_t>(B) * c.vocab, s);
   d->xn = dalloc<float>(static_cast<size_t>(B) * std::max(std::max(D, F), std::max(hq, static_cast<int>(d->nqkv()))), s);
-  if (B > 8 || F > 4096) {  // the GEMM path can run (see PlanBuilder::gemv)
+  if (B >= 4 || F > 4096) {  // the GEMM path can run (see PlanBuilder::gemv)
     d->gemm_ws = dalloc<float>(gemm_ws_floats(), s);
     d->gemm_cnt = dalloc<unsigned>(gemm_cnt_words(), s);
     XE_HIP(hipMemsetAsync(d->gemm_cnt, 0, gemm_cnt_words() * sizeof(unsigned), s));
@@ -618,8 +612,6 @@ void alloc_decoder(xe_decoder *d) {
   XE_HIP(hipMemsetAsync(d->stop_dev, 0xff, 4, s));  // no stop token
   d->arg_v = dalloc<float>(static_cast<size_t>(B) * sdev::kArgBlocks, s);
   d->arg_i = dalloc<int>(static_cast<size_t>(B) * sdev::kArgBlocks, s);
-  d->step_grid = d->dev->num_cus > 0 ? d->dev->num_cus : 256;
-  d->step_flags = dalloc<unsigned int>(static_cast<size_t>(d->step_grid) * 32, s);
   d->step_status = dalloc<unsigned int>(64, s);
   d->ll_forced = dalloc<int32_t>(static_cast<size_t>(c.max_ctx + 1) * B, s);
   // split-K attention: the phase plan of a batch takes attn_splits_for(); the
@@ -660,7 +652,6 @@ void drop_plans(xe_decoder *d) {
   if (d->s) (void)hipStreamSynchronize(d->s);
   for (auto &kv : d->plans) {
     if (kv.second.graph) (void)hipGraphExecDestroy(kv.second.graph);
-    if (kv.second.dev_phases) (void)hipFree(kv.second.dev_phases);
   }
   d->plans.clear();
   for (auto &kv : d->ll_plans) {
@@ -673,7 +664,6 @@ void drop_plans(xe_decoder *d) {
 
 void free_decoder(xe_decoder *d) {
   drop_plans(d);
-  if (d->step_flags) (void)hipFree(d->step_flags);
   for (void *p : d->ll_fc2t)
     if (p) (void)hipFree(p);
   if (d->ll_forced) (void)hipFree(d->ll_forced);
@@ -744,15 +734,13 @@ double gemv_bytes(const GemvCall &g, int batch) {
 
 struct PlanBuilder {
   xe_decoder::Plan &plan;
-  int step_nb;
   float *xn = nullptr;  // GEMM path scratch (null: GEMV only)
   float *ws = nullptr;
   unsigned *cnt = nullptr;
-  void push(const sdev::Phase &ph, const std::string &label, double bytes, size_t lds) {
+  void push(const sdev::Phase &ph, const std::string &label, double bytes) {
     plan.phases.push_back(ph);
     plan.labels.push_back(label);
     plan.bytes.push_back(bytes);
-    plan.step_lds = std::max(plan.step_lds, lds);
   }
   // One projection over `batch` streams.  Up to 8 streams whose activations
   // fit the GEMV's LDS staging: the GEMV, in chunks of 8.  Otherwise the MFMA
@@ -760,7 +748,7 @@ struct PlanBuilder {
   // normalises or adds a residual.
   void gemv(const GemvCall &g, int batch, const std::string &label) {
     const size_t stage = gdev::gemv_lds_floats(std::min(batch, 8), g.m->cols, g.sub != nullptr) * sizeof(float);
-    if (xn && (batch > 8 || stage > 160 * 1024 - 1024)) {
+    if (xn && (gemm_preferred(g.m->rows, g.m->cols, batch) || stage > 160 * 1024 - 1024)) {
       gemm(g, batch, label);
       return;
     }
@@ -798,8 +786,7 @@ struct PlanBuilder {
       const int rows = 4 * (64 / t.lpr) * t.rpl;
       ph.nblocks = (L.m + rows - 1) / rows;
       ph.u.gemv = gdev::to_params(L);
-      push(ph, label, gemv_bytes(g, nb),
-           gdev::gemv_lds_floats(step_nb, L.k, L.sub != nullptr) * sizeof(float));
+      push(ph, label, gemv_bytes(g, nb));
     }
   }
   void gemm(const GemvCall &g, int batch, const std::string &label) {
@@ -833,8 +820,7 @@ struct PlanBuilder {
       ph.kind = sdev::PH_GEMM_PRO;
       ph.nblocks = batch;
       ph.xn = xn;
-      push(ph, label + "_pro", 4.0 * batch * L.k * (2 + (L.sub ? 1 : 0) + (L.res_out ? 1 : 0)),
-           gdev::gemv_lds_floats(1, L.k, L.sub != nullptr) * sizeof(float));
+      push(ph, label + "_pro", 4.0 * batch * L.k * (2 + (L.sub ? 1 : 0) + (L.res_out ? 1 : 0)));
       gdev::GemvParams &q = ph.u.gemv;
       q.x = xn;
       q.ldx = L.k;
@@ -848,7 +834,7 @@ struct PlanBuilder {
     ph.nblocks = ((L.m + 63) / 64) * ((batch + 63) / 64);
     ph.ws = ws;
     ph.cnt = cnt;
-    push(ph, label, gemv_bytes(g, batch), 0);
+    push(ph, label, gemv_bytes(g, batch));
   }
   void attn(const AttnLaunch &a, const std::string &label, double bytes) {
     sdev::Phase ph{};
@@ -857,12 +843,12 @@ struct PlanBuilder {
     ph.g = a.hq / a.hkv;
     ph.nblocks = a.max_splits * a.hkv * a.batch;
     ph.u.attn = adev::to_params(a);
-    push(ph, label, bytes, adev::attn_lds_floats(ph.hd, ph.g) * sizeof(float));
+    push(ph, label, bytes);
     if (a.max_splits > 1 && !a.cnt) {
       ph.kind = sdev::PH_MERGE;
       ph.nblocks = ((ph.g * ph.hd + 255) / 256) * a.hkv * a.batch;
       push(ph, label + "_merge",
-           4.0 * a.batch * a.hq * (a.hd + 2) * std::min(a.max_splits, 64), adev::merge_lds_floats() * sizeof(float));
+           4.0 * a.batch * a.hq * (a.hd + 2) * std::min(a.max_splits, 64));
     }
   }
 };
@@ -875,11 +861,9 @@ void build_plan(xe_decoder *d, int B, xe_decoder::Plan &plan) {
   const bool gem = c.family == XE_GEMMA3, wh = c.family == XE_WHISPER, opt = c.family == XE_OPT;
   const int nq = static_cast<int>(d->nqkv());
   const int norm = gem ? XE_NORM_RMS1P : XE_NORM_LN;
-  plan.step_nb = B <= 1 ? 1 : B <= 2 ? 2 : 4;
-  PlanBuilder pb{plan, plan.step_nb, d->gemm_ws ? d->xn : nullptr, d->gemm_ws, d->gemm_cnt};
-  // beyond 4 streams (no persistent step kernel) the split attention kernel
-  // merges in place; the step kernel keeps a merge phase
-  unsigned *attn_cnt = B > 4 ? d->attn_cnt : nullptr;
+  PlanBuilder pb{plan, d->gemm_ws ? d->xn : nullptr, d->gemm_ws, d->gemm_cnt};
+  // the split attention kernel merges in place (arrival counters)
+  unsigned *attn_cnt = d->attn_cnt;
 
   // embedding
   {
@@ -903,7 +887,7 @@ void build_plan(xe_decoder *d, int B, xe_decoder::Plan &plan) {
     e.batch = B;
     e.x = d->xa;
     ph.nblocks = B * ((D + 255) / 256);
-    pb.push(ph, "embed", static_cast<double>(B) * D * (wbytes(c.wdtype, 1) + 4 + (d->pos_emb ? 4 : 0)), 0);
+    pb.push(ph, "embed", static_cast<double>(B) * D * (wbytes(c.wdtype, 1) + 4 + (d->pos_emb ? 4 : 0)));
   }
   float *xcur = d->xa, *xalt = d->xb;
   const float *pend = nullptr, *pend_post = nullptr;
@@ -1093,16 +1077,11 @@ void build_plan(xe_decoder *d, int B, xe_decoder::Plan &plan) {
     ap.done = d->stop_dev + 1;
     ph.kind = sdev::PH_ARGMAX_PART;
     ph.nblocks = B * sdev::kArgBlocks;
-    pb.push(ph, "argmax", 4.0 * B * c.vocab, 512 * sizeof(float));
+    pb.push(ph, "argmax", 4.0 * B * c.vocab);
     ph.kind = sdev::PH_ARGMAX_FINAL;
     ph.nblocks = B;
-    pb.push(ph, "argmax_final", 8.0 * B * sdev::kArgBlocks, 0);
+    pb.push(ph, "argmax_final", 8.0 * B * sdev::kArgBlocks);
   }
-  bool gemm_phases = false;
-  for (const auto &ph : plan.phases) gemm_phases |= ph.kind == sdev::PH_GEMM || ph.kind == sdev::PH_GEMM_PRO;
-  plan.persistent = !getenv("XE_NO_PERSIST") && B <= 4 && !gemm_phases && !d->cross_i8k && !d->cross_i8v &&
-                    step_kernel_supported(c.wdtype, plan.step_nb, hd, c.n_heads / c.n_kv_heads) &&
-                    plan.step_lds <= 150 * 1024;
 }
 
 xe_decoder::Plan &plan_for(xe_decoder *d, int B) {
@@ -1110,14 +1089,11 @@ xe_decoder::Plan &plan_for(xe_decoder *d, int B) {
   if (it != d->plans.end()) return it->second;
   xe_decoder::Plan &plan = d->plans[B];
   build_plan(d, B, plan);
-  const size_t bytes = plan.phases.size() * sizeof(sdev::Phase);
-  XE_HIP(hipMalloc(reinterpret_cast<void **>(&plan.dev_phases), bytes));
-  XE_HIP(hipMemcpy(plan.dev_phases, plan.phases.data(), bytes, hipMemcpyHostToDevice));
   return plan;
 }
 
 // ---------------------------------------------------------------------------
-// low-latency persistent executor: phase lists per role (ll_dev.h)
+// low-latency executor: phase lists per role (ll_dev.h)
 // ---------------------------------------------------------------------------
 // GEMV tile for `ranks` workgroups of kT threads sharing m rows: lanes per
 // row LPR in {8, 16, 32, 64}, two rows per lane (ll_dev.h gemv_rows).  Each
@@ -1662,16 +1638,13 @@ void run_ll(xe_decoder *d, int B, int n_steps, const int32_t *forced, int n_forc
   d->ll_epoch += static_cast<unsigned>(n_steps);
 }
 
-// Executor choice: the phases as kernels in one HIP graph per token (the
-// default); XE_STEP=persistent selects the persistent step kernel where the
-// plan allows it (one launch per token, a grid barrier between phases);
-// XE_STEP=eager launches the phases one by one (profiling).
-enum class Exec { Persistent, Graph, Eager };
+// Executor choice for the phase kernels: one HIP graph per token (the
+// default); XE_STEP=eager launches the phases one by one (profiling).
+enum class Exec { Graph, Eager };
 
 Exec exec_for(const xe_decoder::Plan &plan) {
   const char *e = getenv("XE_STEP");
   if (getenv("XE_NO_GRAPH") || (e && std::string(e) == "eager")) return Exec::Eager;
-  if (e && std::string(e) == "persistent" && plan.persistent) return Exec::Persistent;
   return Exec::Graph;
 }
 
@@ -1704,30 +1677,14 @@ bool use_ll(xe_decoder *d, int B) {
   return ll_plan_for(d, B).ok;
 }
 
-void run_step(xe_decoder *d, int B, uint64_t *trace = nullptr) {
-  if (!trace && use_ll(d, B)) {
+void run_step(xe_decoder *d, int B) {
+  if (use_ll(d, B)) {
     run_ll(d, B, 1, nullptr, 0, true);
     return;
   }
-  d->last_exec = XE_EXEC_PERSISTENT;
+  d->last_exec = XE_EXEC_GRAPH;
   xe_decoder::Plan &plan = plan_for(d, B);
   switch (exec_for(plan)) {
-    case Exec::Persistent: {
-      StepLaunch L;
-      L.trace = trace;
-      L.phases = plan.dev_phases;
-      L.nphases = static_cast<int>(plan.phases.size());
-      L.flags = d->step_flags;
-      L.status = d->step_status;
-      L.wdtype = d->c.wdtype;
-      L.nb = plan.step_nb;
-      L.hd = d->c.head_dim;
-      L.g = d->c.n_heads / d->c.n_kv_heads;
-      L.lds_bytes = plan.step_lds;
-      L.grid = d->step_grid;
-      launch_step(L, d->s);
-      return;
-    }
     case Exec::Graph:
       XE_HIP(hipGraphLaunch(graph_for(d, plan), d->s));
       return;
@@ -1740,24 +1697,21 @@ void run_step(xe_decoder *d, int B, uint64_t *trace = nullptr) {
 // Run one GEMV over `batch` rows now (standalone kernels; chunks of 8).
 void run_gemv_now(const GemvCall &g, int batch, hipStream_t s) {
   xe_decoder::Plan tmp;
-  PlanBuilder pb{tmp, 1};
+  PlanBuilder pb{tmp};
   pb.gemv(g, batch, "gemv");
   for (const auto &ph : tmp.phases) launch_phase(ph, s);
 }
 
-// After a run of persistent steps: a barrier wait that timed out leaves
-// status set; report it and re-arm the flags.
+// After a run of low-latency launches: a wait that timed out (or a plan the
+// kernel could not run) leaves the status word set; report it and clear it.
 void check_step_status(xe_decoder *d) {
   unsigned st = 0;
   XE_HIP(hipMemcpy(&st, d->step_status, 4, hipMemcpyDeviceToHost));
   if (st) {
-    XE_HIP(hipMemset(d->step_flags, 0, static_cast<size_t>(d->step_grid) * 128));
     XE_HIP(hipMemset(d->step_status, 0, 4));
     if (st == 2u)
       fail("low-latency step kernel: GEMV tile not compiled (host/device tile menus differ); results are invalid");
-    fail(d->last_exec == XE_EXEC_LL
-             ? "low-latency step kernel: an exchange wait timed out (every workgroup stopped); results are invalid"
-             : "persistent step kernel: a phase barrier timed out (flags re-armed); results are invalid");
+    fail("low-latency step kernel: an exchange wait timed out (every workgroup stopped); results are invalid");
   }
 }
 
@@ -2629,42 +2583,6 @@ int xe_decoder_profile_step(xe_decoder *d, int batch, int max_entries, char *lab
       emit("embed", am, em, static_cast<double>(batch) * d->c.d_model * 4);
       return n;
     }
-    if (exec_for(plan) == Exec::Persistent) {
-      // One persistent launch with the wall-clock trace: phase i's time is the
-      // advance of the latest publication (critical path), so the entries sum
-      // to the launch's span from the first workgroup's start.
-      const size_t np = plan.phases.size(), G = static_cast<size_t>(d->step_grid);
-      uint64_t *tr = nullptr;
-      XE_HIP(hipMalloc(reinterpret_cast<void **>(&tr), np * G * 2 * sizeof(uint64_t)));
-      std::vector<uint64_t> h(np * G * 2);
-      try {
-        run_step(d, batch, tr);
-        XE_HIP(hipStreamSynchronize(d->s));
-        XE_HIP(hipMemcpy(h.data(), tr, h.size() * sizeof(uint64_t), hipMemcpyDeviceToHost));
-      } catch (...) {
-        (void)hipFree(tr);
-        throw;
-      }
-      (void)hipFree(tr);
-      check_step_status(d);
-      for (int b = 0; b < batch; b++) d->hpos[b] += 1;
-      int khz = 0;
-      XE_HIP(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, d->dev->ordinal));
-      XE_REQUIRE(khz > 0, "device wall clock rate unknown");
-      const double us_per_tick = 1000.0 / khz;
-      uint64_t prev = ~0ull;
-      for (size_t w = 0; w < G; w++) prev = std::min(prev, h[2 * w]);
-      int n = 0;
-      for (size_t i = 0; i < np && n < max_entries; i++, n++) {
-        uint64_t done = 0;
-        for (size_t w = 0; w < G; w++) done = std::max(done, h[2 * (i * G + w) + 1]);
-        us[n] = done > prev ? (done - prev) * us_per_tick : 0.0;
-        bytes[n] = phase_bytes(i);
-        std::snprintf(labels + 32 * n, 32, "%s", plan.labels[i].c_str());
-        prev = std::max(prev, done);
-      }
-      return n;
-    }
     try {
       d->mark("start", 0.0);
       for (size_t i = 0; i < plan.phases.size(); i++) {  // eager, one event after each launch
@@ -2699,7 +2617,6 @@ int xe_decoder_executor(xe_decoder *d, int batch) {
     DeviceGuard dg(d->dev->ordinal);
     if (use_ll(d, batch)) return XE_EXEC_LL;
     switch (exec_for(plan_for(d, batch))) {
-      case Exec::Persistent: return XE_EXEC_PERSISTENT;
       case Exec::Eager: return XE_EXEC_EAGER;
       case Exec::Graph: break;
     }

@@ -206,9 +206,9 @@ __device__ __forceinline__ void stage_parts(const f32x4 (&x)[4], uint16_t (*xs)[
 // tile ws[tile][z][b][r] with agent-scope stores: the workgroup counts itself
 // in cnt[tile]; the last one to arrive adds the partials in split order (the
 // same order on every run), runs the epilogue and re-arms the counter.
-template <int WT, int BM>
+template <int WT, int BM, int BN = kBN>
 // rq: this thread's row quad, prefetched (its q is the same in every item
-// the thread takes), or null.
+// the thread takes), or null.  BN: streams a tile.
 __device__ __forceinline__ void splitk_finish(const gdev::GemvParams &p, float *ws, unsigned *cnt, int tile, int ks,
                                               int nb, int m0, int b0, int &last, const RowQuad *rq = nullptr) {
   __builtin_amdgcn_s_waitcnt(0);  // this wave's partial stores have completed
@@ -220,7 +220,7 @@ __device__ __forceinline__ void splitk_finish(const gdev::GemvParams &p, float *
   // the reduction: item = (stream bb, row quad q), two items a thread per
   // round; every split's partial of both items in flight at once (ks <=
   // kMaxSplitsK), then summed in split order
-  const __amdgpu_buffer_rsrc_t rws = gdev::coherent_rsrc(ws + static_cast<size_t>(tile) * ks * (BM * kBN));
+  const __amdgpu_buffer_rsrc_t rws = gdev::coherent_rsrc(ws + static_cast<size_t>(tile) * ks * (BM * BN));
   const int items = nb * (BM / 4);
   for (int it0 = threadIdx.x; it0 < items; it0 += 2 * kGT) {
     f32x4 v[2][kMaxSplitsK];
@@ -232,7 +232,7 @@ __device__ __forceinline__ void splitk_finish(const gdev::GemvParams &p, float *
       for (int zz = 0; zz < kMaxSplitsK; zz++)
         v[r][zz] = __builtin_bit_cast(
             f32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                       rws, zz < ks && it < items ? ((zz * kBN + bb) * BM + 4 * q) * 4 : kNoRec, 0, gdev::kCoherentSc1));
+                       rws, zz < ks && it < items ? ((zz * BN + bb) * BM + 4 * q) * 4 : kNoRec, 0, gdev::kCoherentSc1));
     }
 #pragma unroll
     for (int r = 0; r < 2; r++) {
@@ -530,38 +530,41 @@ constexpr int w_slice_dw() {  // dwords of one row's 32-k weight slice
 }
 constexpr int kXD = 36;  // LDS row stride (dwords) of a wave's 32-k activation slice
 
-template <int WT, int MB>
+template <int WT, int MB, int NJ>
 __host__ __device__ constexpr int ks_stage_dw() {  // LDS dwords of one wave's slices
-  return 64 * kXD + 16 * MB * (w_slice_dw<WT>() + 4);
+  return 16 * NJ * kXD + 16 * MB * (w_slice_dw<WT>() + 4);
 }
 
-template <int WT, int MB>
+template <int WT, int MB, int NJ>
 __host__ __device__ constexpr int ks_lds_dw() {
-  return 4 * ks_stage_dw<WT, MB>() > 4 * kBN * (16 * MB + 4) ? 4 * ks_stage_dw<WT, MB>() : 4 * kBN * (16 * MB + 4);
+  return 4 * ks_stage_dw<WT, MB, NJ>() > 4 * 16 * NJ * (16 * MB + 4) ? 4 * ks_stage_dw<WT, MB, NJ>()
+                                                                       : 4 * 16 * NJ * (16 * MB + 4);
 }
 
-template <int WT, int MB>
+// NJ: stream blocks of 16 a tile (BN = 16 NJ streams: 16, 32 or 64).
+template <int WT, int MB, int NJ>
 __global__ __launch_bounds__(kGT) void gemm_ks_kernel(gdev::GemvParams p, float *ws, unsigned *cnt, int spk) {
-  constexpr int BM = 16 * MB;
+  constexpr int BM = 16 * MB, BN = 16 * NJ;
   constexpr int WD = w_slice_dw<WT>(), WDP = WD + 4;
   // the waves' operand slices during the K loop; afterwards the four waves'
   // partial tiles [wave][stream][row] (row stride padded)
   constexpr int kRS = BM + 4;
-  __shared__ __attribute__((aligned(16))) uint32_t lds[ks_lds_dw<WT, MB>()];
-  float(*red)[kBN * kRS] = reinterpret_cast<float(*)[kBN * kRS]>(lds);
+  __shared__ __attribute__((aligned(16))) uint32_t lds[ks_lds_dw<WT, MB, NJ>()];
+  float(*red)[BN * kRS] = reinterpret_cast<float(*)[BN * kRS]>(lds);
   __shared__ int last;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  uint32_t *xst = lds + wave * ks_stage_dw<WT, MB>();  // [64][kXD]
-  uint32_t *wst = xst + 64 * kXD;                       // [BM][WDP]
-  const int m0 = blockIdx.x * BM, b0 = blockIdx.y * kBN;
+  uint32_t *xst = lds + wave * ks_stage_dw<WT, MB, NJ>();  // [BN][kXD]
+  uint32_t *wst = xst + BN * kXD;                           // [BM][WDP]
+  const int m0 = blockIdx.x * BM, b0 = blockIdx.y * BN;
   const int K = p.k;
   const int ks = gridDim.z, z = blockIdx.z;
   const int step0 = z * spk;
   const int nsteps = min((K + kKsBK - 1) / kKsBK, step0 + spk) - step0;
-  const int nb = min(kBN, p.batch - b0);
+  const int nb = min(BN, p.batch - b0);
   const __amdgpu_buffer_rsrc_t rw = gdev::coherent_rsrc(p.w);
   const __amdgpu_buffer_rsrc_t re = gdev::coherent_rsrc(WT == XE_BFP16 ? static_cast<const void *>(p.exps) : p.w);
   const __amdgpu_buffer_rsrc_t rx = gdev::coherent_rsrc(p.x);
+  constexpr int XI = 2 * NJ;  // activation load instructions a step (8 stream rows each)
 
   // MFMA layout: lane feeds row / stream lane % 16 of a block with k
   // 8 * (lane / 16) .. + 7 of the wave's 32-k slice
@@ -570,9 +573,9 @@ __global__ __launch_bounds__(kGT) void gemm_ks_kernel(gdev::GemvParams p, float 
   // coalesced activation loads: instruction i, lane -> stream row 8 i +
   // lane / 8, 16 bytes at k 4 (lane % 8); rows past the batch read zeros
   const int xr = lane >> 3, xc = 4 * (lane & 7);
-  int xoff[8], xlim[8];
+  int xoff[XI], xlim[XI];
 #pragma unroll
-  for (int i = 0; i < 8; i++) {
+  for (int i = 0; i < XI; i++) {
     const int b = 8 * i + xr;
     xoff[i] = (b0 + b) * p.ldx + xc;
     xlim[i] = b < nb ? kend : 0;
@@ -584,12 +587,12 @@ __global__ __launch_bounds__(kGT) void gemm_ks_kernel(gdev::GemvParams p, float 
   struct Stage {
     uint32_t w[MB][WD / 4];
     uint32_t e[MB];  // bfp16: exponent byte (MFMA layout)
-    f32x4 x[8];
+    f32x4 x[XI];
   };
   auto issue = [&](int step, Stage &st) {
     const int k0 = (step0 + step) * kKsBK + 32 * wave;
 #pragma unroll
-    for (int i = 0; i < 8; i++)
+    for (int i = 0; i < XI; i++)
       st.x[i] = __builtin_bit_cast(
           f32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, k0 + xc < xlim[i] ? (xoff[i] + k0) * 4 : kNoRec, 0, 0));
 #pragma unroll
@@ -625,11 +628,11 @@ __global__ __launch_bounds__(kGT) void gemm_ks_kernel(gdev::GemvParams p, float 
   // thread's items all have row quad threadIdx.x % (BM / 4)
   const RowQuad rq = load_quad(p, WT, m0 + 4 * (static_cast<int>(threadIdx.x) % (BM / 4)));
 
-  f32x4 acc[MB][4];
+  f32x4 acc[MB][NJ];
 #pragma unroll
   for (int mb = 0; mb < MB; mb++)
 #pragma unroll
-    for (int j = 0; j < 4; j++) acc[mb][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < NJ; j++) acc[mb][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   // the MFMAs of one stream block interleave the row blocks, and with fewer
   // than four row blocks the stream blocks too (at least four independent
@@ -637,7 +640,7 @@ __global__ __launch_bounds__(kGT) void gemm_ks_kernel(gdev::GemvParams p, float 
   auto compute = [&](const Stage &st) {
     // the step's slices into LDS as loaded
 #pragma unroll
-    for (int i = 0; i < 8; i++) *reinterpret_cast<f32x4 *>(xst + (8 * i + xr) * kXD + xc) = st.x[i];
+    for (int i = 0; i < XI; i++) *reinterpret_cast<f32x4 *>(xst + (8 * i + xr) * kXD + xc) = st.x[i];
 #pragma unroll
     for (int mb = 0; mb < MB; mb++) {
       uint32_t *d = wst + (16 * mb + wr) * WDP + wq * (WD / 4);
@@ -661,9 +664,10 @@ __global__ __launch_bounds__(kGT) void gemm_ks_kernel(gdev::GemvParams p, float 
       if constexpr (WT == XE_BFP16) wl.e = st.e[mb];
       a[mb] = to_bf16x8<WT>(wl);
     }
-    constexpr int JG = MB >= 4 ? 1 : 4 / MB;  // stream blocks a group
+    constexpr int JG0 = MB >= 4 ? 1 : 4 / MB;
+    constexpr int JG = JG0 < NJ ? JG0 : NJ;  // stream blocks a group
 #pragma unroll
-    for (int j0 = 0; j0 < 4; j0 += JG) {
+    for (int j0 = 0; j0 < NJ; j0 += JG) {
       bf16x8 bx[JG][3];
 #pragma unroll
       for (int jj = 0; jj < JG; jj++) {
@@ -702,16 +706,19 @@ __global__ __launch_bounds__(kGT) void gemm_ks_kernel(gdev::GemvParams p, float 
 #pragma unroll
   for (int mb = 0; mb < MB; mb++)
 #pragma unroll
-    for (int j = 0; j < 4; j++)
+    for (int j = 0; j < NJ; j++)
       *reinterpret_cast<f32x4 *>(&red[wave][(16 * j + lr) * kRS + 16 * mb + 4 * (lane >> 4)]) = acc[mb][j];
   __syncthreads();
-  // item = (stream bb, row quad q): 64 x BM / 4 items, MB a thread
+  // item = (stream bb, row quad q): BN x BM / 4 items, RI a thread (the
+  // last round partly empty when there are fewer items than threads)
   constexpr int QN = BM / 4;
-  float sum[MB][4];
+  constexpr int ITEMS = BN * QN;
+  constexpr int RI = (ITEMS + kGT - 1) / kGT;
+  float sum[RI][4];
 #pragma unroll
-  for (int r = 0; r < MB; r++) {
+  for (int r = 0; r < RI; r++) {
     const int it = threadIdx.x + r * kGT;
-    const int bb = it / QN, q = it % QN;
+    const int bb = it < ITEMS ? it / QN : 0, q = it % QN;
     f32x4 t = *reinterpret_cast<const f32x4 *>(&red[0][bb * kRS + 4 * q]);
 #pragma unroll
     for (int w = 1; w < 4; w++) t += *reinterpret_cast<const f32x4 *>(&red[w][bb * kRS + 4 * q]);
@@ -722,25 +729,27 @@ __global__ __launch_bounds__(kGT) void gemm_ks_kernel(gdev::GemvParams p, float 
   }
   if (ks == 1) {
 #pragma unroll
-    for (int r = 0; r < MB; r++) {
+    for (int r = 0; r < RI; r++) {
       const int it = threadIdx.x + r * kGT;
       const int bb = it / QN, q = it % QN;
-      if (bb < nb) epilogue4(p, rq, m0 + 4 * q, b0 + bb, sum[r]);
+      if (it < ITEMS && bb < nb) epilogue4(p, rq, m0 + 4 * q, b0 + bb, sum[r]);
     }
     return;
   }
   const int tile = blockIdx.y * gridDim.x + blockIdx.x;
   // the partial tile with 16-byte sc1 stores (what an agent-scope atomic
   // store compiles to, four dwords at a time)
-  const __amdgpu_buffer_rsrc_t rp = gdev::coherent_rsrc(ws + (static_cast<size_t>(tile) * ks + z) * (BM * kBN));
+  const __amdgpu_buffer_rsrc_t rp = gdev::coherent_rsrc(ws + (static_cast<size_t>(tile) * ks + z) * (BM * BN));
 #pragma unroll
-  for (int r = 0; r < MB; r++) {
+  for (int r = 0; r < RI; r++) {
     const int it = threadIdx.x + r * kGT;
     const int bb = it / QN, q = it % QN;
-    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, f32x4{sum[r][0], sum[r][1], sum[r][2], sum[r][3]}),
-                                           rp, (bb * BM + 4 * q) * 4, 0, gdev::kCoherentSc1);
+    if (it < ITEMS)
+      __builtin_amdgcn_raw_buffer_store_b128(
+          __builtin_bit_cast(u32x4, f32x4{sum[r][0], sum[r][1], sum[r][2], sum[r][3]}), rp, (bb * BM + 4 * q) * 4, 0,
+          gdev::kCoherentSc1);
   }
-  splitk_finish<WT, BM>(p, ws, cnt, tile, ks, nb, m0, b0, last, &rq);
+  splitk_finish<WT, BM, BN>(p, ws, cnt, tile, ks, nb, m0, b0, last, &rq);
 }
 
 // Norm / residual prologue of one stream row (blockIdx.x): p.x, p.sub and
@@ -748,16 +757,16 @@ __global__ __launch_bounds__(kGT) void gemm_ks_kernel(gdev::GemvParams p, float 
 // row goes to xn [batch][k].
 __global__ __launch_bounds__(256) void gemm_prologue_kernel(gdev::GemvParams p, float *xn) {
   extern __shared__ float4 xs4[];
-  __shared__ float red[2 * 4 * gdev::kMaxWaves];
+  __shared__ float red[2 * gdev::kRedN * gdev::kMaxWaves];
   const int b = blockIdx.x;
   gdev::GemvParams q = p;
   q.x = static_cast<const float *>(p.x) + static_cast<size_t>(b) * p.ldx;
   q.sub = p.sub ? p.sub + static_cast<size_t>(b) * p.k : nullptr;
   q.res_out = p.res_out ? p.res_out + static_cast<size_t>(b) * p.k : nullptr;
   q.batch = 1;
-  gdev::gemv_prologue<1, 4, false>(q, xs4, red, true);
+  gdev::gemv_prologue<1, 4>(q, xs4, red, true);
   const float *xs = reinterpret_cast<const float *>(xs4);
-  for (int i = threadIdx.x; i < p.k; i += 256) xn[static_cast<size_t>(b) * p.k + i] = xs[i];
+  for (int i = threadIdx.x; i < p.k; i += 256) xn[static_cast<size_t>(b) * p.k + i] = xs[gdev::xs_elem<1>(i)];
 }
 
 // The Gemma sandwich-norm prologue (x + post-norm(sub) -> res_out, then the
@@ -840,6 +849,7 @@ __global__ __launch_bounds__(256) void gemm_prologue_reg_kernel(gdev::GemvParams
   const int b = blockIdx.x, K = p.k;
   const float fk = static_cast<float>(K);
   const float *xr = static_cast<const float *>(p.x) + static_cast<size_t>(b) * p.ldx;
+  const uint16_t *xh = static_cast<const uint16_t *>(p.x) + static_cast<size_t>(b) * p.ldx;  // bf16 x
   const float *sr = p.sub ? p.sub + static_cast<size_t>(b) * K : nullptr;
   const bool ln = p.norm == XE_NORM_LN;
   float t[NS], sv[NS], g[NS], be[NS];
@@ -848,7 +858,7 @@ __global__ __launch_bounds__(256) void gemm_prologue_reg_kernel(gdev::GemvParams
     const int i = threadIdx.x + j * 256;
     t[j] = sv[j] = g[j] = be[j] = 0.f;
     if (i < K) {
-      t[j] = xr[i];
+      t[j] = p.x_bf16 ? __uint_as_float(static_cast<uint32_t>(xh[i]) << 16) : xr[i];
       if (sr) sv[j] = sr[i];
       if (p.norm != XE_NORM_NONE) g[j] = p.gamma[i];
       if (ln) be[j] = p.beta[i];
@@ -912,22 +922,32 @@ GemmFn pick_mb(int mb) {
   return nullptr;
 }
 
-template <int WT>
+template <int WT, int NJ>
 GemmFn pick_ks_mb(int mb) {
   switch (mb) {
-    case 1: return gemm_ks_kernel<WT, 1>;
-    case 2: return gemm_ks_kernel<WT, 2>;
-    case 4: return gemm_ks_kernel<WT, 4>;
+    case 1: return gemm_ks_kernel<WT, 1, NJ>;
+    case 2: return gemm_ks_kernel<WT, 2, NJ>;
+    case 4: return gemm_ks_kernel<WT, 4, NJ>;
   }
   return nullptr;
 }
 
-GemmFn pick_ks(int wdtype, int mb) {
+template <int WT>
+GemmFn pick_ks_nj(int mb, int nj) {
+  switch (nj) {
+    case 1: return pick_ks_mb<WT, 1>(mb);
+    case 2: return pick_ks_mb<WT, 2>(mb);
+    case 4: return pick_ks_mb<WT, 4>(mb);
+  }
+  return nullptr;
+}
+
+GemmFn pick_ks(int wdtype, int mb, int nj) {
   switch (wdtype) {
-    case XE_I8: return pick_ks_mb<XE_I8>(mb);
-    case XE_BF16: return pick_ks_mb<XE_BF16>(mb);
-    case XE_BFP16: return pick_ks_mb<XE_BFP16>(mb);
-    case XE_I4: return pick_ks_mb<XE_I4>(mb);
+    case XE_I8: return pick_ks_nj<XE_I8>(mb, nj);
+    case XE_BF16: return pick_ks_nj<XE_BF16>(mb, nj);
+    case XE_BFP16: return pick_ks_nj<XE_BFP16>(mb, nj);
+    case XE_I4: return pick_ks_nj<XE_I4>(mb, nj);
   }
   return nullptr;
 }
@@ -948,14 +968,14 @@ GemmFn pick_gemm(int wdtype, int mb) {
 // about four workgroups per CU: at most kMaxSplitsK, at least two K steps
 // each, and a bounded partial workspace.
 struct GemmShape {
-  int mb, ks, spk, tm, tb;
+  int mb, ks, spk, tm, tb, nj;
 };
 
 GemmShape gemm_shape(int m, int k, int batch) {
   const int steps = (k + kBK - 1) / kBK;
   const int tb = (batch + kBN - 1) / kBN;
   const int cus = gdev::cu_count();
-  GemmShape g{1, 1, steps, 0, tb};
+  GemmShape g{1, 1, steps, 0, tb, 4};
   // wide outputs (the lm-head): four row blocks per wave; else one
   g.mb = static_cast<long long>(m) * tb >= 64LL * 4 * 4 * cus ? 4 : 1;
   g.tm = (m + 64 * g.mb - 1) / (64 * g.mb);
@@ -976,32 +996,39 @@ GemmShape gemm_shape(int m, int k, int batch) {
 }
 
 // Shape of a K-sliced launch, or mb = 0 where none fits the chip in one
-// round (outputs wider than 64 rows a CU: the lm-head).  Candidates: 1, 2 or
-// 4 row blocks a wave, each with the most splits of K that keep the grid
-// within one workgroup per CU and at least two steps a split; the cheapest
-// by a cost fitted to b = 64 probes wins (ties to more row blocks): a step
-// costs 2 units for the activation slice plus one a row block, and a split
-// tile's reduction half a unit a row block a split.  (b = 64, us: QKV 1536 x
+// round (outputs wider than 64 rows a CU: the lm-head).  Stream tiles of 16,
+// 32 or 64 (the fewest 16-stream blocks that hold the batch, 64 beyond).
+// Candidates: 1, 2 or 4 row blocks a wave, each with the most splits of K
+// that keep the grid within one workgroup per CU and at least two steps a
+// split; the cheapest by a cost fitted to b = 64 probes wins (ties to more
+// row blocks): a step costs half a unit per 16-stream block for the
+// activation slice plus one a row block, and a split tile's reduction half a
+// unit a row block a split.  (b = 64, us: QKV 1536 x
 // 1152 8.7 / 9.0 / 12.2 at 1 / 2 / 4 row blocks, O 1152 x 1024 7.5 / 8.5 /
 // 11.7, gate/up 13824 x 1152 - / - / 16.6, down 1152 x 6912 18.6 / 14.3 /
 // 16.2; gemm_kernel: 12.8, 12.6, 20.5, 18.9.)
 GemmShape gemm_ks_shape(int m, int k, int batch) {
   const int steps = (k + kKsBK - 1) / kKsBK;
   const int cus = gdev::cu_count();
-  const int tb = (batch + kBN - 1) / kBN;
-  GemmShape best{0, 1, steps, 0, tb};
+  const int nj = batch <= 16 ? 1 : batch <= 32 ? 2 : 4;
+  const int bn = 16 * nj;
+  const int tb = (batch + bn - 1) / bn;
+  // one workgroup a CU (two, with K splits, measured slower at 8 streams:
+  // 14336 x 4096 int8 34.4 against 32.3 us)
+  const int slots = cus;
+  GemmShape best{0, 1, steps, 0, tb, nj};
   int best_work = 0;
   for (int mb = 4; mb >= 1; mb /= 2) {
     const int tm = (m + 16 * mb - 1) / (16 * mb);
     const int tiles = tm * tb;
-    if (tiles > cus) continue;
-    int ks = std::max(1, std::min(std::min(cus / tiles, steps / 2), kMaxSplitsK));
-    while (ks > 1 && static_cast<size_t>(tiles) * ks * 16 * mb * kBN > kGemmWsFloats) ks--;
+    if (tiles > slots) continue;
+    int ks = std::max(1, std::min(std::min(slots / tiles, steps / 2), kMaxSplitsK));
+    while (ks > 1 && static_cast<size_t>(tiles) * ks * 16 * mb * bn > kGemmWsFloats) ks--;
     const int spk = (steps + ks - 1) / ks;
     const int kss = (steps + spk - 1) / spk;
-    const int work = 2 * spk * (2 + mb) + (kss > 1 ? mb * kss : 0);
+    const int work = spk * (nj + 2 * mb) + (kss > 1 ? mb * kss : 0);
     if (best.mb == 0 || work < best_work) {
-      best = GemmShape{mb, kss, spk, tm, tb};
+      best = GemmShape{mb, kss, spk, tm, tb, nj};
       best_work = work;
     }
   }
@@ -1010,13 +1037,36 @@ GemmShape gemm_ks_shape(int m, int k, int batch) {
 
 }  // namespace
 
-bool gemm_needs_prologue(const gdev::GemvParams &p) { return p.sub != nullptr || p.norm != XE_NORM_NONE; }
+bool gemm_needs_prologue(const gdev::GemvParams &p) {
+  return p.sub != nullptr || p.norm != XE_NORM_NONE || p.x_bf16;
+}
+
+// The matrix cores take a projection beyond 8 rows, and from
+// XE_GEMM_MIN_BATCH rows (default 4) when the weight holds at least
+// XE_GEMM_MIN_WEIGHTS elements (default 0: every config-2 shape was as fast
+// or faster there at 4 rows): on the VALU every weight costs one FMA a row,
+// which at 8 rows bounds the GEMV by instruction issue (rocprof: 16.9 M VALU
+// instructions for 14336 x 4096, 0.64 TB/s), while the MFMA GEMM converts
+// each weight once and issues 3 MFMAs per 16 x 32 block (14336 x 4096 int8
+// at 8 rows: 92 -> 32 us).  At 2 rows the GEMV stays faster (23.6 against
+// 29.5 us).
+bool gemm_preferred(int m, int k, int batch) {
+  if (batch > 8) return true;
+  static const int min_batch = [] {
+    const char *e = std::getenv("XE_GEMM_MIN_BATCH");
+    return e ? std::atoi(e) : 4;
+  }();
+  static const long long min_w = [] {
+    const char *e = std::getenv("XE_GEMM_MIN_WEIGHTS");
+    return e ? std::atoll(e) : 0LL;
+  }();
+  return min_batch > 0 && batch >= min_batch && static_cast<long long>(m) * k >= min_w && k % 16 == 0;
+}
 
 // Prologue (when the phase has one) into xn, then the GEMM reading xn.
 void launch_gemm_prologue(const gdev::GemvParams &p, float *xn, hipStream_t s) {
-  XE_REQUIRE(!p.x_bf16, "gemm: fp32 activations only");
   auto al16 = [](const void *q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
-  if (p.sub && p.post_w && p.gamma && (p.norm == XE_NORM_RMS1P || p.norm == XE_NORM_RMS) && p.k % 4 == 0 &&
+  if (!p.x_bf16 && p.sub && p.post_w && p.gamma && (p.norm == XE_NORM_RMS1P || p.norm == XE_NORM_RMS) && p.k % 4 == 0 &&
       p.ldx % 4 == 0 && p.k <= 4096 && al16(p.x) && al16(p.sub) && al16(p.post_w) && al16(p.gamma) &&
       al16(p.res_out) && al16(xn)) {
     const int nv = (p.k / 4 + 255) / 256;
@@ -1062,7 +1112,7 @@ void launch_gemm(const gdev::GemvParams &p, int wdtype, float *ws, unsigned *cnt
   const GemmShape gk = gemm_ks_shape(p.m, p.k, p.batch);
   if (gk.mb > 0) {
     g = gk;
-    fn = pick_ks(wdtype, g.mb);
+    fn = pick_ks(wdtype, g.mb, g.nj);
   } else {
     fn = pick_gemm(wdtype, g.mb);
   }
@@ -1077,12 +1127,13 @@ size_t gemm_op_ws_floats() { return kGemmWsFloats; }
 size_t gemm_op_cnt_words() { return kGemmMaxTiles; }
 
 void launch_gemm_op(const GemvLaunch &L, float *xn, float *ws, unsigned *cnt, hipStream_t s) {
-  XE_REQUIRE(L.x_dtype == XE_F32, "gemm: fp32 activations only");
+  XE_REQUIRE(L.x_dtype == XE_F32 || L.x_dtype == XE_BF16, "gemm: fp32 or bf16 activations");
   gdev::GemvParams p = gdev::to_params(L);
-  if (gemm_needs_prologue(p)) {
+  if (gemm_needs_prologue(p)) {  // bf16 x: the prologue writes it as fp32
     XE_REQUIRE(xn, "gemm: prologue without a row buffer");
     launch_gemm_prologue(p, xn, s);
     p.x = xn;
+    p.x_bf16 = 0;
     p.ldx = p.k;
     p.sub = nullptr;
     p.post_w = nullptr;

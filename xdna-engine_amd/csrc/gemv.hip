@@ -94,9 +94,8 @@ using gdev::Tile;
 template <int WT, int NB, int LPR, int RPL, int WPB>
 __global__ __launch_bounds__(64 * WPB) void gemv_kernel(GemvParams p) {
   extern __shared__ float4 xs4[];
-  __shared__ float red[2 * 4 * gdev::kMaxWaves];
-  gdev::gemv_tiles<WT, NB, LPR, RPL, WPB, false>(p, xs4, red, blockIdx.x, gridDim.x,
-                                                 blockIdx.x == 0, gdev::NoWait{});
+  __shared__ float red[2 * gdev::kRedN * gdev::kMaxWaves];
+  gdev::gemv_tiles<WT, NB, LPR, RPL, WPB>(p, xs4, red, blockIdx.x, gridDim.x, blockIdx.x == 0);
 }
 
 // ---------------------------------------------------------------------------

@@ -13,21 +13,21 @@
 //     whole 128-byte lines from HBM.
 //   * RPL rows per lane share the x chunk held in registers.
 //   * Weight loads run as a ping-pong of two sets of U chunks per row; the
-//     first two sets are issued before the prologue (and, in the persistent
-//     step kernel, before waiting for the inputs), so they overlap HBM
-//     latency and the synchronisation.
-//   * x (after the prologue) lives in LDS as fp32 [b][K]; a lane reads its
-//     16-element chunk as four 16 B words.
+//     first two sets are issued before the prologue, so they overlap HBM
+//     latency.
+//   * x (after the prologue) lives in LDS as fp32 [b][K], each chunk's four
+//     16 B words permuted (xs_word) so a wave's chunk reads are free of bank
+//     conflicts; every row of the batch tile is computed (no branch on the
+//     batch count), rows past the batch being zero.
 //   * The group reduction is an xor-butterfly over LPR lanes.
 //   * int8 -> fp32 dequant happens in registers; the per-row fp32 scale is
 //     applied after the sum, as in Lin::fwd (opt125m_decode.rs:120-122).
 //
-// COH selects how activations (x, sub, residual, y) are accessed: plain
-// loads/stores in standalone kernels (the kernel boundary publishes them), or
-// coherent (sc1) loads and agent-scope stores in the persistent step kernel,
-// where a phase reads what another XCD wrote in the same launch and the XCDs'
-// L2s are not coherent with each other.  Weights are read-only and always use
-// plain streaming loads.
+// act_ld / act_st<COH>: plain loads and stores, or coherent ones (sc1 loads,
+// agent-scope stores) for code that reads in one launch what another XCD
+// wrote (the attention merge inside the split kernel, the low-latency step
+// kernel), since the XCDs' L2s are not coherent with each other.  Weights
+// are read-only and always use plain streaming loads.
 #pragma once
 
 #include "common.h"
@@ -384,158 +384,284 @@ __device__ __forceinline__ float chunk_dot(const Chunk<WT> &ch, const float4 (&x
   }
 }
 
-// LDS the GEMV needs: x rows + one staged sub row (floats).
+// LDS the GEMV needs: x rows + one staged sub row per batch row (floats).
 __host__ __device__ inline size_t gemv_lds_floats(int nb, int k, bool sub) {
-  return static_cast<size_t>(nb + (sub ? 1 : 0)) * k;
+  return static_cast<size_t>(nb) * k * (sub ? 2 : 1);
 }
 
-// Prologue: x (+ post(sub)) -> res_out (block 0) -> norm -> LDS, fp32.
-// Statistics are reduced once per row:
+// x rows sit in LDS as fp32 [b][K].  With more than one row (NB > 1) the
+// four float4 words of each 16-element chunk are permuted by the chunk index:
+// word j of chunk c is stored at float4 slot 4c + (j ^ ((c >> 2) & 3)).  A
+// wave reads word j of the 16 consecutive chunks of its LPR lanes in one
+// ds_read_b128; unpermuted, chunks c and c + 4 are 256 B apart and hit the
+// same banks (4-way conflicts); with the permutation the 16 lanes cover all
+// 64 banks once.  One row is read once per chunk and stays unpermuted (the
+// address arithmetic would cost more than the conflicts).
+template <int NB>
+__host__ __device__ __forceinline__ int xs_word(int i4) { return NB > 1 ? i4 ^ ((i4 >> 4) & 3) : i4; }
+template <int NB>
+__host__ __device__ __forceinline__ int xs_elem(int e) { return 4 * xs_word<NB>(e >> 2) + (e & 3); }
+
+// Block-wide sums of N values over WPB waves with one barrier (red holds
+// 2 * kRedN * kMaxWaves floats, N <= kRedN; `slot` alternates as in
+// block_sums).  Each value: its wave's sum, then the waves' sums in wave
+// order.
+constexpr int kRedN = 32;
+template <int WPB, int N>
+__device__ __forceinline__ void block_sums_wide(float (&v)[N], float *red, int &slot) {
+  static_assert(N <= kRedN, "too many sums");
+#pragma unroll
+  for (int i = 0; i < N; i++) v[i] = wave_sum(v[i]);
+  if constexpr (WPB == 1) return;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  XE_LDS float *r = lptr(red) + slot * kRedN * kMaxWaves;
+  slot ^= 1;
+  if (lane == 0)
+#pragma unroll
+    for (int i = 0; i < N; i++) r[i * kMaxWaves + wave] = v[i];
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < N; i++) {
+    float t = 0.f;
+#pragma unroll
+    for (int w = 0; w < WPB; w++) t += r[i * kMaxWaves + w];
+    v[i] = t;
+  }
+}
+
+// Prologue: x (+ post(sub)) -> res_out (the writer workgroup) -> norm -> LDS,
+// fp32, for every batch row at once (one load round, one reduction per
+// statistic for all rows); rows past the batch are zero in LDS, so the main
+// loop reads them without a branch.  Statistics:
 //   Gemma (sub + post_w, RMS1P): t = x + sub*inv_s*(1+w) and
 //     sum t^2 = sum x^2 + 2 inv_s sum x*s' + inv_s^2 sum s'^2 (s' = sub*(1+w)),
 //     so sum sub^2, sum x^2, sum x*s', sum s'^2 come out of one reduction.
 //   LayerNorm: two passes (sum t, then sum (t - mean)^2) as the reference's
 //     layer_norm (npu-asr-host/src/lib.rs:79-109); one-pass variance loses
 //     everything on near-constant rows.
-// `writer` marks the one workgroup that stores the updated residual.
-template <int NB, int WPB, bool COH>
+// Per row, each thread accumulates its elements in the same order as the
+// batched GEMM's prologue kernels (gemm.hip), so both give the same bits.
+// red: 2 * kRedN * kMaxWaves floats.
+template <int NB, int WPB>
 __device__ __forceinline__ void gemv_prologue(const GemvParams &p, float4 *xs4, float *red, bool writer) {
   constexpr int kThreads = 64 * WPB;
-  constexpr int UNR = 4;  // float4 loads in flight per thread
+  // float4 loads in flight per thread and row (the per-thread element order,
+  // t, t + kThreads, ..., does not depend on it)
+  constexpr int UNR = NB >= 4 ? 1 : NB == 2 ? 2 : 4;
   const int K = p.k, K4 = K / 4;
+  const int nb = p.batch < NB ? p.batch : NB;
   const float fk = static_cast<float>(K);
   float *xs = reinterpret_cast<float *>(xs4);
-  float *sb = xs + static_cast<size_t>(NB) * K;  // sub staging (one row)
+  float *sb = xs + static_cast<size_t>(NB) * K;  // sub staging [NB][K] (unpermuted)
+  const bool fold = p.sub && p.post_w;            // Gemma post-norm + residual
   int slot = 0;
-  for (int b = 0; b < p.batch && b < NB; b++) {
-    float4 *xb4 = xs4 + static_cast<size_t>(b) * K4;
-    float *xb = xs + static_cast<size_t>(b) * K;
-    const float *subr = p.sub ? p.sub + static_cast<size_t>(b) * K : nullptr;
-    const float *xrow = static_cast<const float *>(p.x) + static_cast<size_t>(b) * p.ldx;
-    const bool fold = p.sub && p.post_w;  // Gemma post-norm + residual
-    float acc[4] = {0.f, 0.f, 0.f, 0.f};  // fold: sum sub^2, x^2, x*s', s'^2
-    for (int i0 = threadIdx.x; i0 < K4; i0 += kThreads * UNR) {
-      float4 v[UNR], sv[UNR];
+  // ---- loads: raw x (and sub) to LDS; the fold's four sums per row ----
+  float acc[NB][4];
+#pragma unroll
+  for (int b = 0; b < NB; b++)
+#pragma unroll
+    for (int q = 0; q < 4; q++) acc[b][q] = 0.f;
+  for (int i0 = threadIdx.x; i0 < K4; i0 += kThreads * UNR) {
+    float4 v[NB][UNR], sv[NB][UNR];
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+      if (b >= nb) break;
+      const float *xrow = static_cast<const float *>(p.x) + static_cast<size_t>(b) * p.ldx;
+      const float *subr = p.sub ? p.sub + static_cast<size_t>(b) * K : nullptr;
 #pragma unroll
       for (int u = 0; u < UNR; u++) {
         const int i = i0 + u * kThreads;
         if (i < K4) {
-          if (!COH && p.x_bf16) {
+          if (p.x_bf16) {
             const uint2 r = reinterpret_cast<const uint2 *>(static_cast<const uint16_t *>(p.x) +
                                                             static_cast<size_t>(b) * p.ldx)[i];
-            v[u] = make_float4(__uint_as_float(r.x << 16), __uint_as_float(r.x & 0xffff0000u),
-                               __uint_as_float(r.y << 16), __uint_as_float(r.y & 0xffff0000u));
+            v[b][u] = make_float4(__uint_as_float(r.x << 16), __uint_as_float(r.x & 0xffff0000u),
+                                  __uint_as_float(r.y << 16), __uint_as_float(r.y & 0xffff0000u));
           } else {
-            v[u] = act_ld4<COH>(xrow, 4 * i);
+            v[b][u] = act_ld4<false>(xrow, 4 * i);
           }
-          if (subr) sv[u] = act_ld4<COH>(subr, 4 * i);
+          if (subr) sv[b][u] = act_ld4<false>(subr, 4 * i);
         }
       }
+    }
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+      if (b >= nb) break;
 #pragma unroll
       for (int u = 0; u < UNR; u++) {
         const int i = i0 + u * kThreads;
         if (i >= K4) continue;
-        xb4[i] = v[u];
-        if (subr) reinterpret_cast<float4 *>(sb)[i] = sv[u];
+        xs4[static_cast<size_t>(b) * K4 + xs_word<NB>(i)] = v[b][u];
+        if (p.sub) reinterpret_cast<float4 *>(sb)[static_cast<size_t>(b) * K4 + i] = sv[b][u];
         if (fold) {
           const float4 w = reinterpret_cast<const float4 *>(p.post_w)[i];
-          const float xv[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
-          const float su[4] = {sv[u].x, sv[u].y, sv[u].z, sv[u].w};
+          const float xv[4] = {v[b][u].x, v[b][u].y, v[b][u].z, v[b][u].w};
+          const float su[4] = {sv[b][u].x, sv[b][u].y, sv[b][u].z, sv[b][u].w};
           const float wv[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
           for (int j = 0; j < 4; j++) {
             const float sp = su[j] * (1.0f + wv[j]);
-            acc[0] = __builtin_fmaf(su[j], su[j], acc[0]);
-            acc[1] = __builtin_fmaf(xv[j], xv[j], acc[1]);
-            acc[2] = __builtin_fmaf(xv[j], sp, acc[2]);
-            acc[3] = __builtin_fmaf(sp, sp, acc[3]);
+            acc[b][0] = __builtin_fmaf(su[j], su[j], acc[b][0]);
+            acc[b][1] = __builtin_fmaf(xv[j], xv[j], acc[b][1]);
+            acc[b][2] = __builtin_fmaf(xv[j], sp, acc[b][2]);
+            acc[b][3] = __builtin_fmaf(sp, sp, acc[b][3]);
           }
         }
       }
     }
-    if (fold) {
-      block_sums<WPB, 4>(acc, red, slot);
-      const float inv_s = 1.0f / sqrtf(acc[0] / fk + p.eps);
-      const float st2 = acc[1] + 2.0f * inv_s * acc[2] + inv_s * inv_s * acc[3];
-      const float inv_t = p.norm != XE_NORM_NONE ? 1.0f / sqrtf(fmaxf(st2, 0.f) / fk + p.eps) : 1.f;
-      __syncthreads();  // staging complete (block_sums skips its barrier for one wave)
-      for (int i = threadIdx.x; i < K; i += kThreads) {
-        const float t = xb[i] + sb[i] * inv_s * (1.0f + p.post_w[i]);
-        if (p.res_out && writer) act_st<COH>(p.res_out + static_cast<size_t>(b) * K + i, t);
+  }
+  // rows past the batch: zeros (read by the branch-free main loop)
+  for (int i = threadIdx.x; i < (NB - nb) * K4; i += kThreads)
+    xs4[static_cast<size_t>(nb) * K4 + i] = make_float4(0.f, 0.f, 0.f, 0.f);
+  float inv_t[NB];
+  if (fold) {
+    float sums[NB * 4];
+#pragma unroll
+    for (int b = 0; b < NB; b++)
+#pragma unroll
+      for (int q = 0; q < 4; q++) sums[4 * b + q] = acc[b][q];
+    block_sums_wide<WPB, NB * 4>(sums, red, slot);
+    float inv_s[NB];
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+      inv_s[b] = 1.0f / sqrtf(sums[4 * b] / fk + p.eps);
+      const float st2 = sums[4 * b + 1] + 2.0f * inv_s[b] * sums[4 * b + 2] + inv_s[b] * inv_s[b] * sums[4 * b + 3];
+      inv_t[b] = p.norm != XE_NORM_NONE ? 1.0f / sqrtf(fmaxf(st2, 0.f) / fk + p.eps) : 1.f;
+    }
+    __syncthreads();  // staging complete (block_sums_wide skips its barrier for one wave)
+    for (int i = threadIdx.x; i < K; i += kThreads) {
+      const int pi = xs_elem<NB>(i);
+      const float pw = 1.0f + p.post_w[i];
+      const float g = p.norm == XE_NORM_RMS1P ? 1.0f + p.gamma[i] : p.norm == XE_NORM_RMS ? p.gamma[i] : 0.f;
+#pragma unroll
+      for (int b = 0; b < NB; b++) {
+        if (b >= nb) break;
+        float *xb = xs + static_cast<size_t>(b) * K;
+        const float t = xb[pi] + sb[static_cast<size_t>(b) * K + i] * inv_s[b] * pw;
+        if (p.res_out && writer) act_st<false>(p.res_out + static_cast<size_t>(b) * K + i, t);
         float h = t;
-        if (p.norm == XE_NORM_RMS1P) h = t * inv_t * (1.0f + p.gamma[i]);
-        else if (p.norm == XE_NORM_RMS) h = t * inv_t * p.gamma[i];
-        xb[i] = h;
-      }
-      if (p.norm == XE_NORM_LN) {  // not a model combination; kept exact anyway
-        __syncthreads();
-        float v1[1] = {0.f};
-        for (int i = threadIdx.x; i < K; i += kThreads) v1[0] += xb[i];
-        block_sums<WPB, 1>(v1, red, slot);
-        const float mean = v1[0] / fk;
-        float v2[1] = {0.f};
-        for (int i = threadIdx.x; i < K; i += kThreads) {
-          const float c = xb[i] - mean;
-          v2[0] = __builtin_fmaf(c, c, v2[0]);
-        }
-        block_sums<WPB, 1>(v2, red, slot);
-        const float inv = 1.0f / sqrtf(v2[0] / fk + p.eps);
-        __syncthreads();
-        for (int i = threadIdx.x; i < K; i += kThreads) xb[i] = (xb[i] - mean) * inv * p.gamma[i] + p.beta[i];
-      }
-    } else {
-      __syncthreads();
-      if (subr) {
-        for (int i = threadIdx.x; i < K; i += kThreads) {
-          const float t = xb[i] + sb[i];
-          xb[i] = t;
-          if (p.res_out && writer) act_st<COH>(p.res_out + static_cast<size_t>(b) * K + i, t);
-        }
-        if (p.norm != XE_NORM_NONE) __syncthreads();
-      }
-      if (p.norm == XE_NORM_LN) {
-        float v1[1] = {0.f};
-        for (int i = threadIdx.x; i < K; i += kThreads) v1[0] += xb[i];
-        block_sums<WPB, 1>(v1, red, slot);
-        const float mean = v1[0] / fk;
-        float v2[1] = {0.f};
-        for (int i = threadIdx.x; i < K; i += kThreads) {
-          const float c = xb[i] - mean;
-          v2[0] = __builtin_fmaf(c, c, v2[0]);
-        }
-        block_sums<WPB, 1>(v2, red, slot);
-        const float inv = 1.0f / sqrtf(v2[0] / fk + p.eps);
-        for (int i = threadIdx.x; i < K; i += kThreads) xb[i] = (xb[i] - mean) * inv * p.gamma[i] + p.beta[i];
-      } else if (p.norm != XE_NORM_NONE) {
-        float v1[1] = {0.f};
-        for (int i = threadIdx.x; i < K; i += kThreads) v1[0] = __builtin_fmaf(xb[i], xb[i], v1[0]);
-        block_sums<WPB, 1>(v1, red, slot);
-        const float inv = 1.0f / sqrtf(v1[0] / fk + p.eps);
-        for (int i = threadIdx.x; i < K; i += kThreads)
-          xb[i] = p.norm == XE_NORM_RMS1P ? xb[i] * inv * (1.0f + p.gamma[i]) : xb[i] * inv * p.gamma[i];
+        if (p.norm == XE_NORM_RMS1P || p.norm == XE_NORM_RMS) h = t * inv_t[b] * g;
+        xb[pi] = h;
       }
     }
-    if (subr && b + 1 < p.batch && b + 1 < NB) __syncthreads();  // sub staging is reused
+    if (p.norm == XE_NORM_LN) {  // not a model combination; kept exact anyway
+      __syncthreads();
+      float mean[NB], v1[NB];
+#pragma unroll
+      for (int b = 0; b < NB; b++) v1[b] = 0.f;
+      for (int i = threadIdx.x; i < K; i += kThreads)
+#pragma unroll
+        for (int b = 0; b < NB; b++) v1[b] += xs[static_cast<size_t>(b) * K + xs_elem<NB>(i)];
+      block_sums_wide<WPB, NB>(v1, red, slot);
+#pragma unroll
+      for (int b = 0; b < NB; b++) {
+        mean[b] = v1[b] / fk;
+        v1[b] = 0.f;
+      }
+      for (int i = threadIdx.x; i < K; i += kThreads)
+#pragma unroll
+        for (int b = 0; b < NB; b++) {
+          const float c = xs[static_cast<size_t>(b) * K + xs_elem<NB>(i)] - mean[b];
+          v1[b] = __builtin_fmaf(c, c, v1[b]);
+        }
+      block_sums_wide<WPB, NB>(v1, red, slot);
+      __syncthreads();
+      for (int i = threadIdx.x; i < K; i += kThreads) {
+        const int pi = xs_elem<NB>(i);
+#pragma unroll
+        for (int b = 0; b < NB; b++) {
+          if (b >= nb) break;
+          float *xb = xs + static_cast<size_t>(b) * K;
+          xb[pi] = (xb[pi] - mean[b]) * (1.0f / sqrtf(v1[b] / fk + p.eps)) * p.gamma[i] + p.beta[i];
+        }
+      }
+    }
+  } else {
+    __syncthreads();
+    if (p.sub) {
+      for (int i = threadIdx.x; i < K; i += kThreads) {
+        const int pi = xs_elem<NB>(i);
+#pragma unroll
+        for (int b = 0; b < NB; b++) {
+          if (b >= nb) break;
+          float *xb = xs + static_cast<size_t>(b) * K;
+          const float t = xb[pi] + sb[static_cast<size_t>(b) * K + i];
+          xb[pi] = t;
+          if (p.res_out && writer) act_st<false>(p.res_out + static_cast<size_t>(b) * K + i, t);
+        }
+      }
+      if (p.norm != XE_NORM_NONE) __syncthreads();
+    }
+    if (p.norm == XE_NORM_LN) {
+      float mean[NB], v1[NB];
+#pragma unroll
+      for (int b = 0; b < NB; b++) v1[b] = 0.f;
+      for (int i = threadIdx.x; i < K; i += kThreads)
+#pragma unroll
+        for (int b = 0; b < NB; b++) v1[b] += xs[static_cast<size_t>(b) * K + xs_elem<NB>(i)];
+      block_sums_wide<WPB, NB>(v1, red, slot);
+#pragma unroll
+      for (int b = 0; b < NB; b++) {
+        mean[b] = v1[b] / fk;
+        v1[b] = 0.f;
+      }
+      for (int i = threadIdx.x; i < K; i += kThreads)
+#pragma unroll
+        for (int b = 0; b < NB; b++) {
+          const float c = xs[static_cast<size_t>(b) * K + xs_elem<NB>(i)] - mean[b];
+          v1[b] = __builtin_fmaf(c, c, v1[b]);
+        }
+      block_sums_wide<WPB, NB>(v1, red, slot);
+      float inv[NB];
+#pragma unroll
+      for (int b = 0; b < NB; b++) inv[b] = 1.0f / sqrtf(v1[b] / fk + p.eps);
+      for (int i = threadIdx.x; i < K; i += kThreads) {
+        const int pi = xs_elem<NB>(i);
+        const float g = p.gamma[i], be = p.beta[i];
+#pragma unroll
+        for (int b = 0; b < NB; b++) {
+          if (b >= nb) break;
+          float *xb = xs + static_cast<size_t>(b) * K;
+          xb[pi] = (xb[pi] - mean[b]) * inv[b] * g + be;
+        }
+      }
+    } else if (p.norm != XE_NORM_NONE) {
+      float v1[NB];
+#pragma unroll
+      for (int b = 0; b < NB; b++) v1[b] = 0.f;
+      for (int i = threadIdx.x; i < K; i += kThreads)
+#pragma unroll
+        for (int b = 0; b < NB; b++) {
+          const float x = xs[static_cast<size_t>(b) * K + xs_elem<NB>(i)];
+          v1[b] = __builtin_fmaf(x, x, v1[b]);
+        }
+      block_sums_wide<WPB, NB>(v1, red, slot);
+      float inv[NB];
+#pragma unroll
+      for (int b = 0; b < NB; b++) inv[b] = 1.0f / sqrtf(v1[b] / fk + p.eps);
+      for (int i = threadIdx.x; i < K; i += kThreads) {
+        const int pi = xs_elem<NB>(i);
+        const float g = p.norm == XE_NORM_RMS1P ? 1.0f + p.gamma[i] : p.gamma[i];
+#pragma unroll
+        for (int b = 0; b < NB; b++) {
+          if (b >= nb) break;
+          float *xb = xs + static_cast<size_t>(b) * K;
+          xb[pi] = xb[pi] * inv[b] * g;
+        }
+      }
+    }
   }
   __syncthreads();
 }
 
-struct NoWait {
-  __device__ void operator()() const {}
-};
-
-// Row tiles first_tile, first_tile + stride, ... of one GEMV.  `wait` runs
-// after the first tile's weight loads are issued and before the prologue
-// reads any activation (the persistent kernel waits for its inputs there).
-// Returns false when this workgroup had no tile (wait was still called).
-template <int WT, int NB, int LPR, int RPL, int WPB, bool COH, typename Wait>
+// Row tiles first_tile, first_tile + stride, ... of one GEMV; the first
+// tile's weight loads are issued before the prologue.
+template <int WT, int NB, int LPR, int RPL, int WPB>
 __device__ __forceinline__ void gemv_tiles(const GemvParams &p, float4 *xs4, float *red, int first_tile, int stride,
-                           bool writer, Wait wait) {
+                           bool writer) {
   constexpr int RG = 64 / LPR;
-  // Chunks per row in one load set.  Two sets are in flight (ping-pong).  The
-  // persistent kernel runs one wave per SIMD, so it needs deeper sets than a
-  // standalone launch, where other waves cover the latency.
-  constexpr int U = COH ? ((RPL >= 2) ? 4 : 8) : ((RPL >= 2) ? 2 : 4);
+  // Chunks per row in one load set.  Two sets are in flight (ping-pong).
+  constexpr int U = (RPL >= 2) ? 2 : 4;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int rg = lane / LPR, kl = lane % LPR;
   constexpr int rows_per_wave = RG * RPL;
@@ -543,12 +669,9 @@ __device__ __forceinline__ void gemv_tiles(const GemvParams &p, float4 *xs4, flo
   const int K = p.k, nch = K / 16;
   const int n_it = (nch + LPR - 1) / LPR;
   const int ntiles = (p.m + rows_per_block - 1) / rows_per_block;
-  const float *xs = reinterpret_cast<const float *>(xs4);
+  const int K4 = K / 4;
 
-  if (first_tile >= ntiles) {
-    wait();
-    return;
-  }
+  if (first_tile >= ntiles) return;
   for (int tile = first_tile; tile < ntiles; tile += stride) {
     const int row0 = tile * rows_per_block + wave * rows_per_wave + rg * RPL;
     bool row_ok[RPL];
@@ -576,10 +699,7 @@ __device__ __forceinline__ void gemv_tiles(const GemvParams &p, float4 *xs4, flo
     };
     load_set(ca, 0);
     if (U < n_it) load_set(cb, U);
-    if (tile == first_tile) {
-      wait();
-      gemv_prologue<NB, WPB, COH>(p, xs4, red, writer);
-    }
+    if (tile == first_tile) gemv_prologue<NB, WPB>(p, xs4, red, writer);
 
     float acc[NB][RPL];
 #pragma unroll
@@ -587,17 +707,18 @@ __device__ __forceinline__ void gemv_tiles(const GemvParams &p, float4 *xs4, flo
 #pragma unroll
       for (int i = 0; i < RPL; i++) acc[b][i] = 0.f;
 
+    // every row of the batch tile, without a branch on the batch count:
+    // LDS rows past the batch are zero and their sums are dropped
     auto compute = [&](const Chunk<WT>(&chs)[RPL], int c) {
+      const int sw = NB > 1 ? (c >> 2) & 3 : 0;  // the chunk's word permutation (xs_word)
 #pragma unroll
       for (int b = 0; b < NB; b++) {
-        if (b < p.batch) {
-          float4 xv[4];
-          const float4 *xr = reinterpret_cast<const float4 *>(xs + static_cast<size_t>(b) * K + c * 16);
+        float4 xv[4];
+        const float4 *xr = xs4 + static_cast<size_t>(b) * K4 + 4 * c;
 #pragma unroll
-          for (int j = 0; j < 4; j++) xv[j] = xr[j];
+        for (int j = 0; j < 4; j++) xv[j] = xr[j ^ sw];
 #pragma unroll
-          for (int i = 0; i < RPL; i++) acc[b][i] = chunk_dot<WT>(chs[i], xv, acc[b][i]);
-        }
+        for (int i = 0; i < RPL; i++) acc[b][i] = chunk_dot<WT>(chs[i], xv, acc[b][i]);
       }
     };
 
@@ -654,7 +775,7 @@ __device__ __forceinline__ void gemv_tiles(const GemvParams &p, float4 *xs4, flo
 #pragma unroll
           for (int i = 0; i + 1 < RPL; i += 2)
             if (row_ok[i])
-              act_st<COH>(p.y + static_cast<size_t>(b) * p.ldy + row[i] / 2,
+              act_st<false>(p.y + static_cast<size_t>(b) * p.ldy + row[i] / 2,
                           gelu_tanh(v[i]) * v[i + 1] * p.out_scale);
         } else {
 #pragma unroll
@@ -663,7 +784,7 @@ __device__ __forceinline__ void gemv_tiles(const GemvParams &p, float4 *xs4, flo
             float t = v[i];
             if (p.act == ACT_RELU) t = t > 0.f ? t : 0.f;
             else if (p.act == ACT_GELU_ERF) t = gelu_erf(t);
-            act_st<COH>(p.y + static_cast<size_t>(b) * p.ldy + row[i], t * p.out_scale);
+            act_st<false>(p.y + static_cast<size_t>(b) * p.ldy + row[i], t * p.out_scale);
           }
         }
       }

@@ -1,7 +1,6 @@
-// step_dev.h -- one decode step as a list of phases, shared by the two
-// executors: standalone kernel launches (one per phase, captured in a HIP
-// graph) and the persistent step kernel (persist.hip), which runs every phase
-// in one launch with a grid-wide flag barrier between phases.
+// step_dev.h -- one decode step as a list of phases for the phase-kernel
+// executors: one standalone kernel launch per phase (phases.hip), captured in
+// a HIP graph per batch size or launched eagerly.
 //
 // Phase kinds: token embedding, norm+GEMV (gemv_dev.h), attention split
 // partials and merge (attn_dev.h), greedy argmax partials and final.
@@ -15,7 +14,7 @@ namespace sdev {
 
 // PH_GEMM_PRO / PH_GEMM: a projection over more streams than the GEMV tile
 // holds (gemm.hip): the norm / residual prologue into Phase::xn, then the
-// MFMA GEMM.  Standalone launches only (not in the persistent step kernel).
+// MFMA GEMM.
 enum PhaseKind {
   PH_EMBED = 0,
   PH_GEMV = 1,
@@ -203,20 +202,5 @@ void launch_gemm_prologue(const gdev::GemvParams &p, float *xn, hipStream_t s);
 void launch_gemm(const gdev::GemvParams &p, int wdtype, float *ws, unsigned *cnt, hipStream_t s);
 size_t gemm_ws_floats();
 size_t gemm_cnt_words();
-// Persistent execution of a whole step (persist.hip).  phases: device array.
-// flags: one 128-byte slot per workgroup (zeroed at allocation); status[0]
-// becomes non-zero if a barrier wait timed out.
-struct StepLaunch {
-  const sdev::Phase *phases = nullptr;
-  int nphases = 0;
-  unsigned int *flags = nullptr;
-  unsigned int *status = nullptr;
-  uint64_t *trace = nullptr;  // optional: [nphases][grid][2] wall-clock ticks (ready, done)
-  int wdtype = XE_I8, nb = 1, hd = 64, g = 1;
-  size_t lds_bytes = 0;
-  int grid = 0;
-};
-bool step_kernel_supported(int wdtype, int nb, int hd, int g);
-void launch_step(const StepLaunch &L, hipStream_t s);
 
 }  // namespace xe

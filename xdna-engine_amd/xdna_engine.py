@@ -30,7 +30,7 @@ XE_Q8_LIN, XE_Q8_ELF = 0, 1
 XE_NORM_NONE, XE_NORM_LN, XE_NORM_RMS, XE_NORM_RMS1P = 0, 1, 2, 3
 XE_LAYOUT_MK, XE_LAYOUT_KN = 0, 1
 XE_OPT, XE_WHISPER, XE_GEMMA3 = 0, 1, 2
-EXECUTORS = {0: "graph", 1: "persistent", 2: "eager", 3: "ll"}
+EXECUTORS = {0: "graph", 2: "eager", 3: "ll"}
 
 EXPORTS = [
     "xe_last_error", "xe_abi_version", "xe_device_count", "xe_device_open", "xe_device_close",
