@@ -323,10 +323,13 @@ def gemv_case(xe, dev, ctx, wd, m, k, batches, seed, eager):
     return out
 
 
-def attn_case(xe, dev, ctx, hq, hkv, hd, mc, b, seed, eager):
-    """Config 3: one query per stream over a bf16 cache, lengths U[mc/2, mc]."""
+def attn_case(xe, dev, ctx, hq, hkv, hd, mc, b, seed, eager, fixed_len=0, reps=0):
+    """Config 3: one query per stream over a bf16 cache, lengths U[mc/2, mc]
+    (or every stream at fixed_len)."""
     rng = np.random.default_rng(seed)
     lens = rng.integers(mc // 2, mc + 1, b).astype(np.int32)
+    if fixed_len:
+        lens[:] = fixed_len
     nkv = b * hkv * mc * hd
     kb, vb = xe.Buf(dev, nkv * 2), xe.Buf(dev, nkv * 2)
     kb.fill_synthetic(xe.XE_BF16, seed, 11, nkv)
@@ -336,12 +339,13 @@ def attn_case(xe, dev, ctx, hq, hkv, hd, mc, b, seed, eager):
     lb = xe.Buf.from_array(dev, lens)
     ob = xe.Buf(dev, b * hq * hd * 4)
     by = int(lens.astype(np.int64).sum()) * hkv * hd * 4 + b * hq * hd * 8
-    reps = int(max(3, min(200, 2e5 / max(by / 5e6, 1.0))))
+    reps = reps or int(max(3, min(200, 2e5 / max(by / 5e6, 1.0))))
     us = ctx.probe_attn(qb.ptr, kb.ptr, vb.ptr, lb.ptr, b, hq, hkv, hd, mc, 1.0 / hd ** 0.5,
                         ob.ptr, reps, eager)
     for buf in (kb, vb, qb, lb, ob):
         buf.free()
-    rec = {"kernel": "mha_decode %dq/%dkv x %d ctx %d b=%d" % (hq, hkv, hd, mc, b),
+    rec = {"kernel": "mha_decode %dq/%dkv x %d ctx %d b=%d%s" % (hq, hkv, hd, mc, b,
+                                                             " len %d" % fixed_len if fixed_len else ""),
            "us": round(us, 2), "bytes": by, "gbps": round(by / us / 1e3, 1),
            "frac": round(by / us / 1e3 / HBM_PEAK_GBPS, 4)}
     print("[kernels] %s" % rec, file=sys.stderr, flush=True)
@@ -393,6 +397,10 @@ def run_kernels(args):
         for name, m, k in GEMM_SHAPES:
             recs.append(gemm_case(xe, dev, ctx, name, m, k, 64, args.seed + m + k, args.eager,
                                   args.reps, args.copies))
+        # and the b = 64 step's attention at the bench's mean context (every
+        # stream at length 2311 of a 4096-row cache, Gemma's 4q / 1kv x 256)
+        recs.append(attn_case(xe, dev, ctx, 4, 1, 256, 4096, 64, args.seed, args.eager,
+                              fixed_len=2311, reps=args.reps))
         ctx.close()
         dev.close()
         return {"metric": "batched GEMM (b = 64 projections)", "unit": "GB/s", "peak": HBM_PEAK_GBPS,
@@ -483,7 +491,8 @@ def main():
     ap.add_argument("--kernels", action="store_true",
                     help="only the isolated kernels: config-2 GEMVs and config-3 mha_decode")
     ap.add_argument("--gemm-only", action="store_true",
-                    help="with --kernels: only the b = 64 projection GEMMs")
+                    help="with --kernels: only the b = 64 step's kernels (projection GEMMs, "
+                         "attention at the mean context)")
     ap.add_argument("--reps", type=int, default=0, help="--kernels GEMMs: repetitions (0: by size)")
     ap.add_argument("--copies", type=int, default=0, help="--kernels GEMMs: weight copies (0: >= 512 MB)")
     ap.add_argument("--eager", action="store_true",

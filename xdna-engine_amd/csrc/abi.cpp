@@ -844,10 +844,17 @@ int xe_w8a8_linear(xe_ctx *ctx, const xe_weight *w, const float *x, int batch, f
   }, -1);
 }
 
-// Splits per (stream, kv head): about four workgroups per CU in total, at
-// most one per 64 cache rows and at most 64.
+// Splits per (stream, kv head): about XE_ATTN_WG_PER_CU (default 2)
+// workgroups per CU in total, at most one per 64 cache rows and at most 64.
+// With the merge inside the split kernel, 2 a CU against 4 (graph replays,
+// config 3): GQA 4q/1kv x 256 b = 64 ctx 4096 52.3 / 58.3 us, b = 16 ctx
+// 4096 33.0 / 47.1, b = 64 ctx 1024 26.2 / 37.2; ctx 32768 within 4 %.
 static int attn_splits(const xe_ctx *ctx, int batch, int hkv, int max_ctx) {
-  const int target = 4 * ctx->dev->num_cus;
+  static const int per_cu = [] {
+    const char *e = std::getenv("XE_ATTN_WG_PER_CU");
+    return e && std::atoi(e) > 0 ? std::atoi(e) : 2;
+  }();
+  const int target = per_cu * ctx->dev->num_cus;
   int ms = target / (batch * hkv);
   const int cap = (max_ctx + 63) / 64;
   ms = ms < 1 ? 1 : ms;
