@@ -60,6 +60,12 @@ HBM_PEAK_GBPS = 8000.0
 # numbers in profiles/ll_traffic_gemma3_1b_b1.md.  Measured offline (counters
 # need their own profiler run); null for any other workload.
 LL_TRAFFIC_BYTES_PER_STEP = 1345337816
+# HBM bytes per b = 64 step of the projection family (26 x the four layer
+# GEMMs + the lm-head GEMM, the b = 64 line's dominant kernels): per-dispatch
+# FETCH_SIZE and WRITE_SIZE of the same kernels at the decoder's shapes,
+# launched through the op layer (bench.py --kernels --gemm-only --eager), scaled
+# like the b = 1 figure; profiles/b64_step_kernels_traffic.md.
+B64_GEMM_TRAFFIC_BYTES_PER_STEP = 2231000000
 
 
 def load_xe():
@@ -250,7 +256,9 @@ def run_batch(xe, dev, cfg, args, B, steps, warmup, profile):
                      "achieved": round(r_gbps, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(r_gbps / HBM_PEAK_GBPS, 4),
                      "traffic": (LL_TRAFFIC_BYTES_PER_STEP if executor == "ll" and B == 1 and
-                                 args.prompt == 512 and args.ctx == 4096 and args.steps == 0 else None),
+                                 args.prompt == 512 and args.ctx == 4096 and args.steps == 0 else
+                                 B64_GEMM_TRAFFIC_BYTES_PER_STEP if B == 64 and r_kernel.startswith("gemm_ks") and
+                                 args.prompt == 512 and args.ctx == 4096 else None),
                      "traffic_unit": "bytes per step",
                      "bytes": int(r_bytes), "us": round(r_us, 2)},
     }
