@@ -441,20 +441,29 @@ def run_configs(xe, dev):
     ms/step, scripts/measure_phase2_sweep.sh:81).  Greedy decode of seeded
     synthetic int8 weights, timed with the device synchronised on both sides;
     the prompt is fed untimed.  Whisper decodes against a synthetic encoder
-    output (1500 frames, N(0, 1) rounded to bf16)."""
+    output (1500 frames, N(0, 1) rounded to bf16).  Also config 4 with the
+    fused decoder's per-utterance int8 cross K / V, and config 5's bf16
+    baseline (Gemma-3-1B with bf16 weights, 2.0 GB a token; no reference
+    number), whose line adds its weight-stream rate."""
     res = {}
     runs = [("opt125m_b1", xe.OPT_125M, 0, 1, 32, 128),
             ("whisper_small_b1", xe.WHISPER_SMALL, 1, 1, 4, 224),
-            ("whisper_small_b32", xe.WHISPER_SMALL, 1, 32, 4, 224)]
+            ("whisper_small_b1_int8cross", xe.WHISPER_SMALL, 1, 1, 4, 224),
+            ("whisper_small_b32", xe.WHISPER_SMALL, 1, 32, 4, 224),
+            ("gemma3_1b_bf16_b1", xe.GEMMA3_1B.replace(wdtype=xe.XE_BF16, max_ctx=4096), 2, 1, 512, 520)]
     ref_ms = {"opt125m_b1": (47.0, "reference host CPU path, README.md:38"),
               "whisper_small_b1": (75.0, "reference fused decoder on the XDNA2 NPU, "
                                          "docs/data-movement-thesis.md:41"),
+              "whisper_small_b1_int8cross": (75.0, "reference fused decoder on the XDNA2 NPU, "
+                                                   "docs/data-movement-thesis.md:41"),
               "whisper_small_b32": (16.13 / 16.0, "reference B=16 lockstep on the XDNA2 NPU, per "
                                                   "stream-token, scripts/measure_phase2_sweep.sh:81")}
     for name, cfg, seed, B, n_prompt, n_new in runs:
         dec = xe.Decoder(dev, cfg, max_batch=B)
         dec.init_synthetic(seed)
         if cfg.family == xe.XE_WHISPER:
+            if name.endswith("int8cross"):
+                dec.set_cross_int8(True, True)
             dec.precompute_cross(None)
         rng = np.random.default_rng(seed)
         dec.feed(rng.integers(0, cfg.vocab, (B, n_prompt)).astype(np.int32))
@@ -466,13 +475,20 @@ def run_configs(xe, dev):
         el = time.perf_counter() - t0
         k = n_new - 8
         ms_tok = el / k * 1e3
-        rms, rsrc = ref_ms[name]
-        res[name] = {"tok_s": round(B * k / el, 1), "ms_per_step": round(ms_tok, 4), "batch": B,
-                     "executor": dec.executor(B), "timed_steps": k,
-                     "workload": "%s int8, prompt %d, greedy steps %d..%d" % (
-                         name.split("_b")[0], n_prompt, n_prompt + 8, n_prompt + n_new - 1),
-                     "reference_ms_per_token": rms, "reference": rsrc,
-                     "speedup_vs_reference": round(rms / (ms_tok / B), 1)}
+        wname = {xe.XE_I8: "int8", xe.XE_BF16: "bf16", xe.XE_BFP16: "bfp16"}[cfg.wdtype]
+        r = {"tok_s": round(B * k / el, 1), "ms_per_step": round(ms_tok, 4), "batch": B,
+             "executor": dec.executor(B), "timed_steps": k,
+             "workload": "%s %s%s, prompt %d, greedy steps %d..%d" % (
+                 name.split("_b")[0], wname, " (int8 cross K / V)" if name.endswith("int8cross") else "",
+                 n_prompt, n_prompt + 8, n_prompt + n_new - 1)}
+        if name in ref_ms:
+            rms, rsrc = ref_ms[name]
+            r.update({"reference_ms_per_token": rms, "reference": rsrc,
+                      "speedup_vs_reference": round(rms / (ms_tok / B), 1)})
+        else:  # weight bytes streamed per step over the step time
+            gbps = dec.weight_bytes() / (el / k) / 1e9
+            r.update({"weight_gbps": round(gbps, 1), "weight_frac": round(gbps / HBM_PEAK_GBPS, 4)})
+        res[name] = r
         dec.close()
     return res
 

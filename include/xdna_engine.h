@@ -421,8 +421,9 @@ int xe_decoder_set_cross(xe_decoder *dec, const float *enc);
  * scale s = max_t|x| / 127, q = round(x / s); scores use q * s_k, the
  * attention output is scaled by s_v.  Half the cross-attention bytes per
  * token.  Takes effect at the next xe_decoder_set_cross (call it again
- * after switching); such a decoder steps on the phase kernels (graph
- * executor). */
+ * after switching).  With K and V both int8 the low-latency executor reads
+ * the int8 rows inside its step; K or V alone steps on the phase kernels
+ * (graph executor). */
 int xe_decoder_set_cross_int8(xe_decoder *dec, int k_int8, int v_int8);
 /* step(tok, pos) -> logits (whisper_decoder.rs:1293-1349) for `batch`
  * streams with per-stream positions.  logits [batch, vocab] may be NULL;

@@ -167,20 +167,27 @@ def test_whisper_small_short(gpu, xe, executor):
 
 # ---- per-utterance int8 cross K / V (gen_decode.py:263-282) ----
 
-@pytest.mark.parametrize("k8,v8", [(1, 0), (0, 1), (1, 1)])
-def test_whisper_int8_cross_kv(gpu, xe, k8, v8):
+@pytest.mark.parametrize("k8,v8,step", [(1, 0, None), (0, 1, None), (1, 1, None), (1, 1, "graph")])
+def test_whisper_int8_cross_kv(gpu, xe, monkeypatch, k8, v8, step):
     """int8 cross K and/or V with per-channel scales, quantised on the GPU
-    from the fp32 projections (whisper_decoder.rs:1186-1219) and read by the
-    phase kernels: step logits and a greedy stream against the oracle with
-    the same quantisation; the decoder runs the graph executor."""
+    from the fp32 projections (whisper_decoder.rs:1186-1219): step logits and
+    a greedy stream against the oracle with the same quantisation.  K and V
+    both int8 run inside the low-latency step (int8 rows converted exactly
+    for the matrix-core Q.K, the K scale on q, the V scale on the partial
+    sums); K or V alone, or XE_STEP=graph, on the phase kernels."""
+    if step:
+        monkeypatch.setenv("XE_STEP", step)
+    else:
+        monkeypatch.delenv("XE_STEP", raising=False)
     dev, _ = gpu
     cfg = tiny(xe, xe.XE_WHISPER, xe.XE_I8)
-    print("[case] tiny whisper int8 cross k=%d v=%d" % (k8, v8), flush=True)
+    print("[case] tiny whisper int8 cross k=%d v=%d %s" % (k8, v8, step or "default"), flush=True)
     dec = xe.Decoder(dev, cfg, max_batch=2)
     dec.init_synthetic(9)
     dec.set_cross_int8(k8, v8)
     dec.precompute_cross(None)
-    assert dec.executor(1) == "graph" and dec.executor(2) == "graph"
+    want_exec = "ll" if k8 and v8 and step is None else "graph"
+    assert dec.executor(1) == want_exec and dec.executor(2) == want_exec
     om = O.OracleModel(oracle_cfg(cfg), 9, 2)
     om.set_cross_i8(k8, v8)
     om.set_cross(None)
@@ -200,9 +207,10 @@ def test_whisper_int8_cross_kv(gpu, xe, k8, v8):
     om.set_cross(None)
     greedy_identity(got, om, pr, "whisper-int8-cross-k%d-v%d" % (k8, v8))
     om.close()
-    # back to bf16 cross K / V: the low-latency executor again, oracle's stream
+    # back to bf16 cross K / V: the default executor again, oracle's stream
     dec.set_cross_int8(0, 0)
     dec.precompute_cross(None)
+    assert dec.executor(1) == (step or "ll")
     dec.reset()
     got = dec.generate(pr[:1], 12)
     om = O.OracleModel(oracle_cfg(cfg), 9, 1)
@@ -212,21 +220,34 @@ def test_whisper_int8_cross_kv(gpu, xe, k8, v8):
     dec.close()
 
 
-def test_whisper_small_int8_cross(gpu, xe):
-    """Config 4 shape (Whisper-small, 1500 frames) with int8 cross K and V:
-    a short greedy stream against the oracle."""
+def test_whisper_small_int8_cross(gpu, xe, monkeypatch):
+    """Config 4 shape (Whisper-small, 1500 frames) with int8 cross K and V on
+    the low-latency executor (two streams, one starting later): a greedy
+    stream against the oracle, then step logits."""
+    monkeypatch.delenv("XE_STEP", raising=False)
     dev, _ = gpu
     cfg = xe.WHISPER_SMALL
-    dec = xe.Decoder(dev, cfg, max_batch=1)
+    dec = xe.Decoder(dev, cfg, max_batch=2)
     dec.init_synthetic(1)
     dec.set_cross_int8(1, 1)
     dec.precompute_cross(None)
-    om = O.OracleModel(oracle_cfg(cfg), 1, 1)
+    assert dec.executor(1) == "ll" and dec.executor(2) == "ll"
+    om = O.OracleModel(oracle_cfg(cfg), 1, 2)
     om.set_cross_i8(1, 1)
     om.set_cross(None)
-    pr = prompts(cfg, 1, 4, seed=1)
-    got = dec.generate(pr, 12)
+    pr = prompts(cfg, 2, 4, seed=1)
+    got = dec.generate(pr, 40)
     greedy_identity(got, om, pr, "whisper-small-int8-cross", eps=5e-3)
+    tok = got[:, -1].copy()
+    pos = np.full(2, 4 + 40 - 1, np.int32)
+    g, _ = dec.step(tok, pos)
+    om.reset()
+    for p in range(4):
+        om.step(pr[:, p], np.full(2, p, np.int32))
+    for i in range(39):
+        om.step(got[:, i], np.full(2, 4 + i, np.int32))
+    w = om.step(tok, pos)
+    compare_logits(g, w, "whisper-small-int8-cross-step", atol=5e-3)
     dec.close()
     om.close()
 

@@ -396,6 +396,7 @@ struct xe_decoder {
     uint64_t *arena = nullptr;  // every exchange vector of the step
     ll::Vec arg{};
     int kin_a = 0, kin_f = 0, scratch = 0, nb_t = 1, grid = 0, hd = 64, g = 1;
+    bool kv8 = false;  // int8 cross K / V (its own kernel instantiation)
     int stage_a = 0, stage_f = 0;  // LDS weight stage bytes per role (ll::StageLayout), 0: none staged
     int kv_floats = 0;             // LDS key/value stage (attention side), 0: none
     size_t lds_bytes = 0;
@@ -1140,6 +1141,10 @@ int plan_kv_stage(std::vector<ll::Phase> &list, int hd, int max_ctx, long budget
   for (int j = 1; j < static_cast<int>(list.size()); j++) {
     if (list[j].kind != ll::LK_ATTN) continue;
     ll::AttnD &a = list[j].u.attn;
+    if (a.k_scale) {  // int8 rows are read where they are used, not staged
+      a.kv_cap = 0;
+      continue;
+    }
     int chunk, nsplits;
     ll::ll_split(a.fixed_len > 0 ? a.fixed_len : max_ctx, a.max_splits, hd, chunk, nsplits);
     int cap = std::min(chunk, ll::kRoundKeys);
@@ -1225,11 +1230,15 @@ void build_ll_plan(xe_decoder *d, int B, xe_decoder::LLPlan &P) {
   const int g = c.n_heads / c.n_kv_heads;
   P.ok = false;
   if (B > ll::kMaxNB) { P.why = "batch > 4"; return; }
-  if (d->cross_i8k || d->cross_i8v) { P.why = "int8 cross K/V runs on the phase kernels"; return; }
+  if (d->cross_i8k != d->cross_i8v) { P.why = "int8 cross K or V alone runs on the phase kernels"; return; }
   P.nb_t = B <= 1 ? 1 : B <= 2 ? 2 : 4;
   P.hd = hd;
   P.g = g;
-  if (!ll::step_supported(c.wdtype, P.nb_t, hd, g)) { P.why = "head_dim / group not instantiated"; return; }
+  P.kv8 = d->cross_i8k && d->cross_i8v;
+  if (!ll::step_supported(c.wdtype, P.nb_t, hd, g, P.kv8)) {
+    P.why = P.kv8 ? "int8 cross K/V with non-int8 weights runs on the phase kernels" : "head_dim / group not instantiated";
+    return;
+  }
   if (hd % ll::kDM != 0) { P.why = "head_dim not a multiple of 16"; return; }
   for (int k : {D, F, hq}) if (k % 16) { P.why = "K not a multiple of 16"; return; }
   P.grid = d->dev->num_cus > 0 ? d->dev->num_cus : 256;
@@ -1438,6 +1447,12 @@ void build_ll_plan(xe_decoder *d, int B, xe_decoder::LLPlan &P) {
       attn(v_xq, D, 0, 0, 0, false, l.ck, l.cv, 0, c.n_cross, c.n_heads, c.n_heads,
            1.0f / sqrtf(static_cast<float>(hd)), c.n_cross, nullptr, nullptr, false, ms_cross, v_xpart, v_xatt, 0,
            "attn_cross");
+      if (d->cross_i8k && d->cross_i8v) {  // int8 cross K and V (the attention phase, before its merge)
+        ll::AttnD &ca = P.a[P.a.size() - 2].u.attn;
+        ca.k_scale = l.cks;
+        ca.v_scale = l.cvs;
+        P.a_bytes[P.a_bytes.size() - 2] = 2.0 * c.n_cross * c.n_heads * hd * B;
+      }
       gemv(P.a, n_a, l.xo, l.xo_b, v_xatt, XE_NORM_NONE, nullptr, nullptr, ACT_NONE, v_xo, "gemv_xo");
     }
     // ---- F side ----
@@ -1634,7 +1649,7 @@ void run_ll(xe_decoder *d, int B, int n_steps, const int32_t *forced, int n_forc
   // a traced launch keeps its marks in LDS behind the scratch area
   sp.trace_slots = trace ? static_cast<int>(ll_trace_slots(P)) : 0;
   const size_t lds = P.lds_bytes + (trace ? sizeof(uint64_t) * (sp.trace_slots + 1) : 0);
-  ll::launch(sp, c.wdtype, P.nb_t, P.hd, P.g, lds, P.grid, d->s);
+  ll::launch(sp, c.wdtype, P.nb_t, P.hd, P.g, P.kv8, lds, P.grid, d->s);
   d->ll_epoch += static_cast<unsigned>(n_steps);
 }
 

@@ -3,6 +3,6 @@
 
 namespace xe {
 namespace ll {
-StepFn pick_ll_bfp16(int nb, int hd, int g) { return pick_nb<XE_BFP16>(nb, hd, g); }
+StepFn pick_ll_bfp16(int nb, int hd, int g, bool kv8) { return pick_nb<XE_BFP16>(nb, hd, g, kv8); }
 }  // namespace ll
 }  // namespace xe

@@ -121,6 +121,9 @@ struct AttnD {
   // most kv_cap keys has its rows and head constants copied into LDS by the
   // phase before (Phase::kv_issue)
   int kv_cap;
+  // int8 K and V rows (Whisper's per-utterance cross K / V, both or neither):
+  // channel scales [heads * hd]; kc / vc then hold int8 [head][key][hd]
+  const float *k_scale, *v_scale;
 };
 
 struct MergeD {
@@ -1407,6 +1410,24 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return static_cast<uint32_t>(adev::f32_to_bf16_rne(lo)) | static_cast<uint32_t>(adev::f32_to_bf16_rne(hi)) << 16;
 }
 
+// Signed byte j of w as a float.
+__device__ __forceinline__ float i8_at(uint32_t w, int j) {
+  return static_cast<float>(static_cast<int>(static_cast<int8_t>(w >> (8 * j))));
+}
+
+// Eight int8 values (k order) as eight bf16, exactly (at most 8 significant
+// bits): the upper halves of their fp32 values, paired.
+__device__ __forceinline__ u32x4 i8x8_to_bf16x8(u32x2 w) {
+  uint32_t p[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const uint32_t word = i < 2 ? w.x : w.y;
+    const int j = 2 * (i & 1);
+    p[i] = __builtin_amdgcn_perm(__float_as_uint(i8_at(word, j + 1)), __float_as_uint(i8_at(word, j)), 0x07060302u);
+  }
+  return u32x4{p[0], p[1], p[2], p[3]};
+}
+
 // One split block of (stream b, kv head kvh): keys [split*chunk, ...), the G
 // query heads of the group at once.
 //   Q.K: per wave one 16-key tile as v_mfma_f32_16x16x32_bf16 steps, K rows
@@ -1423,7 +1444,13 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 // key at the last position is not read back from the cache: lanes that hold
 // it take the bf16-rounded values from LDS.  Partial out: (m, l, acc[hd]) per
 // query head, m in log2 units of the scaled score.
-template <int HD, int G, typename AD, typename Prep, typename Sub>
+// KV8: int8 K and V rows (the per-utterance cross K / V,
+// route_b_kernels/decode_fused/gen_decode.py:263-282): K bytes convert to
+// bf16 exactly for the MFMA, q is multiplied by the K channel scales before
+// its three-part split (scores = sum_d (q[d] s_k[d]) k8[d]), and the partial
+// sums are multiplied by the V channel scales (out[d] = s_v[d] sum_t p_t
+// v8[t][d]); no append, no K/V stage.
+template <int HD, int G, bool KV8, typename AD, typename Prep, typename Sub>
 __device__ __forceinline__ bool attn_block(const AD &a, int split, int kvh, int b, int len, const float *qin,
                                            float *scr, unsigned ep, Prep prep, Sub tsub, float *kvs,
                                            bool staged) {
@@ -1448,9 +1475,13 @@ __device__ __forceinline__ bool attn_block(const AD &a, int split, int kvh, int 
 
   uint16_t *kbase = a.kc + a.kv_bstride * b + static_cast<size_t>(kvh) * a.max_ctx * HD;
   uint16_t *vbase = a.vc + a.kv_bstride * b + static_cast<size_t>(kvh) * a.max_ctx * HD;
-  const __amdgpu_buffer_rsrc_t krs = gdev::coherent_rsrc(kbase);
-  const __amdgpu_buffer_rsrc_t vrs = gdev::coherent_rsrc(vbase);
-  const bool appender = a.append && split == nsplits - 1;
+  // int8 rows: the same element offsets, in bytes
+  const size_t kvoff8 = a.kv_bstride * b + static_cast<size_t>(kvh) * a.max_ctx * HD;
+  const __amdgpu_buffer_rsrc_t krs =
+      gdev::coherent_rsrc(KV8 ? static_cast<const void *>(reinterpret_cast<const uint8_t *>(a.kc) + kvoff8) : kbase);
+  const __amdgpu_buffer_rsrc_t vrs =
+      gdev::coherent_rsrc(KV8 ? static_cast<const void *>(reinterpret_cast<const uint8_t *>(a.vc) + kvoff8) : vbase);
+  const bool appender = !KV8 && a.append && split == nsplits - 1;
 
   // lane roles: Q.K row (key) lane & 15, dims 8 (lane >> 4) + 32 j;
   // P.V key slot lane / LPK, dims 4 (lane % LPK) .. + 4
@@ -1458,15 +1489,28 @@ __device__ __forceinline__ bool attn_block(const AD &a, int split, int kvh, int 
   const int pv_slot = lane / LPK, pv_dim = 4 * (lane % LPK);
   u32x4 kf[NJ];
   u32x2 vf[PVK];
+  u32x2 kf8[NJ];     // KV8: 8 int8 of a key
+  uint32_t vf8[PVK]; // KV8: 4 int8 of a value row
   auto load_round = [&](int rb) {
     const int kq = rb + wave * kKeyTile + qk_row;
     const bool kok = kq < s1;
+    if constexpr (KV8) {
 #pragma unroll
-    for (int j = 0; j < NJ; j++) kf[j] = ld_kv(krs, kok ? (kq * HD + 32 * j + qk_dim) * 2 : kNoRecord);
+      for (int j = 0; j < NJ; j++) kf8[j] = ld_kv8(krs, kok ? kq * HD + 32 * j + qk_dim : kNoRecord);
 #pragma unroll
-    for (int i = 0; i < PVK; i++) {
-      const int kv = rb + (i * kW + wave) * KPI + pv_slot;
-      vf[i] = ld_kv8(vrs, kv < s1 ? (kv * HD + pv_dim) * 2 : kNoRecord);
+      for (int i = 0; i < PVK; i++) {
+        const int kv = rb + (i * kW + wave) * KPI + pv_slot;
+        vf8[i] = __builtin_amdgcn_raw_buffer_load_b32(vrs, kv < s1 ? kv * HD + pv_dim : kNoRecord, 0,
+                                                      gdev::kCoherentSc1);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < NJ; j++) kf[j] = ld_kv(krs, kok ? (kq * HD + 32 * j + qk_dim) * 2 : kNoRecord);
+#pragma unroll
+      for (int i = 0; i < PVK; i++) {
+        const int kv = rb + (i * kW + wave) * KPI + pv_slot;
+        vf[i] = ld_kv8(vrs, kv < s1 ? (kv * HD + pv_dim) * 2 : kNoRecord);
+      }
     }
   };
   HeadConsts<HD> hc;
@@ -1503,8 +1547,10 @@ __device__ __forceinline__ bool attn_block(const AD &a, int split, int kvh, int 
   // Columns from 3 G on are never written: their products land in C columns
   // that nothing reads.
   XE_LDS uint16_t *bfh = reinterpret_cast<XE_LDS uint16_t *>(bfr);
+  const float *ksc = KV8 ? a.k_scale + kvh * HD : nullptr;
   for (int gg = wave; gg < G; gg += kW) {
     head_xform<HD>(qrow + a.q_off + (kvh * G + gg) * HD, [&](int d, float x) {
+      if constexpr (KV8) x = x * ksc[d];  // the K channel scale rides on q
       const uint32_t hi = __float_as_uint(x) & 0xffff0000u;
       const float r = x - __uint_as_float(hi);
       const uint32_t mid = __float_as_uint(r) & 0xffff0000u;
@@ -1547,7 +1593,11 @@ __device__ __forceinline__ bool attn_block(const AD &a, int split, int kvh, int 
     if (rb != s0) load_round(rb);
     // ---- Q.K: this wave's 16-key tile ----
     const int tile0 = rb + wave * kKeyTile;
-    if (staged && tile0 < s1) {
+    if constexpr (KV8) {
+#pragma unroll
+      for (int j = 0; j < NJ; j++) kf[j] = i8x8_to_bf16x8(kf8[j]);
+    }
+    if (!KV8 && staged && tile0 < s1) {
       const int kq = min(wave * kKeyTile + qk_row, last);
 #pragma unroll
       for (int j = 0; j < NJ; j++)
@@ -1620,7 +1670,7 @@ __device__ __forceinline__ bool attn_block(const AD &a, int split, int kvh, int 
         for (int e = 0; e < 4; e++) acc[gg][e] *= corr;
       }
     }
-    if (staged) {
+    if (!KV8 && staged) {
       // this wave's key slots (slot i * kW + wave, KPI keys each) hold keys
       // up to the block's last; four slots' reads are issued together
       const int nact = wave * KPI <= last ? (last / KPI - wave) / kW + 1 : 0;
@@ -1654,10 +1704,18 @@ __device__ __forceinline__ bool attn_block(const AD &a, int split, int kvh, int 
       for (int i = 0; i < PVK; i++) {
         if (rb + (i * kW + wave) * KPI >= s1) continue;  // wave-uniform: slots past the split
         const int key_l = (i * kW + wave) * KPI + pv_slot;
-        u32x2 v = vf[i];
-        if (appender && rb + key_l == posi) v = *reinterpret_cast<const XE_LDS u32x2 *>(kvb + HD / 2 + pv_dim / 2);
-        const float vv[4] = {__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xffff0000u),
-                             __uint_as_float(v.y << 16), __uint_as_float(v.y & 0xffff0000u)};
+        float vv[4];
+        if constexpr (KV8) {
+#pragma unroll
+          for (int e = 0; e < 4; e++) vv[e] = i8_at(vf8[i], e);
+        } else {
+          u32x2 v = vf[i];
+          if (appender && rb + key_l == posi) v = *reinterpret_cast<const XE_LDS u32x2 *>(kvb + HD / 2 + pv_dim / 2);
+          vv[0] = __uint_as_float(v.x << 16);
+          vv[1] = __uint_as_float(v.x & 0xffff0000u);
+          vv[2] = __uint_as_float(v.y << 16);
+          vv[3] = __uint_as_float(v.y & 0xffff0000u);
+        }
         float p[G];
         if constexpr (G == 4) {
           const f32x4_t p4 = *reinterpret_cast<const XE_LDS f32x4_t *>(sc + key_l * G);
@@ -1724,6 +1782,7 @@ __device__ __forceinline__ bool attn_block(const AD &a, int split, int kvh, int 
       v = rv[0];
 #pragma unroll
       for (int w = 1; w < kW; w++) v += rv[w];
+      if constexpr (KV8) v = v * a.v_scale[kvh * HD + e - 2];  // the V channel scale
     }
     put(a.part, b, ((kvh * G + gg) * a.max_splits + split) * (HD + 2) + e, v, ep);
   }
@@ -1835,8 +1894,9 @@ __device__ __noinline__ bool merge_block(const XE_CONST MergeD &mg, int b, int h
 }
 
 // host side (ll_launch.hip)
-bool step_supported(int wdtype, int nb_t, int hd, int g);
-void launch(const StepParams &sp, int wdtype, int nb_t, int hd, int g, size_t lds_bytes, int grid, hipStream_t s);
+bool step_supported(int wdtype, int nb_t, int hd, int g, bool kv8);
+void launch(const StepParams &sp, int wdtype, int nb_t, int hd, int g, bool kv8, size_t lds_bytes, int grid,
+            hipStream_t s);
 
 }  // namespace ll
 }  // namespace xe

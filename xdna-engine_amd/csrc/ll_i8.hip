@@ -3,6 +3,6 @@
 
 namespace xe {
 namespace ll {
-StepFn pick_ll_i8(int nb, int hd, int g) { return pick_nb<XE_I8>(nb, hd, g); }
+StepFn pick_ll_i8(int nb, int hd, int g, bool kv8) { return pick_nb<XE_I8>(nb, hd, g, kv8); }
 }  // namespace ll
 }  // namespace xe

@@ -80,7 +80,9 @@ __device__ __noinline__ HeadOut head_gemv(const HeadArgs h, int nb, int r0, int 
   return o;
 }
 
-template <int WT, int NB, int HD, int G>
+// KV8: the plan has int8 cross K / V (its own instantiation, so the bf16
+// kernels keep their register allocation).
+template <int WT, int NB, int HD, int G, bool KV8>
 __global__ __launch_bounds__(kT) void ll_step_kernel(StepParams sp) {
   extern __shared__ float4 lds4[];
   __shared__ float red[2 * 4 * gdev::kMaxWaves];
@@ -238,7 +240,15 @@ __global__ __launch_bounds__(kT) void ll_step_kernel(StepParams sp) {
             // every attention phase of a plan has group G (host checks)
             // this rank's first block may sit in the key/value stage
             const bool staged = vb == rank && kv_staged(a, split, len);
-            ok = attn_block<HD, G>(a, split, kvh, b, len, xin, scr, ep, prep, tsub, kvs, staged);
+            // int8 cross K / V: Whisper's 64-wide single-query-head groups only
+            if constexpr (KV8 && HD == 64 && G == 1) {
+              if (a.k_scale)
+                ok = attn_block<HD, G, true>(a, split, kvh, b, len, xin, scr, ep, prep, tsub, kvs, staged);
+              else
+                ok = attn_block<HD, G, false>(a, split, kvh, b, len, xin, scr, ep, prep, tsub, kvs, staged);
+            } else {
+              ok = attn_block<HD, G, false>(a, split, kvh, b, len, xin, scr, ep, prep, tsub, kvs, staged);
+            }
           }
           break;
         }
@@ -401,27 +411,33 @@ __global__ __launch_bounds__(kT) void ll_step_kernel(StepParams sp) {
 
 using StepFn = void (*)(StepParams);
 
+// int8 cross K / V (kv8) is instantiated for int8 weights (the fused decode
+// ELF's combination); other weight types with it run the phase kernels.
 template <int WT, int NB>
-StepFn pick_head(int hd, int g) {
-  if (hd == 64 && g == 1) return ll_step_kernel<WT, NB, 64, 1>;
-  if (hd == 256 && g == 4) return ll_step_kernel<WT, NB, 256, 4>;
+StepFn pick_head(int hd, int g, bool kv8) {
+  if (hd == 64 && g == 1) {
+    if constexpr (WT == XE_I8)
+      if (kv8) return ll_step_kernel<WT, NB, 64, 1, true>;
+    return kv8 ? nullptr : ll_step_kernel<WT, NB, 64, 1, false>;
+  }
+  if (hd == 256 && g == 4 && !kv8) return ll_step_kernel<WT, NB, 256, 4, false>;
   return nullptr;
 }
 
 template <int WT>
-StepFn pick_nb(int nb, int hd, int g) {
+StepFn pick_nb(int nb, int hd, int g, bool kv8) {
   switch (nb) {
-    case 1: return pick_head<WT, 1>(hd, g);
-    case 2: return pick_head<WT, 2>(hd, g);
-    case 4: return pick_head<WT, 4>(hd, g);
+    case 1: return pick_head<WT, 1>(hd, g, kv8);
+    case 2: return pick_head<WT, 2>(hd, g, kv8);
+    case 4: return pick_head<WT, 4>(hd, g, kv8);
   }
   return nullptr;
 }
 
 // one translation unit per weight dtype (ll_i8.hip, ll_bf16.hip, ll_bfp16.hip)
-StepFn pick_ll_i8(int nb, int hd, int g);
-StepFn pick_ll_bf16(int nb, int hd, int g);
-StepFn pick_ll_bfp16(int nb, int hd, int g);
+StepFn pick_ll_i8(int nb, int hd, int g, bool kv8);
+StepFn pick_ll_bf16(int nb, int hd, int g, bool kv8);
+StepFn pick_ll_bfp16(int nb, int hd, int g, bool kv8);
 
 }  // namespace ll
 }  // namespace xe

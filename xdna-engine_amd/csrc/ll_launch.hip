@@ -8,21 +8,23 @@ namespace xe {
 namespace ll {
 
 namespace {
-StepFn pick(int wdtype, int nb_t, int hd, int g) {
+StepFn pick(int wdtype, int nb_t, int hd, int g, bool kv8) {
   switch (wdtype) {
-    case XE_I8: return pick_ll_i8(nb_t, hd, g);
-    case XE_BF16: return pick_ll_bf16(nb_t, hd, g);
-    case XE_BFP16: return pick_ll_bfp16(nb_t, hd, g);
+    case XE_I8: return pick_ll_i8(nb_t, hd, g, kv8);
+    case XE_BF16: return pick_ll_bf16(nb_t, hd, g, kv8);
+    case XE_BFP16: return pick_ll_bfp16(nb_t, hd, g, kv8);
   }
   return nullptr;
 }
 }  // namespace
 
-bool step_supported(int wdtype, int nb_t, int hd, int g) { return pick(wdtype, nb_t, hd, g) != nullptr; }
+bool step_supported(int wdtype, int nb_t, int hd, int g, bool kv8) {
+  return pick(wdtype, nb_t, hd, g, kv8) != nullptr;
+}
 
-void launch(const StepParams &sp, int wdtype, int nb_t, int hd, int g, size_t lds_bytes, int grid,
+void launch(const StepParams &sp, int wdtype, int nb_t, int hd, int g, bool kv8, size_t lds_bytes, int grid,
             hipStream_t s) {
-  StepFn fn = pick(wdtype, nb_t, hd, g);
+  StepFn fn = pick(wdtype, nb_t, hd, g, kv8);
   XE_REQUIRE(fn, "low-latency step: unsupported (weight dtype, batch, head_dim, group)");
   XE_REQUIRE(lds_bytes <= 160 * 1024 - 2048, "low-latency step: LDS need too large");
   XE_REQUIRE(sp.nb >= 1 && sp.nb <= nb_t && nb_t <= kMaxNB, "low-latency step: bad stream count");
