@@ -294,6 +294,44 @@ def test_tiny_batched_step_logits(gpu, xe, family):
     om.close()
 
 
+PARTS_CASES = [("gemma", 64, "gemv_gateup_pro"), ("whisper", 32, "gemv_fc1_pro"), ("opt", 16, "gemv_fc1_pro")]
+
+
+@pytest.mark.parametrize("family,batch,pro", PARTS_CASES)
+def test_gemm_split_partials_in_prologue(gpu, xe, monkeypatch, family, batch, pro):
+    """A GEMM that splits K hands its split partials to the next phase's
+    prologue, which adds them in split order and applies the GEMM's epilogue
+    (GemvParams::sub_part), instead of the GEMM's own arrival counter and
+    finishing workgroup: forced steps on the real shapes give logits bit for
+    bit equal to XE_GEMM_DEFER=0 (the GEMM's own finish), and the prologue
+    does read the partials (its profiled bytes grow by the extra splits)."""
+    dev, _ = gpu
+    cfg = {"gemma": xe.GEMMA3_1B.replace(n_layers=2, max_ctx=64),
+           "whisper": xe.WHISPER_SMALL.replace(n_layers=2),
+           "opt": xe.OPT_125M.replace(n_layers=2)}[family]
+    print("[case] split partials %s b=%d" % (family, batch), flush=True)
+    rng = np.random.default_rng(3)
+    toks = rng.integers(0, cfg.vocab, (4, batch)).astype(np.int32)
+    outs, pro_bytes = [], []
+    for defer in ("0", "1"):
+        monkeypatch.setenv("XE_GEMM_DEFER", defer)
+        dec = xe.Decoder(dev, cfg, max_batch=batch)
+        dec.init_synthetic(5)
+        if family == "whisper":
+            dec.precompute_cross(None)
+        assert dec.executor(batch) == "graph"
+        logits = []
+        for i in range(4):
+            g, _ = dec.step(toks[i], np.full(batch, i, np.int32))
+            logits.append(g.copy())
+        pro_bytes.append(sum(by for lab, _, by in dec.profile_step(batch) if lab == pro))
+        outs.append(np.stack(logits))
+        dec.close()
+    monkeypatch.delenv("XE_GEMM_DEFER", raising=False)
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+    assert pro_bytes[1] > pro_bytes[0] > 0, pro_bytes
+
+
 def test_tiny_gemma_b64(gpu, xe):
     """64 streams (the config-5 batch) on the tiny Gemma shape."""
     cfg = tiny(xe, xe.XE_GEMMA3, xe.XE_I8)

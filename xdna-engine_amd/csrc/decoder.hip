@@ -738,10 +738,37 @@ struct PlanBuilder {
   float *xn = nullptr;  // GEMM path scratch (null: GEMV only)
   float *ws = nullptr;
   unsigned *cnt = nullptr;
+  int last_gemm = -1;  // the last phase pushed, when it is a GEMM
   void push(const sdev::Phase &ph, const std::string &label, double bytes) {
     plan.phases.push_back(ph);
     plan.labels.push_back(label);
     plan.bytes.push_back(bytes);
+    last_gemm = ph.kind == sdev::PH_GEMM ? static_cast<int>(plan.phases.size()) - 1 : -1;
+  }
+  // A prologue whose `sub` is the output of the GEMM pushed just before it,
+  // when that GEMM splits K, adds the GEMM's split partials itself (in split
+  // order, then the GEMM's own epilogue: the same values): the GEMM stores
+  // each split's raw sums to the workspace and loses its arrival counter and
+  // finishing workgroup, one memory round trip of its critical path.
+  // XE_GEMM_DEFER=0 (read when a plan is built) keeps the GEMM's own finish.
+  void adopt_parts(gdev::GemvParams &q) {
+    const char *env = std::getenv("XE_GEMM_DEFER");
+    if ((env && std::string(env) == "0") || !q.sub || last_gemm < 0 || !ws) return;
+    sdev::Phase &pp = plan.phases[last_gemm];
+    gdev::GemvParams &g = pp.u.gemv;
+    if (g.y != q.sub || g.act != ACT_NONE || g.ldy != g.m || g.m != q.k || g.batch != q.batch || g.part) return;
+    const int ks = gemm_defer_splits(g.m, g.k, g.batch);
+    if (ks < 2 || static_cast<size_t>(ks) * g.batch * g.m > gemm_ws_floats()) return;
+    gdev::GemvParams t = q;
+    t.sub = nullptr;
+    t.sub_part = ws;
+    t.sub_ks = ks;
+    t.sub_scale = (pp.variant == XE_I8 || pp.variant == XE_I4) ? g.scale : nullptr;
+    t.sub_bias = g.bias;
+    t.sub_out_scale = g.out_scale;
+    if (!gemm_prologue_takes_parts(t, xn)) return;
+    g.part = ws;
+    q = t;
   }
   // One projection over `batch` streams.  Up to 8 streams whose activations
   // fit the GEMV's LDS staging: the GEMV, in chunks of 8.  Otherwise the MFMA
@@ -821,11 +848,14 @@ struct PlanBuilder {
       ph.kind = sdev::PH_GEMM_PRO;
       ph.nblocks = batch;
       ph.xn = xn;
-      push(ph, label + "_pro", 4.0 * batch * L.k * (2 + (L.sub ? 1 : 0) + (L.res_out ? 1 : 0)));
+      adopt_parts(ph.u.gemv);
+      const int sub_reads = ph.u.gemv.sub_part ? ph.u.gemv.sub_ks : (L.sub ? 1 : 0);
+      push(ph, label + "_pro", 4.0 * batch * L.k * (2 + sub_reads + (L.res_out ? 1 : 0)));
       gdev::GemvParams &q = ph.u.gemv;
       q.x = xn;
       q.ldx = L.k;
       q.sub = nullptr;
+      q.sub_part = nullptr;
       q.post_w = nullptr;
       q.res_out = nullptr;
       q.norm = XE_NORM_NONE;

@@ -736,6 +736,26 @@ __global__ __launch_bounds__(kGT) void gemm_ks_kernel(gdev::GemvParams p, float 
     }
     return;
   }
+  if (p.part) {
+    // the consumer adds the splits: this split's raw sums, no counter
+    float *dst = p.part + (static_cast<size_t>(z) * p.batch + b0) * p.m;
+#pragma unroll
+    for (int r = 0; r < RI; r++) {
+      const int it = threadIdx.x + r * kGT;
+      const int bb = it / QN, q = it % QN;
+      if (it >= ITEMS || bb >= nb) continue;
+      const int r0 = m0 + 4 * q;
+      float *d = dst + static_cast<size_t>(bb) * p.m + r0;
+      if ((p.m & 3) == 0 && r0 < p.m) {
+        *reinterpret_cast<float4 *>(d) = make_float4(sum[r][0], sum[r][1], sum[r][2], sum[r][3]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+          if (r0 + i < p.m) d[i] = sum[r][i];
+      }
+    }
+    return;
+  }
   const int tile = blockIdx.y * gridDim.x + blockIdx.x;
   // the partial tile with 16-byte sc1 stores (what an agent-scope atomic
   // store compiles to, four dwords at a time)
@@ -769,6 +789,51 @@ __global__ __launch_bounds__(256) void gemm_prologue_kernel(gdev::GemvParams p, 
   for (int i = threadIdx.x; i < p.k; i += 256) xn[static_cast<size_t>(b) * p.k + i] = xs[gdev::xs_elem<1>(i)];
 }
 
+// `sub` from a GEMM's split partials (GemvParams::sub_part): every split's
+// value in flight at once, added in split order from zero, then the
+// producer's epilogue (scale, bias, output scale), as splitk_finish and
+// epilogue4 would have stored it.
+__device__ __forceinline__ float sub_finish(const gdev::GemvParams &p, int i, float s) {
+  const float sc = p.sub_scale ? p.sub_scale[i] : 1.0f;
+  const float bi = p.sub_bias ? p.sub_bias[i] : 0.0f;
+  return (s * sc + bi) * p.sub_out_scale;
+}
+
+// float4 chunk i4 of stream b
+__device__ __forceinline__ float4 sub_parts4(const gdev::GemvParams &p, int b, int i4) {
+  float4 v[kMaxSplitsK];
+#pragma unroll
+  for (int z = 0; z < kMaxSplitsK; z++)
+    if (z < p.sub_ks)
+      v[z] = reinterpret_cast<const float4 *>(p.sub_part + (static_cast<size_t>(z) * p.batch + b) * p.k)[i4];
+  float s[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int z = 0; z < kMaxSplitsK; z++) {
+    if (z < p.sub_ks) {
+      s[0] += v[z].x;
+      s[1] += v[z].y;
+      s[2] += v[z].z;
+      s[3] += v[z].w;
+    }
+  }
+  const int i = 4 * i4;
+  return make_float4(sub_finish(p, i, s[0]), sub_finish(p, i + 1, s[1]), sub_finish(p, i + 2, s[2]),
+                     sub_finish(p, i + 3, s[3]));
+}
+
+// element i of stream b
+__device__ __forceinline__ float sub_parts1(const gdev::GemvParams &p, int b, int i) {
+  float v[kMaxSplitsK];
+#pragma unroll
+  for (int z = 0; z < kMaxSplitsK; z++)
+    if (z < p.sub_ks) v[z] = p.sub_part[(static_cast<size_t>(z) * p.batch + b) * p.k + i];
+  float s = 0.f;
+#pragma unroll
+  for (int z = 0; z < kMaxSplitsK; z++)
+    if (z < p.sub_ks) s += v[z];
+  return sub_finish(p, i, s);
+}
+
 // The Gemma sandwich-norm prologue (x + post-norm(sub) -> res_out, then the
 // pre-norm) with every operand in registers: x, sub, post_w and gamma arrive
 // in one memory round trip, one block reduction gives both statistics, and
@@ -782,7 +847,7 @@ __global__ __launch_bounds__(256) void gemm_prologue_fold_kernel(gdev::GemvParam
   const int K = p.k, K4 = K / 4;
   const float fk = static_cast<float>(K);
   const float4 *x4 = reinterpret_cast<const float4 *>(static_cast<const float *>(p.x) + static_cast<size_t>(b) * p.ldx);
-  const float4 *s4 = reinterpret_cast<const float4 *>(p.sub + static_cast<size_t>(b) * K);
+  const float4 *s4 = p.sub_part ? nullptr : reinterpret_cast<const float4 *>(p.sub + static_cast<size_t>(b) * K);
   const float4 *w4 = reinterpret_cast<const float4 *>(p.post_w);
   const float4 *g4 = reinterpret_cast<const float4 *>(p.gamma);
   float4 v[NV], sv[NV], w[NV], g[NV];
@@ -791,7 +856,7 @@ __global__ __launch_bounds__(256) void gemm_prologue_fold_kernel(gdev::GemvParam
     const int i = threadIdx.x + j * 256;
     if (i < K4) {
       v[j] = x4[i];
-      sv[j] = s4[i];
+      sv[j] = p.sub_part ? sub_parts4(p, b, i) : s4[i];
       w[j] = w4[i];
       g[j] = g4[i];
     }
@@ -851,6 +916,7 @@ __global__ __launch_bounds__(256) void gemm_prologue_reg_kernel(gdev::GemvParams
   const float *xr = static_cast<const float *>(p.x) + static_cast<size_t>(b) * p.ldx;
   const uint16_t *xh = static_cast<const uint16_t *>(p.x) + static_cast<size_t>(b) * p.ldx;  // bf16 x
   const float *sr = p.sub ? p.sub + static_cast<size_t>(b) * K : nullptr;
+  const bool has_sub = sr || p.sub_part;
   const bool ln = p.norm == XE_NORM_LN;
   float t[NS], sv[NS], g[NS], be[NS];
 #pragma unroll
@@ -859,12 +925,12 @@ __global__ __launch_bounds__(256) void gemm_prologue_reg_kernel(gdev::GemvParams
     t[j] = sv[j] = g[j] = be[j] = 0.f;
     if (i < K) {
       t[j] = p.x_bf16 ? __uint_as_float(static_cast<uint32_t>(xh[i]) << 16) : xr[i];
-      if (sr) sv[j] = sr[i];
+      if (has_sub) sv[j] = p.sub_part ? sub_parts1(p, b, i) : sr[i];
       if (p.norm != XE_NORM_NONE) g[j] = p.gamma[i];
       if (ln) be[j] = p.beta[i];
     }
   }
-  if (sr) {
+  if (has_sub) {
 #pragma unroll
     for (int j = 0; j < NS; j++) {
       const int i = threadIdx.x + j * 256;
@@ -1038,7 +1104,14 @@ GemmShape gemm_ks_shape(int m, int k, int batch) {
 }  // namespace
 
 bool gemm_needs_prologue(const gdev::GemvParams &p) {
-  return p.sub != nullptr || p.norm != XE_NORM_NONE || p.x_bf16;
+  return p.sub != nullptr || p.sub_part != nullptr || p.norm != XE_NORM_NONE || p.x_bf16;
+}
+
+// Splits of K the K-sliced GEMM takes for this shape when it splits (the
+// consumer may then add the partials itself: GemvParams::part), else 0.
+int gemm_defer_splits(int m, int k, int batch) {
+  const GemmShape g = gemm_ks_shape(m, k, batch);
+  return g.mb > 0 && g.ks > 1 ? g.ks : 0;
 }
 
 // The matrix cores take a projection beyond 8 rows, and from
@@ -1063,12 +1136,32 @@ bool gemm_preferred(int m, int k, int batch) {
   return min_batch > 0 && batch >= min_batch && static_cast<long long>(m) * k >= min_w && k % 16 == 0;
 }
 
+namespace {
+// The register prologues: the Gemma fold (x + post-norm(sub), then the
+// norm), and the plain one (optional residual add, then LN / RMS / none).
+// Only these two take `sub` as split partials.
+bool fold_prologue(const gdev::GemvParams &p, const float *xn) {
+  auto al16 = [](const void *q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
+  const float *sub = p.sub_part ? p.sub_part : p.sub;
+  return !p.x_bf16 && sub && p.post_w && p.gamma && (p.norm == XE_NORM_RMS1P || p.norm == XE_NORM_RMS) &&
+         p.k % 4 == 0 && p.ldx % 4 == 0 && p.k <= 4096 && al16(p.x) && al16(sub) && al16(p.post_w) &&
+         al16(p.gamma) && al16(p.res_out) && al16(xn);
+}
+bool reg_prologue(const gdev::GemvParams &p) {
+  const bool has_sub = p.sub || p.sub_part;
+  return !(has_sub && p.post_w) && p.k <= 4096 && (p.norm == XE_NORM_NONE || p.gamma) &&
+         (p.norm != XE_NORM_LN || p.beta);
+}
+}  // namespace
+
+bool gemm_prologue_takes_parts(const gdev::GemvParams &p, const float *xn) {
+  return p.sub_part && p.sub_ks >= 1 && p.sub_ks <= kMaxSplitsK && (fold_prologue(p, xn) || reg_prologue(p));
+}
+
 // Prologue (when the phase has one) into xn, then the GEMM reading xn.
 void launch_gemm_prologue(const gdev::GemvParams &p, float *xn, hipStream_t s) {
-  auto al16 = [](const void *q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
-  if (!p.x_bf16 && p.sub && p.post_w && p.gamma && (p.norm == XE_NORM_RMS1P || p.norm == XE_NORM_RMS) && p.k % 4 == 0 &&
-      p.ldx % 4 == 0 && p.k <= 4096 && al16(p.x) && al16(p.sub) && al16(p.post_w) && al16(p.gamma) &&
-      al16(p.res_out) && al16(xn)) {
+  XE_REQUIRE(!p.sub_part || gemm_prologue_takes_parts(p, xn), "gemm prologue: split partials on an unsupported path");
+  if (fold_prologue(p, xn)) {
     const int nv = (p.k / 4 + 255) / 256;
     auto fn = nv <= 1 ? gemm_prologue_fold_kernel<1> : nv <= 2 ? gemm_prologue_fold_kernel<2>
                                                                 : gemm_prologue_fold_kernel<4>;
@@ -1076,8 +1169,7 @@ void launch_gemm_prologue(const gdev::GemvParams &p, float *xn, hipStream_t s) {
     XE_HIP(hipGetLastError());
     return;
   }
-  if (!(p.sub && p.post_w) && p.k <= 4096 && (p.norm == XE_NORM_NONE || p.gamma) &&
-      (p.norm != XE_NORM_LN || p.beta)) {
+  if (reg_prologue(p)) {
     auto fn = p.k <= 1024 ? gemm_prologue_reg_kernel<4> : p.k <= 2048 ? gemm_prologue_reg_kernel<8>
                                                                        : gemm_prologue_reg_kernel<16>;
     hipLaunchKernelGGL(fn, dim3(p.batch), dim3(256), 0, s, p, xn);
@@ -1119,6 +1211,10 @@ void launch_gemm(const gdev::GemvParams &p, int wdtype, float *ws, unsigned *cnt
   XE_REQUIRE(fn, "gemm: unsupported weight dtype");
   XE_REQUIRE(g.ks == 1 || (ws && cnt && static_cast<size_t>(g.tm) * g.tb <= kGemmMaxTiles),
              "gemm: split-K workspace missing or too many tiles");
+  // partials for the consumer: the split count it was built for
+  XE_REQUIRE(!p.part || (gk.mb > 0 && g.ks > 1 && g.ks == gemm_defer_splits(p.m, p.k, p.batch) &&
+                         p.act == ACT_NONE),
+             "gemm: split partials need the K-sliced kernel with a K split");
   hipLaunchKernelGGL(fn, dim3(g.tm, g.tb, g.ks), dim3(kGT), 0, s, p, ws, cnt, g.spk);
   XE_HIP(hipGetLastError());
 }

@@ -58,6 +58,19 @@ struct GemvParams {
   float out_scale;
   float *y;
   int ldy;
+  // The MFMA GEMM's split-K partials handed to the consumer: with part set
+  // and K split over z, split z stores its raw sums (before scale, bias and
+  // activation) to part[(z * batch + b) * m + r] and no epilogue runs.
+  float *part;
+  // `sub` of a GEMM prologue given as such partials (sub_ks splits): sub[b][i]
+  // = ((sum over z in order of sub_part[(z * batch + b) * k + i]) * sub_scale[i]
+  // + sub_bias[i]) * sub_out_scale, null scale / bias meaning 1 / 0: the
+  // producer's own epilogue, so the values are the ones it would have stored.
+  const float *sub_part;
+  const float *sub_scale;
+  const float *sub_bias;
+  float sub_out_scale;
+  int sub_ks;
 };
 
 // ---- coherent (agent-scope) or plain activation access ----
