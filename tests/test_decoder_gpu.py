@@ -332,6 +332,38 @@ def test_gemm_split_partials_in_prologue(gpu, xe, monkeypatch, family, batch, pr
     assert pro_bytes[1] > pro_bytes[0] > 0, pro_bytes
 
 
+def test_gemma_lmhead_int8_digits(gpu, xe, monkeypatch):
+    """XE_GEMM_I8=1: the 262144-row lm-head at 64 streams on the int8 matrix
+    cores (gemm_i8_kernel): the final norm writes each stream's row as four
+    int8 digit planes of rint(x 2^(30 - E)), the weights are the int8 MFMA
+    operand as stored, the four int32 sums combine exactly in fp64.  Forced
+    steps on the real Gemma-3-1B shape (2 layers): logits within the oracle's
+    bar, and not bit-equal to the bf16-plane path (the digit path ran)."""
+    dev, _ = gpu
+    cfg = xe.GEMMA3_1B.replace(n_layers=2, max_ctx=64)
+    batch = 64
+    print("[case] gemma lm-head int8 digits b=%d" % batch, flush=True)
+    om = O.OracleModel(oracle_cfg(cfg), 6, batch)
+    rng = np.random.default_rng(8)
+    toks = rng.integers(0, cfg.vocab, (3, batch)).astype(np.int32)
+    outs = []
+    for flag in ("1", "0"):
+        monkeypatch.setenv("XE_GEMM_I8", flag)
+        dec = xe.Decoder(dev, cfg, max_batch=batch)
+        dec.init_synthetic(6)
+        outs.append(np.stack([dec.step(toks[i], np.full(batch, i, np.int32))[0].copy() for i in range(3)]))
+        dec.close()
+    monkeypatch.delenv("XE_GEMM_I8", raising=False)
+    om.reset()
+    for i in range(3):
+        want = om.step(toks[i], np.full(batch, i, np.int32))
+        # the bars of the bf16 path at this depth and batch (test_long_gpu.py B64_DEPTHS)
+        compare_logits(outs[0][i], want, "gemma-lmhead-i8-pos%d" % i, rel_l2=5e-4, atol=5e-3)
+    assert not np.array_equal(outs[0], outs[1])
+    assert np.abs(outs[0] - outs[1]).max() < 1e-4
+    om.close()
+
+
 def test_tiny_gemma_b64(gpu, xe):
     """64 streams (the config-5 batch) on the tiny Gemma shape."""
     cfg = tiny(xe, xe.XE_GEMMA3, xe.XE_I8)

@@ -361,6 +361,8 @@ struct xe_decoder {
   float *xn = nullptr;  // GEMM path: normalised activations [max_batch][max K]
   float *gemm_ws = nullptr;  // GEMM split-K partials
   unsigned *gemm_cnt = nullptr;  // GEMM split-K counters (zeroed once, self-resetting)
+  int8_t *gemm_xd = nullptr;     // int8 digit planes of a prologue's rows (the int8-MFMA GEMM)
+  int *gemm_xe = nullptr;        // their per-stream exponents
   uint16_t *kc = nullptr, *vc = nullptr;  // [L][B][hkv][max_ctx][hd]
   float *rope_cos = nullptr, *rope_sin = nullptr;
   int32_t *tokens = nullptr, *pos = nullptr, *next = nullptr, *hist = nullptr;
@@ -601,6 +603,8 @@ void alloc_decoder(xe_decoder *d) {
     d->gemm_ws = dalloc<float>(gemm_ws_floats(), s);
     d->gemm_cnt = dalloc<unsigned>(gemm_cnt_words(), s);
     XE_HIP(hipMemsetAsync(d->gemm_cnt, 0, gemm_cnt_words() * sizeof(unsigned), s));
+    d->gemm_xd = dalloc<int8_t>(static_cast<size_t>(4) * B * D, s);
+    d->gemm_xe = dalloc<int>(B, s);
   }
   const size_t kvn = d->kv_layer_elems() * c.n_layers;
   d->kc = dalloc<uint16_t>(kvn, s);
@@ -698,6 +702,7 @@ void free_decoder(xe_decoder *d) {
                   static_cast<void *>(d->stop_dev), static_cast<void *>(d->arg_v), static_cast<void *>(d->arg_i),
                   static_cast<void *>(d->attn_work), static_cast<void *>(d->xn),
                   static_cast<void *>(d->gemm_ws), static_cast<void *>(d->gemm_cnt),
+                  static_cast<void *>(d->gemm_xd), static_cast<void *>(d->gemm_xe),
                   static_cast<void *>(d->attn_cnt)})
     if (p) (void)hipFree(p);
   if (d->host_tok) (void)hipHostFree(d->host_tok);
@@ -738,6 +743,9 @@ struct PlanBuilder {
   float *xn = nullptr;  // GEMM path scratch (null: GEMV only)
   float *ws = nullptr;
   unsigned *cnt = nullptr;
+  int8_t *xd = nullptr;  // digit planes (4 x batch x K bytes, K <= xd_k) and exponents
+  int *xe = nullptr;
+  int xd_k = 0;
   int last_gemm = -1;  // the last phase pushed, when it is a GEMM
   void push(const sdev::Phase &ph, const std::string &label, double bytes) {
     plan.phases.push_back(ph);
@@ -849,6 +857,14 @@ struct PlanBuilder {
       ph.nblocks = batch;
       ph.xn = xn;
       adopt_parts(ph.u.gemv);
+      // int8 weights too wide for the K-sliced kernel (the lm-head): the
+      // prologue writes the rows' int8 digit planes for the int8 matrix cores
+      if (xd && L.k <= xd_k && gemm_i8_preferred(L.m, L.k, batch, L.wdtype)) {
+        gdev::GemvParams t = ph.u.gemv;
+        t.xd = xd;
+        t.xe = xe;
+        if (gemm_prologue_takes_digits(t, xn)) ph.u.gemv = t;
+      }
       const int sub_reads = ph.u.gemv.sub_part ? ph.u.gemv.sub_ks : (L.sub ? 1 : 0);
       push(ph, label + "_pro", 4.0 * batch * L.k * (2 + sub_reads + (L.res_out ? 1 : 0)));
       gdev::GemvParams &q = ph.u.gemv;
@@ -892,7 +908,7 @@ void build_plan(xe_decoder *d, int B, xe_decoder::Plan &plan) {
   const bool gem = c.family == XE_GEMMA3, wh = c.family == XE_WHISPER, opt = c.family == XE_OPT;
   const int nq = static_cast<int>(d->nqkv());
   const int norm = gem ? XE_NORM_RMS1P : XE_NORM_LN;
-  PlanBuilder pb{plan, d->gemm_ws ? d->xn : nullptr, d->gemm_ws, d->gemm_cnt};
+  PlanBuilder pb{plan, d->gemm_ws ? d->xn : nullptr, d->gemm_ws, d->gemm_cnt, d->gemm_xd, d->gemm_xe, c.d_model};
   // the split attention kernel merges in place (arrival counters)
   unsigned *attn_cnt = d->attn_cnt;
 

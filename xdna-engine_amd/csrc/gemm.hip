@@ -420,6 +420,123 @@ __global__ __launch_bounds__(kGT) __attribute__((amdgpu_waves_per_eu(2))) void g
   splitk_finish<WT, BM>(p, ws, cnt, tile, ks, nb, m0, b0, last);
 }
 
+// ---- int8 weights x int8 digit planes on v_mfma_i32_16x16x64_i8 ----
+//
+// For int8 weights whose activations come out of a GEMM prologue (the norm
+// in front of the lm-head): the prologue writes each stream's row as four
+// signed base-256 digit planes of rint(x 2^(30 - E)) (GemvParams::xd / xe),
+// so that
+//   sum_k W[m][k] x[k] = 2^(E - 30) (C0 2^24 + C1 2^16 + C2 2^8 + C3),
+//   C_d = sum_k W[m][k] d_k[k]   (exact in int32: |W| <= 127, |d| <= 128).
+// The int8 weights are the MFMA A operand as stored (no conversion) and each
+// digit plane a B operand: 4 MFMAs a 16 x 16 x 64 block, against 6 for the
+// three bf16 parts of the fp32 path.  The four sums combine exactly in fp64
+// and round once to fp32: the exact dot product of x rounded to 2^(E - 31),
+// i.e. to 2^-30 of the stream's largest |x| (fp32 itself keeps 2^-24 of each
+// element).  Workgroup: 8 waves of 32 weight rows (two 16-row blocks) x 64
+// streams, K in steps of 64 whose digit planes are staged in LDS
+// (double-buffered, one barrier a step); the next step's weights and digits
+// are loaded before the current step's MFMAs.
+constexpr int kI8MB = 2;   // 16-row blocks a wave
+constexpr int kI8W = 8;    // waves a workgroup
+constexpr int kI8T = 64 * kI8W;
+constexpr int kI8XS = 80;  // LDS row stride (bytes) of a staged 64-k digit row: conflict-free 16-byte reads
+
+__global__ __launch_bounds__(kI8T) __attribute__((amdgpu_waves_per_eu(2))) void gemm_i8_kernel(gdev::GemvParams p) {
+  typedef int i32x4 __attribute__((ext_vector_type(4)));
+  typedef int i32x2 __attribute__((ext_vector_type(2)));
+  constexpr int MB = kI8MB, BM = 16 * kI8W * MB;
+  __shared__ __attribute__((aligned(16))) int8_t xs[2][4][kBN * kI8XS];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int m0 = blockIdx.x * BM, b0 = blockIdx.y * kBN;
+  const int K = p.k;
+  const int nsteps = (K + 63) / 64;
+  const int nb = min(kBN, p.batch - b0);
+  const __amdgpu_buffer_rsrc_t rw = gdev::coherent_rsrc(p.w);
+  const __amdgpu_buffer_rsrc_t rx = gdev::coherent_rsrc(p.xd);
+  // A operand: this lane's rows (one a row block), k 16 (lane / 16) .. + 16
+  // of the step; B operand: stream lane % 16 of a block, the same k
+  const int wbase = m0 + wave * 16 * MB + (lane & 15);
+  const int wk = 16 * (lane >> 4);
+  // staging: thread t -> stream t / 8, k 8 (t % 8) .. + 8, all four planes
+  const int srow = threadIdx.x >> 3, sk = 8 * (threadIdx.x & 7);
+  const int plane = p.batch * K;
+  struct Stage {
+    i32x4 w[MB];
+    i32x2 x[4];
+  };
+  auto issue = [&](int step, Stage &st) {
+    const int k0 = step * 64;
+    const bool xok = srow < nb && k0 + sk < K;
+#pragma unroll
+    for (int d = 0; d < 4; d++)
+      st.x[d] = __builtin_bit_cast(
+          i32x2, __builtin_amdgcn_raw_buffer_load_b64(rx, xok ? d * plane + (b0 + srow) * K + k0 + sk : kNoRec, 0, 0));
+#pragma unroll
+    for (int mb = 0; mb < MB; mb++) {
+      const int row = wbase + 16 * mb;
+      st.w[mb] = __builtin_bit_cast(
+          i32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, row < p.m && k0 + wk < K ? row * K + k0 + wk : kNoRec, 0, 2));
+    }
+  };
+  i32x4 acc[MB][4][4];
+#pragma unroll
+  for (int mb = 0; mb < MB; mb++)
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+#pragma unroll
+      for (int d = 0; d < 4; d++) acc[mb][j][d] = i32x4{0, 0, 0, 0};
+  // step s stages into buffer s & 1 and reads it after one barrier (a wave
+  // writes buffer s & 1 only after the barrier of step s - 1, which every
+  // wave reaches after its reads of step s - 2)
+  auto compute = [&](int step, const Stage &st) {
+    int8_t(*xb)[kBN * kI8XS] = xs[step & 1];
+#pragma unroll
+    for (int d = 0; d < 4; d++) *reinterpret_cast<i32x2 *>(&xb[d][srow * kI8XS + sk]) = st.x[d];
+    __syncthreads();
+#pragma unroll
+    for (int d = 0; d < 4; d++) {
+      i32x4 bx[4];
+#pragma unroll
+      for (int j = 0; j < 4; j++) bx[j] = *reinterpret_cast<const i32x4 *>(&xb[d][(16 * j + (lane & 15)) * kI8XS + wk]);
+#pragma unroll
+      for (int j = 0; j < 4; j++)
+#pragma unroll
+        for (int mb = 0; mb < MB; mb++)
+          acc[mb][j][d] = __builtin_amdgcn_mfma_i32_16x16x64_i8(st.w[mb], bx[j], acc[mb][j][d], 0, 0, 0);
+    }
+  };
+  Stage s0, s1;
+  issue(0, s0);
+  int s = 0;
+  for (; s + 2 <= nsteps; s += 2) {
+    issue(s + 1, s1);
+    compute(s, s0);
+    issue(s + 2, s0);
+    compute(s + 1, s1);
+  }
+  if (s < nsteps) compute(s, s0);
+  // lane holds rows rl + i (i = 0..3) of stream 16 j + lane % 16
+#pragma unroll
+  for (int mb = 0; mb < MB; mb++) {
+    const int rl = wave * 16 * MB + 16 * mb + 4 * (lane >> 4);
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int b = 16 * j + (lane & 15);
+      if (b >= nb) continue;
+      const int E = p.xe[b0 + b];
+      float a4[4];
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const double sum = ((static_cast<double>(acc[mb][j][0][i]) * 256.0 + static_cast<double>(acc[mb][j][1][i])) * 256.0 +
+                            static_cast<double>(acc[mb][j][2][i])) * 256.0 + static_cast<double>(acc[mb][j][3][i]);
+        a4[i] = static_cast<float>(ldexp(sum, E - 30));
+      }
+      epilogue4(p, XE_I8, m0 + rl, b0 + b, a4);
+    }
+  }
+}
+
 // ---- K-sliced GEMM: no LDS staging inside the K loop ----
 //
 // Workgroup tile: 64 weight rows x 64 streams, K in steps of 128.  Wave w
@@ -834,6 +951,52 @@ __device__ __forceinline__ float sub_parts1(const gdev::GemvParams &p, int b, in
   return sub_finish(p, i, s);
 }
 
+// ---- int8 digit planes of a normalised row (GemvParams::xd / xe) ----
+// Block maximum over the prologue's 256 threads; mx: 4 floats of LDS.
+__device__ __forceinline__ float block_max256(float v, float *mx) {
+  v = gdev::wave_max(v);
+  if ((threadIdx.x & 63) == 0) mx[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return fmaxf(fmaxf(mx[0], mx[1]), fmaxf(mx[2], mx[3]));
+}
+
+// The exponent E with every |x| < 2^E given the row's largest |x| (0 for
+// a zero row).
+__device__ __forceinline__ int digit_exp(float amax) {
+  int e = 0;
+  if (amax > 0.f) (void)frexpf(amax, &e);
+  return e;
+}
+
+// Four signed base-256 digits of rint(v 2^(30 - E)) (|v| < 2^E, so the
+// integer is at most 2^30): d3 the low byte read as signed, then d2, d1 of
+// what remains, and d0 (at most 64 in magnitude).
+__device__ __forceinline__ void digits_of(float v, int E, int (&d)[4]) {
+  const int xi = __float2int_rn(__builtin_ldexpf(v, 30 - E));
+  d[3] = static_cast<int8_t>(xi & 0xff);
+  int r = (xi - d[3]) >> 8;
+  d[2] = static_cast<int8_t>(r & 0xff);
+  r = (r - d[2]) >> 8;
+  d[1] = static_cast<int8_t>(r & 0xff);
+  d[0] = (r - d[1]) >> 8;
+}
+
+// Elements i .. i + 3 of stream b (i a multiple of 4): one 4-byte store a plane.
+__device__ __forceinline__ void put_digits4(const gdev::GemvParams &p, int b, int i, const float (&v)[4], int E) {
+  uint32_t w[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int c = 0; c < 4; c++) {
+    int d[4];
+    digits_of(v[c], E, d);
+#pragma unroll
+    for (int q = 0; q < 4; q++) w[q] |= (static_cast<uint32_t>(d[q]) & 0xffu) << (8 * c);
+  }
+  const size_t plane = static_cast<size_t>(p.batch) * p.k;
+#pragma unroll
+  for (int q = 0; q < 4; q++)
+    *reinterpret_cast<uint32_t *>(p.xd + q * plane + static_cast<size_t>(b) * p.k + i) = w[q];
+}
+
 // The Gemma sandwich-norm prologue (x + post-norm(sub) -> res_out, then the
 // pre-norm) with every operand in registers: x, sub, post_w and gamma arrive
 // in one memory round trip, one block reduction gives both statistics, and
@@ -883,6 +1046,8 @@ __global__ __launch_bounds__(256) void gemm_prologue_fold_kernel(gdev::GemvParam
   const float st2 = acc[1] + 2.0f * inv_s * acc[2] + inv_s * inv_s * acc[3];
   const float inv_t = 1.0f / sqrtf(fmaxf(st2, 0.f) / fk + p.eps);
   const bool one_p = p.norm == XE_NORM_RMS1P;
+  float h[NV][4];
+  float amax = 0.f;
 #pragma unroll
   for (int j = 0; j < NV; j++) {
     const int i = threadIdx.x + j * 256;
@@ -891,15 +1056,27 @@ __global__ __launch_bounds__(256) void gemm_prologue_fold_kernel(gdev::GemvParam
     const float su[4] = {sv[j].x, sv[j].y, sv[j].z, sv[j].w};
     const float wv[4] = {w[j].x, w[j].y, w[j].z, w[j].w};
     const float gv[4] = {g[j].x, g[j].y, g[j].z, g[j].w};
-    float t[4], h[4];
+    float t[4];
 #pragma unroll
     for (int c = 0; c < 4; c++) {
       t[c] = xv[c] + su[c] * inv_s * (1.0f + wv[c]);
-      h[c] = one_p ? t[c] * inv_t * (1.0f + gv[c]) : t[c] * inv_t * gv[c];
+      h[j][c] = one_p ? t[c] * inv_t * (1.0f + gv[c]) : t[c] * inv_t * gv[c];
+      amax = fmaxf(amax, fabsf(h[j][c]));
     }
     if (p.res_out)
       reinterpret_cast<float4 *>(p.res_out + static_cast<size_t>(b) * K)[i] = make_float4(t[0], t[1], t[2], t[3]);
-    reinterpret_cast<float4 *>(xn + static_cast<size_t>(b) * K)[i] = make_float4(h[0], h[1], h[2], h[3]);
+    if (!p.xd)
+      reinterpret_cast<float4 *>(xn + static_cast<size_t>(b) * K)[i] = make_float4(h[j][0], h[j][1], h[j][2], h[j][3]);
+  }
+  if (p.xd) {
+    __shared__ float mx[4];
+    const int E = digit_exp(block_max256(amax, mx));
+    if (threadIdx.x == 0) p.xe[b] = E;
+#pragma unroll
+    for (int j = 0; j < NV; j++) {
+      const int i = threadIdx.x + j * 256;
+      if (i < K4) put_digits4(p, b, 4 * i, h[j], E);
+    }
   }
 }
 
@@ -968,6 +1145,26 @@ __global__ __launch_bounds__(256) void gemm_prologue_reg_kernel(gdev::GemvParams
 #pragma unroll
     for (int j = 0; j < NS; j++)
       t[j] = p.norm == XE_NORM_RMS1P ? t[j] * inv * (1.0f + g[j]) : t[j] * inv * g[j];
+  }
+  if (p.xd) {
+    __shared__ float mx[4];
+    float amax = 0.f;
+#pragma unroll
+    for (int j = 0; j < NS; j++)
+      if (threadIdx.x + j * 256 < K) amax = fmaxf(amax, fabsf(t[j]));
+    const int E = digit_exp(block_max256(amax, mx));
+    if (threadIdx.x == 0) p.xe[b] = E;
+    const size_t plane = static_cast<size_t>(p.batch) * K;
+#pragma unroll
+    for (int j = 0; j < NS; j++) {
+      const int i = threadIdx.x + j * 256;
+      if (i >= K) continue;
+      int d[4];
+      digits_of(t[j], E, d);
+#pragma unroll
+      for (int q = 0; q < 4; q++) p.xd[q * plane + static_cast<size_t>(b) * K + i] = static_cast<int8_t>(d[q]);
+    }
+    return;
   }
 #pragma unroll
   for (int j = 0; j < NS; j++) {
@@ -1107,6 +1304,21 @@ bool gemm_needs_prologue(const gdev::GemvParams &p) {
   return p.sub != nullptr || p.sub_part != nullptr || p.norm != XE_NORM_NONE || p.x_bf16;
 }
 
+// int8 weights on the int8 matrix cores (gemm_i8_kernel) for outputs too wide
+// for the K-sliced kernel (the lm-head), when the activations come out of a
+// prologue that can write the digit planes: with XE_GEMM_I8=1 only.  At the
+// Gemma-3-1B lm-head (262144 x 1152, 64 streams) it measured 167 us against
+// 160 us for the bf16 path (one box, A/B; 4 waves x 32 rows at one or two
+// waves a SIMD: 197 / 168 us): neither kernel is bound by its matrix cores,
+// and the per-step staging of four digit planes costs what the 1.5x fewer
+// MFMAs save.
+bool gemm_i8_preferred(int m, int k, int batch, int wdtype) {
+  const char *e = std::getenv("XE_GEMM_I8");
+  if (!(e && std::string(e) == "1")) return false;
+  return wdtype == XE_I8 && k % 16 == 0 && gemm_ks_shape(m, k, batch).mb == 0 &&
+         static_cast<long long>(batch) * k * 4 < (1LL << 31);
+}
+
 // Splits of K the K-sliced GEMM takes for this shape when it splits (the
 // consumer may then add the partials itself: GemvParams::part), else 0.
 int gemm_defer_splits(int m, int k, int batch) {
@@ -1154,6 +1366,10 @@ bool reg_prologue(const gdev::GemvParams &p) {
 }
 }  // namespace
 
+bool gemm_prologue_takes_digits(const gdev::GemvParams &p, const float *xn) {
+  return p.xd && p.xe && p.k % 4 == 0 && (fold_prologue(p, xn) || reg_prologue(p));
+}
+
 bool gemm_prologue_takes_parts(const gdev::GemvParams &p, const float *xn) {
   return p.sub_part && p.sub_ks >= 1 && p.sub_ks <= kMaxSplitsK && (fold_prologue(p, xn) || reg_prologue(p));
 }
@@ -1161,6 +1377,7 @@ bool gemm_prologue_takes_parts(const gdev::GemvParams &p, const float *xn) {
 // Prologue (when the phase has one) into xn, then the GEMM reading xn.
 void launch_gemm_prologue(const gdev::GemvParams &p, float *xn, hipStream_t s) {
   XE_REQUIRE(!p.sub_part || gemm_prologue_takes_parts(p, xn), "gemm prologue: split partials on an unsupported path");
+  XE_REQUIRE(!p.xd || gemm_prologue_takes_digits(p, xn), "gemm prologue: digit planes on an unsupported path");
   if (fold_prologue(p, xn)) {
     const int nv = (p.k / 4 + 255) / 256;
     auto fn = nv <= 1 ? gemm_prologue_fold_kernel<1> : nv <= 2 ? gemm_prologue_fold_kernel<2>
@@ -1199,6 +1416,15 @@ void launch_gemm(const gdev::GemvParams &p, int wdtype, float *ws, unsigned *cnt
   const size_t wb = static_cast<size_t>(p.m) * p.k * (wdtype == XE_BF16 ? 2 : 1);
   XE_REQUIRE(wb < (size_t(1) << 31) && static_cast<size_t>(p.batch) * p.ldx * 4 < (size_t(1) << 31),
              "gemm: operand above 2 GB");
+  if (p.xd) {  // int8 digit planes of the activations: the int8 matrix cores
+    XE_REQUIRE(wdtype == XE_I8 && p.xe && p.act != ACT_GEGLU_TANH && !p.part,
+               "gemm: digit planes need int8 weights and a plain epilogue");
+    XE_REQUIRE(static_cast<long long>(p.batch) * p.k * 4 < (1LL << 31), "gemm: digit planes above 2 GB");
+    const int bm = 16 * kI8W * kI8MB;
+    hipLaunchKernelGGL(gemm_i8_kernel, dim3((p.m + bm - 1) / bm, (p.batch + kBN - 1) / kBN), dim3(kI8T), 0, s, p);
+    XE_HIP(hipGetLastError());
+    return;
+  }
   GemmShape g = gemm_shape(p.m, p.k, p.batch);
   GemmFn fn = nullptr;
   const GemmShape gk = gemm_ks_shape(p.m, p.k, p.batch);

@@ -71,6 +71,13 @@ struct GemvParams {
   const float *sub_bias;
   float sub_out_scale;
   int sub_ks;
+  // int8 digit planes of the normalised activations (the int8-MFMA GEMM):
+  // a GEMM prologue writes them when xd is set, the GEMM reads them instead
+  // of x.  Stream b's row is x = 2^(xe[b] - 30) (d0 2^24 + d1 2^16 + d2 2^8
+  // + d3), plane d at xd[(d * batch + b) * k + i], xe[b] the exponent with
+  // every |x| < 2^xe[b].
+  int8_t *xd;
+  int *xe;
 };
 
 // ---- coherent (agent-scope) or plain activation access ----

@@ -199,6 +199,8 @@ void launch_phase(const sdev::Phase &ph, hipStream_t s);
 // gemm.hip
 bool gemm_needs_prologue(const gdev::GemvParams &p);
 int gemm_defer_splits(int m, int k, int batch);
+bool gemm_i8_preferred(int m, int k, int batch, int wdtype);
+bool gemm_prologue_takes_digits(const gdev::GemvParams &p, const float *xn);
 bool gemm_prologue_takes_parts(const gdev::GemvParams &p, const float *xn);
 void launch_gemm_prologue(const gdev::GemvParams &p, float *xn, hipStream_t s);
 void launch_gemm(const gdev::GemvParams &p, int wdtype, float *ws, unsigned *cnt, hipStream_t s);
