@@ -175,7 +175,8 @@ def run_batch(xe, dev, cfg, args, B, steps, warmup, profile):
     rng = np.random.default_rng(args.seed)
     prompt = rng.integers(0, cfg.vocab, (B, args.prompt)).astype(np.int32)
     dec.feed(prompt)
-    room = args.ctx - args.prompt - (1 if profile else 0)  # one profiled step at the end
+    reps = max(1, args.profile_reps) if profile else 0
+    room = args.ctx - args.prompt - reps  # the profiled steps at the end
     W = min(warmup, room)
     K = steps if steps > 0 else room - W
     if W + K > room:
@@ -197,11 +198,18 @@ def run_batch(xe, dev, cfg, args, B, steps, warmup, profile):
     prof_pos = last + 1
     if profile and executor != "ll":
         # the phase kernels' profiled step runs at the timed region's mean
-        # position: every stream's cache primed (synthetic bf16 rows) to it
-        prof_pos = int(round(mean_ctx)) - 1
+        # position (or --profile-pos): every stream's cache primed (synthetic
+        # bf16 rows) to it
+        prof_pos = args.profile_pos if args.profile_pos > 0 else int(round(mean_ctx)) - 1
+        if prof_pos + reps > args.ctx:
+            sys.exit("bench.py: --profile-pos + --profile-reps exceed the context")
         for b in range(B):
             dec.prime_kv(b, prof_pos, 7000 + b)
-    prof = dec.profile_step() if profile else []
+    # --profile-reps steps, each an event after every launch; per-step means
+    prof = []
+    for _ in range(reps):
+        prof += dec.profile_step()
+    prof = [(l, u / reps, b / reps) for l, u, b in prof]
     by_label = {}
     for l, u, b in prof:
         e = by_label.setdefault(l, [0, 0.0, 0.0])
@@ -258,7 +266,7 @@ def run_batch(xe, dev, cfg, args, B, steps, warmup, profile):
                      "traffic": (LL_TRAFFIC_BYTES_PER_STEP if executor == "ll" and B == 1 and
                                  args.prompt == 512 and args.ctx == 4096 and args.steps == 0 else
                                  B64_GEMM_TRAFFIC_BYTES_PER_STEP if B == 64 and r_kernel.startswith("gemm_ks") and
-                                 args.prompt == 512 and args.ctx == 4096 else None),
+                                 args.prompt == 512 and args.ctx == 4096 and args.profile_pos == 0 else None),
                      "traffic_unit": "bytes per step",
                      "bytes": int(r_bytes), "us": round(r_us, 2)},
     }
@@ -266,7 +274,7 @@ def run_batch(xe, dev, cfg, args, B, steps, warmup, profile):
         # per-phase device time of one traced step at the end context (the
         # low-latency kernel's phases overlap loads staged by earlier phases,
         # so no per-phase bandwidth is derived from them)
-        res["phases"] = {l: {"launches": v[0], "us": round(v[1], 2)}
+        res["phases"] = {l: {"launches": v[0] // reps, "us": round(v[1], 2)}
                          for l, v in by_label.items()}
     dec.close()
     print("[bench] b=%d: %.1f tok/s, %.3f ms/step (%s)" % (B, tok_s, step_s * 1e3, executor),
@@ -522,6 +530,11 @@ def main():
     ap.add_argument("--eager", action="store_true",
                     help="--kernels with plain launches instead of graph replays (for runs under "
                          "rocprofv3's kernel trace, which has crashed on graph launches here)")
+    ap.add_argument("--profile-reps", type=int, default=1,
+                    help="profiled steps after the timed region (per-step means are reported)")
+    ap.add_argument("--profile-pos", type=int, default=0,
+                    help="position of the phase kernels' profiled steps (caches primed to it; "
+                         "0: the timed region's mean context)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build runs on one GPU only (every GPU box here has one); "
