@@ -1231,7 +1231,9 @@ void plan_stage(std::vector<ll::Phase> &list, int ranks, int wt, long budget, in
     ll::GemvD &g = list[j].u.gemv;
     const int at = last + 1;
     if (!g.in_vec || at >= j) continue;  // input from the previous phase; an earlier phase to ride on
-    const int unit = g.act == ACT_GEGLU_TANH ? 2 : 1;
+    // the kernel's row split (ll_kernel.h: GeGLU pairs, and activations kept
+    // in LDS for the split FFN output on multiples of four of them)
+    const int unit = (g.act == ACT_GEGLU_TANH ? 2 : 1) * (g.out_lds ? 4 : 1);
     const int rows = (g.m / unit + ranks - 1) / ranks * unit;
     const int need = ll::stage_layout(wt, rows, g.k, g.bias != nullptr).total;
     if (need > budget) continue;
