@@ -164,17 +164,21 @@ __device__ __forceinline__ void head_transform(const AttnParams &p, const float 
 
 // A lane's eight elements of one key row, loaded raw (16 bytes of bf16 or 8
 // of int8) and converted at use, so the loads of a block stay in flight
-// while earlier keys compute.
+// while earlier keys compute.  The rows are read once a step: nontemporal
+// loads (a 168 MB stream over 256 workgroups: 24.9 against 27.9 us with
+// plain loads; b = 64 decode +1.3 %).
 template <bool I8>
 struct Raw8 {
   uint32_t w[I8 ? 2 : 4];
   __device__ __forceinline__ void load(const uint16_t *base, size_t elem) {
     if constexpr (I8) {
-      const uint2 v = *reinterpret_cast<const uint2 *>(reinterpret_cast<const int8_t *>(base) + elem);
+      typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+      const u32x2 v =
+          __builtin_nontemporal_load(reinterpret_cast<const u32x2 *>(reinterpret_cast<const int8_t *>(base) + elem));
       w[0] = v.x;
       w[1] = v.y;
     } else {
-      const uint4 v = *reinterpret_cast<const uint4 *>(base + elem);
+      const gdev::u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const gdev::u32x4 *>(base + elem));
       w[0] = v.x;
       w[1] = v.y;
       w[2] = v.z;

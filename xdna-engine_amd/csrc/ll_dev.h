@@ -956,6 +956,127 @@ __device__ __forceinline__ bool gemv_any(const GD &g, int nb, int r0, int r1, co
   return gemv_rows<WT, NB, HEAD>(g, nb, r0, r1, xs, ep, prep, logits, vocab, last_max, best, tsub, stage, staged,
                                  kred, lout, lout_ld);
 }
+
+// The lm-head slice with its tiles pipelined: tile t + 1's weight chunks are
+// requested before tile t's dot products, so the weight stream does not stop
+// for a memory round trip at every tile (gemv_rows issues a tile's loads only
+// after the previous tile is done).  For a head whose rows take one load
+// round (n_it <= NIT chunk iterations a lane).  One row a lane group (gemv_rows
+// takes two), so the two tiles in flight hold the registers of one of its
+// tiles: more would raise the step kernel's spills around this call.  Each
+// row's arithmetic is gemv_rows' HEAD path (same chunks in the same order,
+// the same lane sums, scale and tie rule), so the logits and the argmax are
+// bit-identical to it.  The tied head has no bias.  Tiles past the slice
+// load zeros (rows past r1 read nothing).
+template <int WT>
+__host__ __device__ constexpr bool head_one_round(int k, int lpr) {
+  return (k / 16 + lpr - 1) / lpr <= Round<WT>::NIT;
+}
+
+template <int WT, int NB, typename GD, typename Prep>
+__device__ __forceinline__ bool head_rows(const GD &g, int nb, int r0, int r1, const float *xs, Prep prep,
+                                          float *logits, int vocab, int last_max, ArgBest &best) {
+  using gdev::Chunk;
+  constexpr int RPL = 1;
+  constexpr int NIT = Round<WT>::NIT;
+  const int lpr_log = __builtin_ctz(static_cast<unsigned>(g.lpr));
+  const int LPR = 1 << lpr_log;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int rg = lane >> lpr_log, kl = lane & (LPR - 1);
+  const int rows_per_wave = (64 >> lpr_log) * RPL;
+  const int rows_per_tile = kW * rows_per_wave;
+  const int K = g.k, nch = K / 16;
+  const int n_it = (nch + LPR - 1) >> lpr_log;
+  const int ntiles = r1 > r0 ? (r1 - r0 + rows_per_tile - 1) / rows_per_tile : 0;
+  if (ntiles == 0) return prep();
+  WRsrc rs;
+  rs.w = gdev::coherent_rsrc(g.w);
+  rs.e = gdev::coherent_rsrc(WT == XE_BFP16 ? static_cast<const void *>(g.exps) : g.w);
+  struct TileW {
+    Chunk<WT> w[NIT][RPL];
+    float scale[RPL];
+  };
+  auto first_row = [&](int tile) { return r0 + tile * rows_per_tile + wave * rows_per_wave + rg * RPL; };
+  auto load_tile = [&](int tile, TileW &t) {
+    const int row0 = first_row(tile);
+#pragma unroll
+    for (int u = 0; u < NIT; u++) {
+      const int cc = (u << lpr_log) + kl;
+      const bool valid = u < n_it && cc < nch;
+#pragma unroll
+      for (int i = 0; i < RPL; i++) load_chunk_buf<WT>(rs, row0 + i, K, cc, valid && row0 + i < r1, t.w[u][i]);
+    }
+#pragma unroll
+    for (int i = 0; i < RPL; i++) t.scale[i] = WT == XE_I8 ? gptr(g.scale)[row0 + i < r1 ? row0 + i : r0] : 1.0f;
+  };
+  auto compute_tile = [&](int tile, const TileW &t) {
+    const int row0 = first_row(tile);
+    float acc4[NB][RPL][4];
+#pragma unroll
+    for (int b = 0; b < NB; b++)
+#pragma unroll
+      for (int i = 0; i < RPL; i++)
+#pragma unroll
+        for (int q = 0; q < 4; q++) acc4[b][i][q] = 0.f;
+#pragma unroll
+    for (int u = 0; u < NIT; u++) {
+      if (u < n_it) {
+        const int cx = min((u << lpr_log) + kl, nch - 1);
+#pragma unroll
+        for (int b = 0; b < NB; b++) {
+          typedef float f32x4 __attribute__((ext_vector_type(4)));
+          float4 xv[4];
+          const XE_LDS f32x4 *xr =
+              reinterpret_cast<const XE_LDS f32x4 *>(lptr(xs) + static_cast<size_t>(b) * xstride(K) + cx * 20);
+#pragma unroll
+          for (int j = 0; j < 4; j++) {
+            const f32x4 v = xr[j];
+            xv[j] = make_float4(v.x, v.y, v.z, v.w);
+          }
+#pragma unroll
+          for (int i = 0; i < RPL; i++) chunk_dot4<WT>(t.w[u][i], xv, acc4[b][i]);
+        }
+      }
+    }
+    float flat[NB * RPL];
+#pragma unroll
+    for (int b = 0; b < NB; b++)
+#pragma unroll
+      for (int i = 0; i < RPL; i++)
+        flat[b * RPL + i] = (acc4[b][i][0] + acc4[b][i][1]) + (acc4[b][i][2] + acc4[b][i][3]);
+    gdev::group_sums<NB * RPL>(flat, lpr_log);
+    if (kl == 0) {
+#pragma unroll
+      for (int b = 0; b < NB; b++) {
+        if (b >= nb) break;
+#pragma unroll
+        for (int i = 0; i < RPL; i++) {
+          const int row = row0 + i;
+          if (row >= r1) continue;
+          float v = flat[b * RPL + i];
+          if (WT == XE_I8) v = v * t.scale[i];
+          if (logits) gptr_w(logits)[static_cast<size_t>(b) * vocab + row] = v;
+          if (sdev::better(v, row, best.v[b], best.i[b], last_max)) {
+            best.v[b] = v;
+            best.i[b] = row;
+          }
+        }
+      }
+    }
+  };
+  TileW ta, tb;
+  load_tile(0, ta);
+  if (!prep()) return false;  // the final norm overlaps the first tile's loads
+  for (int tile = 0; tile < ntiles; tile += 2) {
+    load_tile(tile + 1, tb);
+    compute_tile(tile, ta);
+    if (tile + 1 >= ntiles) break;
+    load_tile(tile + 2, ta);
+    compute_tile(tile + 1, tb);
+  }
+  return true;
+}
+
 struct NoSub {
   __device__ void operator()(int) const {}
 };

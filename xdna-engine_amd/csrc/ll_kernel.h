@@ -76,7 +76,10 @@ __device__ __noinline__ HeadOut head_gemv(const HeadArgs h, int nb, int r0, int 
     norm_rows(xr, nb, h.d, h.norm, h.eps, xin, red, nw);
     return true;
   };
-  o.ok = gemv_any<WT, NB, true>(hg, nb, r0, r1, xin, ep, prep, h.logits, h.vocab, h.last_max, o.best, c, NoSub{}) ? 1 : 0;
+  if (head_one_round<WT>(h.d, h.lpr))
+    o.ok = head_rows<WT, NB>(hg, nb, r0, r1, xin, prep, h.logits, h.vocab, h.last_max, o.best) ? 1 : 0;
+  else
+    o.ok = gemv_any<WT, NB, true>(hg, nb, r0, r1, xin, ep, prep, h.logits, h.vocab, h.last_max, o.best, c, NoSub{}) ? 1 : 0;
   return o;
 }
 
