@@ -754,18 +754,20 @@ __device__ __forceinline__ bool gemv_rows(const GD &g, int nb, int r0, int r1, c
   // the fourth finish last, with their SIMD's other wave's work on top.
   // Waves 0..3 keep groups 0..3; waves 4..7 share the rest, each taking a K
   // segment (one group: quarters, two: halves); the segment sums meet in LDS.
-  const int nrg = (r1 - r0 + rows_per_wave - 1) / rows_per_wave;
+  const int rpw_log = 7 - lpr_log;  // log2(rows_per_wave): RPL = 2
+  const int nrg = (r1 - r0 + rows_per_wave - 1) >> rpw_log;
   const int tail = (!HEAD && g.tail_split && ks_log == 0 && (nrg == 5 || nrg == 6)) ? nrg - 4 : 0;
   if (tail > 0 && wave >= 4) {
     S = tail == 1 ? 4 : 2;
-    seg = (wave - 4) % S;
-    wgrp = 4 + (wave - 4) / S;
+    seg = (wave - 4) & (S - 1);
+    wgrp = 4 + ((wave - 4) >> (tail == 1 ? 2 : 1));
   }
   const int K = g.k, nch = K / 16;
-  const int seg_ch = (nch + S - 1) / S;
+  const int s_log = S == 4 ? 2 : S == 2 ? 1 : ks_log;
+  const int seg_ch = (nch + S - 1) >> s_log;
   const int c_lo = seg * seg_ch, c_hi = min(nch, c_lo + seg_ch);
   const int n_it = (seg_ch + LPR - 1) >> lpr_log;
-  const int ntiles = r1 > r0 ? (r1 - r0 + rows_per_tile - 1) / rows_per_tile : 0;
+  const int ntiles = r1 > r0 ? (r1 - r0 + rows_per_tile - 1) >> (rpw_log + 3 - ks_log) : 0;
   const bool ksum = ks_log > 0 || tail > 0;  // some wave holds a K segment
   WRsrc rs;
   rs.w = gdev::coherent_rsrc(g.w);
@@ -987,7 +989,7 @@ __device__ __forceinline__ bool head_rows(const GD &g, int nb, int r0, int r1, c
   const int rows_per_tile = kW * rows_per_wave;
   const int K = g.k, nch = K / 16;
   const int n_it = (nch + LPR - 1) >> lpr_log;
-  const int ntiles = r1 > r0 ? (r1 - r0 + rows_per_tile - 1) / rows_per_tile : 0;
+  const int ntiles = r1 > r0 ? (r1 - r0 + rows_per_tile - 1) >> (9 - lpr_log) : 0;
   if (ntiles == 0) return prep();
   WRsrc rs;
   rs.w = gdev::coherent_rsrc(g.w);
@@ -1081,8 +1083,16 @@ struct NoSub {
   __device__ void operator()(int) const {}
 };
 
-// Rows of rank r out of n ranks (balanced contiguous split).
+// Rows of rank r out of n ranks (balanced contiguous split).  Every phase
+// computes its rows after its input arrives: the 32-bit quotient where the
+// products fit (every plan here) is a fraction of the 64-bit one's
+// instructions.
 __device__ __forceinline__ void rank_rows(int m, int r, int n, int &r0, int &r1) {
+  if (static_cast<unsigned>(m) * static_cast<unsigned>(n) < (1u << 31)) {
+    r0 = static_cast<int>(static_cast<unsigned>(m * r) / static_cast<unsigned>(n));
+    r1 = static_cast<int>(static_cast<unsigned>(m * (r + 1)) / static_cast<unsigned>(n));
+    return;
+  }
   r0 = static_cast<int>((static_cast<long long>(m) * r) / n);
   r1 = static_cast<int>((static_cast<long long>(m) * (r + 1)) / n);
 }

@@ -148,10 +148,10 @@ __global__ __launch_bounds__(kT) void ll_step_kernel(StepParams sp) {
           dpart_stage_issue<WT>(sd, k0, k1, stage);
         } else {
           const XE_CONST GemvD &sg = ph[issue].u.gemv;
-          const int unit = (sg.act == ACT_GEGLU_TANH ? 2 : 1) * (sg.out_lds ? 4 : 1);
+          const int ulog = (sg.act == ACT_GEGLU_TANH ? 1 : 0) + (sg.out_lds ? 2 : 0);
           int s0, s1;
-          rank_rows(sg.m / unit, rank, nranks, s0, s1);
-          stage_issue<WT>(sg, s0 * unit, s1 * unit, stage);
+          rank_rows(sg.m >> ulog, rank, nranks, s0, s1);
+          stage_issue<WT>(sg, s0 << ulog, s1 << ulog, stage);
         }
       }
       if (kv_issue >= 0) {  // the next attention block's keys / values into the key/value stage
@@ -176,11 +176,11 @@ __global__ __launch_bounds__(kT) void ll_step_kernel(StepParams sp) {
           const XE_CONST FoldD *gf = g.folds;
           // GeGLU rows come in (gate, up) pairs: split on pair boundaries;
           // activations kept for LK_DPART: on multiples of four of them
-          const int unit = (g.act == ACT_GEGLU_TANH ? 2 : 1) * (g.out_lds ? 4 : 1);
+          const int ulog = (g.act == ACT_GEGLU_TANH ? 1 : 0) + (g.out_lds ? 2 : 0);
           int r0, r1;
-          rank_rows(g.m / unit, rank, nranks, r0, r1);
-          r0 *= unit;
-          r1 *= unit;
+          rank_rows(g.m >> ulog, rank, nranks, r0, r1);
+          r0 <<= ulog;
+          r1 <<= ulog;
           auto prep = [&]() -> bool {
             bool r = true;
             // the last fold and an RMS norm share one reduction
