@@ -1774,6 +1774,8 @@ void check_step_status(xe_decoder *d) {
     XE_HIP(hipMemset(d->step_status, 0, 4));
     if (st == 2u)
       fail("low-latency step kernel: GEMV tile not compiled (host/device tile menus differ); results are invalid");
+    if (st == 3u)
+      fail("low-latency step kernel: a phase kind on a role not compiled for it (plan error); results are invalid");
     fail("low-latency step kernel: an exchange wait timed out (every workgroup stopped); results are invalid");
   }
 }

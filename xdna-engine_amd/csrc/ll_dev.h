@@ -262,6 +262,13 @@ __device__ __forceinline__ void raise_stop(const Ctl &c) {
   *lptr(c.bad) = 1;
 }
 
+// A phase kind on a role whose step loop is not compiled with it (each
+// role's loop holds only its own kinds): status 3; every other wait ends.
+__device__ __forceinline__ void wrong_role(const Ctl &c) {
+  __hip_atomic_store(gptr_w(c.status), 3u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  *lptr(c.bad) = 1;
+}
+
 // Byte offset past every buffer's range (num_records 0x7ffffff0): a buffer
 // load there returns zeros without touching memory.
 constexpr int kNoRecord = 0x7ffffff0;

@@ -83,20 +83,22 @@ __device__ __noinline__ HeadOut head_gemv(const HeadArgs h, int nb, int r0, int 
   return o;
 }
 
+// One role's step loop (IS_A: the attention side, else the FFN side),
+// compiled once per role: each copy holds only its role's phase kinds (the
+// attention side: folds, GEMVs, attention, merge and the key/value stage; the
+// FFN side: folds, GEMVs, the FFN-output partials and their reduction), so
+// neither carries the other's live state through the register allocation
+// (one loop for both: b = 1 1 186 against 1 228 tok/s).  A phase kind the
+// plan gives the wrong role stops the launch (status 3).
 // KV8: the plan has int8 cross K / V (its own instantiation, so the bf16
 // kernels keep their register allocation).
-template <int WT, int NB, int HD, int G, bool KV8>
-__global__ __launch_bounds__(kT) void ll_step_kernel(StepParams sp) {
-  extern __shared__ float4 lds4[];
-  __shared__ float red[2 * 4 * gdev::kMaxWaves];
-  __shared__ int bad;
-  __shared__ int s_tok[kMaxNB], s_pos[kMaxNB], s_done[kMaxNB];
-  __shared__ float s_bv[kW][kMaxNB];
-  __shared__ int s_bi[kW][kMaxNB];
+template <int WT, int NB, int HD, int G, bool KV8, bool IS_A>
+__device__ __forceinline__ void step_role(const StepParams &sp, float4 *lds4, float *red, int &bad, int *s_tok,
+                                          int *s_pos, int *s_done, float (*s_bv)[kMaxNB], int (*s_bi)[kMaxNB]) {
   float *lds = reinterpret_cast<float *>(lds4);
   const int nb = sp.nb, D = sp.d;
   const int grid = static_cast<int>(gridDim.x);
-  const bool is_a = blockIdx.x % kRoleStride == 0;
+  constexpr bool is_a = IS_A;
   // the role's LDS layout (floats; every part 16-byte aligned)
   const int kin = is_a ? sp.kin_a : sp.kin_f, stage_floats = is_a ? sp.stage_a : sp.stage_f;
   const int nph = is_a ? sp.n_a : sp.n_f;
@@ -141,11 +143,13 @@ __global__ __launch_bounds__(kT) void ll_step_kernel(StepParams sp) {
       const int kind = ph[i].kind, issue = ph[i].issue, kv_issue = ph[i].kv_issue;
       if (issue >= 0 || kv_issue >= 0) lds_barrier();  // the stages' previous readers are done
       if (issue >= 0) {  // a later phase's weight slice into the stage
-        if (ph[issue].kind == LK_DPART) {
-          const XE_CONST DpartD &sd = ph[issue].u.dpart;
-          int k0, k1;
-          dpart_slice(sd, rank, nranks, k0, k1);
-          dpart_stage_issue<WT>(sd, k0, k1, stage);
+        if (!IS_A && ph[issue].kind == LK_DPART) {
+          if constexpr (!IS_A) {
+            const XE_CONST DpartD &sd = ph[issue].u.dpart;
+            int k0, k1;
+            dpart_slice(sd, rank, nranks, k0, k1);
+            dpart_stage_issue<WT>(sd, k0, k1, stage);
+          }
         } else {
           const XE_CONST GemvD &sg = ph[issue].u.gemv;
           const int ulog = (sg.act == ACT_GEGLU_TANH ? 1 : 0) + (sg.out_lds ? 2 : 0);
@@ -154,13 +158,15 @@ __global__ __launch_bounds__(kT) void ll_step_kernel(StepParams sp) {
           stage_issue<WT>(sg, s0 << ulog, s1 << ulog, stage);
         }
       }
-      if (kv_issue >= 0) {  // the next attention block's keys / values into the key/value stage
-        const XE_CONST AttnD &ka = ph[kv_issue].u.attn;
-        const int split = rank % ka.max_splits, rest = rank / ka.max_splits;
-        const int kvh = rest % ka.hkv, b = rest / ka.hkv;
-        if (b < nb) {
-          const int len = ka.fixed_len > 0 ? ka.fixed_len : s_pos[b] + 1;
-          if (kv_staged(ka, split, len)) kv_stage_issue<HD>(ka, split, kvh, b, len, kvs);
+      if constexpr (IS_A) {
+        if (kv_issue >= 0) {  // the next attention block's keys / values into the key/value stage
+          const XE_CONST AttnD &ka = ph[kv_issue].u.attn;
+          const int split = rank % ka.max_splits, rest = rank / ka.max_splits;
+          const int kvh = rest % ka.hkv, b = rest / ka.hkv;
+          if (b < nb) {
+            const int len = ka.fixed_len > 0 ? ka.fixed_len : s_pos[b] + 1;
+            if (kv_staged(ka, split, len)) kv_stage_issue<HD>(ka, split, kvh, b, len, kvs);
+          }
         }
       }
       switch (kind) {
@@ -220,72 +226,92 @@ __global__ __launch_bounds__(kT) void ll_step_kernel(StepParams sp) {
           break;
         }
         case LK_ATTN: {
-          const XE_CONST AttnD &a = ph[i].u.attn;
-          // the first block's K/V loads overlap the wait for q (prep runs once)
-          bool need_q = true;
-          const int nblk = a.max_splits * a.hkv * nb;
-          for (int vb = rank; vb < nblk && ok; vb += nranks) {
-            const int split = vb % a.max_splits, rest = vb / a.max_splits;
-            const int kvh = rest % a.hkv, b = rest / a.hkv;
-            const int len = a.fixed_len > 0 ? a.fixed_len : s_pos[b] + 1;
-            int chunk, nsplits;
-            ll_split(len, a.max_splits, HD, chunk, nsplits);
-            if (split >= nsplits) continue;
-            auto prep = [&]() -> bool {
-              if (!need_q) return true;
-              need_q = false;
-              const bool r = get(a.q, nb, a.qn, xin, a.qn, ep, c);
-              mark_ready(step, i);
-              return r;
-            };
-            // sub-stage trace: input ready, q/k staged, keys done
-            auto tsub = [&](int sub) { mark(step, tslots + 4 + sp.n_a + sp.n_f + kSubSlots * ((is_a ? 0 : sp.n_a) + i) + sub); };
-            // every attention phase of a plan has group G (host checks)
-            // this rank's first block may sit in the key/value stage
-            const bool staged = vb == rank && kv_staged(a, split, len);
-            // int8 cross K / V: Whisper's 64-wide single-query-head groups only
-            if constexpr (KV8 && HD == 64 && G == 1) {
-              if (a.k_scale)
-                ok = attn_block<HD, G, true>(a, split, kvh, b, len, xin, scr, ep, prep, tsub, kvs, staged);
-              else
+          if constexpr (IS_A) {
+            const XE_CONST AttnD &a = ph[i].u.attn;
+            // the first block's K/V loads overlap the wait for q (prep runs once)
+            bool need_q = true;
+            const int nblk = a.max_splits * a.hkv * nb;
+            for (int vb = rank; vb < nblk && ok; vb += nranks) {
+              const int split = vb % a.max_splits, rest = vb / a.max_splits;
+              const int kvh = rest % a.hkv, b = rest / a.hkv;
+              const int len = a.fixed_len > 0 ? a.fixed_len : s_pos[b] + 1;
+              int chunk, nsplits;
+              ll_split(len, a.max_splits, HD, chunk, nsplits);
+              if (split >= nsplits) continue;
+              auto prep = [&]() -> bool {
+                if (!need_q) return true;
+                need_q = false;
+                const bool r = get(a.q, nb, a.qn, xin, a.qn, ep, c);
+                mark_ready(step, i);
+                return r;
+              };
+              // sub-stage trace: input ready, q/k staged, keys done
+              auto tsub = [&](int sub) { mark(step, tslots + 4 + sp.n_a + sp.n_f + kSubSlots * ((is_a ? 0 : sp.n_a) + i) + sub); };
+              // every attention phase of a plan has group G (host checks)
+              // this rank's first block may sit in the key/value stage
+              const bool staged = vb == rank && kv_staged(a, split, len);
+              // int8 cross K / V: Whisper's 64-wide single-query-head groups only
+              if constexpr (KV8 && HD == 64 && G == 1) {
+                if (a.k_scale)
+                  ok = attn_block<HD, G, true>(a, split, kvh, b, len, xin, scr, ep, prep, tsub, kvs, staged);
+                else
+                  ok = attn_block<HD, G, false>(a, split, kvh, b, len, xin, scr, ep, prep, tsub, kvs, staged);
+              } else {
                 ok = attn_block<HD, G, false>(a, split, kvh, b, len, xin, scr, ep, prep, tsub, kvs, staged);
-            } else {
-              ok = attn_block<HD, G, false>(a, split, kvh, b, len, xin, scr, ep, prep, tsub, kvs, staged);
+              }
             }
+          } else {
+            wrong_role(c);
+            ok = false;
           }
           break;
         }
         case LK_DPART: {  // this rank's share of the FFN output projection, as partials
-          const XE_CONST DpartD &dp = ph[i].u.dpart;
-          int k0, k1;
-          dpart_slice(dp, rank, nranks, k0, k1);
-          auto tsub = [&](int sub) { mark(step, tslots + 4 + sp.n_a + sp.n_f + kSubSlots * ((is_a ? 0 : sp.n_a) + i) + sub); };
-          // the stage copies (issued by the phase before) have landed in every wave
-          __builtin_amdgcn_s_waitcnt(0);
-          tsub(0);
-          __syncthreads();
-          mark_ready(step, i);
-          dpart_block<WT, NB>(dp, nb, k1 - k0, xin + dp.act_off, kin, stage, scr, rank, ep, tsub);
+          if constexpr (!IS_A) {
+            const XE_CONST DpartD &dp = ph[i].u.dpart;
+            int k0, k1;
+            dpart_slice(dp, rank, nranks, k0, k1);
+            auto tsub = [&](int sub) { mark(step, tslots + 4 + sp.n_a + sp.n_f + kSubSlots * ((is_a ? 0 : sp.n_a) + i) + sub); };
+            // the stage copies (issued by the phase before) have landed in every wave
+            __builtin_amdgcn_s_waitcnt(0);
+            tsub(0);
+            __syncthreads();
+            mark_ready(step, i);
+            dpart_block<WT, NB>(dp, nb, k1 - k0, xin + dp.act_off, kin, stage, scr, rank, ep, tsub);
+          } else {
+            wrong_role(c);
+            ok = false;
+          }
           break;
         }
         case LK_REDUCE: {  // the partials summed for this rank's outputs
-          const XE_CONST ReduceD &rd = ph[i].u.reduce;
-          int r0, r1;
-          rank_rows(rd.d, rank, nranks, r0, r1);
-          auto tsub = [&](int sub) { mark(step, tslots + 4 + sp.n_a + sp.n_f + kSubSlots * ((is_a ? 0 : sp.n_a) + i) + sub); };
-          mark_ready(step, i);
-          ok = reduce_block<NB>(rd, nb, r0, r1, scr, ep, c, tsub);
+          if constexpr (!IS_A) {
+            const XE_CONST ReduceD &rd = ph[i].u.reduce;
+            int r0, r1;
+            rank_rows(rd.d, rank, nranks, r0, r1);
+            auto tsub = [&](int sub) { mark(step, tslots + 4 + sp.n_a + sp.n_f + kSubSlots * ((is_a ? 0 : sp.n_a) + i) + sub); };
+            mark_ready(step, i);
+            ok = reduce_block<NB>(rd, nb, r0, r1, scr, ep, c, tsub);
+          } else {
+            wrong_role(c);
+            ok = false;
+          }
           break;
         }
         case LK_MERGE: {
-          const XE_CONST MergeD &mg = ph[i].u.merge;
-          const int per_head = mg.hd / kDM;
-          const int nblk = nb * mg.hq * per_head;
-          for (int vb = rank; vb < nblk && ok; vb += nranks) {
-            const int e0 = (vb % per_head) * kDM, rest = vb / per_head;
-            const int h = rest % mg.hq, b = rest / mg.hq;
-            const int len = mg.fixed_len > 0 ? mg.fixed_len : s_pos[b] + 1;
-            ok = merge_block(mg, b, h, e0, len, scr, ep, c);
+          if constexpr (IS_A) {
+            const XE_CONST MergeD &mg = ph[i].u.merge;
+            const int per_head = mg.hd / kDM;
+            const int nblk = nb * mg.hq * per_head;
+            for (int vb = rank; vb < nblk && ok; vb += nranks) {
+              const int e0 = (vb % per_head) * kDM, rest = vb / per_head;
+              const int h = rest % mg.hq, b = rest / mg.hq;
+              const int len = mg.fixed_len > 0 ? mg.fixed_len : s_pos[b] + 1;
+              ok = merge_block(mg, b, h, e0, len, scr, ep, c);
+            }
+          } else {
+            wrong_role(c);
+            ok = false;
           }
           break;
         }
@@ -410,6 +436,20 @@ __global__ __launch_bounds__(kT) void ll_step_kernel(StepParams sp) {
         gptr_w(sp.trace)[static_cast<size_t>(t) * grid + blockIdx.x] = lptr(tlds)[t];
     }
   }
+}
+
+template <int WT, int NB, int HD, int G, bool KV8>
+__global__ __launch_bounds__(kT) void ll_step_kernel(StepParams sp) {
+  extern __shared__ float4 lds4[];
+  __shared__ float red[2 * 4 * gdev::kMaxWaves];
+  __shared__ int bad;
+  __shared__ int s_tok[kMaxNB], s_pos[kMaxNB], s_done[kMaxNB];
+  __shared__ float s_bv[kW][kMaxNB];
+  __shared__ int s_bi[kW][kMaxNB];
+  if (blockIdx.x % kRoleStride == 0)
+    step_role<WT, NB, HD, G, KV8, true>(sp, lds4, red, bad, s_tok, s_pos, s_done, s_bv, s_bi);
+  else
+    step_role<WT, NB, HD, G, KV8, false>(sp, lds4, red, bad, s_tok, s_pos, s_done, s_bv, s_bi);
 }
 
 using StepFn = void (*)(StepParams);
