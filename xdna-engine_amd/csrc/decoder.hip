@@ -1230,7 +1230,9 @@ void plan_stage(std::vector<ll::Phase> &list, int ranks, int wt, long budget, in
     if (list[j].kind != ll::LK_GEMV) continue;
     ll::GemvD &g = list[j].u.gemv;
     const int at = last + 1;
-    if (!g.in_vec || at >= j) continue;  // input from the previous phase; an earlier phase to ride on
+    // input from the previous phase, no residual update (the kernel's staged
+    // path waits for the input vector alone); an earlier phase to ride on
+    if (!g.in_vec || g.nfold > 0 || at >= j) continue;
     // the kernel's row split (ll_kernel.h: GeGLU pairs, and activations kept
     // in LDS for the split FFN output on multiples of four of them)
     const int unit = (g.act == ACT_GEGLU_TANH ? 2 : 1) * (g.out_lds ? 4 : 1);
@@ -1363,7 +1365,9 @@ void build_ll_plan(xe_decoder *d, int B, xe_decoder::LLPlan &P) {
     gd.m = m.rows;
     gd.k = m.cols;
     ll_tile(m.rows, ranks, m.cols, act == ACT_GEGLU_TANH, m.wdtype, gd.lpr, gd.rpl);
-    gd.tail_split = tail_mode == 2 || (tail_mode == 1 && out_lds > 0) ? 1 : 0;
+    // the tail K split runs on the FFN side only (the attention side's step
+    // loop is compiled without it; on every GEMV it measured -1.4 %)
+    gd.tail_split = &list == &P.f && (tail_mode == 2 || (tail_mode == 1 && out_lds > 0)) ? 1 : 0;
     gd.in_vec = in_vec >= 0 ? 1 : 0;
     gd.norm = norm_kind;
     gd.gamma = gamma;

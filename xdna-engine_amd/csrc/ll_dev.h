@@ -89,9 +89,6 @@ struct GemvD {
   // 1: this rank's weight slice (and epilogue constants) sits in the LDS
   // stage area, copied there by an earlier phase (Phase::issue)
   int staged;
-  // the waves split K into 1 << ks_log segments (rows the rank holds too few
-  // to keep every wave busy); their partial sums meet in LDS
-  int ks_log;
   // 1: one tile's row groups past the fourth are K-split over waves 4..7
   // (waves w and w + 4 share a SIMD; see gemv_rows)
   int tail_split;
@@ -737,25 +734,27 @@ __device__ __forceinline__ void chunk_dot4(const gdev::Chunk<WT> &ch, const floa
   }
 }
 
-template <int WT, int NB, bool HEAD, typename GD, typename Prep, typename Sub>
+// ST: 1 / 0 compiles only the staged / streamed weight path (-1: staged_rt
+// decides at run time); TAIL: false compiles the tail K split out.
+template <int WT, int NB, bool HEAD, typename GD, typename Prep, typename Sub, int ST = -1, bool TAIL = true>
 __device__ __forceinline__ bool gemv_rows(const GD &g, int nb, int r0, int r1, const float *xs, unsigned ep,
                                           Prep prep, float *logits, int vocab, int last_max, ArgBest &best,
-                                          Sub tsub, const float *stage, bool staged, float *kred, float *lout,
+                                          Sub tsub, const float *stage, bool staged_rt, float *kred, float *lout,
                                           int lout_ld) {
   using gdev::Chunk;
+  const bool staged = ST >= 0 ? ST != 0 : staged_rt;
   constexpr int RPL = 2;
   constexpr int NIT = Round<WT>::NIT;
   const int lpr_log = __builtin_ctz(static_cast<unsigned>(g.lpr));
   const int LPR = 1 << lpr_log;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int rg = lane >> lpr_log, kl = lane & (LPR - 1);
-  // K segments: wave w takes segment w % S of the chunks for the rows of
-  // its group w / S
-  const int ks_log = HEAD ? 0 : g.ks_log;
-  int S = 1 << ks_log;
-  int seg = wave & (S - 1), wgrp = wave >> ks_log;
+  // K segments (the tail split below): wave w takes segment seg of the
+  // chunks for the rows of its group wgrp
+  int S = 1;
+  int seg = 0, wgrp = wave;
   const int rows_per_wave = (64 >> lpr_log) * RPL;
-  const int rows_per_tile = (kW >> ks_log) * rows_per_wave;
+  const int rows_per_tile = kW * rows_per_wave;
   // Tail split: waves w and w + 4 share SIMD w % 4 (the older wave issues
   // first), so in one tile of 5 or 6 row groups (one a wave) the waves past
   // the fourth finish last, with their SIMD's other wave's work on top.
@@ -763,19 +762,19 @@ __device__ __forceinline__ bool gemv_rows(const GD &g, int nb, int r0, int r1, c
   // segment (one group: quarters, two: halves); the segment sums meet in LDS.
   const int rpw_log = 7 - lpr_log;  // log2(rows_per_wave): RPL = 2
   const int nrg = (r1 - r0 + rows_per_wave - 1) >> rpw_log;
-  const int tail = (!HEAD && g.tail_split && ks_log == 0 && (nrg == 5 || nrg == 6)) ? nrg - 4 : 0;
+  const int tail = (TAIL && !HEAD && g.tail_split && (nrg == 5 || nrg == 6)) ? nrg - 4 : 0;
   if (tail > 0 && wave >= 4) {
     S = tail == 1 ? 4 : 2;
     seg = (wave - 4) & (S - 1);
     wgrp = 4 + ((wave - 4) >> (tail == 1 ? 2 : 1));
   }
   const int K = g.k, nch = K / 16;
-  const int s_log = S == 4 ? 2 : S == 2 ? 1 : ks_log;
+  const int s_log = S == 4 ? 2 : S == 2 ? 1 : 0;
   const int seg_ch = (nch + S - 1) >> s_log;
   const int c_lo = seg * seg_ch, c_hi = min(nch, c_lo + seg_ch);
   const int n_it = (seg_ch + LPR - 1) >> lpr_log;
-  const int ntiles = r1 > r0 ? (r1 - r0 + rows_per_tile - 1) >> (rpw_log + 3 - ks_log) : 0;
-  const bool ksum = ks_log > 0 || tail > 0;  // some wave holds a K segment
+  const int ntiles = r1 > r0 ? (r1 - r0 + rows_per_tile - 1) >> (rpw_log + 3) : 0;
+  const bool ksum = tail > 0;  // some wave holds a K segment
   WRsrc rs;
   rs.w = gdev::coherent_rsrc(g.w);
   rs.e = gdev::coherent_rsrc(WT == XE_BFP16 ? static_cast<const void *>(g.exps) : g.w);

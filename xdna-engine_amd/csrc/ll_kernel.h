@@ -220,9 +220,27 @@ __device__ __forceinline__ void step_role(const StepParams &sp, float4 *lds4, fl
             return r;
           };
           auto tsub = [&](int sub) { mark(step, tslots + 4 + sp.n_a + sp.n_f + kSubSlots * ((is_a ? 0 : sp.n_a) + i) + sub); };
-          // K-segment sums go to the scratch area (its norm gains are read by then)
-          ok = gemv_any<WT, NB, false>(g, nb, r0, r1, xin, ep, prep, nullptr, 0, 0, none, c, tsub, stage,
-                                       g.staged != 0, scr, xin + g.out_lds, kin);
+          // A staged GEMV's input is an exchange vector and it applies no
+          // residual update (plan_stage stages no other), so its wait is the
+          // vector's get alone.
+          auto prep_in = [&]() -> bool {
+            // one round of loads covers the whole input up to kT * 8 pairs
+            // (a second round waits for the first to complete)
+            const bool r = nb * g.k > kT * 8 ? get<8>(g.in, nb, g.k, xin, xstride(g.k), ep, c, true)
+                                             : get(g.in, nb, g.k, xin, xstride(g.k), ep, c, true);
+            mark_ready(step, i);
+            return r;
+          };
+          // staged and streamed weights, and the K-split tail (FFN side
+          // only), as separate code paths: each holds only its own state
+          // (one path for both: b = 1 1 231 against 1 255 tok/s).  K-segment
+          // sums go to the scratch area (its norm gains are read by then).
+          if (g.staged)
+            ok = gemv_rows<WT, NB, false, XE_CONST GemvD, decltype(prep_in), decltype(tsub), 1, !IS_A>(
+                g, nb, r0, r1, xin, ep, prep_in, nullptr, 0, 0, none, tsub, stage, true, scr, xin + g.out_lds, kin);
+          else
+            ok = gemv_rows<WT, NB, false, XE_CONST GemvD, decltype(prep), decltype(tsub), 0, !IS_A>(
+                g, nb, r0, r1, xin, ep, prep, nullptr, 0, 0, none, tsub, stage, false, scr, xin + g.out_lds, kin);
           break;
         }
         case LK_ATTN: {
