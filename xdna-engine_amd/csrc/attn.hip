@@ -49,10 +49,12 @@ namespace {
 using adev::AttnParams;
 using adev::kThreads;
 
-template <int HD, int G, int KV8 = 0>
+// NT: nontemporal key / value loads (per-stream caches; false for a cache
+// every stream of the batch reads).
+template <int HD, int G, int KV8 = 0, bool NT = true>
 __global__ __launch_bounds__(kThreads) void attn_kernel(AttnParams p) {
   __shared__ float lds[adev::attn_lds_floats(HD, G)];
-  adev::attn_split_block<HD, G, false, KV8>(p, blockIdx.x, blockIdx.y, blockIdx.z, lds);
+  adev::attn_split_block<HD, G, false, KV8, NT>(p, blockIdx.x, blockIdx.y, blockIdx.z, lds);
 }
 
 template <int HD, int G>
@@ -64,9 +66,9 @@ __global__ __launch_bounds__(kThreads) void attn_merge_kernel(AttnParams p) {
 using AttnFn = void (*)(AttnParams);
 
 template <int HD>
-AttnFn pick_g(int g, bool merge) {
+AttnFn pick_g(int g, bool merge, bool shared) {
   switch (g) {
-    case 1: return merge ? attn_merge_kernel<HD, 1> : attn_kernel<HD, 1>;
+    case 1: return merge ? attn_merge_kernel<HD, 1> : shared ? attn_kernel<HD, 1, 0, false> : attn_kernel<HD, 1>;
     case 2: return merge ? attn_merge_kernel<HD, 2> : attn_kernel<HD, 2>;
     case 4: return merge ? attn_merge_kernel<HD, 4> : attn_kernel<HD, 4>;
     case 8: return merge ? attn_merge_kernel<HD, 8> : attn_kernel<HD, 8>;
@@ -75,18 +77,21 @@ AttnFn pick_g(int g, bool merge) {
 }
 
 // int8 K and/or V (kv8 bit 0 / bit 1): one query head a KV head (Whisper's
-// cross attention).
+// cross attention, its cache shared by the batch: plain loads).
 template <int HD>
 AttnFn pick_kv8(int kv8) {
   switch (kv8) {
-    case 1: return attn_kernel<HD, 1, 1>;
-    case 2: return attn_kernel<HD, 1, 2>;
-    case 3: return attn_kernel<HD, 1, 3>;
+    case 1: return attn_kernel<HD, 1, 1, false>;
+    case 2: return attn_kernel<HD, 1, 2, false>;
+    case 3: return attn_kernel<HD, 1, 3, false>;
   }
   return nullptr;
 }
 
-AttnFn pick(int hd, int g, bool merge, int kv8 = 0) {
+// shared: one K / V cache for every stream of the batch (batch stride 0),
+// which then loads with plain loads (one query head a KV head: cross
+// attention; other groups keep the nontemporal kernel).
+AttnFn pick(int hd, int g, bool merge, int kv8 = 0, bool shared = false) {
   if (kv8 && !merge) {
     if (g != 1) return nullptr;
     switch (hd) {
@@ -97,9 +102,9 @@ AttnFn pick(int hd, int g, bool merge, int kv8 = 0) {
     return nullptr;
   }
   switch (hd) {
-    case 64: return pick_g<64>(g, merge);
-    case 128: return pick_g<128>(g, merge);
-    case 256: return pick_g<256>(g, merge);
+    case 64: return pick_g<64>(g, merge, shared);
+    case 128: return pick_g<128>(g, merge, shared);
+    case 256: return pick_g<256>(g, merge, shared);
   }
   return nullptr;
 }
@@ -114,7 +119,7 @@ void launch_attn_phase(const sdev::Phase &ph, hipStream_t s) {
   const AttnParams &p = ph.u.attn;
   const bool merge = ph.kind == sdev::PH_MERGE;
   if (merge && p.cnt) return;
-  AttnFn fn = pick(ph.hd, ph.g, merge, kv8_of(p));
+  AttnFn fn = pick(ph.hd, ph.g, merge, kv8_of(p), p.kv_bstride == 0 && p.batch > 1);
   XE_REQUIRE(fn, "attn phase: unsupported head_dim / group (int8 K/V: one query head a KV head)");
   if (merge) {
     const int blocks = (ph.g * ph.hd + kThreads - 1) / kThreads;
@@ -167,7 +172,7 @@ void launch_attn(const AttnLaunch &L, hipStream_t s) {
   XE_REQUIRE(L.work, "attn: workspace missing");
   const int g = L.hq / L.hkv;
   const AttnParams p = adev::to_params(L);
-  AttnFn fn = pick(L.hd, g, false, kv8_of(p));
+  AttnFn fn = pick(L.hd, g, false, kv8_of(p), p.kv_bstride == 0 && p.batch > 1);
   AttnFn merge = pick(L.hd, g, true);
   XE_REQUIRE(fn && merge, "attn: unsupported head_dim / GQA group (hd 64/128/256, group 1/2/4/8; "
                           "int8 K/V: group 1)");

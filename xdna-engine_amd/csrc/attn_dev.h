@@ -164,21 +164,29 @@ __device__ __forceinline__ void head_transform(const AttnParams &p, const float 
 
 // A lane's eight elements of one key row, loaded raw (16 bytes of bf16 or 8
 // of int8) and converted at use, so the loads of a block stay in flight
-// while earlier keys compute.  The rows are read once a step: nontemporal
-// loads (a 168 MB stream over 256 workgroups: 24.9 against 27.9 us with
-// plain loads; b = 64 decode +1.3 %).
-template <bool I8>
+// while earlier keys compute.  NT: rows each stream reads once a step
+// (per-stream caches) come in with nontemporal loads (a 168 MB stream over
+// 256 workgroups: 24.9 against 27.9 us with plain loads; b = 64 decode
+// +1.3 %); rows every stream reads (a cross-attention cache shared by the
+// batch) with plain ones, so they stay cached between streams (Whisper-small
+// b = 32: 34.8k tok/s against 33.8k with nontemporal loads).
+template <bool I8, bool NT = true>
 struct Raw8 {
   uint32_t w[I8 ? 2 : 4];
   __device__ __forceinline__ void load(const uint16_t *base, size_t elem) {
     if constexpr (I8) {
       typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
-      const u32x2 v =
-          __builtin_nontemporal_load(reinterpret_cast<const u32x2 *>(reinterpret_cast<const int8_t *>(base) + elem));
+      const u32x2 *src = reinterpret_cast<const u32x2 *>(reinterpret_cast<const int8_t *>(base) + elem);
+      u32x2 v;
+      if constexpr (NT) v = __builtin_nontemporal_load(src);
+      else v = *src;
       w[0] = v.x;
       w[1] = v.y;
     } else {
-      const gdev::u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const gdev::u32x4 *>(base + elem));
+      const gdev::u32x4 *src = reinterpret_cast<const gdev::u32x4 *>(base + elem);
+      gdev::u32x4 v;
+      if constexpr (NT) v = __builtin_nontemporal_load(src);
+      else v = *src;
       w[0] = v.x;
       w[1] = v.y;
       w[2] = v.z;
@@ -297,7 +305,8 @@ __device__ __forceinline__ void merge_heads(const AttnParams &p, int kvh, int b,
 }
 
 // One split block: keys [split*chunk, ...) of (stream b, kv head kvh).
-template <int HD, int G, bool COH, int KV8 = 0>
+// NT: the key / value loads are nontemporal (Raw8).
+template <int HD, int G, bool COH, int KV8 = 0, bool NT = true>
 __device__ __forceinline__ void attn_split_block(const AttnParams &p, int split, int kvh, int b, float *lds) {
   constexpr bool K8 = (KV8 & 1) != 0, V8 = (KV8 & 2) != 0;
   constexpr int EPL = 8;       // elements per lane per key (16 B of bf16, 8 B of int8)
@@ -330,7 +339,7 @@ __device__ __forceinline__ void attn_split_block(const AttnParams &p, int split,
   const int base0 = s0 + wave * KPW + kg;
   const bool appender = !K8 && !V8 && p.k_new && split == nsplits - 1;
   // UK keys' K and V rows from `base` (keys past the range read key s0)
-  auto load_block = [&](int base, Raw8<K8> (&kv)[UK], Raw8<V8> (&vv)[UK], bool (&ok)[UK]) {
+  auto load_block = [&](int base, Raw8<K8, NT> (&kv)[UK], Raw8<V8, NT> (&vv)[UK], bool (&ok)[UK]) {
 #pragma unroll
     for (int u = 0; u < UK; u++) {
       const int key = base + u * STEP;
@@ -343,8 +352,8 @@ __device__ __forceinline__ void attn_split_block(const AttnParams &p, int split,
   // the first block's loads go out before the head transforms, so their HBM
   // latency overlaps the prologue (not in the appender's block: it reads
   // back the row it appends)
-  Raw8<K8> kv0[UK];
-  Raw8<V8> vv0[UK];
+  Raw8<K8, NT> kv0[UK];
+  Raw8<V8, NT> vv0[UK];
   bool ok0[UK];
   if (!appender) load_block(base0, kv0, vv0, ok0);
 
@@ -384,7 +393,7 @@ __device__ __forceinline__ void attn_split_block(const AttnParams &p, int split,
   const float sc2 = p.scale * kLog2e;
 
   // one block of UK keys per lane group: scores, online softmax, P.V
-  auto block = [&](const Raw8<K8>(&kv)[UK], const Raw8<V8>(&vv)[UK], const bool(&ok)[UK]) {
+  auto block = [&](const Raw8<K8, NT>(&kv)[UK], const Raw8<V8, NT>(&vv)[UK], const bool(&ok)[UK]) {
     // the block's UK x G partial dot products, then their sums over the L
     // lanes of each key, level by level through DPP and permlane swaps (no
     // LDS crossbar round trips)
@@ -436,8 +445,8 @@ __device__ __forceinline__ void attn_split_block(const AttnParams &p, int split,
   // two blocks in flight: the next block's loads go out before this block's
   // arithmetic (keys past the range read key s0 and are masked)
   constexpr int BS = STEP * UK;
-  Raw8<K8> kb[UK];
-  Raw8<V8> vb[UK];
+  Raw8<K8, NT> kb[UK];
+  Raw8<V8, NT> vb[UK];
   bool ob[UK];
   if (appender) load_block(base0, kv0, vv0, ok0);
   for (int base = base0; base < s1; base += 2 * BS) {
