@@ -65,7 +65,7 @@ LL_TRAFFIC_BYTES_PER_STEP = 1335060927
 # FETCH_SIZE and WRITE_SIZE of the same kernels at the decoder's shapes,
 # launched through the op layer (bench.py --kernels --gemm-only --eager), scaled
 # like the b = 1 figure; profiles/b64_step_kernels_traffic.md.
-B64_GEMM_TRAFFIC_BYTES_PER_STEP = 2231000000
+B64_GEMM_TRAFFIC_BYTES_PER_STEP = 2233000000
 
 
 def load_xe():
