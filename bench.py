@@ -442,9 +442,9 @@ def run_kernels(args):
 
 
 def run_configs(xe, dev):
-    """BASELINE configs 1 and 4, the workloads the reference publishes its own
-    per-token times for (OPT-125m host CPU path 47
-    ms/token, README.md:38; Whisper-small fused decoder ~75 ms/token on the
+    """Benchmark configs 1 and 4, the workloads the reference publishes its own
+    per-token times for (OPT-125m host CPU path 47 ms/token, the reference's
+    README.md:38; Whisper-small fused decoder ~75 ms/token on the
     XDNA2 NPU, docs/data-movement-thesis.md:41; batched B=16 lockstep 16.13
     ms/step, scripts/measure_phase2_sweep.sh:81).  Greedy decode of seeded
     synthetic int8 weights, timed with the device synchronised on both sides;
