@@ -111,7 +111,12 @@ __device__ __forceinline__ bool better(float v, int i, float bv, int bi, int las
 
 // Block k of row b reduces its slice of the logits (Iterator::max_by keeps
 // the LAST of equal maxima, opt125m_decode.rs:303; strict > keeps the first,
-// whisper.rs:749-757).  lds: 512 floats.
+// whisper.rs:749-757).  `better` orders every (value, index) pair totally, so
+// the winner does not depend on the order of the compares: a thread's loads
+// go out together (up to kArgU of them, one memory round trip for a slice of
+// 256 kArgU logits), then a 64-lane butterfly and the four waves' winners.
+// lds: at least 8 floats.
+constexpr int kArgU = 16;
 template <bool COH>
 __device__ __forceinline__ void argmax_part_block(const ArgmaxParams &p, int vb, float *lds) {
   const int b = vb / kArgBlocks, k = vb % kArgBlocks;
@@ -121,32 +126,45 @@ __device__ __forceinline__ void argmax_part_block(const ArgmaxParams &p, int vb,
   const float *row = p.logits + static_cast<size_t>(b) * p.vocab;
   float bv = -INFINITY;
   int bi = -1;
-  for (int i = lo + threadIdx.x; i < hi; i += 256) {
-    const float v = gdev::act_ld<COH>(row, i);
-    if (better(v, i, bv, bi, p.last_max)) {
-      bv = v;
-      bi = i;
+  for (int i0 = lo + static_cast<int>(threadIdx.x); i0 < hi; i0 += 256 * kArgU) {
+    float v[kArgU];
+#pragma unroll
+    for (int u = 0; u < kArgU; u++) v[u] = i0 + 256 * u < hi ? gdev::act_ld<COH>(row, i0 + 256 * u) : 0.f;
+#pragma unroll
+    for (int u = 0; u < kArgU; u++) {
+      const int i = i0 + 256 * u;
+      if (i < hi && better(v[u], i, bv, bi, p.last_max)) {
+        bv = v[u];
+        bi = i;
+      }
+    }
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const float ov = __shfl_xor(bv, off, 64);
+    const int oi = __shfl_xor(bi, off, 64);
+    if (oi >= 0 && better(ov, oi, bv, bi, p.last_max)) {
+      bv = ov;
+      bi = oi;
     }
   }
   float *sv = lds;
-  int *si = reinterpret_cast<int *>(lds + 256);
-  sv[threadIdx.x] = bv;
-  si[threadIdx.x] = bi;
-  __syncthreads();
-  for (int w = 128; w >= 1; w >>= 1) {
-    if (threadIdx.x < w) {
-      const float ov = sv[threadIdx.x + w];
-      const int oi = si[threadIdx.x + w];
-      if (oi >= 0 && better(ov, oi, sv[threadIdx.x], si[threadIdx.x], p.last_max)) {
-        sv[threadIdx.x] = ov;
-        si[threadIdx.x] = oi;
-      }
-    }
-    __syncthreads();
+  int *si = reinterpret_cast<int *>(lds + 4);
+  if ((threadIdx.x & 63) == 0) {
+    sv[threadIdx.x >> 6] = bv;
+    si[threadIdx.x >> 6] = bi;
   }
+  __syncthreads();
   if (threadIdx.x == 0) {
-    gdev::act_st<COH>(p.part_v + b * kArgBlocks + k, sv[0]);
-    gdev::act_st<COH>(reinterpret_cast<float *>(p.part_i) + b * kArgBlocks + k, __int_as_float(si[0]));
+    float v = sv[0];
+    int idx = si[0];
+    for (int w = 1; w < 4; w++)
+      if (si[w] >= 0 && better(sv[w], si[w], v, idx, p.last_max)) {
+        v = sv[w];
+        idx = si[w];
+      }
+    gdev::act_st<COH>(p.part_v + b * kArgBlocks + k, v);
+    gdev::act_st<COH>(reinterpret_cast<float *>(p.part_i) + b * kArgBlocks + k, __int_as_float(idx));
   }
   __syncthreads();
 }
