@@ -294,6 +294,60 @@ def test_tiny_batched_step_logits(gpu, xe, family):
     om.close()
 
 
+@pytest.mark.parametrize("family", ["gemma", "opt"])
+@pytest.mark.parametrize("batch", [1, 3, 20])
+def test_argmax_tie_rule_on_planted_ties(gpu, xe, family, batch):
+    """Exact ties among the largest logits: rows of the tied embedding /
+    lm-head planted equal (+c e_0 at several vocab positions, -c e_0 at
+    others), so their logits are bit-identical and, for most streams, the
+    largest.  The token the device argmax picks is the family rule's on
+    the same logits (the oracle's argmax: first max for Gemma, whisper.rs:
+    749-757; last max for OPT, opt125m_decode.rs:303), with the tied rows
+    spread over different argmax blocks, lanes and workgroups: 1 and 3
+    streams (the low-latency kernel's argmax over its 256 workgroups), 20
+    (the argmax partial and final kernels)."""
+    dev, _ = gpu
+    fam = {"opt": xe.XE_OPT, "gemma": xe.XE_GEMMA3}[family]
+    cfg = tiny(xe, fam, xe.XE_I8)
+    V, D = cfg.vocab, cfg.d_model
+    print("[case] planted ties %s b=%d" % (family, batch), flush=True)
+    dec = xe.Decoder(dev, cfg, max_batch=batch)
+    dec.init_synthetic(3)
+    om = O.OracleModel(oracle_cfg(cfg), 3, 1)
+    rows, cols = xe.tensor_shape(cfg, O.XE_T_TOK_EMB, -1)
+    q, sc = dec.get_tensor_q8(O.XE_T_TOK_EMB, -1, rows, cols)
+    emb = q.astype(np.float32) * sc[:, None]
+    plus = [3, 4, 130, V // 2 + 7, V - 1]
+    minus = [5, 131, V // 2 + 8, V - 2]
+    for r in plus:
+        emb[r] = 0.0
+        emb[r, 0] = 4.0
+    for r in minus:
+        emb[r] = 0.0
+        emb[r, 0] = -4.0
+    dec.set_tensor(O.XE_T_TOK_EMB, -1, emb)
+    planted = set(plus) | set(minus)
+    rng = np.random.default_rng(5)
+    hits = 0
+    for step in range(4):
+        toks = rng.integers(0, V, batch).astype(np.int32)
+        toks = np.array([t if t not in planted else (t + 11) % V for t in toks], np.int32)
+        pos = np.full(batch, step, np.int32)
+        logits, nxt = dec.step(toks, pos)
+        for b in range(batch):
+            want = om.argmax(logits[b])
+            assert nxt[b] == want, (step, b, int(nxt[b]), int(want))
+            if want in planted:
+                group = plus if want in plus else minus
+                vals = logits[b][group].view(np.uint32)
+                assert np.all(vals == vals[0]), (step, b)
+                assert want == (max(group) if family == "opt" else min(group)), (step, b, want)
+                hits += 1
+    dec.close()
+    om.close()
+    assert hits >= 2 * batch, hits
+
+
 PARTS_CASES = [("gemma", 64, "gemv_gateup_pro"), ("whisper", 32, "gemv_fc1_pro"), ("opt", 16, "gemv_fc1_pro")]
 
 
