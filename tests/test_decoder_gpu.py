@@ -107,6 +107,25 @@ def test_tiny_greedy_identity(gpu, xe, executor, family, wd):
     om.close()
 
 
+@pytest.mark.parametrize("family", ["opt", "gemma"])
+def test_tiny_greedy_four_streams(gpu, xe, executor, family):
+    """Four streams: the widest low-latency step (its 4-stream instantiation
+    with every stream live) and, on the graph executor, the smallest batch
+    whose projections run on the MFMA GEMM (one 16-stream tile, 12 rows
+    empty)."""
+    fam = {"opt": xe.XE_OPT, "gemma": xe.XE_GEMMA3}[family]
+    cfg = tiny(xe, fam, xe.XE_I8)
+    batch = 4
+    print("[case] tiny %s i8 batch %d %s" % (family, batch, executor), flush=True)
+    dec, om = build(xe, gpu, cfg, seed=17, batch=batch)
+    assert dec.executor(batch) == executor, dec.executor(batch)
+    pr = prompts(cfg, batch, 5, seed=2)
+    got = dec.generate(pr, 32)
+    greedy_identity(got, om, pr, "tiny-%s-b4-%s" % (family, executor))
+    dec.close()
+    om.close()
+
+
 @pytest.mark.parametrize("family", ["opt", "whisper", "gemma"])
 def test_tiny_step_logits(gpu, xe, executor, family):
     """step() logits (per-stream positions) vs the oracle's, step by step."""
