@@ -992,11 +992,11 @@ __device__ __forceinline__ bool head_rows(const GD &g, int nb, int r0, int r1, c
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int rg = lane >> lpr_log, kl = lane & (LPR - 1);
   const int rows_per_wave = (64 >> lpr_log) * RPL;
-  const int rows_per_tile = kW * rows_per_wave;
   const int K = g.k, nch = K / 16;
   const int n_it = (nch + LPR - 1) >> lpr_log;
-  const int ntiles = r1 > r0 ? (r1 - r0 + rows_per_tile - 1) >> (9 - lpr_log) : 0;
-  if (ntiles == 0) return prep();
+  // wave tiles: a wave's rows_per_wave rows at a time
+  const int nwt = r1 > r0 ? (r1 - r0 + rows_per_wave - 1) >> (6 - lpr_log) : 0;
+  if (nwt == 0) return prep();
   WRsrc rs;
   rs.w = gdev::coherent_rsrc(g.w);
   rs.e = gdev::coherent_rsrc(WT == XE_BFP16 ? static_cast<const void *>(g.exps) : g.w);
@@ -1004,7 +1004,7 @@ __device__ __forceinline__ bool head_rows(const GD &g, int nb, int r0, int r1, c
     Chunk<WT> w[NIT][RPL];
     float scale[RPL];
   };
-  auto first_row = [&](int tile) { return r0 + tile * rows_per_tile + wave * rows_per_wave + rg * RPL; };
+  auto first_row = [&](int wt) { return r0 + wt * rows_per_wave + rg * RPL; };
   auto load_tile = [&](int tile, TileW &t) {
     const int row0 = first_row(tile);
 #pragma unroll
@@ -1072,15 +1072,33 @@ __device__ __forceinline__ bool head_rows(const GD &g, int nb, int r0, int r1, c
       }
     }
   };
+  // Wave tiles are handed out one at a time from an LDS counter: each wave
+  // starts with tile `wave`, then takes the next free one, so the waves of a
+  // SIMD pair (the older one issues first) stream until the slice is done
+  // instead of the younger ones finishing alone (with equal static shares
+  // the last wave of a workgroup ended ~6 us after its first).  Every row is
+  // computed as before; the argmax order is total, so neither the logits nor
+  // the winner depend on which wave takes a row.
+  __shared__ int s_next;
+  auto grab = [&]() -> int {
+    int v = 0;
+    if (lane == 0) v = __hip_atomic_fetch_add(&s_next, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    return __builtin_amdgcn_readfirstlane(v);
+  };
+  if (threadIdx.x == 0) s_next = kW;
   TileW ta, tb;
-  load_tile(0, ta);
-  if (!prep()) return false;  // the final norm overlaps the first tile's loads
-  for (int tile = 0; tile < ntiles; tile += 2) {
-    load_tile(tile + 1, tb);
-    compute_tile(tile, ta);
-    if (tile + 1 >= ntiles) break;
-    load_tile(tile + 2, ta);
-    compute_tile(tile + 1, tb);
+  int cur = wave;
+  load_tile(cur, ta);         // tiles past the slice read nothing
+  if (!prep()) return false;  // the final norm overlaps the first tile's loads; its barrier orders s_next
+  while (cur < nwt) {
+    const int nxt = grab();
+    load_tile(nxt, tb);
+    compute_tile(cur, ta);
+    if (nxt >= nwt) break;
+    const int nn = grab();
+    load_tile(nn, ta);
+    compute_tile(nxt, tb);
+    cur = nn;
   }
   return true;
 }
