@@ -59,7 +59,7 @@ HBM_PEAK_GBPS = 8000.0
 # counter reads for a 1 GiB device copy (bench.py --copy-probe); commands and
 # numbers in profiles/ll_traffic_gemma3_1b_b1.md.  Measured offline (counters
 # need their own profiler run); null for any other workload.
-LL_TRAFFIC_BYTES_PER_STEP = 1335060927
+LL_TRAFFIC_BYTES_PER_STEP = 1335802645
 # HBM bytes per b = 64 step of the projection family (26 x the four layer
 # GEMMs + the lm-head GEMM, the b = 64 line's dominant kernels): per-dispatch
 # FETCH_SIZE and WRITE_SIZE of the same kernels at the decoder's shapes,
