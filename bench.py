@@ -451,14 +451,15 @@ def run_configs(xe, dev):
     the prompt is fed untimed.  Whisper decodes against a synthetic encoder
     output (1500 frames, N(0, 1) rounded to bf16).  Also config 4 with the
     fused decoder's per-utterance int8 cross K / V, and config 5's bf16
-    baseline (Gemma-3-1B with bf16 weights, 2.0 GB a token; no reference
-    number), whose line adds its weight-stream rate."""
+    baseline at b = 1 and b = 64 (Gemma-3-1B with bf16 weights, 2.0 GB a
+    step; no reference number), whose lines add their weight-stream rate."""
     res = {}
     runs = [("opt125m_b1", xe.OPT_125M, 0, 1, 32, 128),
             ("whisper_small_b1", xe.WHISPER_SMALL, 1, 1, 4, 224),
             ("whisper_small_b1_int8cross", xe.WHISPER_SMALL, 1, 1, 4, 224),
             ("whisper_small_b32", xe.WHISPER_SMALL, 1, 32, 4, 224),
-            ("gemma3_1b_bf16_b1", xe.GEMMA3_1B.replace(wdtype=xe.XE_BF16, max_ctx=4096), 2, 1, 512, 520)]
+            ("gemma3_1b_bf16_b1", xe.GEMMA3_1B.replace(wdtype=xe.XE_BF16, max_ctx=4096), 2, 1, 512, 520),
+            ("gemma3_1b_bf16_b64", xe.GEMMA3_1B.replace(wdtype=xe.XE_BF16, max_ctx=4096), 2, 64, 512, 520)]
     ref_ms = {"opt125m_b1": (47.0, "reference host CPU path, README.md:38"),
               "whisper_small_b1": (75.0, "reference fused decoder on the XDNA2 NPU, "
                                          "docs/data-movement-thesis.md:41"),

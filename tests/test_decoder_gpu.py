@@ -461,6 +461,23 @@ def test_gemma3_1b_batched_short(gpu, xe):
     om.close()
 
 
+def test_gemma3_1b_bf16_b64_short(gpu, xe):
+    """Config 5's bf16 baseline at its second batch: the real Gemma-3-1B
+    shapes with bf16 weights at 64 streams (the MFMA GEMM's bf16 weight path,
+    64-stream tiles, the 262144-row lm-head), greedy streams against the
+    oracle."""
+    cfg = xe.GEMMA3_1B.replace(wdtype=xe.XE_BF16, max_ctx=64)
+    batch = 64
+    print("[case] gemma3-1b bf16 b=%d" % batch, flush=True)
+    dec, om = build(xe, gpu, cfg, seed=2, batch=batch)
+    assert dec.executor(batch) == "graph"
+    pr = prompts(cfg, batch, 2, seed=6)
+    got = dec.generate(pr, 2)
+    greedy_identity(got, om, pr, "gemma3-1b-bf16-b64", eps=1e-2)
+    dec.close()
+    om.close()
+
+
 def test_decode_bounds_follow_step_positions(gpu, xe):
     """decode() bounds every stream by its own position, as step() left it:
     feed 4 tokens, step one stream at max_ctx - 1, then decode must refuse
