@@ -288,10 +288,11 @@ GEMV_SHAPES = [(3072, 768), (768, 3072), (6912, 1152), (4096, 4096), (14336, 409
 ROTATE_BYTES = 512 << 20   # weight copies per shape: >= 2x the 256 MB last-level cache
 
 
-def gemv_case(xe, dev, ctx, wd, m, k, batches, seed, eager):
+def gemv_case(xe, dev, ctx, wd, m, k, batches, seed, eager, reps=0):
     """Config 2: LayerNorm(x) then W x for one weight format and shape, over
     enough device-resident copies of W (synthetic) to stream >= 512 MB per
-    rotation; returns one record per batch size."""
+    rotation; returns one record per batch size.  reps: passes over the
+    copies (0: sized from the bytes)."""
     es = {xe.XE_I8: 1.0, xe.XE_BFP16: 1.125, xe.XE_BF16: 2.0}[wd]
     per = int(m * k * es) + (4 * m if wd == xe.XE_I8 else 0)
     n = max(2, min(256, -(-ROTATE_BYTES // per)))
@@ -323,8 +324,8 @@ def gemv_case(xe, dev, ctx, wd, m, k, batches, seed, eager):
     name = {xe.XE_I8: "int8", xe.XE_BFP16: "bfp16", xe.XE_BF16: "bf16"}[wd]
     for b in batches:
         est_us = per / 5e6
-        reps = int(max(3, min(400, 3e5 / (n * est_us))))
-        us = ctx.probe_gemv(views, xb.ptr, xe.XE_BF16, b, yb.ptr, reps, eager)
+        nrep = reps or int(max(3, min(400, 3e5 / (n * est_us))))
+        us = ctx.probe_gemv(views, xb.ptr, xe.XE_BF16, b, yb.ptr, nrep, eager)
         by = per + b * k * 2 + b * m * 4 + 8 * k
         out.append({"kernel": "LN+GEMV %s %dx%d b=%d" % (name, m, k, b), "us": round(us, 3),
                     "bytes": by, "gbps": round(by / us / 1e3, 1),
@@ -423,14 +424,14 @@ def run_kernels(args):
                 "kernels": recs}
     for wd in (xe.XE_I8, xe.XE_BFP16, xe.XE_BF16):
         for (m, k) in GEMV_SHAPES:
-            recs += gemv_case(xe, dev, ctx, wd, m, k, (1, 4, 8), args.seed + m + k, args.eager)
+            recs += gemv_case(xe, dev, ctx, wd, m, k, (1, 4, 8), args.seed + m + k, args.eager, args.reps)
     for (hq, hkv, hd) in ((12, 12, 64), (4, 1, 256)):
         for mc in (128, 1024, 4096, 32768):
             for b in (1, 16, 64):
                 recs.append(attn_case(xe, dev, ctx, hq, hkv, hd, mc, b, args.seed + mc + b,
-                                      args.eager))
+                                      args.eager, reps=args.reps))
     for name, m, k in GEMM_SHAPES:
-        recs.append(gemm_case(xe, dev, ctx, name, m, k, 64, args.seed + m + k, args.eager))
+        recs.append(gemm_case(xe, dev, ctx, name, m, k, 64, args.seed + m + k, args.eager, args.reps))
     ctx.close()
     dev.close()
     return {"metric": "isolated kernel HBM GB/s (BASELINE configs 2 and 3)", "unit": "GB/s",
@@ -526,7 +527,8 @@ def main():
     ap.add_argument("--gemm-only", action="store_true",
                     help="with --kernels: only the b = 64 step's kernels (projection GEMMs, "
                          "attention at the mean context)")
-    ap.add_argument("--reps", type=int, default=0, help="--kernels GEMMs: repetitions (0: by size)")
+    ap.add_argument("--reps", type=int, default=0,
+                    help="--kernels: repetitions of every case (0: by size; small for counter runs)")
     ap.add_argument("--copies", type=int, default=0, help="--kernels GEMMs: weight copies (0: >= 512 MB)")
     ap.add_argument("--eager", action="store_true",
                     help="--kernels with plain launches instead of graph replays (for runs under "
