@@ -658,8 +658,17 @@ __host__ __device__ constexpr int ks_lds_dw() {
                                                                        : 4 * 16 * NJ * (16 * MB + 4);
 }
 
-// NJ: stream blocks of 16 a tile (BN = 16 NJ streams: 16, 32 or 64).
-template <int WT, int MB, int NJ>
+// NJ: stream blocks of 16 a tile (BN = 16 NJ streams: 16, 32 or 64).  EC
+// (bfp16): the exponent bytes read with plain (L2-cached) loads instead of
+// streaming ones.  Each 128-byte line of a row's exponents serves several
+// steps, and a streamed line was fetched again (14336 x 4096 at 4 / 8
+// streams: 1.35x the algorithmic bytes, 47.0 / 49.2 us; cached 40.4 / 41.6
+// us, 4096 x 4096: -2 / -4 %), but a small tile, bound by latency rather
+// than bytes, loses with cached loads (3072 x 768 at 4 / 8 streams, 16 rows
+// x 768 a tile: 7.9 / 8.2 against 8.9 / 9.0 us).  So cached from kEcElems
+// weights a split tile.
+constexpr int kEcElems = 65536;
+template <int WT, int MB, int NJ, bool EC = false>
 __global__ __launch_bounds__(kGT) void gemm_ks_kernel(gdev::GemvParams p, float *ws, unsigned *cnt, int spk) {
   constexpr int BM = 16 * MB, BN = 16 * NJ;
   constexpr int WD = w_slice_dw<WT>(), WDP = WD + 4;
@@ -736,7 +745,7 @@ __global__ __launch_bounds__(kGT) void gemm_ks_kernel(gdev::GemvParams p, float 
       if constexpr (WT == XE_BFP16) {
         const int erow = m0 + 16 * mb + lr, ek = k0 + 8 * lq;
         st.e[mb] = __builtin_amdgcn_raw_buffer_load_b8(re, erow < p.m && ek < kend ? erow * (K / 8) + ek / 8 : kNoRec,
-                                                      0, 2);
+                                                      0, EC ? 0 : 2);
       }
     }
   };
@@ -1185,31 +1194,34 @@ GemmFn pick_mb(int mb) {
   return nullptr;
 }
 
-template <int WT, int NJ>
+template <int WT, int NJ, bool EC = false>
 GemmFn pick_ks_mb(int mb) {
   switch (mb) {
-    case 1: return gemm_ks_kernel<WT, 1, NJ>;
-    case 2: return gemm_ks_kernel<WT, 2, NJ>;
-    case 4: return gemm_ks_kernel<WT, 4, NJ>;
+    case 1: return gemm_ks_kernel<WT, 1, NJ, EC>;
+    case 2: return gemm_ks_kernel<WT, 2, NJ, EC>;
+    case 4: return gemm_ks_kernel<WT, 4, NJ, EC>;
   }
   return nullptr;
 }
 
-template <int WT>
+template <int WT, bool EC = false>
 GemmFn pick_ks_nj(int mb, int nj) {
   switch (nj) {
-    case 1: return pick_ks_mb<WT, 1>(mb);
-    case 2: return pick_ks_mb<WT, 2>(mb);
-    case 4: return pick_ks_mb<WT, 4>(mb);
+    case 1: return pick_ks_mb<WT, 1, EC>(mb);
+    case 2: return pick_ks_mb<WT, 2, EC>(mb);
+    case 4: return pick_ks_mb<WT, 4, EC>(mb);
   }
   return nullptr;
 }
 
-GemmFn pick_ks(int wdtype, int mb, int nj) {
+// spk: steps a K split spans (bfp16 exponents cached from kEcElems weights a
+// split tile: 16 mb rows x spk steps of kKsBK)
+GemmFn pick_ks(int wdtype, int mb, int nj, int spk) {
   switch (wdtype) {
     case XE_I8: return pick_ks_nj<XE_I8>(mb, nj);
     case XE_BF16: return pick_ks_nj<XE_BF16>(mb, nj);
-    case XE_BFP16: return pick_ks_nj<XE_BFP16>(mb, nj);
+    case XE_BFP16:
+      return 16 * mb * spk * kKsBK >= kEcElems ? pick_ks_nj<XE_BFP16, true>(mb, nj) : pick_ks_nj<XE_BFP16>(mb, nj);
     case XE_I4: return pick_ks_nj<XE_I4>(mb, nj);
   }
   return nullptr;
@@ -1430,7 +1442,7 @@ void launch_gemm(const gdev::GemvParams &p, int wdtype, float *ws, unsigned *cnt
   const GemmShape gk = gemm_ks_shape(p.m, p.k, p.batch);
   if (gk.mb > 0) {
     g = gk;
-    fn = pick_ks(wdtype, g.mb, g.nj);
+    fn = pick_ks(wdtype, g.mb, g.nj, g.spk);
   } else {
     fn = pick_gemm(wdtype, g.mb);
   }
